@@ -1,0 +1,106 @@
+// Internal declarations shared by the HIP sources of libdj.so (runtime, kernels, launchers).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+#include <unordered_map>
+#include <vector>
+#include "../../include/dj.h"
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- errors
+int dj_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+#define DJ_HIP(call)                                                                                   \
+  do {                                                                                                 \
+    hipError_t e_ = (call);                                                                            \
+    if (e_ != hipSuccess) return dj_fail(DJ_EHIP, "decision.js: %s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+#define DJ_REQUIRE(cond, ...)                       \
+  do {                                              \
+    if (!(cond)) return dj_fail(DJ_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+// ---------------------------------------------------------------- objects
+struct dj_weight {
+  int N = 0, K = 0, bits = 0, layout = 0;
+  uint8_t *codes = nullptr;   // device: plain [N, K*bits/8] or the MFMA block layout
+  void *scales = nullptr;     // device: plain f16 [N, K/32] or packed u32 pairs (MFMA)
+  size_t code_bytes = 0, scale_bytes = 0;
+};
+
+struct dj_snapshot {
+  void *staging;  // device copy taken in stream order
+  size_t bytes;
+  void *host;
+};
+
+struct dj_graph_entry {
+  hipGraphExec_t exec = nullptr;
+  std::vector<void *> staging;  // snapshot buffers written by the graph, reused on replay
+  std::vector<size_t> staging_bytes;
+};
+
+struct dj_prof_slot {
+  const char *name;
+  hipEvent_t a, b;
+};
+
+struct dj_ctx {
+  int device = 0;
+  int cus = 0;
+  hipStream_t stream = nullptr;
+  std::unordered_map<void *, size_t> buffers;
+  std::vector<dj_weight *> weights;
+  // pinned staging for dj_upload (bump allocated, reset when the stream is drained)
+  uint8_t *pinned = nullptr;
+  size_t pinned_cap = 0, pinned_used = 0;
+  // graph cache
+  std::unordered_map<uint64_t, dj_graph_entry> graphs;
+  dj_rec *active = nullptr;
+  // timers
+  hipEvent_t t0 = nullptr, t1 = nullptr;
+  // profiling
+  bool profiling = false;
+  std::vector<dj_prof_slot> prof_pending;
+  std::vector<hipEvent_t> event_pool;
+  std::unordered_map<std::string, std::pair<double, int64_t>> prof;
+  std::vector<std::string> prof_order;
+  std::string fault_op;  // DJ_FAULT_INJECT
+};
+
+struct dj_rec {
+  dj_ctx *ctx = nullptr;
+  uint64_t key = 0;
+  bool capturing = false;
+  bool replay = false;
+  size_t snap_index = 0;
+  std::vector<dj_snapshot> snaps;
+  int error = 0;
+};
+
+// ---------------------------------------------------------------- launch plumbing
+// Opens an op: validates the recorder, honours replay (ops ignored) and fault injection, and starts a
+// profiling slot. Returns 1 if the op must be skipped (replay), 0 to launch, or a negative status.
+int dj_op_begin(dj_rec *rec, const char *name);
+// Closes an op after its kernel launches: checks the launch and ends the profiling slot.
+int dj_op_end(dj_rec *rec, const char *name);
+
+#define DJ_OP_BEGIN(rec, name)                   \
+  do {                                           \
+    int s_ = dj_op_begin((rec), (name));         \
+    if (s_ == 1) return DJ_OK;                   \
+    if (s_ < 0) return -s_;                      \
+  } while (0)
+
+// ---------------------------------------------------------------- launchers (one per kernel family)
+int dj_launch_gemm(hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
+                   const char **name);
+int dj_launch_attention(hipStream_t s, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
+                        dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, uint16_t *O);
+int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);
+
+static inline int dj_cdiv(long a, long b) { return (int)((a + b - 1) / b); }

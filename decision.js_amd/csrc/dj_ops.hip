@@ -1,0 +1,424 @@
+// Memory-bound kernels of the scoring path and their C-ABI entry points: embedding gather, residual +
+// RMSNorm, sandwich norm, q/k(/v) norm + RoPE, KV store, answer-row logits, readout, pooling, the small
+// f32 dense head, and the copy used by snapshots. One wave (64 lanes) owns a row wherever a row is
+// reduced, so reductions are shuffles, not shared-memory trees.
+#include <math.h>
+#include "dj_internal.h"
+
+#define WAVE 64
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ _Float16 u2h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
+__device__ __forceinline__ uint16_t h2u(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
+__device__ __forceinline__ float hf(uint16_t u) { return (float)u2h(u); }
+
+// ---------------------------------------------------------------- gather (kernels.ts:6-21, 292-296)
+// X = f16(f16(code) - f16(zp)) * scale: both operands are f16, the product is rounded once (RNE).
+template <int BITS>
+__global__ void k_gather(const uint32_t *__restrict__ ids, int T, int H, int V, const uint8_t *__restrict__ codes,
+                         const uint16_t *__restrict__ scales, uint16_t *__restrict__ X) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = H / 8;
+  if (i >= (long)T * per) return;
+  const int t = (int)(i / per), k0 = (int)(i % per) * 8;
+  uint32_t row = ids[t];
+  if (row >= (uint32_t)V) row = V - 1;
+  const _Float16 s = u2h(scales[(size_t)row * (H / 32) + k0 / 32]);
+  const _Float16 zp = BITS == 8 ? (_Float16)128.0f : (_Float16)8.0f;
+  h8 out;
+  if (BITS == 8) {
+    const uint2 raw = *(const uint2 *)(codes + (size_t)row * H + k0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t c = ((j < 4 ? raw.x : raw.y) >> (8 * (j & 3))) & 255u;
+      out[j] = ((_Float16)(float)c - zp) * s;
+    }
+  } else {
+    const uint32_t raw = *(const uint32_t *)(codes + (size_t)row * (H / 2) + k0 / 2);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = ((_Float16)(float)((raw >> (4 * j)) & 15u) - zp) * s;
+  }
+  *(h8 *)(X + (size_t)t * H + k0) = out;
+}
+
+extern "C" int dj_gather_q(dj_rec *rec, const uint32_t *ids, int T, const dj_weight *e, uint16_t *X) {
+  DJ_REQUIRE(e && e->layout == DJ_W_PLAIN, "decision.js: gather needs a plain (untiled) embedding");
+  DJ_REQUIRE(ids && X && T >= 0 && e->K % 32 == 0, "decision.js: gather: bad arguments");
+  DJ_OP_BEGIN(rec, "gather_q");
+  if (T > 0) {
+    const long n = (long)T * (e->K / 8);
+    if (e->bits == 8)
+      k_gather<8><<<dj_cdiv(n, 256), 256, 0, rec->ctx->stream>>>(ids, T, e->K, e->N, e->codes, (const uint16_t *)e->scales, X);
+    else
+      k_gather<4><<<dj_cdiv(n, 256), 256, 0, rec->ctx->stream>>>(ids, T, e->K, e->N, e->codes, (const uint16_t *)e->scales, X);
+  }
+  return dj_op_end(rec, "gather_q");
+}
+
+// ---------------------------------------------------------------- residual + RMSNorm (kernels.ts:23-46)
+// One wave per row, 8 halves per lane per step; up to MAXC steps stay in registers.
+#define MAXC 8
+__global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, float eps, uint16_t *__restrict__ X,
+                                                     const uint16_t *__restrict__ Y, const uint16_t *__restrict__ W,
+                                                     uint16_t *__restrict__ O) {
+  const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  if (row >= T) return;
+  const size_t base = (size_t)row * H;
+  h8 xs[MAXC];
+  float ss = 0.f;
+  int c = 0;
+  for (int k = lane * 8; k < H; k += WAVE * 8, ++c) {
+    h8 x = *(const h8 *)(X + base + k);
+    if (add) {
+      const h8 y = *(const h8 *)(Y + base + k);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = (float)x[j] + (float)y[j];
+        ss += v * v;  // the unrounded sum, as the reference squares v before storing it
+        x[j] = (_Float16)v;
+      }
+      *(h8 *)(X + base + k) = x;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += (float)x[j] * (float)x[j];
+    }
+    if (c < MAXC) xs[c] = x;
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+  c = 0;
+  for (int k = lane * 8; k < H; k += WAVE * 8, ++c) {
+    const h8 x = c < MAXC ? xs[c] : *(const h8 *)(X + base + k);
+    const h8 w = *(const h8 *)(W + k);
+    h8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)x[j] * inv * (float)w[j]);
+    *(h8 *)(O + base + k) = o;
+  }
+}
+
+extern "C" int dj_add_rmsnorm(dj_rec *rec, int T, int H, int add, float eps, uint16_t *X, const uint16_t *Y,
+                              const uint16_t *W, uint16_t *O) {
+  DJ_REQUIRE(X && W && O && (Y || !add) && T >= 0 && H > 0 && H % 8 == 0,
+             "decision.js: add_rmsnorm: bad arguments (H = %d must be a multiple of 8)", H);
+  DJ_OP_BEGIN(rec, "add_rmsnorm");
+  if (T > 0) k_add_rmsnorm<<<dj_cdiv(T, 4), 256, 0, rec->ctx->stream>>>(T, H, add, eps, X, Y, W, O);
+  return dj_op_end(rec, "add_rmsnorm");
+}
+
+// ---------------------------------------------------------------- sandwich (eg2-kernels.ts:15-48)
+__global__ __launch_bounds__(256) void k_sandwich(int T, int H, float eps, float scale, uint16_t *__restrict__ X,
+                                                  const uint16_t *__restrict__ Y, const uint16_t *__restrict__ W1,
+                                                  const uint16_t *__restrict__ W2, uint16_t *__restrict__ O) {
+  const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  if (row >= T) return;
+  const size_t base = (size_t)row * H;
+  float iy = 0.f;
+  if (Y) {
+    float ss = 0.f;
+    for (int k = lane * 8; k < H; k += WAVE * 8) {
+      const h8 y = *(const h8 *)(Y + base + k);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += (float)y[j] * (float)y[j];
+    }
+    iy = 1.0f / sqrtf(wave_sum(ss) / (float)H + eps);
+  }
+  float ss2 = 0.f;
+  for (int k = lane * 8; k < H; k += WAVE * 8) {
+    h8 x = *(const h8 *)(X + base + k);
+    if (Y) {
+      const h8 y = *(const h8 *)(Y + base + k);
+      const h8 w1 = *(const h8 *)(W1 + k);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = (_Float16)(((float)x[j] + (float)y[j] * iy * (float)w1[j]) * scale);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = (_Float16)((float)x[j] * scale);
+    }
+    *(h8 *)(X + base + k) = x;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss2 += (float)x[j] * (float)x[j];  // the stored residual, as the next block reads it
+  }
+  if (!W2) return;
+  const float ix = 1.0f / sqrtf(wave_sum(ss2) / (float)H + eps);
+  for (int k = lane * 8; k < H; k += WAVE * 8) {
+    const h8 x = *(const h8 *)(X + base + k);
+    const h8 w2 = *(const h8 *)(W2 + k);
+    h8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)x[j] * ix * (float)w2[j]);
+    *(h8 *)(O + base + k) = o;
+  }
+}
+
+extern "C" int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, uint16_t *X, const uint16_t *Y,
+                           const uint16_t *W1, const uint16_t *W2, uint16_t *O) {
+  DJ_REQUIRE(X && (W1 || !Y) && (O || !W2) && T >= 0 && H > 0 && H % 8 == 0, "decision.js: sandwich: bad arguments");
+  DJ_OP_BEGIN(rec, "sandwich");
+  if (T > 0) k_sandwich<<<dj_cdiv(T, 4), 256, 0, rec->ctx->stream>>>(T, H, eps, scale, X, Y, W1, W2, O);
+  return dj_op_end(rec, "sandwich");
+}
+
+// ---------------------------------------------------------------- q/k(/v) norm + RoPE
+// One wave per (token, head). Lane i owns rotation pairs (d, d + rot/2) for d = i, i + 64, ... < rot/2 and
+// the unrotated dims rot + i, rot + i + 64, ... < D.
+__global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, int D, int stride, uint16_t *__restrict__ Z,
+                                                      const uint16_t *__restrict__ qn, const uint16_t *__restrict__ kn,
+                                                      int vnorm, const int32_t *__restrict__ pos, int pos_stride, float eps,
+                                                      float theta, int rot, int mode) {
+  const int per = heads + kv + (vnorm ? kv : 0);
+  const long item = (long)blockIdx.x * 4 + threadIdx.x / WAVE;
+  const int lane = threadIdx.x % WAVE;
+  if (item >= (long)T * per) return;
+  const int t = (int)(item / per), h = (int)(item % per);
+  const bool isQ = h < heads, isK = !isQ && h < heads + kv;
+  const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
+  const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
+  uint16_t *z = Z + (size_t)t * stride + (size_t)h * D;
+  const int half = rot / 2;
+  float a[4], b[4], e[8];
+  float ss = 0.f;
+  int np = 0, ne = 0;
+  for (int d = lane; d < half; d += WAVE, ++np) {
+    a[np] = hf(z[d]);
+    b[np] = hf(z[d + half]);
+    ss += a[np] * a[np] + b[np] * b[np];
+  }
+  for (int d = rot + lane; d < D; d += WAVE, ++ne) {
+    e[ne] = hf(z[d]);
+    ss += e[ne] * e[ne];
+  }
+  float inv = 1.f;
+  if (norm) inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
+  np = 0;
+  ne = 0;
+  const float ps = (float)pos[(size_t)t * pos_stride];
+  for (int d = lane; d < half; d += WAVE, ++np) {
+    float x = a[np] * inv, y = b[np] * inv;
+    if (nw) {
+      x *= hf(nw[d]);
+      y *= hf(nw[d + half]);
+    }
+    if (isQ || isK) {
+      const float ex = (float)(2 * d) / (float)rot;
+      const float f = mode == DJ_ROPE_POW_NEG ? powf(theta, -ex) : 1.0f / powf(theta, ex);
+      const float ang = ps * f;
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      const float x2 = x * cs - y * sn, y2 = y * cs + x * sn;
+      x = x2;
+      y = y2;
+    }
+    z[d] = h2u((_Float16)x);
+    z[d + half] = h2u((_Float16)y);
+  }
+  for (int d = rot + lane; d < D; d += WAVE, ++ne) {
+    float x = e[ne] * inv;
+    if (nw) x *= hf(nw[d]);
+    z[d] = h2u((_Float16)x);
+  }
+}
+
+extern "C" int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
+                               const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta,
+                               int rot, int mode) {
+  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 && rot > 0 && rot <= D && rot % 2 == 0 &&
+                 rot / 2 <= 4 * WAVE && D - rot <= 8 * WAVE && stride >= (heads + 2 * kv) * D,
+             "decision.js: qk_norm_rope: unsupported shape (D %d, rot %d, stride %d)", D, rot, stride);
+  DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: qk_norm_rope: unknown rope mode");
+  DJ_OP_BEGIN(rec, "qk_norm_rope");
+  const long items = (long)T * (heads + kv + (vnorm ? kv : 0));
+  if (items > 0)
+    k_qk_norm_rope<<<dj_cdiv(items, 4), 256, 0, rec->ctx->stream>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos,
+                                                                    pos_stride, eps, theta, rot, mode);
+  return dj_op_end(rec, "qk_norm_rope");
+}
+
+// ---------------------------------------------------------------- KV store (kept prefix of a shared state)
+__global__ void k_kv_store(int T, int width, const uint16_t *__restrict__ Z, int stride, int k_col, uint16_t *__restrict__ C,
+                           int row0) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int per = width / 8;
+  if (i >= (long)T * per) return;
+  const int t = (int)(i / per), c = (int)(i % per) * 8;
+  *(h8 *)(C + (size_t)(row0 + t) * width + c) = *(const h8 *)(Z + (size_t)t * stride + k_col + c);
+}
+
+extern "C" int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z, int stride, int k_col, uint16_t *C, int row0) {
+  const int width = 2 * kv * D;
+  DJ_REQUIRE(Z && C && T >= 0 && row0 >= 0 && width % 8 == 0 && k_col % 8 == 0 && stride % 8 == 0 &&
+                 k_col + width <= stride,
+             "decision.js: kv_store: bad arguments");
+  DJ_OP_BEGIN(rec, "kv_store");
+  const long n = (long)T * (width / 8);
+  if (n > 0) k_kv_store<<<dj_cdiv(n, 256), 256, 0, rec->ctx->stream>>>(T, width, Z, stride, k_col, C, row0);
+  return dj_op_end(rec, "kv_store");
+}
+
+// ---------------------------------------------------------------- block reduction helper (256 threads)
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / WAVE;
+  __syncthreads();
+  if ((threadIdx.x % WAVE) == 0) red[w] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// ---------------------------------------------------------------- answer-row logits (kernels.ts:149-185)
+// normed = f32(X) * inv * f32(w) (kept in f32), dot with (f32(code) - zp) * f32(scale), all in f32.
+template <int BITS>
+__global__ __launch_bounds__(256) void k_leaf_logits(int T, int H, int nIds, float eps, const uint16_t *__restrict__ X,
+                                                     const uint32_t *__restrict__ leaves, const uint16_t *__restrict__ W,
+                                                     const uint32_t *__restrict__ ids, int V, const uint8_t *__restrict__ codes,
+                                                     const uint16_t *__restrict__ scales, float *__restrict__ out) {
+  extern __shared__ float normed[];
+  __shared__ float red[4];
+  const int leaf = blockIdx.x;
+  uint32_t r = leaves[leaf];
+  if (r >= (uint32_t)T) r = T - 1;
+  const size_t row = (size_t)r * H;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < H; k += 256) {
+    const float v = hf(X[row + k]);
+    ss += v * v;
+  }
+  const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
+  for (int k = threadIdx.x; k < H; k += 256) normed[k] = hf(X[row + k]) * inv * hf(W[k]);
+  __syncthreads();
+  const float zp = BITS == 8 ? 128.f : 8.f;
+  for (int j = 0; j < nIds; ++j) {
+    uint32_t id = ids[(size_t)leaf * nIds + j];
+    if (id >= (uint32_t)V) id = V - 1;
+    float dot = 0.f;
+    for (int k = threadIdx.x; k < H; k += 256) {
+      const uint32_t c = BITS == 8 ? codes[(size_t)id * H + k] : (codes[(size_t)id * (H / 2) + k / 2] >> ((k & 1) * 4)) & 15u;
+      dot += normed[k] * ((float)c - zp) * hf(scales[(size_t)id * (H / 32) + k / 32]);
+    }
+    dot = block_sum256(dot, red);
+    if (threadIdx.x == 0) out[(size_t)leaf * nIds + j] = dot;
+  }
+}
+
+extern "C" int dj_leaf_logits(dj_rec *rec, int T, int L, int H, int nIds, float eps, const uint16_t *X, const uint32_t *leaves,
+                              const uint16_t *W, const uint32_t *ids, const dj_weight *e, float *out) {
+  DJ_REQUIRE(e && e->layout == DJ_W_PLAIN && e->K == H, "decision.js: leaf_logits needs the plain embedding [V, %d]", H);
+  DJ_REQUIRE(X && leaves && W && ids && out && T > 0 && L >= 0 && nIds >= 0 && H % 32 == 0 && H <= 16384,
+             "decision.js: leaf_logits: bad arguments");
+  DJ_OP_BEGIN(rec, "leaf_logits");
+  if (L > 0 && nIds > 0) {
+    const size_t sh = (size_t)H * 4;
+    if (e->bits == 8)
+      k_leaf_logits<8><<<L, 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
+                                                         (const uint16_t *)e->scales, out);
+    else
+      k_leaf_logits<4><<<L, 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
+                                                         (const uint16_t *)e->scales, out);
+  }
+  return dj_op_end(rec, "leaf_logits");
+}
+
+// ---------------------------------------------------------------- readout (d3-kernels.ts:242-260)
+__global__ __launch_bounds__(256) void k_readout(int T, int H, const uint16_t *__restrict__ X, const float *__restrict__ R,
+                                                 int codes, const uint32_t *__restrict__ pairs, float *__restrict__ out) {
+  __shared__ float red[4];
+  const int k = blockIdx.x;
+  uint32_t r = pairs[2 * k], c = pairs[2 * k + 1];
+  if (r >= (uint32_t)T) r = T - 1;
+  if (c >= (uint32_t)codes) c = codes - 1;
+  float s = 0.f;
+  for (int d = threadIdx.x; d < H; d += 256) s += hf(X[(size_t)r * H + d]) * R[(size_t)c * H + d];
+  s = block_sum256(s, red);
+  if (threadIdx.x == 0) out[k] = s;
+}
+
+extern "C" int dj_readout(dj_rec *rec, int T, int P, int H, const uint16_t *X, const float *R, int codes, const uint32_t *pairs,
+                          float *out) {
+  DJ_REQUIRE(X && R && pairs && out && T > 0 && P >= 0 && H > 0 && codes > 0, "decision.js: readout: bad arguments");
+  DJ_OP_BEGIN(rec, "readout");
+  if (P > 0) k_readout<<<P, 256, 0, rec->ctx->stream>>>(T, H, X, R, codes, pairs, out);
+  return dj_op_end(rec, "readout");
+}
+
+// ---------------------------------------------------------------- mean pooling (eg2-kernels.ts:202-219)
+__global__ __launch_bounds__(256) void k_mean_pool(int T, int H, const uint16_t *__restrict__ X, const uint32_t *__restrict__ seqs,
+                                                   float *__restrict__ out) {
+  const int s = blockIdx.x;
+  uint32_t a = seqs[2 * s], b = seqs[2 * s + 1];
+  if (b > (uint32_t)T) b = T;
+  if (a > b) a = b;
+  const float n = (float)(b - a);
+  for (int k = threadIdx.x; k < H; k += 256) {
+    float acc = 0.f;
+    for (uint32_t t = a; t < b; ++t) acc += hf(X[(size_t)t * H + k]);
+    out[(size_t)s * H + k] = acc / n;
+  }
+}
+
+extern "C" int dj_mean_pool(dj_rec *rec, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out) {
+  DJ_REQUIRE(X && seqs && out && T > 0 && S >= 0 && H > 0, "decision.js: mean_pool: bad arguments");
+  DJ_OP_BEGIN(rec, "mean_pool");
+  if (S > 0) k_mean_pool<<<S, 256, 0, rec->ctx->stream>>>(T, H, X, seqs, out);
+  return dj_op_end(rec, "mean_pool");
+}
+
+// ---------------------------------------------------------------- small f32 dense (pooled head)
+template <int BITS>
+__global__ __launch_bounds__(256) void k_dense_f32(int M, int N, int K, const float *__restrict__ in, const uint8_t *__restrict__ codes,
+                                                   const uint16_t *__restrict__ scales, float *__restrict__ out) {
+  const int n = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
+  if (n >= N) return;
+  const float zp = BITS == 8 ? 128.f : 8.f;
+  for (int m0 = 0; m0 < M; m0 += 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int k = lane; k < K; k += WAVE) {
+      const uint32_t c = BITS == 8 ? codes[(size_t)n * K + k] : (codes[(size_t)n * (K / 2) + k / 2] >> ((k & 1) * 4)) & 15u;
+      const float w = ((float)c - zp) * hf(scales[(size_t)n * (K / 32) + k / 32]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (m0 + i < M) acc[i] += in[(size_t)(m0 + i) * K + k] * w;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float v = wave_sum(acc[i]);
+      if (lane == 0 && m0 + i < M) out[(size_t)(m0 + i) * N + n] = v;
+    }
+  }
+}
+
+extern "C" int dj_dense_f32(dj_rec *rec, int M, const float *in, const dj_weight *w, float *out) {
+  DJ_REQUIRE(w && w->layout == DJ_W_PLAIN, "decision.js: dense_f32 needs a plain weight");
+  DJ_REQUIRE(in && out && M >= 0, "decision.js: dense_f32: bad arguments");
+  DJ_OP_BEGIN(rec, "dense_f32");
+  if (M > 0) {
+    if (w->bits == 8)
+      k_dense_f32<8><<<dj_cdiv(w->N, 4), 256, 0, rec->ctx->stream>>>(M, w->N, w->K, in, w->codes, (const uint16_t *)w->scales, out);
+    else
+      k_dense_f32<4><<<dj_cdiv(w->N, 4), 256, 0, rec->ctx->stream>>>(M, w->N, w->K, in, w->codes, (const uint16_t *)w->scales, out);
+  }
+  return dj_op_end(rec, "dense_f32");
+}
+
+// ---------------------------------------------------------------- copy (snapshots; a kernel, so it can be captured)
+__global__ void k_copy(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src, size_t bytes) {
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 16;
+  if (i + 16 <= bytes) {
+    *(uint4 *)(dst + i) = *(const uint4 *)(src + i);
+  } else {
+    for (size_t j = i; j < bytes; ++j) dst[j] = src[j];
+  }
+}
+
+int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes) {
+  if (!bytes) return DJ_OK;
+  DJ_REQUIRE(((uintptr_t)dst | (uintptr_t)src) % 16 == 0, "decision.js: snapshot buffers must be 16-byte aligned");
+  k_copy<<<dj_cdiv((long)((bytes + 15) / 16), 256), 256, 0, s>>>((uint8_t *)dst, (const uint8_t *)src, bytes);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return dj_fail(DJ_EHIP, "decision.js: snapshot copy: %s", hipGetErrorString(e));
+  return DJ_OK;
+}

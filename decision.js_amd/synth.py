@@ -1,0 +1,134 @@
+"""Seeded synthetic models in the decision.js format, shaped as the benchmark configurations.
+
+Weights are N(0, 0.02) from numpy PCG64 with seed [0, crc32(tensor name)], quantized with fmt.quantize8 /
+fmt.quantize4 (the exporters' encodings). Norm weights are 1.0 (an untrained model's init) unless
+`norm_std` asks for 1 + N(0, norm_std) (the tests use that, so a wrong norm index cannot hide).
+Layouts follow the exporters: fused qkv = [q; k; v] (export-3b.py:48), fused w13 = [w1; w3]
+(export-3b.py:54) or gate|up (export-eg2.py:206), the tied embedding also read as the LM head (export-3b.py:34).
+"""
+import concurrent.futures as cf
+import copy
+import math
+import os
+import zlib
+
+import numpy as np
+
+from . import fmt
+
+# The BASELINE.json configurations. Choices the configurations leave open are recorded in the config
+# itself ("choices") and written to the manifest.
+CONFIGS = {
+    # Qwen3-0.6B-shaped causal decoder, q8 (the bench workload)
+    "qwen3-0.6b-q8": dict(model="decoder", bits=8, layers=28, hidden=1024, intermediate=3072, heads=16, kv_heads=8,
+                          head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=True,
+                          choices={"norm_weights": 1.0}),
+    # Qwen2.5-3B-shaped causal decoder, q4. No QK-norm; theta and the absent qkv bias are choices.
+    "qwen2.5-3b-q4": dict(model="decoder", bits=4, layers=36, hidden=2048, intermediate=11008, heads=16, kv_heads=2,
+                          head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=False,
+                          choices={"norm_weights": 1.0, "rope_theta": "1e6 (not stated; Qwen2.5's)", "qkv_bias": "none"}),
+    # ~0.8B q8 causal decoder for the shared-state case. QK-norm is a choice (Qwen3 family).
+    "d3lite-0.8b-q8": dict(model="decoder", bits=8, layers=20, hidden=1536, intermediate=4608, heads=12, kv_heads=2,
+                           head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=True,
+                           choices={"norm_weights": 1.0, "qk_norm": "yes (not stated)", "rope_theta": "1e6 (not stated)"}),
+    # EmbeddingGemma-shaped bidirectional encoder, q8, mean-pool + 768->3072->768 head
+    "eg2-encoder-q8": dict(model="encoder", bits=8, layers=24, hidden=768, intermediate=1152, heads=3, kv_heads=1,
+                           head_dim=256, vocab=262144, eps=1e-6, rope_theta=1e4, head_width=3072, embed_dim=768,
+                           choices={"norm_weights": 1.0, "rope_theta": "1e4 (not stated)",
+                                    "embed_scale": "sqrt(hidden) folded into the embedding (export-eg2.py:100)",
+                                    "head": "Linear 768->3072, Linear 3072->768, no activation, q8, f32 on the GPU",
+                                    "attention_scale": 1.0, "layer_scalars": 1.0, "window": "none (all layers global)"}),
+}
+
+
+def reduced(name: str, **over) -> dict:
+    """A configuration with some fields replaced (tests use fewer layers and a smaller vocabulary)."""
+    c = copy.deepcopy(CONFIGS[name])
+    c.update(over)
+    return c
+
+
+def _rng(name: str, seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64([seed, zlib.crc32(name.encode())]))
+
+
+def normal(name: str, shape, std: float = 0.02, seed: int = 0) -> np.ndarray:
+    return (_rng(name, seed).standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def _norm(name, n, norm_std, seed):
+    if not norm_std:
+        return np.ones(n, dtype=np.float32)
+    return 1.0 + normal(name, (n,), norm_std, seed)
+
+
+def tensor_plan(cfg: dict):
+    """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
+    H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
+    plan = [("embed", "q", (V, H))]
+    if cfg["model"] == "decoder":
+        plan.append(("final_norm", "n", (H,)))
+        for i in range(L):
+            p = f"layers.{i}."
+            plan += [(p + "operator_norm", "n", (H,)), (p + "ffn_norm", "n", (H,)), (p + "qkv", "q", ((h + 2 * kv) * D, H)),
+                     (p + "o_proj", "q", (H, h * D)), (p + "w13", "q", (2 * I, H)), (p + "w2", "q", (H, I))]
+            if cfg.get("qk_norm"):
+                plan += [(p + "q_norm", "n", (D,)), (p + "k_norm", "n", (D,))]
+    else:
+        for i in range(L):
+            p = f"layers.{i}."
+            plan += [(p + "qkv", "q", ((h + 2 * kv) * D, H)), (p + "q_norm", "n", (D,)), (p + "k_norm", "n", (D,)),
+                     (p + "o", "q", (H, h * D)), (p + "gu", "q", (2 * I, H)), (p + "down", "q", (H, I))]
+            for n in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm", "post_feedforward_layernorm"):
+                plan.append((p + n, "n", (H,)))
+        plan += [("final_norm", "n", (H,)), ("head.dense1", "q", (cfg["head_width"], H)),
+                 ("head.dense2", "q", (cfg["embed_dim"], cfg["head_width"]))]
+    return plan
+
+
+def manifest_config(cfg: dict) -> dict:
+    c = {k: v for k, v in cfg.items() if k not in ("bits",)}
+    c["layer_types"] = ["full_attention"] * cfg["layers"]
+    if cfg["model"] == "decoder":
+        c["model"] = "decoder"
+    else:
+        c["model"] = "eg2-encoder"
+        c["layer_scalars"] = [1.0] * cfg["layers"]
+        c["attention_scale"] = 1.0
+        c["embed_scale"] = math.sqrt(cfg["hidden"])
+    return c
+
+
+def _make(cfg, name, kind, shape, seed, norm_std):
+    if kind == "n":
+        return name, kind, _norm(name, shape[0], norm_std, seed), None
+    w = normal(name, shape, 0.02, seed)
+    if name == "embed" and cfg["model"] != "decoder":
+        w = w * np.float32(math.sqrt(cfg["hidden"]))  # Gemma's sqrt(hidden) embedding scale, folded in
+    q = fmt.quantize8(w) if cfg["bits"] == 8 else fmt.quantize4(w)
+    return name, kind, q[0], q[1]
+
+
+def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads: int = 8) -> str:
+    """Writes manifest.json + weights.bin for `cfg` under `out`; returns `out`. Skips the work when a
+    manifest with the same configuration and seed already exists there."""
+    mc = manifest_config(cfg)
+    mc["synthetic"] = {"seed": seed, "norm_std": norm_std}
+    if os.path.exists(os.path.join(out, "manifest.json")):
+        try:
+            if fmt.load_manifest(out)["config"] == mc:
+                return out
+        except Exception:  # noqa: BLE001 (a broken earlier write: regenerate)
+            pass
+    blob = fmt.Blob(out, mc, cfg["bits"])
+    plan = tensor_plan(cfg)
+    with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+        futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std) for n, k, s in plan]
+        for (name, kind, shape), fut in zip(plan, futs):
+            _, _, a, b = fut.result()
+            if kind == "n":
+                blob.f16(name, a)
+            else:
+                blob.put_quant(name, a, b, shape, cfg["bits"])
+    blob.close({"repo": "synthetic", "revision": None, "seed": seed})
+    return out

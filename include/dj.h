@@ -1,0 +1,218 @@
+/* dj.h — the C ABI of the MI355X (gfx950) scoring path of decision.js.
+ *
+ * It replaces the WebGPU layer of the reference: src/gpu.ts (device, weight upload, tiled weights,
+ * recorder, profiling) and the WGSL kernels of src/kernels.ts, src/d3-kernels.ts, src/eg2-kernels.ts and
+ * src/encoder-kernels.ts. The engines (host packing + dispatch order) stay on the host side and call this
+ * library; every pointer called `dev` below is device memory from dj_buf_alloc, every `host` pointer is
+ * ordinary host memory. No type from PyTorch or any other framework appears here.
+ *
+ * Conventions
+ *  - Every function returns DJ_OK (0) or a nonzero DJ_E* status; dj_last_error() then holds a message
+ *    ("decision.js: ..."), thread-local, like the reference's thrown Error (gpu.ts:260, d1.ts:68).
+ *  - Activations are IEEE binary16 stored as uint16_t; reductions run in f32 (kernels.ts:1).
+ *  - Ops take a recorder (dj_rec): they are queued on the context's HIP stream in call order and run when
+ *    dj_rec_finish() is called, as the reference records one command buffer per forward (gpu.ts:176-281).
+ *  - One forward at a time per context (the reference's D1.queue, d1.ts:112-119). Not thread-safe.
+ */
+#ifndef DJ_H
+#define DJ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DJ_ABI_VERSION 1
+
+enum {
+  DJ_OK = 0,
+  DJ_EINVAL = 1,    /* bad argument (shape, null pointer, unsupported combination) */
+  DJ_EHIP = 2,      /* the HIP runtime reported an error */
+  DJ_ENOMEM = 3,    /* device or host allocation failed */
+  DJ_ESTATE = 4,    /* call out of order (e.g. an op outside a recorder) */
+  DJ_EINJECT = 5,   /* an error forced by DJ_FAULT_INJECT (tests of the host's error path) */
+};
+
+typedef struct dj_ctx dj_ctx;
+typedef struct dj_rec dj_rec;
+typedef struct dj_weight dj_weight;
+
+/* ---------------------------------------------------------------- errors, version */
+
+/* The message of the last failed call on this thread ("" if none).
+ * Replaces: the thrown `Error("decision.js: ...")` of gpu.ts:66, 78, 260 and d1.ts:68. */
+const char *dj_last_error(void);
+int dj_abi_version(void);
+
+/* ---------------------------------------------------------------- device (gpu.ts:38-54) */
+
+/* Opens HIP device `ordinal` with one stream of default priority.
+ * Replaces: requestDevice() (gpu.ts:38-54) and `new GpuEngine(device, ...)` (gpu.ts:101-105). */
+int dj_init(int ordinal, dj_ctx **out);
+/* Frees everything the context still owns (buffers, weights, cached graphs).
+ * Replaces: GpuEngine.destroy (gpu.ts:108-110) / D1.destroy (d1.ts:108-110). */
+int dj_destroy(dj_ctx *ctx);
+/* Device name (gcnArchName), compute units and total memory; `name` gets at most `cap` bytes. */
+int dj_device_info(dj_ctx *ctx, char *name, size_t cap, int *compute_units, size_t *total_mem);
+
+/* ---------------------------------------------------------------- buffers (gpu.ts:148-174, 235-267) */
+
+/* Device buffer of `bytes` (rounded up to 256). Replaces storage()/activations()/activationRows(). */
+int dj_buf_alloc(dj_ctx *ctx, size_t bytes, void **dev);
+int dj_buf_free(dj_ctx *ctx, void *dev);
+/* Synchronous copies between host and device memory (load-time uploads: queue.writeBuffer, gpu.ts:69). */
+int dj_buf_write(dj_ctx *ctx, void *dev, const void *host, size_t bytes);
+int dj_buf_read(dj_ctx *ctx, void *host, const void *dev, size_t bytes);
+
+/* ---------------------------------------------------------------- weights (gpu.ts:6-11, 57-88, 114-133) */
+
+enum {
+  DJ_W_PLAIN = 0,   /* kept in the file's layout: rows gathered (GATHER_Q8/Q4) and read as LM head (LEAF_LOGITS) */
+  DJ_W_MFMA = 1,    /* repacked for the q8/q4 block-dequant MFMA GEMM (dj_matmul) */
+  DJ_W_MFMA_GLU = 2 /* as DJ_W_MFMA for a fused [w1; w3] (N = 2I), 16-column blocks of w1 and w3 interleaved
+                       so one output tile holds a gate column and its up column (dj_matmul_glu) */
+};
+
+/* A quantized weight [N, K] from the weights.bin encodings of export_common.py:4-7, 64-97:
+ *   bits 8: codes u8 [N, K] (code = q + 128), scales f16 [N, K/32]
+ *   bits 4: codes u8 [N, K/2] (two codes per byte, low nibble first, code = q + 8), scales f16 [N, K/32]
+ * `codes`/`scales` are host pointers; the device copy is repacked per `layout` and owned by the context.
+ * Replaces: loadWeights' per-tensor upload (gpu.ts:63-85) and tileWeights (gpu.ts:114-133,
+ * kernels.ts:522-543), keeping the weights quantized. K % 32 == 0; N % 16 == 0 and K % 64 == 0 for MFMA. */
+int dj_weight_q(dj_ctx *ctx, const void *codes, const void *scales, int N, int K, int bits, int layout,
+                dj_weight **out);
+int dj_weight_free(dj_ctx *ctx, dj_weight *w);
+/* Device bytes the weight occupies (codes + scales). */
+size_t dj_weight_bytes(const dj_weight *w);
+
+/* ---------------------------------------------------------------- recorder (gpu.ts:176-281) */
+
+/* Starts recording a forward. graph_key == 0: ops are launched as they are recorded. graph_key != 0: the
+ * forward is captured once into a HIP graph cached under that key; on later calls with the same key
+ * *replay is set to 1, the host may skip the op calls (they are ignored) and dj_rec_finish relaunches
+ * the graph. The key must change whenever a shape, a pointer or a scalar argument of any op changes.
+ * Replaces: recorder() (gpu.ts:177-183). */
+int dj_rec_begin(dj_ctx *ctx, uint64_t graph_key, dj_rec **out, int *replay);
+/* Asynchronous host->device copy ordered before the recorder's ops (per-forward metadata: ids, meta,
+ * leaves...). `host` is copied into pinned staging memory at once, so it may be reused on return.
+ * Replaces: storage(view) (gpu.ts:148-152). Not allowed while capturing a graph: upload first. */
+int dj_upload(dj_ctx *ctx, void *dev, const void *host, size_t bytes);
+/* Copies `bytes` of device memory into `host` once the forward has run (filled by dj_rec_finish).
+ * Replaces: snapshot(buf, bytes, type) (gpu.ts:237-244). */
+int dj_rec_snapshot(dj_rec *rec, const void *dev, size_t bytes, void *host);
+/* Runs (or replays) the forward, waits for it, fills the snapshots, and frees the recorder.
+ * Replaces: finish(tokens) (gpu.ts:245-279). */
+int dj_rec_finish(dj_rec *rec);
+/* Drops every cached graph (call after reallocating buffers a cached graph points to). */
+int dj_graph_clear(dj_ctx *ctx);
+
+/* ---------------------------------------------------------------- timing and profiling (gpu.ts:29-34, 185-197) */
+
+/* HIP events on the context's stream around whatever is queued between begin and end; end waits. */
+int dj_timer_begin(dj_ctx *ctx);
+int dj_timer_end(dj_ctx *ctx, float *ms);
+/* Per-kernel GPU time: when on, every op launch is bracketed by events and its time is added to a table
+ * keyed by kernel name (the reference's globalThis.__d1Profile map). Ops in a captured graph are not
+ * profiled. dj_profile_get copies up to `cap` entries and returns the count in *n. */
+int dj_profile_enable(dj_ctx *ctx, int on);
+typedef struct { char name[48]; double ms; int64_t launches; } dj_profile_entry;
+int dj_profile_get(dj_ctx *ctx, dj_profile_entry *out, int cap, int *n);
+int dj_profile_reset(dj_ctx *ctx);
+
+/* ---------------------------------------------------------------- ops: embedding and norms */
+
+/* X[t, :] = dequant(embed row ids[t]) in f16, X = f16(f16(code) - f16(zp)) * scale (RNE), t < T.
+ * `embed` must be DJ_W_PLAIN, q8 or q4; ids past the vocabulary read its last row (as WebGPU's robust
+ * buffer access keeps such reads in bounds). Replaces GATHER_Q8 / GATHER_Q4 (kernels.ts:6-21, 292-296). */
+int dj_gather_q(dj_rec *rec, const uint32_t *ids_dev, int T, const dj_weight *embed, uint16_t *X_dev);
+
+/* Per row t < T of H: if add, X += Y (stored f16); O = f16(f32(X) * rsqrt(mean(x^2) + eps) * w), where the
+ * sum of squares uses the unrounded sum and the product the stored X.
+ * Replaces ADD_RMSNORM (kernels.ts:23-46). */
+int dj_add_rmsnorm(dj_rec *rec, int T, int H, int add, float eps, uint16_t *X_dev, const uint16_t *Y_dev,
+                   const uint16_t *w_dev, uint16_t *O_dev);
+
+/* Gemma sandwich norm per row: X = f16((X + rmsnorm(Y) * w1) * scale); if w2_dev, O = rmsnorm(f16 X) * w2.
+ * Replaces SANDWICH (eg2-kernels.ts:15-48) for any H (the reference hard-codes 512). Y_dev may be NULL
+ * (a zero branch: X is only renormalized, eg2-engine.ts:336). */
+int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, uint16_t *X_dev, const uint16_t *Y_dev,
+                const uint16_t *w1_dev, const uint16_t *w2_dev, uint16_t *O_dev);
+
+/* ---------------------------------------------------------------- ops: quantized matmul */
+
+/* Y[M, N] = X[M, K] . W^T, f16 in and out, f32 accumulation on f16 MFMA, W dequantized in registers
+ * exactly as the gather (bit-exact f16 weights). `w` must be DJ_W_MFMA. X rows are M (no padding needed).
+ * Replaces recorder().matmul (gpu.ts:202-226) and MATMUL_Q8/Q4_SG32, MATMUL_DIRECT, matmulSplitK,
+ * matmulPortable* (kernels.ts:298-385, 441-520, 545-768). */
+int dj_matmul(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *Y_dev, int M);
+
+enum { DJ_ACT_SILU = 0, DJ_ACT_GELU_TANH = 1 };
+/* Fused gated MLP input: for w = [w1; w3] (N = 2I, layout DJ_W_MFMA_GLU), Hout[M, I] =
+ * f16(act(a) * b) with a = f16(X . w1^T), b = f16(X . w3^T) (rounded as the f16 matmul output).
+ * act SILU: a / (1 + exp(-a)) (SILU_MUL / MATMUL_SWIGLU, kernels.ts:48-60, 591-599);
+ * act GELU_TANH: 0.5 a (1 + tanh(0.7978845608 (a + 0.044715 a^3))), tanh argument clamped to +-15
+ * (GELU_MUL, eg2-kernels.ts:9-13, 165-177). Replaces recorder().swiglu (gpu.ts:229-234). */
+int dj_matmul_glu(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *H_dev, int M, int act);
+
+/* ---------------------------------------------------------------- ops: q/k norm + rope, attention */
+
+enum { DJ_ROPE_POW_NEG = 0,  /* ang = pos * pow(theta, -2d/rot)   (kernels.ts:106, d3-kernels.ts:172) */
+       DJ_ROPE_INV_POW = 1   /* ang = pos * (1 / pow(theta, 2d/rot)) (eg2-kernels.ts:86) */ };
+/* In place on fused rows Z[T, stride] holding [q heads | k heads | v heads] of D each:
+ * per (token, q or k head) RMSNorm over D times qn / kn (skipped when the pointer is NULL: plain RoPE as
+ * encoder-kernels.ts:5-23); if vnorm, v heads get a plain RMSNorm (eg2-kernels.ts:76-81); then half-split
+ * (rotate-half) RoPE on the first `rot` dims (rot == D, or 64 with D = 256 as d3-kernels.ts:169) at
+ * position pos[t * pos_stride]. f32 math, f16 store; the normed value is not rounded before RoPE.
+ * Replaces QK_NORM_ROPE (kernels.ts:86-112), QK_NORM_ROPE_256 (d3-kernels.ts:151-178), ROPE
+ * (encoder-kernels.ts:5-23), QKV_NORM_ROPE (eg2-kernels.ts:50-96), for any even D <= 512. */
+int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, uint16_t *Z_dev,
+                    const uint16_t *qn_dev, const uint16_t *kn_dev, int vnorm, const int32_t *pos_dev,
+                    int pos_stride, float eps, float theta, int rot, int rope_mode);
+
+/* Key/value source of dj_attention: `rows` rows of `stride` halves; K of kv head j at column k_col + j*D,
+ * V at v_col + j*D. Key indices outside [0, rows) are clamped (never read out of bounds). */
+typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_col; } dj_kv_src;
+
+/* O[t, h*D + d] for t < T, h < heads: softmax(scale * q . k) . v over the keys of query t's two ranges
+ * rng[t] = (a0, a1, b0, b1): key rows [a0, a1) of `kvA` and [b0, b1) of `kvB` (empty ranges allowed).
+ * Q rows are Z[t * q_stride + h * D]. GQA: query head h reads kv head h / (heads / kv). f32 scores and
+ * online softmax (m0 = -1e30), output f16(acc / l). This covers the causal forest of ATTENTION
+ * (kernels.ts:114-147; mask of line 135 as ranges), the bidirectional/windowed ranges of eg2 attention
+ * (eg2-kernels.ts:98-163) and the trunk+branch ranges of attention256 (d3-kernels.ts:180-240, without its
+ * gate), and a kept prefix KV (kvA = the cache) for the shared-state mode. D in {64, 128, 256}. */
+int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
+                 dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, uint16_t *O_dev);
+
+/* Copies K and V of rows [0, T) of the fused rows Z into cache rows [row0, row0 + T) of layout
+ * [rows, 2 * kv * D] (K heads then V heads): the kept KV of a prefilled shared state. */
+int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z_dev, int stride, int k_col,
+                uint16_t *cache_dev, int row0);
+
+/* ---------------------------------------------------------------- ops: readouts and pooling */
+
+/* out[l * nIds + j] = rmsnorm_f32(X[leaves[l]]) * w  .  dequant_f32(embed row ids[l * nIds + j]) in f32:
+ * the final norm is recomputed in f32 (not rounded) and the embedding dequantized in f32
+ * ((f32(code) - zp) * f32(scale)). embed q8 or q4, DJ_W_PLAIN. Replaces LEAF_LOGITS (kernels.ts:149-185),
+ * which is q4-only with H <= 2048 in the reference. Leaf rows are clamped to [0, T), ids to the vocabulary. */
+int dj_leaf_logits(dj_rec *rec, int T, int L, int H, int nIds, float eps, const uint16_t *X_dev,
+                   const uint32_t *leaves_dev, const uint16_t *w_dev, const uint32_t *ids_dev,
+                   const dj_weight *embed, float *out_dev);
+
+/* out[k] = X[pairs[2k]] . R[pairs[2k+1]] in f32 (R f32 [codes, H]). Replaces READOUT (d3-kernels.ts:242-260). */
+int dj_readout(dj_rec *rec, int T, int P, int H, const uint16_t *X_dev, const float *R_dev, int codes,
+               const uint32_t *pairs_dev, float *out_dev);
+
+/* out[s, :] = mean of X rows [seqs[2s], seqs[2s+1]) in f32. The pooling half of POOL_PROJECT
+ * (eg2-kernels.ts:202-228), for any H. */
+int dj_mean_pool(dj_rec *rec, int T, int S, int H, const uint16_t *X_dev, const uint32_t *seqs_dev, float *out_dev);
+
+/* out[M, N] = in[M, K] . dequant_f32(W)^T in f32 (f32 activations, weights as LEAF_LOGITS dequantizes them),
+ * for the small dense head after pooling (the projection half of POOL_PROJECT, generalised). W DJ_W_PLAIN. */
+int dj_dense_f32(dj_rec *rec, int M, const float *in_dev, const dj_weight *w, float *out_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DJ_H */

@@ -1,0 +1,467 @@
+"""numpy restatement of decision.js's scoring path (test infrastructure: see oracle/__init__.py).
+
+Precision contract of the reference: activations stored as f16 at the points the WGSL kernels store them,
+every reduction in f32 (kernels.ts:1). Functions take an `acc` dtype (float32 by default; float64 for the
+checks that want a tighter reference).
+"""
+import math
+
+import numpy as np
+
+F16, F32, F64 = np.float16, np.float32, np.float64
+
+
+def f16(x):
+    return np.asarray(x).astype(F16)
+
+
+# ---------------------------------------------------------------- weights (export_common.py, kernels.ts)
+
+def dequant_f16(codes: np.ndarray, scales: np.ndarray, bits: int) -> np.ndarray:
+    """f16 weights [N, K] as the GEMM / gather use them: (f16(code) - f16(zp)) * scale rounded once to f16
+    (kernels.ts:20, 296, 319, 321, 541). The f32 product of two f16 values is exact, so rounding it to f16
+    is the f16 multiply's RNE result."""
+    q = unpack_codes(codes, bits).astype(F32) - (128.0 if bits == 8 else 8.0)
+    s = np.repeat(scales.astype(F32), 32, axis=1)
+    return (q * s).astype(F16)
+
+
+def dequant_f32(codes, scales, bits) -> np.ndarray:
+    """f32 weights as LEAF_LOGITS reads them: (f32(code) - zp) * f32(scale) (kernels.ts:177-178)."""
+    q = unpack_codes(codes, bits).astype(F32) - (128.0 if bits == 8 else 8.0)
+    return q * np.repeat(scales.astype(F32), 32, axis=1)
+
+
+def unpack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """u8 codes [N, K] from the stored bytes (q4: low nibble first, export_common.py:87)."""
+    if bits == 8:
+        return codes
+    lo, hi = codes & 15, codes >> 4
+    return np.stack([lo, hi], axis=-1).reshape(codes.shape[0], -1)
+
+
+def gather(ids, codes, scales, bits):
+    """GATHER_Q8 / GATHER_Q4 (kernels.ts:6-21, 292-296): rows of the f16-dequantized embedding."""
+    ids = np.minimum(np.asarray(ids, dtype=np.int64), codes.shape[0] - 1)
+    return dequant_f16(codes[ids], scales[ids], bits)
+
+
+# ---------------------------------------------------------------- norms
+
+def add_rmsnorm(X, Y, w, eps, add=True, acc=F32):
+    """ADD_RMSNORM (kernels.ts:23-46): v = f32(X) + f32(Y), X <- f16(v); the sum of squares of the unrounded
+    v; O = f16(f32(X_f16) * inv * f32(w)). Returns (X_new, O)."""
+    x = X.astype(acc)
+    if add:
+        x = x + Y.astype(acc)
+    ss = (x * x).sum(-1, keepdims=True, dtype=acc)
+    Xn = x.astype(F16)
+    inv = (1.0 / np.sqrt(ss / X.shape[-1] + eps)).astype(acc)
+    O = (Xn.astype(acc) * inv * w.astype(acc)).astype(F16)
+    return Xn, O
+
+
+def sandwich(X, Y, w1, w2, eps, scale, acc=F32):
+    """SANDWICH (eg2-kernels.ts:15-48): X = f16((X + rmsnorm(Y) w1) * scale); O = f16(rmsnorm(f16 X) w2)."""
+    H = X.shape[-1]
+    x = X.astype(acc)
+    if Y is not None:
+        y = Y.astype(acc)
+        iy = 1.0 / np.sqrt((y * y).sum(-1, keepdims=True) / H + eps)
+        x = x + y * iy * w1.astype(acc)
+    Xn = (x * acc(scale)).astype(F16)
+    if w2 is None:
+        return Xn, None
+    a = Xn.astype(acc)
+    ix = 1.0 / np.sqrt((a * a).sum(-1, keepdims=True) / H + eps)
+    return Xn, (a * ix * w2.astype(acc)).astype(F16)
+
+
+# ---------------------------------------------------------------- matmul and gated MLP
+
+def matmul(X, W16, acc=F32):
+    """Y = f16(X . W^T) with W the f16-dequantized weight; f32 (or f64) accumulation (kernels.ts:441-520
+    portable path; the matrix-unit path adds f16 partials every 128 K, kernels.ts:301-302)."""
+    return (X.astype(acc) @ W16.astype(acc).T).astype(F16)
+
+
+def silu_mul(a16, b16, acc=F32):
+    """SILU_MUL (kernels.ts:48-60) / MATMUL_SWIGLU (kernels.ts:597): f16(a / (1 + exp(-a)) * b), a, b the
+    f16 matmul outputs."""
+    a, b = a16.astype(acc), b16.astype(acc)
+    return (a / (1.0 + np.exp(-a)) * b).astype(F16)
+
+
+def gelu_tanh(x):
+    """gelu of eg2-kernels.ts:9-13: tanh form with the argument clamped to +-15."""
+    u = np.clip(0.7978845608 * (x + 0.044715 * x * x * x), -15.0, 15.0)
+    e = np.exp(2.0 * u)
+    return 0.5 * x * (1.0 + (e - 1.0) / (e + 1.0))
+
+
+def gelu_mul(a16, b16, acc=F32):
+    """GELU_MUL (eg2-kernels.ts:165-177): f16(gelu(a) * b)."""
+    return (gelu_tanh(a16.astype(acc)) * b16.astype(acc)).astype(F16)
+
+
+# ---------------------------------------------------------------- q/k norm + rope
+
+def inv_freq(theta, rot, mode=0):
+    """Angle per position of dim pair d: pow(theta, -2d/rot) (kernels.ts:106) or 1/pow(theta, 2d/rot)
+    (eg2-kernels.ts:86), in f32."""
+    d = np.arange(rot // 2, dtype=F32)
+    ex = (F32(2) * d) / F32(rot)
+    if mode == 0:
+        return np.power(F32(theta), -ex).astype(F32)
+    return (F32(1) / np.power(F32(theta), ex)).astype(F32)
+
+
+def qk_norm_rope(Z, heads, kv, D, pos, qn=None, kn=None, vnorm=False, eps=1e-6, theta=1e6, rot=None, mode=0, acc=F32):
+    """QK_NORM_ROPE (kernels.ts:86-112) generalised (QK_NORM_ROPE_256 d3-kernels.ts:151-178, ROPE
+    encoder-kernels.ts:5-23, QKV_NORM_ROPE eg2-kernels.ts:50-96): per head RMSNorm over D times the weight
+    (q with qn, k with kn, v plain when vnorm), then rotate-half RoPE on the first `rot` dims; the normed value
+    is not rounded before RoPE. Z [T, (heads + 2kv) D] f16; returns a new array."""
+    rot = D if rot is None else rot
+    T = Z.shape[0]
+    Z = Z.copy()
+    x = Z[:, :(heads + 2 * kv) * D].reshape(T, heads + 2 * kv, D).astype(acc)
+    out = x.copy()
+
+    def norm(v, w):
+        inv = 1.0 / np.sqrt((v * v).sum(-1, keepdims=True) / D + eps)
+        v = v * inv
+        return v * w.astype(acc) if w is not None else v
+
+    if qn is not None:
+        out[:, :heads] = norm(x[:, :heads], qn)
+    if kn is not None:
+        out[:, heads:heads + kv] = norm(x[:, heads:heads + kv], kn)
+    if vnorm:
+        out[:, heads + kv:] = norm(x[:, heads + kv:], None)
+    f = inv_freq(theta, rot, mode)
+    ang = (np.asarray(pos, dtype=F32)[:, None] * f[None, :]).astype(F32)  # f32 angle, as the kernels
+    c, s = np.cos(ang.astype(F64)).astype(acc), np.sin(ang.astype(F64)).astype(acc)
+    half = rot // 2
+    for sl in (slice(0, heads), slice(heads, heads + kv)):
+        a = out[:, sl, :half].copy()
+        b = out[:, sl, half:rot].copy()
+        out[:, sl, :half] = a * c[:, None, :] - b * s[:, None, :]
+        out[:, sl, half:rot] = b * c[:, None, :] + a * s[:, None, :]
+    Z[:, :(heads + 2 * kv) * D] = out.reshape(T, -1).astype(F16)
+    return Z
+
+
+# ---------------------------------------------------------------- packing (host side of the engines)
+
+def pack_forest(trees):
+    """D13BEngine.run's packing (d1-3b-engine.ts:46-72): per token ids, pos (branch positions continue after
+    the trunk), meta (treeStart, treeEnd, branch or -1, pos); leaves = each branch's last token; leafIds =
+    the flattened answer groups, zero-padded to nIds. trees: [{"trunk", "branches", "groups"}]."""
+    ids, pos, meta, leaves, leaf_ids = [], [], [], [], []
+    for tr in trees:
+        start = len(ids)
+        total = len(tr["trunk"]) + sum(len(b) for b in tr["branches"])
+        p = len(tr["trunk"])
+        for i, t in enumerate(tr["trunk"]):
+            ids.append(t); pos.append(i); meta.append((start, start + total, -1, i))
+        for b, br in enumerate(tr["branches"]):
+            for o, t in enumerate(br):
+                ids.append(t); pos.append(p + o); meta.append((start, start + total, b, p + o))
+            leaves.append(len(ids) - 1)
+            leaf_ids.append([x for g in tr["groups"][b] for x in g])
+    L = len(leaves)
+    n_ids = max((len(x) for x in leaf_ids), default=0)
+    flat = np.zeros(L * n_ids, dtype=np.uint32)
+    for i, g in enumerate(leaf_ids):
+        flat[i * n_ids:i * n_ids + len(g)] = g
+    return (np.array(ids, dtype=np.uint32), np.array(pos, dtype=np.int32), np.array(meta, dtype=np.int32).reshape(-1, 4),
+            np.array(leaves, dtype=np.uint32), flat, n_ids)
+
+
+def forest_mask(meta, bidir=False):
+    """Boolean [T, T] key mask of ATTENTION (kernels.ts:133-136): key k in [start, end) of the query's tree,
+    and (bidir or (k is a trunk token and (the query is a branch token or pos_k <= pos_q)) or (same branch,
+    not the trunk, pos_k <= pos_q))."""
+    T = meta.shape[0]
+    m = np.zeros((T, T), dtype=bool)
+    for t in range(T):
+        s, e, br, p = meta[t]
+        for k in range(s, e):
+            ks, ke, kb, kp = meta[k]
+            ok = bidir or (kb == -1 and (br != -1 or kp <= p)) or (kb == br and br != -1 and kp <= p)
+            m[t, k] = ok
+    return m
+
+
+def forest_ranges(meta):
+    """The forest mask as two key ranges per query (a0, a1, b0, b1): a trunk token i sees [start, start+i+1);
+    a branch token sees the trunk [start, start+P) and its own branch [branch start, itself]."""
+    T = meta.shape[0]
+    rng = np.zeros((T, 4), dtype=np.int32)
+    t = 0
+    while t < T:
+        s, e = meta[t, 0], meta[t, 1]
+        # the trunk: tokens of this tree with branch -1 come first
+        P = 0
+        while s + P < e and meta[s + P, 2] == -1:
+            P += 1
+        for i in range(P):
+            rng[s + i] = (s, s + i + 1, 0, 0)
+        k = s + P
+        while k < e:
+            b, bs = meta[k, 2], k
+            while k < e and meta[k, 2] == b:
+                rng[k] = (s, s + P, bs, k + 1)
+                k += 1
+        t = e
+    return rng
+
+
+def ranges_mask(rng, T_keys):
+    m = np.zeros((rng.shape[0], T_keys), dtype=bool)
+    for t, (a0, a1, b0, b1) in enumerate(rng):
+        m[t, max(a0, 0):max(a1, 0)] = True
+        m[t, max(b0, 0):max(b1, 0)] = True
+    return m
+
+
+def pack_shared(seqs, groups=None):
+    """D3Engine.logits's packing (d3-engine.ts:67-93): per request group, the common id prefix P (at least one
+    token left per question) laid once with rng [ts, ts+P); each question's rest with rng = trunk + itself
+    (bidirectional within the ranges); pairs (last row, option k). seqs: [{"ids", "options"}]."""
+    ids, meta, rng, pairs = [], [], [], []
+    sizes = groups if groups is not None else [1] * len(seqs)
+    si = 0
+    for n in sizes:
+        group = seqs[si:si + n]
+        si += n
+        P = 0
+        if n > 1:
+            lim = min(len(s["ids"]) for s in group) - 1
+            while P < lim and all(s["ids"][P] == group[0]["ids"][P] for s in group):
+                P += 1
+        ts = len(ids)
+        for i in range(P):
+            ids.append(group[0]["ids"][i]); meta.append((ts, ts + P, -1, i)); rng.append((ts, ts + P, 0, 0))
+        for s in group:
+            bs = len(ids)
+            be = bs + len(s["ids"]) - P
+            for i in range(P, len(s["ids"])):
+                ids.append(s["ids"][i]); meta.append((bs, be, -1, i))
+                rng.append((ts if P else bs, ts + P if P else be, bs if P else 0, be if P else 0))
+            for k in range(s["options"]):
+                pairs.append((be - 1, k))
+    return (np.array(ids, dtype=np.uint32), np.array(meta, dtype=np.int32).reshape(-1, 4), np.array(rng, dtype=np.int32).reshape(-1, 4),
+            np.array(pairs, dtype=np.uint32).reshape(-1, 2))
+
+
+def pack_encoder(seqs, window=None):
+    """Eg2Engine.embed's packing (eg2-engine.ts:74-86): meta (start, end, -1, i), full range [start, end),
+    window range [max(start, t-w), min(end, t+w+1)), and per sequence (start, end)."""
+    ids, meta, full, slide, ranges = [], [], [], [], []
+    for s in seqs:
+        start, end = len(ids), len(ids) + len(s)
+        for i, t_id in enumerate(s):
+            t = start + i
+            ids.append(t_id); meta.append((start, end, -1, i)); full.append((start, end, 0, 0))
+            if window is not None:
+                slide.append((max(start, t - window), min(end, t + window + 1), 0, 0))
+        ranges.append((start, end))
+    return (np.array(ids, dtype=np.uint32), np.array(meta, dtype=np.int32).reshape(-1, 4), np.array(full, dtype=np.int32).reshape(-1, 4),
+            np.array(slide, dtype=np.int32).reshape(-1, 4) if window is not None else None, np.array(ranges, dtype=np.uint32).reshape(-1, 2))
+
+
+# ---------------------------------------------------------------- attention
+
+def attention(Z, heads, kv, D, mask, scale, acc=F32, q_stride=None, kv_rows=None):
+    """softmax(scale q.k) v over the allowed keys, per query and head (ATTENTION kernels.ts:114-147 and its
+    tiled/eg2/d3 variants); f32 scores and sums, output f16(acc / l). mask [T, Tk] boolean. Z holds
+    [q | k | v] rows; kv_rows (optional) is a separate [Tk, 2 kv D] array of [k | v] rows."""
+    T = Z.shape[0]
+    q = Z[:, :heads * D].reshape(T, heads, D).astype(acc)
+    if kv_rows is None:
+        k = Z[:, heads * D:(heads + kv) * D].reshape(T, kv, D).astype(acc)
+        v = Z[:, (heads + kv) * D:(heads + 2 * kv) * D].reshape(T, kv, D).astype(acc)
+    else:
+        k = kv_rows[:, :kv * D].reshape(-1, kv, D).astype(acc)
+        v = kv_rows[:, kv * D:2 * kv * D].reshape(-1, kv, D).astype(acc)
+    g = heads // kv
+    out = np.zeros((T, heads, D), dtype=acc)
+    for h in range(heads):
+        s = (q[:, h, :] * acc(scale)) @ k[:, h // g, :].T
+        s = np.where(mask, s, -np.inf)
+        m = np.maximum(s.max(-1, keepdims=True), -1e30)
+        p = np.where(mask, np.exp(s - m), 0.0)
+        out[:, h, :] = (p @ v[:, h // g, :]) / p.sum(-1, keepdims=True)
+    return out.reshape(T, heads * D).astype(F16)
+
+
+# ---------------------------------------------------------------- readouts
+
+def leaf_logits(X, leaves, w, ids, n_ids, codes, scales, bits, eps, acc=F32):
+    """LEAF_LOGITS (kernels.ts:149-185): normed = f32(X[leaf]) * inv * f32(w) (not rounded); dot with the
+    f32-dequantized embedding rows of the leaf's ids; f32 out [L * nIds]."""
+    L = len(leaves)
+    out = np.zeros(L * n_ids, dtype=acc)
+    for l in range(L):
+        x = X[leaves[l]].astype(acc)
+        inv = 1.0 / np.sqrt((x * x).sum(dtype=acc) / X.shape[1] + eps)
+        normed = x * inv * w.astype(acc)
+        for j in range(n_ids):
+            r = int(ids[l * n_ids + j])
+            e = dequant_f32(codes[r:r + 1], scales[r:r + 1], bits)[0].astype(acc)
+            out[l * n_ids + j] = (normed * e).sum(dtype=acc)
+    return out
+
+
+def readout(X, R, pairs):
+    """READOUT (d3-kernels.ts:242-260): out[k] = f32(X[row]) . R[code]."""
+    return np.array([(X[r].astype(F32) * R[c]).sum(dtype=F32) for r, c in pairs], dtype=F32)
+
+
+def mean_pool(X, ranges):
+    """POOL_PROJECT's mean (eg2-kernels.ts:214-218), f32."""
+    return np.stack([X[a:b].astype(F32).mean(0) for a, b in ranges])
+
+
+def dense_f32(inp, codes, scales, bits):
+    """f32 activations times the f32-dequantized weight (the pooled head)."""
+    return (inp.astype(F32) @ dequant_f32(codes, scales, bits).T).astype(F32)
+
+
+# ---------------------------------------------------------------- host tail (gpu.ts, d1.ts, questions.ts)
+
+def softmax(s):
+    """softmax of gpu.ts:294-297 in float64."""
+    s = np.asarray(s, dtype=F64)
+    e = np.exp(s - s.max())
+    return e / e.sum()
+
+
+def group_max(out, n_ids, groups_per_leaf):
+    """The readout of d1-3b-engine.ts:112-121: each option scores the max over its group."""
+    scores = []
+    for leaf, groups in enumerate(groups_per_leaf):
+        j, s = 0, []
+        for g in groups:
+            s.append(max(float(out[leaf * n_ids + j + i]) for i in range(len(g))))
+            j += len(g)
+        scores.append(s)
+    return scores
+
+
+# ---------------------------------------------------------------- whole forwards
+
+class Model:
+    """A decision.js-format model read into host arrays (manifest config + tensors)."""
+
+    def __init__(self, base):
+        import json
+        import os
+        with open(os.path.join(base, "manifest.json")) as f:
+            self.m = json.load(f)
+        self.c = self.m["config"]
+        mm = np.memmap(os.path.join(base, "weights.bin"), dtype=np.uint8, mode="r")
+        self.t = {}
+        for name, info in self.m["tensors"].items():
+            raw = np.asarray(mm[info["offset"]:info["offset"] + info["bytes"]])
+            if info["dtype"] in ("q4", "q8"):
+                N, K = info["shape"]
+                sc = np.asarray(mm[info["scales"]:info["scales"] + info["scales_bytes"]]).view(F16).reshape(N, K // 32)
+                self.t[name] = (raw.reshape(N, -1), sc, 8 if info["dtype"] == "q8" else 4)
+            else:
+                self.t[name] = raw.view(F16 if info["dtype"] == "f16" else F32).reshape(info["shape"])
+        self._w16 = {}
+
+    def w16(self, name):
+        if name not in self._w16:
+            c, s, b = self.t[name]
+            self._w16[name] = dequant_f16(c, s, b)
+        return self._w16[name]
+
+
+def decoder_forward(model: Model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=F32, layers=None, kv_prefix=None,
+                    keep_kv=False, debug_layers=()):
+    """The causal decoder forward of D13BEngine.run (d1-3b-engine.ts:86-106) on attention-only layers:
+    gather -> rmsnorm -> per layer [qkv, qk-norm+rope, attention, o_proj, add+rmsnorm, w13+SwiGLU, w2,
+    add+rmsnorm] -> LEAF_LOGITS at the leaves. kv_prefix: per-layer [P, 2 kv D] kept K/V rows that the mask's
+    first P columns refer to (shared-state mode). Returns (logits [L * nIds], per-layer K/V rows if keep_kv,
+    debug {layer: x})."""
+    c = model.c
+    H, I, h, kv, D, eps = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
+    L = c["layers"] if layers is None else layers
+    ec, es, eb = model.t["embed"]
+    x = gather(ids, ec, es, eb)
+    T = x.shape[0]
+    o = np.zeros_like(x)
+    x, normed = add_rmsnorm(x, o, model.t["layers.0.operator_norm"], eps, add=False, acc=acc)
+    kept, dbg = [], {}
+    for i in range(L):
+        p = f"layers.{i}."
+        z = matmul(normed, model.w16(p + "qkv"), acc)
+        z = qk_norm_rope(z, h, kv, D, pos, model.t.get(p + "q_norm"), model.t.get(p + "k_norm"), False, eps,
+                         c["rope_theta"], acc=acc)
+        if keep_kv:
+            kept.append(z[:, h * D:(h + 2 * kv) * D].copy())
+        if kv_prefix is not None:
+            rows = np.concatenate([kv_prefix[i], z[:, h * D:(h + 2 * kv) * D]])
+            y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc, kv_rows=rows)
+        else:
+            y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc)
+        o = matmul(y, model.w16(p + "o_proj"), acc)
+        x, normed = add_rmsnorm(x, o, model.t[p + "ffn_norm"], eps, acc=acc)
+        ab = matmul(normed, model.w16(p + "w13"), acc)
+        hh = silu_mul(ab[:, :I], ab[:, I:], acc)
+        o = matmul(hh, model.w16(p + "w2"), acc)
+        nxt = f"layers.{i + 1}.operator_norm" if i + 1 < L else "final_norm"
+        x, normed = add_rmsnorm(x, o, model.t[nxt], eps, acc=acc)
+        if i in debug_layers:
+            dbg[i] = x.copy()
+    logits = leaf_logits(x, leaves, model.t["final_norm"], leaf_ids, n_ids, ec, es, eb, eps, acc) if len(leaves) else None
+    return logits, kept, dbg
+
+
+def encoder_forward(model: Model, seqs, acc=F32, layers=None):
+    """The EmbeddingGemma-shaped encoder (Eg2Engine.embed, eg2-engine.ts:103-139, without per-layer embeddings)
+    and the configured head: sandwich norms, q/k/v norm + RoPE, bidirectional attention (scale 1), GeGLU
+    (tanh), mean pool (f32), Linear 768->3072 -> Linear 3072->768 in f32, L2 normalisation."""
+    c = model.c
+    H, I, h, kv, D, eps = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
+    L = c["layers"] if layers is None else layers
+    ids, meta, full, _, ranges = pack_encoder(seqs)
+    mask = ranges_mask(full, len(ids))
+    ec, es, eb = model.t["embed"]
+    x = gather(ids, ec, es, eb)
+    x, normed = sandwich(x, None, None, model.t["layers.0.input_layernorm"], eps, 1.0, acc)
+    for i in range(L):
+        p = f"layers.{i}."
+        z = matmul(normed, model.w16(p + "qkv"), acc)
+        z = qk_norm_rope(z, h, kv, D, meta[:, 3], model.t[p + "q_norm"], model.t[p + "k_norm"], True, eps,
+                         c["rope_theta"], mode=1, acc=acc)
+        y = attention(z, h, kv, D, mask, c.get("attention_scale", 1.0), acc)
+        o = matmul(y, model.w16(p + "o"), acc)
+        x, normed = sandwich(x, o, model.t[p + "post_attention_layernorm"], model.t[p + "pre_feedforward_layernorm"], eps, 1.0, acc)
+        gu = matmul(normed, model.w16(p + "gu"), acc)
+        hh = gelu_mul(gu[:, :I], gu[:, I:], acc)
+        o = matmul(hh, model.w16(p + "down"), acc)
+        nxt = f"layers.{i + 1}.input_layernorm" if i + 1 < L else "final_norm"
+        x, normed = sandwich(x, o, model.t[p + "post_feedforward_layernorm"], model.t[nxt], eps,
+                             c.get("layer_scalars", [1.0] * L)[i], acc)
+    pooled = mean_pool(normed, ranges)
+    d1c, d1s, d1b = model.t["head.dense1"]
+    d2c, d2s, d2b = model.t["head.dense2"]
+    e = dense_f32(dense_f32(pooled, d1c, d1s, d1b), d2c, d2s, d2b)
+    n = np.maximum(np.sqrt((e.astype(F64) ** 2).sum(-1, keepdims=True)), 1e-12)
+    return (e / n).astype(F32)
+
+
+def cosine_scores(state_e, question_e, option_es):
+    """The cosine prior of Eg2Head.logits (eg2-head.ts:82-84, 97): cos(option, state + question)."""
+    anchor = state_e.astype(F64) + question_e.astype(F64)
+    an = max(np.sqrt((anchor ** 2).sum()), 1e-12)
+    out = []
+    for o in option_es:
+        o = o.astype(F64)
+        on = o / max(np.sqrt((o ** 2).sum()), 1e-12)
+        out.append(float((on * anchor).sum() / an))
+    return out

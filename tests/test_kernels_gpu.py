@@ -1,0 +1,392 @@
+"""Kernel-level parity of libdj.so against the oracle (GPU). Every call goes through the C ABI."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _dj():
+    from decision_js_amd import _dj
+    return _dj
+
+
+def _fmt():
+    from decision_js_amd import fmt
+    return fmt
+
+
+def rand_f16(rng, shape, std=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float16)
+
+
+def f16_close(got, want, ulps=1.0, atol=1e-5):
+    """|got - want| <= ulps * 2^-10 |want| + atol, elementwise; returns the worst ratio to the bound."""
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    bound = ulps * 2.0 ** -10 * np.abs(w) + atol
+    return float((np.abs(g - w) / bound).max())
+
+
+def quant(rng, N, K, bits, std=0.02):
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32(std)
+    return (_fmt().quantize8 if bits == 8 else _fmt().quantize4)(w)[:2]
+
+
+def run(ctx, fn):
+    rec = ctx.recorder()
+    fn(rec)
+    return rec.finish()
+
+
+# ---------------------------------------------------------------- gather
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_gather_bit_exact(pkg, ctx, bits):
+    dj = _dj()
+    rng = np.random.default_rng(bits)
+    V, H, T = 300, 1024, 257
+    codes, scales = quant(rng, V, H, bits)
+    # every code value in row 0 and extreme scales in row 1, to cover the whole table
+    c = ref.unpack_codes(codes, bits).copy()
+    c[0] = np.arange(H) % (256 if bits == 8 else 16)
+    codes = c.astype(np.uint8) if bits == 8 else (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+    scales[1] = np.array([6.1e-5, 65504.0 / 300, 1e-3, 0.5] * (H // 128), dtype=np.float16)
+    ids = rng.integers(0, V, T).astype(np.uint32)
+    ids[:3] = [0, 1, V + 50]  # an id past the vocabulary reads the last row
+    E = ctx.weight_q(codes, scales, V, H, bits, dj.W_PLAIN)
+    d_ids, X = ctx.array(ids), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.gather_q(d_ids, T, E, X))
+    got = X.read(np.uint16, (T, H))
+    want = ref.gather(ids, codes, scales, bits).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- norms
+
+@pytest.mark.parametrize("H,add", [(1024, True), (1024, False), (768, True), (2048, True), (1536, True), (4160, True)])
+def test_add_rmsnorm(pkg, ctx, H, add):
+    rng = np.random.default_rng(H + add)
+    T = 133
+    X, Y = rand_f16(rng, (T, H)), rand_f16(rng, (T, H))
+    w = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    dX, dY, dw, dO = ctx.array(X), ctx.array(Y), ctx.array(w), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.add_rmsnorm(T, H, add, 1e-6, dX, dY, dw, dO))
+    Xn, O = ref.add_rmsnorm(X, Y, w, 1e-6, add=add, acc=np.float64)
+    assert np.array_equal(dX.read(np.float16, (T, H)).view(np.uint16), Xn.view(np.uint16))  # f16(f32 sum): exact
+    assert f16_close(dO.read(np.float16, (T, H)), O, ulps=1.0) <= 1.0
+
+
+@pytest.mark.parametrize("with_y,with_w2", [(True, True), (True, False), (False, True)])
+def test_sandwich(pkg, ctx, with_y, with_w2):
+    rng = np.random.default_rng(7)
+    T, H = 50, 768
+    X, Y = rand_f16(rng, (T, H)), rand_f16(rng, (T, H))
+    w1, w2 = (1 + rng.standard_normal(H) * 0.1).astype(np.float16), (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    dX, dY, d1, d2, dO = ctx.array(X), ctx.array(Y), ctx.array(w1), ctx.array(w2), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.sandwich(T, H, 1e-6, 0.75, dX, dY if with_y else None, d1 if with_y else None, d2 if with_w2 else None, dO))
+    Xn, O = ref.sandwich(X, Y if with_y else None, w1, w2 if with_w2 else None, 1e-6, 0.75, np.float64)
+    assert f16_close(dX.read(np.float16, (T, H)), Xn, ulps=1.0) <= 1.0
+    if with_w2:
+        assert f16_close(dO.read(np.float16, (T, H)), O, ulps=2.0) <= 1.0
+
+
+# ---------------------------------------------------------------- quantized matmul
+
+@pytest.mark.parametrize("M,N,K,bits", [
+    (384, 4096, 1024, 8), (384, 1024, 3072, 8), (1152, 6144, 1024, 8),  # the minimum slice's shapes
+    (77, 1040, 128, 8), (2304, 256, 512, 8), (5, 1024, 1536, 8),
+    (512, 2560, 2048, 4), (300, 2048, 11008, 4), (2100, 512, 256, 4), (33, 48, 64, 4),
+])
+def test_matmul(pkg, ctx, M, N, K, bits):
+    dj = _dj()
+    rng = np.random.default_rng(M * 7 + N + K + bits)
+    codes, scales = quant(rng, N, K, bits)
+    W16 = ref.dequant_f16(codes, scales, bits)
+    X = rand_f16(rng, (M, K))
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA)
+    dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+    run(ctx, lambda r: r.matmul(dX, W, dY, M))
+    got = dY.read(np.float16, (M, N))
+    want = ref.matmul(X, W16, np.float64)
+    worst = f16_close(got, want, ulps=1.0, atol=2e-5)
+    print(f"matmul {M}x{N}x{K} q{bits}: worst/bound {worst:.3f}")
+    assert worst <= 1.0
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_matmul_weights_bit_exact(pkg, ctx, bits):
+    """X = identity: Y = W16^T exactly (one nonzero product per output), so the in-register dequantization
+    must give the reference's f16 weights bit for bit."""
+    dj = _dj()
+    rng = np.random.default_rng(11 + bits)
+    N, K = 384, 256
+    codes, scales = quant(rng, N, K, bits, std=0.5)
+    X = np.eye(K, dtype=np.float16)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA)
+    dX, dY = ctx.array(X), ctx.alloc(K * N * 2)
+    run(ctx, lambda r: r.matmul(dX, W, dY, K))
+    got = dY.read(np.uint16, (K, N))
+    assert np.array_equal(got, np.ascontiguousarray(ref.dequant_f16(codes, scales, bits).T).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,I,K,bits,act", [(384, 3072, 1024, 8, 0), (70, 1152, 768, 8, 1), (2200, 1024, 512, 4, 0), (19, 64, 128, 8, 1)])
+def test_matmul_glu(pkg, ctx, M, I, K, bits, act):
+    dj = _dj()
+    rng = np.random.default_rng(M + I + K + act)
+    codes, scales = quant(rng, 2 * I, K, bits)
+    W16 = ref.dequant_f16(codes, scales, bits)
+    X = rand_f16(rng, (M, K), std=2.0)
+    W = ctx.weight_q(codes, scales, 2 * I, K, bits, dj.W_MFMA_GLU)
+    dX, dH = ctx.array(X), ctx.alloc(M * I * 2)
+    run(ctx, lambda r: r.matmul_glu(dX, W, dH, M, act))
+    got = dH.read(np.float16, (M, I))
+    ab = ref.matmul(X, W16, np.float64)
+    want = (ref.silu_mul if act == 0 else ref.gelu_mul)(ab[:, :I], ab[:, I:], np.float64)
+    # a and b are f16 matmul outputs and may each differ from the oracle's by one f16 ulp (their own
+    # rounding); propagate that through act(a) * b, plus one ulp of the result
+    a, b = ab[:, :I].astype(np.float64), ab[:, I:].astype(np.float64)
+    f = ref.silu_mul if act == 0 else ref.gelu_mul
+    act_a = (a / (1 + np.exp(-a))) if act == 0 else ref.gelu_tanh(a)
+    hstep = np.maximum(np.abs(a) * 1e-4, 1e-6)
+    act_fn = (lambda x: x / (1 + np.exp(-x))) if act == 0 else ref.gelu_tanh
+    dact = (act_fn(a + hstep) - act_fn(a - hstep)) / (2 * hstep)
+    u = 2.0 ** -10
+    bound = u * (np.abs(dact * a * b) + np.abs(act_a * b)) + u * np.abs(want.astype(np.float64)) + 1e-5
+    worst = float((np.abs(got.astype(np.float64) - want.astype(np.float64)) / bound).max())
+    assert f is not None
+    print(f"matmul_glu {M}x{I}x{K} q{bits} act{act}: worst/bound {worst:.3f}")
+    assert worst <= 1.0
+
+
+# ---------------------------------------------------------------- q/k norm + rope
+
+@pytest.mark.parametrize("heads,kv,D,qk,vnorm,mode,rot", [
+    (16, 8, 128, True, False, 0, None), (16, 2, 128, False, False, 0, None), (12, 2, 128, True, False, 0, None),
+    (3, 1, 256, True, True, 1, None), (8, 2, 256, True, False, 0, 64), (4, 4, 64, True, False, 0, None),
+])
+def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
+    rng = np.random.default_rng(heads * D + kv)
+    T = 97
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride))
+    pos = rng.integers(0, 1100, T).astype(np.int32)
+    qn, kn = (1 + rng.standard_normal(D) * 0.1).astype(np.float16), (1 + rng.standard_normal(D) * 0.1).astype(np.float16)
+    dZ, dpos, dq, dk = ctx.array(Z), ctx.array(pos), ctx.array(qn), ctx.array(kn)
+    theta = 1e6 if mode == 0 else 1e4
+    run(ctx, lambda r: r.qk_norm_rope(T, heads, kv, D, stride, dZ, dq if qk else None, dk if qk else None, vnorm, dpos, 1,
+                                      1e-6, theta, rot, mode))
+    want = ref.qk_norm_rope(Z, heads, kv, D, pos, qn if qk else None, kn if qk else None, vnorm, 1e-6, theta, rot, mode, np.float64)
+    got = dZ.read(np.float16, (T, stride))
+    worst = f16_close(got, want, ulps=2.0, atol=2e-4)
+    print(f"qk_norm_rope h{heads} kv{kv} D{D}: worst/bound {worst:.3f}")
+    assert worst <= 1.0
+
+
+# ---------------------------------------------------------------- attention
+
+def _forest_case(rng, trunks_branches):
+    trees = []
+    for trunk, branches in trunks_branches:
+        trees.append({"trunk": list(rng.integers(0, 1000, trunk)), "branches": [list(rng.integers(0, 1000, b)) for b in branches],
+                      "groups": [[[1], [2]] for _ in branches]})
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest(trees)
+    return meta, ref.forest_ranges(meta)
+
+
+@pytest.mark.parametrize("heads,kv,D", [(16, 8, 128), (16, 2, 128), (12, 2, 128), (3, 1, 256), (4, 2, 64)])
+def test_attention_forest(pkg, ctx, heads, kv, D):
+    dj = _dj()
+    rng = np.random.default_rng(heads + kv + D)
+    meta, rng4 = _forest_case(rng, [(100, [20, 37, 5]), (70, [64, 1]), (0, [90]), (130, [])])
+    T = meta.shape[0]
+    mask = ref.forest_mask(meta)
+    assert np.array_equal(ref.ranges_mask(rng4, T), mask)
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride))
+    dZ, drng, dO = ctx.array(Z), ctx.array(rng4), ctx.alloc(T * heads * D * 2)
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    scale = 1.0 / math.sqrt(D)
+    run(ctx, lambda r: r.attention(T, heads, kv, D, dZ, stride, src, src, drng, scale, dO))
+    got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+    want = ref.attention(Z, heads, kv, D, mask, scale, np.float64).astype(np.float64)
+    err = np.abs(got - want).max()
+    print(f"attention h{heads} kv{kv} D{D} T{T}: max abs err {err:.2e}")
+    assert err < 4e-3
+
+
+@pytest.mark.parametrize("D", [128, 256])
+def test_attention_bidirectional_and_windows(pkg, ctx, D):
+    dj = _dj()
+    rng = np.random.default_rng(D)
+    heads, kv = 3, 1
+    seqs = [list(range(n)) for n in (256, 24, 24, 24, 8, 8, 8, 8, 8, 8, 8, 300)]
+    ids, meta, full, slide, ranges = ref.pack_encoder(seqs, window=40)
+    T = len(ids)
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride), std=0.5)
+    dZ, dO = ctx.array(Z), ctx.alloc(T * heads * D * 2)
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    for r4 in (full, slide):
+        drng = ctx.array(r4)
+        run(ctx, lambda r: r.attention(T, heads, kv, D, dZ, stride, src, src, drng, 1.0, dO))
+        got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+        want = ref.attention(Z, heads, kv, D, ref.ranges_mask(r4, T), 1.0, np.float64).astype(np.float64)
+        assert np.abs(got - want).max() < 4e-3
+
+
+def test_attention_kept_prefix(pkg, ctx):
+    """Source A = a kept K/V cache (the shared state), source B = the current rows: same result as one pass."""
+    dj = _dj()
+    rng = np.random.default_rng(5)
+    heads, kv, D = 12, 2, 128
+    P, branches = 300, [32, 32, 17, 32]
+    stride = (heads + 2 * kv) * D
+    T = sum(branches)
+    Zp = rand_f16(rng, (P, stride))
+    Zb = rand_f16(rng, (T, stride))
+    cache = np.ascontiguousarray(Zp[:, heads * D:(heads + 2 * kv) * D])
+    rng4 = []
+    s = 0
+    for b in branches:
+        for o in range(b):
+            rng4.append((0, P, s, s + o + 1))
+        s += b
+    rng4 = np.array(rng4, dtype=np.int32)
+    dZ, dC, drng, dO = ctx.array(Zb), ctx.array(cache), ctx.array(rng4), ctx.alloc(T * heads * D * 2)
+    A = dj.kv_src(dC, P, 2 * kv * D, 0, kv * D)
+    B = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    run(ctx, lambda r: r.attention(T, heads, kv, D, dZ, stride, A, B, drng, 1 / math.sqrt(D), dO))
+    got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+    kvrows = np.concatenate([cache, Zb[:, heads * D:(heads + 2 * kv) * D]])
+    mask = np.zeros((T, P + T), dtype=bool)
+    for t, (a0, a1, b0, b1) in enumerate(rng4):
+        mask[t, a0:a1] = True
+        mask[t, P + b0:P + b1] = True
+    want = ref.attention(Zb, heads, kv, D, mask, 1 / math.sqrt(D), np.float64, kv_rows=kvrows).astype(np.float64)
+    assert np.abs(got - want).max() < 4e-3
+
+
+def test_kv_store(pkg, ctx):
+    rng = np.random.default_rng(3)
+    heads, kv, D, T = 4, 2, 128, 70
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride))
+    dZ, dC = ctx.array(Z), ctx.alloc((T + 10) * 2 * kv * D * 2)
+    run(ctx, lambda r: r.kv_store(T, kv, D, dZ, stride, heads * D, dC, 10))
+    got = dC.read(np.uint16, (T + 10, 2 * kv * D))[10:]
+    assert np.array_equal(got, Z[:, heads * D:].view(np.uint16))
+
+
+# ---------------------------------------------------------------- readouts
+
+@pytest.mark.parametrize("bits,H", [(8, 1024), (4, 2048), (8, 1536)])
+def test_leaf_logits(pkg, ctx, bits, H):
+    dj = _dj()
+    rng = np.random.default_rng(bits + H)
+    V, T, L, n_ids = 500, 64, 5, 7
+    codes, scales = quant(rng, V, H, bits)
+    X = rand_f16(rng, (T, H), std=3.0)
+    w = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    leaves = rng.integers(0, T, L).astype(np.uint32)
+    ids = rng.integers(0, V, L * n_ids).astype(np.uint32)
+    E = ctx.weight_q(codes, scales, V, H, bits, dj.W_PLAIN)
+    dX, dl, dw, di, do = ctx.array(X), ctx.array(leaves), ctx.array(w), ctx.array(ids), ctx.alloc(L * n_ids * 4)
+    run(ctx, lambda r: r.leaf_logits(T, L, H, n_ids, 1e-6, dX, dl, dw, di, E, do))
+    got = do.read(np.float32, (L * n_ids,))
+    want = ref.leaf_logits(X, leaves, w, ids, n_ids, codes, scales, bits, 1e-6, np.float64)
+    assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max() + 1e-6
+
+
+def test_readout_pool_dense(pkg, ctx):
+    dj = _dj()
+    rng = np.random.default_rng(9)
+    T, H, codes_n = 80, 768, 10
+    X = rand_f16(rng, (T, H))
+    R = rng.standard_normal((codes_n, H)).astype(np.float32)
+    pairs = np.array([(5, 1), (79, 9), (0, 0), (40, 3)], dtype=np.uint32)
+    dX, dR, dp, do = ctx.array(X), ctx.array(R), ctx.array(pairs), ctx.alloc(4 * 4)
+    ranges = np.array([(0, 30), (30, 31), (31, 80)], dtype=np.uint32)
+    dr, dpool = ctx.array(ranges), ctx.alloc(3 * H * 4)
+    c, s = quant(rng, 96, H, 8)
+    W = ctx.weight_q(c, s, 96, H, 8, dj.W_PLAIN)
+    dd = ctx.alloc(3 * 96 * 4)
+
+    def body(r):
+        r.readout(T, 4, H, dX, dR, codes_n, dp, do)
+        r.mean_pool(T, 3, H, dX, dr, dpool)
+        r.dense_f32(3, dpool, W, dd)
+    run(ctx, body)
+    assert np.allclose(do.read(np.float32, (4,)), ref.readout(X, R, pairs), rtol=1e-5, atol=1e-4)
+    pooled = ref.mean_pool(X, ranges)
+    assert np.allclose(dpool.read(np.float32, (3, H)), pooled, rtol=1e-5, atol=1e-6)
+    assert np.allclose(dd.read(np.float32, (3, 96)), ref.dense_f32(pooled, c, s, 8), rtol=1e-4, atol=1e-5)
+
+
+# ---------------------------------------------------------------- recorder: snapshots, graphs, errors
+
+def test_graph_replay_matches_eager(pkg, ctx):
+    """A captured forward replayed several times, with eager work and syncs in between, equals eager."""
+    dj = _dj()
+    rng = np.random.default_rng(21)
+    T, H, N = 96, 1024, 2048
+    codes, scales = quant(rng, N, H, 8)
+    ec, es = quant(rng, 400, H, 8)
+    W = ctx.weight_q(codes, scales, N, H, 8, dj.W_MFMA)
+    E = ctx.weight_q(ec, es, 400, H, 8, dj.W_PLAIN)
+    w = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    dw, dids = ctx.array(w), ctx.alloc(T * 4)
+    dX, dO, dY = ctx.alloc(T * H * 2), ctx.alloc(T * H * 2), ctx.alloc(T * N * 2)
+
+    def forward(key, ids):
+        dids.write(ids)
+        rec = ctx.recorder(key)
+        rec.gather_q(dids, T, E, dX)
+        rec.add_rmsnorm(T, H, False, 1e-6, dX, dX, dw, dO)
+        rec.matmul(dO, W, dY, T)
+        i = rec.snapshot(dY, T * N * 2, np.float16, (T, N))
+        replay = rec.replay
+        return rec.finish()[i], replay
+
+    key = 0xD1_0001
+    ctx.graph_clear()
+    for it in range(4):
+        ids = rng.integers(0, 400, T).astype(np.uint32)
+        eager, _ = forward(0, ids)
+        graph, replayed = forward(key, ids)
+        assert replayed == (it > 0)
+        assert np.array_equal(eager.view(np.uint16), graph.view(np.uint16))
+    ctx.graph_clear()
+
+
+def test_profile_and_timer(pkg, ctx):
+    dj = _dj()
+    rng = np.random.default_rng(2)
+    codes, scales = quant(rng, 256, 256, 8)
+    W = ctx.weight_q(codes, scales, 256, 256, 8, dj.W_MFMA)
+    dX, dY = ctx.array(rand_f16(rng, (64, 256))), ctx.alloc(64 * 256 * 2)
+    ctx.profile_reset()
+    ctx.profile(True)
+    ctx.timer_begin()
+    for _ in range(3):
+        run(ctx, lambda r: r.matmul(dX, W, dY, 64))
+    ms = ctx.timer_end()
+    ctx.profile(False)
+    table = ctx.profile_table()
+    assert ms > 0 and any(k.startswith("matmul_q8") and v[1] == 3 for k, v in table.items())
+
+
+def test_errors_surface(pkg, ctx):
+    dj = _dj()
+    rng = np.random.default_rng(1)
+    codes, scales = quant(rng, 64, 64, 8)
+    W = ctx.weight_q(codes, scales, 64, 64, 8, dj.W_PLAIN)
+    dX = ctx.alloc(64 * 64 * 2)
+    rec = ctx.recorder()
+    with pytest.raises(dj.DJError, match="decision.js: matmul needs an MFMA-tiled weight"):
+        rec.matmul(dX, W, dX, 64)
+    rec.finish()
+    with pytest.raises(dj.DJError, match="K must be a multiple of 32"):
+        ctx.weight_q(np.zeros((4, 40), np.uint8), np.zeros((4, 1), np.float16), 4, 40, 8, dj.W_PLAIN)
