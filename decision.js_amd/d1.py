@@ -1,0 +1,193 @@
+"""The Decision API of decision.js (src/d1.ts): load, system_one, system_one_batch, probabilities,
+probabilities_batch, destroy — same names (snake_case), argument meaning and error behaviour.
+
+Text-to-ids (prompts, tokenizers) is upstream of the scoring path and not part of this build; a `prompt`
+object turns states and questions into token ids. The default, IdPrompt, takes them already tokenized:
+  state:     a list of token ids
+  question:  the reference's question dict plus "ids" (its token ids) and "options" (one token-id group per
+             option, [yes, no] for a noul: each option scores its best token, d1-3b-engine.ts:112-121);
+             for the encoder, "option_ids" (one token-id list per option text)
+"""
+import threading
+
+import numpy as np
+
+from . import questions as Q
+from .encoder import EncoderEngine, cosine_logits
+from .engine import DecoderEngine
+
+
+def softmax(s):
+    """gpu.ts:294-297: max-subtracted exp in float64."""
+    s = np.asarray(s, dtype=np.float64)
+    e = np.exp(s - s.max())
+    return list(e / e.sum())
+
+
+class IdPrompt:
+    """Pre-tokenized states and questions (see the module docstring)."""
+
+    def trunk(self, state):
+        return [int(t) for t in (state["ids"] if isinstance(state, dict) else state)]
+
+    def branch(self, q):
+        return [int(t) for t in q["ids"]]
+
+    def readout_ids(self, q):
+        groups = q["options"]
+        if len(groups) != Q.n_options(q):
+            raise Q.QuestionError(f"decision.js: {len(groups)} option groups for a {q['type']} with {Q.n_options(q)} options")
+        return [[int(t) for t in g] for g in groups]
+
+    def texts(self, state, q):
+        return self.trunk(state), self.branch(q), [[int(t) for t in o] for o in q["option_ids"]]
+
+
+class Decision:
+    """D1 (d1.ts:38-227): a model and the serial queue of its calls."""
+
+    def __init__(self, kind, engine, prompt, tokens_per_pass, share_state=False):
+        self.kind, self.engine, self.prompt = kind, engine, prompt
+        self.tokens_per_pass = tokens_per_pass
+        self.share_state = share_state
+        self._lock = threading.Lock()  # one call at a time on the GPU (d1.ts:112-119)
+        self._states = {}  # share_state: prefilled states by their ids (oldest dropped first)
+        self._embeddings = {}  # encoder: normalized embeddings of the texts seen so far (d1.ts:44, 206-209)
+
+    @classmethod
+    def load(cls, base: str, opts: dict = None):
+        """A model in the decision.js format at `base` (manifest.json + weights.bin). opts: device,
+        on_progress, share_state, tokens_per_pass, graphs, prompt. The kind comes from manifest.config.model
+        (d1.ts:63-64)."""
+        opts = dict(opts or {})
+        from .fmt import load_manifest
+        model = load_manifest(base if base.endswith("/") else base + "/")["config"].get("model")
+        if model in ("decoder", "d1-3b"):
+            kind, engine = "decoder", DecoderEngine.load(base, opts)
+        elif model == "eg2-encoder":
+            kind, engine = "encoder", EncoderEngine.load(base, opts)
+        else:
+            raise ValueError(f"decision.js: unknown model kind {model!r}")
+        # MI355X default: one pass holds every request that fits 128k tokens (d1.ts:78 uses 4096 / 8192 to
+        # bound the memory of browser GPUs; activations here are ~25 KB per token of 288 GB)
+        tpp = opts.get("tokens_per_pass") or 131072
+        return cls(kind, engine, opts.get("prompt") or IdPrompt(), tpp, bool(opts.get("share_state")))
+
+    # ---- the public calls (d1.ts:81-110)
+    def system_one(self, state, questions: dict):
+        return self.system_one_batch([(state, questions)])[0]
+
+    def system_one_batch(self, requests, on_progress=None):
+        done = self._run([(s, list(qs.values())) for s, qs in requests], on_progress)
+        out = []
+        for (s, qs), d in zip(requests, done):
+            names = list(qs.keys())
+            out.append({"answers": {n: Q.answer(qs[n], d["probs"][j]) for j, n in enumerate(names)},
+                        "usage": {"input_tokens": d["tokens"], "output_tokens": 0}})
+        return out
+
+    def probabilities(self, state, qs):
+        return self._run([(state, list(qs))], None)[0]["probs"]
+
+    def probabilities_batch(self, requests, on_progress=None):
+        return [r["probs"] for r in self._run([(s, list(qs)) for s, qs in requests], on_progress)]
+
+    def destroy(self):
+        for st in self._states.values():
+            st.free()
+        self._states = {}
+        self.engine.destroy()
+
+    # ---- internals
+    def _run(self, requests, on_progress):
+        for _, qs in requests:
+            for q in qs:
+                Q.check_question(q)
+        with self._lock:  # a failed call releases the lock: the queue does not wedge (d1.ts:117)
+            if self.kind == "decoder":
+                return self._run_shared(requests, on_progress) if self.share_state else self._run_decoder(requests, on_progress)
+            return self._run_encoder(requests, on_progress)
+
+    def _passes(self, sizes):
+        """Whole requests per pass up to the token budget; a pass always takes at least one (d1.ts:217-219)."""
+        i = 0
+        while i < len(sizes):
+            j, used = i, 0
+            while True:
+                used += sizes[j]
+                j += 1
+                if not (j < len(sizes) and used + sizes[j] <= self.tokens_per_pass):
+                    break
+            yield i, j
+            i = j
+
+    def _run_decoder(self, requests, on_progress):
+        """run3B (d1.ts:211-226): a forest per request (the state as trunk, each question a branch)."""
+        p = self.prompt
+        trees = [{"trunk": p.trunk(s), "branches": [p.branch(q) for q in qs], "groups": [p.readout_ids(q) for q in qs]}
+                 for s, qs in requests]
+        sizes = [len(t["trunk"]) + sum(len(b) for b in t["branches"]) for t in trees]
+        out = [{"probs": [], "tokens": n} for n in sizes]
+        for i, j in self._passes(sizes):
+            scores = self.engine.run(trees[i:j])["scores"]
+            for r, per_q in enumerate(scores):
+                out[i + r]["probs"] = [softmax(s) for s in per_q]
+            if on_progress:
+                on_progress(j, len(trees))
+        return out
+
+    def _run_shared(self, requests, on_progress):
+        """Shared state: each request's state is prefilled once and its K/V kept (reused by later calls on the
+        same state); the questions then run against it."""
+        p = self.prompt
+        out = []
+        for k, (s, qs) in enumerate(requests):
+            trunk = p.trunk(s)
+            key = tuple(trunk)
+            st = self._states.get(key)
+            if st is None:
+                if len(self._states) >= 64:
+                    old = next(iter(self._states))
+                    self._states.pop(old).free()
+                st = self._states[key] = self.engine.prefill(trunk)
+            branches = [p.branch(q) for q in qs]
+            scores = self.engine.run_shared(st, branches, [p.readout_ids(q) for q in qs])
+            out.append({"probs": [softmax(x) for x in scores], "tokens": len(trunk) + sum(len(b) for b in branches)})
+            if on_progress:
+                on_progress(k + 1, len(requests))
+        return out
+
+    def _run_encoder(self, requests, on_progress):
+        """runEg2 (d1.ts:172-204): every distinct text embedded once (cached), then the head on the host."""
+        p = self.prompt
+        asked = [[p.texts(s, q) for q in qs] for s, qs in requests]
+        todo, tokens = {}, [0] * len(requests)
+        for r, per_q in enumerate(asked):
+            for st, qi, opts in per_q:
+                for t in [st, qi, *opts]:
+                    key = tuple(t)
+                    if key in self._embeddings or key in todo:
+                        continue
+                    todo[key] = t
+                    tokens[r] += len(t)
+        texts = list(todo.values())
+        sizes = [len(t) for t in texts]
+        for i, j in self._passes(sizes) if texts else []:
+            emb = self.engine.embed(texts[i:j])["embeddings"]
+            for k, e in enumerate(emb):
+                self._remember(tuple(texts[i + k]), e)
+            if on_progress:
+                on_progress(j, len(texts))
+        out = []
+        for r, (s, qs) in enumerate(requests):
+            probs = []
+            for q, (st, qi, opts) in zip(qs, asked[r]):
+                z = cosine_logits(self._embeddings[tuple(st)], self._embeddings[tuple(qi)], [self._embeddings[tuple(o)] for o in opts])
+                probs.append(softmax(z))
+            out.append({"probs": probs, "tokens": tokens[r]})
+        return out
+
+    def _remember(self, key, e):
+        if len(self._embeddings) >= 8192:
+            self._embeddings.pop(next(iter(self._embeddings)))  # the oldest text first (d1.ts:207)
+        self._embeddings[key] = e

@@ -1,0 +1,349 @@
+"""Engines of the scoring path: weights on the device (gpu.ts loadWeights / GpuEngine) and the causal decoder
+engine (d1-3b-engine.ts's forest; d3-engine.ts's shared prefix) driving libdj.so.
+
+A forward is recorded into one dj recorder, as the reference records one command buffer (gpu.ts:176-281);
+with `graphs` on (the default), a forward whose shapes were seen before replays a captured HIP graph.
+"""
+import math
+import zlib
+
+import numpy as np
+
+from . import _dj, fmt
+
+# ---------------------------------------------------------------- weights (gpu.ts:57-88, 114-133)
+
+
+def default_layout(name: str, info: dict) -> int:
+    """Which device layout a quantized tensor gets: the embedding and the pooled head stay plain (gathered /
+    read row-wise), fused gated-MLP inputs are interleaved for the GLU epilogue, every other linear is
+    repacked for the MFMA GEMM (the reference's tileWeights keeps `embed` quantized the same way,
+    d1-3b-engine.ts:29)."""
+    if name == "embed" or name.startswith("head.dense"):
+        return _dj.W_PLAIN
+    if name.endswith("w13") or name.endswith(".gu"):
+        return _dj.W_MFMA_GLU
+    return _dj.W_MFMA
+
+
+def load_weights(base: str, opts: dict = None, layout=default_layout):
+    """The manifest and every tensor of `base` on the device: (ctx, manifest, weights). opts: device (an
+    existing _dj.Context), on_progress(loaded, total). Quantized tensors become _dj.Weight, f16/f32 ones
+    DevBuf (with the host array kept as .host). Mirrors loadWeights (gpu.ts:57-88): range reads, a length
+    check per read, and a refusal when a tensor exceeds what the device can hold."""
+    opts = opts or {}
+    if not base.endswith("/"):
+        base += "/"
+    m = fmt.load_manifest(base)
+    ctx = opts.get("device") or _dj.Context(0)
+    tf = fmt.TensorFile(base)
+    total_mem = ctx.info()["memory"]
+    largest = max(t["bytes"] for t in m["tensors"].values())
+    if largest > total_mem:
+        raise _dj.DJError(_dj.DJ_ENOMEM, f"decision.js: this GPU holds {total_mem / 1e6:.0f} MB, this model needs a {largest / 1e6:.0f} MB tensor")
+    w, loaded = {}, 0
+    for name, info in m["tensors"].items():
+        if info["dtype"] in ("q4", "q8"):
+            codes, scales = tf.tensor(info)
+            N, K = info["shape"]
+            w[name] = ctx.weight_q(codes, scales, N, K, 8 if info["dtype"] == "q8" else 4, layout(name, info))
+            loaded += info["bytes"] + info["scales_bytes"]
+        else:
+            arr = np.array(tf.tensor(info))
+            b = ctx.array(arr)
+            b.host = arr
+            w[name] = b
+            loaded += info["bytes"]
+        cb = opts.get("on_progress")
+        if cb:
+            cb(loaded, m["bytes"])
+    return ctx, m, w
+
+
+class GpuEngine:
+    """gpu.ts GpuEngine: a device context, the model's weights and counters."""
+
+    def __init__(self, ctx: _dj.Context, m: dict, w: dict, opts: dict = None):
+        self.ctx, self.m, self.w = ctx, m, w
+        self.opts = opts or {}
+        self.graphs = self.opts.get("graphs", True)
+        self.stats = {"forwards": 0, "tokens": 0, "gpu_ms": 0.0}
+        self._bufs = {}
+        self._gen = 0  # bumped whenever buffers are reallocated: cached graphs point at the old ones
+        self.owns_ctx = "device" not in self.opts
+
+    def destroy(self):
+        """Frees every weight and buffer (gpu.ts:108-110)."""
+        for b in self._bufs.values():
+            b.free()
+        self._bufs = {}
+        for v in self.w.values():
+            v.free()
+        self.w = {}
+        if self.owns_ctx:
+            self.ctx.close()
+
+    def _alloc(self, spec: dict):
+        """(Re)allocates the named buffers {name: bytes}."""
+        for b in self._bufs.values():
+            b.free()
+        self._bufs = {k: self.ctx.alloc(v) for k, v in spec.items()}
+        self._gen += 1
+        self.ctx.graph_clear()
+
+    def _key(self, *parts) -> int:
+        """Graph key of a forward: every shape and pointer generation that the recorded ops depend on."""
+        if not self.graphs:
+            return 0
+        return zlib.crc32(repr((id(self), self._gen) + parts).encode()) | (1 << 40)
+
+
+# ---------------------------------------------------------------- packing (host side, d1-3b-engine.ts:46-72)
+
+
+def pack_forest(trees):
+    """Forest packing of D13BEngine.run (d1-3b-engine.ts:46-72). Each tree {trunk, branches, groups}: its
+    trunk read once, each branch continuing it. Per token ids (u32), pos (branch positions continue after
+    the trunk), meta (treeStart, treeEnd, branch or -1, pos); leaves = each branch's last token; leafIds =
+    the flattened groups, zero-padded to nIds. Also the attention key ranges per token (a0, a1, b0, b1) that
+    equal the forest mask of kernels.ts:135: trunk token i -> [start, start+i+1); branch token -> the trunk
+    [start, start+P) and its own branch up to itself."""
+    T = sum(len(t["trunk"]) + sum(len(b) for b in t["branches"]) for t in trees)
+    ids = np.empty(T, dtype=np.uint32)
+    pos = np.empty(T, dtype=np.int32)
+    meta = np.empty((T, 4), dtype=np.int32)
+    rng = np.zeros((T, 4), dtype=np.int32)
+    leaves, leaf_ids = [], []
+    off = 0
+    for tr in trees:
+        start = off
+        total = len(tr["trunk"]) + sum(len(b) for b in tr["branches"])
+        p = len(tr["trunk"])
+        i = np.arange(p, dtype=np.int32)
+        ids[off:off + p] = tr["trunk"]
+        pos[off:off + p] = i
+        meta[off:off + p] = np.stack([np.full(p, start), np.full(p, start + total), np.full(p, -1), i], 1)
+        rng[off:off + p, 0] = start
+        rng[off:off + p, 1] = start + i + 1
+        off += p
+        for b, br in enumerate(tr["branches"]):
+            n = len(br)
+            o = np.arange(n, dtype=np.int32)
+            ids[off:off + n] = br
+            pos[off:off + n] = p + o
+            meta[off:off + n] = np.stack([np.full(n, start), np.full(n, start + total), np.full(n, b), p + o], 1)
+            rng[off:off + n] = np.stack([np.full(n, start), np.full(n, start + p), np.full(n, off), off + o + 1], 1)
+            off += n
+            leaves.append(off - 1)
+            leaf_ids.append([x for g in tr["groups"][b] for x in g])
+    L = len(leaves)
+    n_ids = max((len(x) for x in leaf_ids), default=0)
+    flat = np.zeros(max(L * n_ids, 1), dtype=np.uint32)
+    for k, g in enumerate(leaf_ids):
+        flat[k * n_ids:k * n_ids + len(g)] = g
+    return {"ids": ids, "pos": pos, "meta": meta, "rng": rng, "leaves": np.array(leaves, dtype=np.uint32),
+            "leaf_ids": flat, "n_ids": n_ids, "T": T, "L": L}
+
+
+def common_prefix(seqs) -> int:
+    """The shared prefix of a request's question sequences, leaving at least one token per question
+    (d3-engine.ts:76-80)."""
+    if len(seqs) < 2:
+        return 0
+    lim = min(len(s) for s in seqs) - 1
+    P = 0
+    while P < lim and all(s[P] == seqs[0][P] for s in seqs):
+        P += 1
+    return P
+
+
+def group_max(out: np.ndarray, n_ids: int, trees):
+    """Readout of d1-3b-engine.ts:112-121: each option scores the max over its token group."""
+    scores, leaf = [], 0
+    for tr in trees:
+        per_q = []
+        for groups in tr["groups"]:
+            j, s = 0, []
+            for g in groups:
+                s.append(max(float(out[leaf * n_ids + j + k]) for k in range(len(g))))
+                j += len(g)
+            per_q.append(s)
+            leaf += 1
+        scores.append(per_q)
+    return scores
+
+
+# ---------------------------------------------------------------- the causal decoder engine
+
+
+class SharedState:
+    """A prefilled state: its token count and the K/V rows of every layer, kept on the device."""
+    _serial = 0
+
+    def __init__(self, P: int, cache: _dj.DevBuf, ids):
+        self.P, self.cache, self.ids = P, cache, tuple(ids)
+        SharedState._serial += 1
+        self.serial = SharedState._serial  # graph keys use this, never id(): ids are reused after a free
+
+    def free(self):
+        self.cache.free()
+
+
+class DecoderEngine(GpuEngine):
+    """A causal decoder (config model "decoder", or the reference's "d1-3b" naming on attention layers): many
+    rows packed as a forest, answer-set logits at each branch's last token (D13BEngine, d1-3b-engine.ts).
+    Layers: qkv -> q/k RMSNorm (when the model has it) + RoPE -> attention -> o_proj -> residual + RMSNorm
+    -> w13 with the SwiGLU epilogue -> w2 -> residual + RMSNorm."""
+
+    @classmethod
+    def load(cls, base: str, opts: dict = None):
+        ctx, m, w = load_weights(base, opts)
+        if m["config"].get("model") not in ("decoder", "d1-3b"):
+            raise ValueError(f"decision.js: {base} is not a causal decoder ({m['config'].get('model')})")
+        if any(t != "full_attention" for t in m["config"].get("layer_types", [])):
+            raise ValueError("decision.js: only attention layers are supported (LFM2 conv layers are not on this path)")
+        return cls(ctx, m, w, opts)
+
+    def __init__(self, ctx, m, w, opts=None):
+        super().__init__(ctx, m, w, opts)
+        c = m["config"]
+        self.H, self.I, self.h, self.kv, self.D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
+        self.layers = c.get("layers", len(c.get("layer_types", [])))
+        self.eps, self.theta = c["eps"], c["rope_theta"]
+        self.stride = (self.h + 2 * self.kv) * self.D
+        self.capacity = 0
+        self.leaf_capacity = 0
+
+    # -- buffers (d1-3b-engine.ts:33-42: grown, never shrunk)
+    def ensure(self, T: int, L: int = 0, n_ids: int = 0):
+        if T <= self.capacity and L * max(n_ids, 1) <= self.leaf_capacity:
+            return
+        cap = max(T, self.capacity, 256)
+        cap = (cap + 63) // 64 * 64
+        lcap = max(L * max(n_ids, 1), self.leaf_capacity, 1024)
+        H, I = self.H, self.I
+        self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * self.stride * 2,
+                     "y": cap * self.h * self.D * 2, "h": cap * I * 2, "ids": cap * 4, "pos": cap * 4, "rng": cap * 16,
+                     "leaves": lcap * 4, "leaf_ids": lcap * 4, "out": lcap * 4})
+        self.capacity, self.leaf_capacity = cap, lcap
+
+    def _layers(self, rec, T, B, kv_a=None, kv_store=None, debug=(), snaps=None):
+        """The per-layer loop (d1-3b-engine.ts:88-105) on the recorder."""
+        c, w = self.m["config"], self.w
+        H, h, kv, D, eps = self.H, self.h, self.kv, self.D, self.eps
+        z = B["z"]
+        src = _dj.kv_src(z, T, self.stride, h * D, (h + kv) * D)
+        rec.gather_q(B["ids"], T, w["embed"], B["x"])
+        rec.add_rmsnorm(T, H, False, eps, B["x"], B["o"], w["layers.0.operator_norm"], B["normed"])
+        for i in range(self.layers):
+            p = f"layers.{i}."
+            rec.matmul(B["normed"], w[p + "qkv"], z, T)
+            rec.qk_norm_rope(T, h, kv, D, self.stride, z, w.get(p + "q_norm"), w.get(p + "k_norm"), False, B["pos"], 1, eps, self.theta)
+            if kv_store is not None:
+                rec.kv_store(T, kv, D, z, self.stride, h * D, kv_store.at(i * T * 2 * kv * D * 2), 0)
+            a = src if kv_a is None else kv_a(i)
+            rec.attention(T, h, kv, D, z, self.stride, a, src, B["rng"], 1.0 / math.sqrt(D), B["y"])
+            rec.matmul(B["y"], w[p + "o_proj"], B["o"], T)
+            rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[p + "ffn_norm"], B["normed"])
+            rec.matmul_glu(B["normed"], w[p + "w13"], B["h"], T, _dj.ACT_SILU)
+            rec.matmul(B["h"], w[p + "w2"], B["o"], T)
+            nxt = f"layers.{i + 1}.operator_norm" if i + 1 < self.layers else "final_norm"
+            rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[nxt], B["normed"])
+            if i in debug and snaps is not None:
+                snaps[i] = rec.snapshot(B["x"], T * H * 2, np.float16, (T, H))
+
+    def _finish(self, rec, T):
+        got = rec.finish()
+        self.stats["forwards"] += 1
+        self.stats["tokens"] += T
+        return got
+
+    def run(self, trees, debug_layers=()):
+        """Option scores for every question of every tree: [tree][question][option] (max over the option's
+        token group), plus {layer: hidden state x} for the requested debug layers (D13BEngine.run)."""
+        debug_layers = tuple(sorted(set(debug_layers)))
+        pk = pack_forest(trees)
+        T, L, n_ids = pk["T"], pk["L"], pk["n_ids"]
+        if T == 0:
+            return {"scores": [[] for _ in trees], "debug": {}}
+        self.ensure(T, L, n_ids)
+        B = self._bufs
+        B["ids"].upload(pk["ids"])
+        B["pos"].upload(pk["pos"])
+        B["rng"].upload(pk["rng"])
+        if L:
+            B["leaves"].upload(pk["leaves"])
+            B["leaf_ids"].upload(pk["leaf_ids"])
+        rec = self.ctx.recorder(self._key("run", T, L, n_ids, tuple(debug_layers)))
+        snaps = {}
+        if not rec.replay:
+            self._layers(rec, T, B, debug=debug_layers, snaps=snaps)
+            if L and n_ids:
+                rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
+                                self.w["embed"], B["out"])
+        else:
+            for i in debug_layers:
+                snaps[i] = rec.snapshot(B["x"], T * self.H * 2, np.float16, (T, self.H))
+        oi = rec.snapshot(B["out"], max(L * n_ids, 1) * 4, np.float32, (max(L * n_ids, 1),)) if L and n_ids else None
+        got = self._finish(rec, T)
+        out = got[oi] if oi is not None else np.zeros(0, np.float32)
+        return {"scores": group_max(out, n_ids, trees), "debug": {i: got[k] for i, k in snaps.items()}, "logits": out}
+
+    # -- shared state: prefill once, keep the KV, answer questions against it
+    def prefill(self, trunk) -> SharedState:
+        """Runs the state alone (causal) and keeps every layer's K/V rows on the device."""
+        P = len(trunk)
+        if P == 0:
+            raise ValueError("decision.js: an empty state has nothing to prefill")
+        self.ensure(P)
+        B = self._bufs
+        i = np.arange(P, dtype=np.int32)
+        B["ids"].upload(np.asarray(trunk, dtype=np.uint32))
+        B["pos"].upload(i)
+        B["rng"].upload(np.stack([np.zeros(P, np.int32), i + 1, np.zeros(P, np.int32), np.zeros(P, np.int32)], 1))
+        cache = self.ctx.alloc(self.layers * P * 2 * self.kv * self.D * 2)
+        rec = self.ctx.recorder(0)  # the cache pointer is new each time: no graph
+        self._layers(rec, P, B, kv_store=cache)
+        self._finish(rec, P)
+        return SharedState(P, cache, trunk)
+
+    def run_shared(self, state: SharedState, branches, groups):
+        """Scores of each branch (question) continuing a prefilled state: each branch token attends to the
+        kept state K/V and to its own branch up to itself; positions continue after the state. Equal to
+        run([{trunk, branches, groups}]) up to float reassociation (the model is causal)."""
+        P = state.P
+        T = sum(len(b) for b in branches)
+        if T == 0:
+            return [[] for _ in branches]
+        ids, pos, rng, leaves, leaf_ids = [], [], [], [], []
+        off = 0
+        for b, br in enumerate(branches):
+            n = len(br)
+            o = np.arange(n, dtype=np.int32)
+            ids.append(np.asarray(br, dtype=np.uint32))
+            pos.append(P + o)
+            rng.append(np.stack([np.zeros(n, np.int32), np.full(n, P, np.int32), np.full(n, off, np.int32), off + o + 1], 1))
+            off += n
+            leaves.append(off - 1)
+            leaf_ids.append([x for g in groups[b] for x in g])
+        L = len(leaves)
+        n_ids = max(len(x) for x in leaf_ids)
+        flat = np.zeros(L * n_ids, dtype=np.uint32)
+        for k, g in enumerate(leaf_ids):
+            flat[k * n_ids:k * n_ids + len(g)] = g
+        self.ensure(T, L, n_ids)
+        B = self._bufs
+        B["ids"].upload(np.concatenate(ids))
+        B["pos"].upload(np.concatenate(pos))
+        B["rng"].upload(np.concatenate(rng))
+        B["leaves"].upload(np.array(leaves, dtype=np.uint32))
+        B["leaf_ids"].upload(flat)
+        width = 2 * self.kv * self.D
+        rec = self.ctx.recorder(self._key("shared", state.serial, T, L, n_ids))
+        if not rec.replay:
+            self._layers(rec, T, B, kv_a=lambda i: _dj.kv_src(state.cache.at(i * P * width * 2), P, width, 0, self.kv * self.D))
+            rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
+                            self.w["embed"], B["out"])
+        oi = rec.snapshot(B["out"], L * n_ids * 4, np.float32, (L * n_ids,))
+        out = self._finish(rec, T)[oi]
+        return group_max(out, n_ids, [{"groups": groups}])[0]

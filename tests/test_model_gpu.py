@@ -1,0 +1,258 @@
+"""Whole-forward parity on the GPU: the decoder and encoder engines and the Decision API against the oracle
+on seeded synthetic models (reduced layer counts and vocabularies; the shapes per layer are the configs').
+
+Bars: answer probabilities within 1e-3 absolute, final hidden states within 2e-2
+relative L2, token packing bit-exact."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+PROB_TOL = 1e-3
+HIDDEN_TOL = 2e-2
+
+
+def rel_l2(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return float(np.sqrt(((a - b) ** 2).sum()) / np.sqrt((b ** 2).sum()))
+
+
+@pytest.fixture(scope="module")
+def models(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    root = tmp_path_factory.mktemp("models")
+    out = {}
+    specs = {
+        "q8": synth.reduced("qwen3-0.6b-q8", layers=3, vocab=4096),
+        "q4": synth.reduced("qwen2.5-3b-q4", layers=2, vocab=4096),
+        "shared": synth.reduced("d3lite-0.8b-q8", layers=2, vocab=4096),
+        "enc": synth.reduced("eg2-encoder-q8", layers=2, vocab=4096),
+    }
+    for k, cfg in specs.items():
+        out[k] = synth.generate(cfg, str(root / k), seed=0, norm_std=0.1)
+    return out
+
+
+def _tree(rng, V, trunk, branches, n_opts=(2, 3, 5)):
+    groups = []
+    for b in range(len(branches)):
+        n = n_opts[b % len(n_opts)]
+        ids = rng.choice(V, size=n * 2, replace=False)
+        groups.append([[int(ids[2 * i])] if i % 2 else [int(ids[2 * i]), int(ids[2 * i + 1])] for i in range(n)])
+    return {"trunk": [int(x) for x in rng.integers(0, V, trunk)],
+            "branches": [[int(x) for x in rng.integers(0, V, b)] for b in branches], "groups": groups}
+
+
+def _oracle_forest(model, trees, debug=()):
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest(trees)
+    mask = ref.ranges_mask(ref.forest_ranges(meta), len(ids))
+    logits, _, dbg = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64, debug_layers=debug)
+    scores = []
+    leaf = 0
+    for tr in trees:
+        per_q = []
+        for groups in tr["groups"]:
+            per_q.append(ref.group_max(logits[leaf * n_ids:(leaf + 1) * n_ids], n_ids, [groups])[0])
+            leaf += 1
+        scores.append(per_q)
+    return scores, dbg
+
+
+def test_forest_packing_matches_oracle(pkg):
+    """The engine's vectorized packing equals the oracle's restatement of d1-3b-engine.ts:46-72, bit for bit,
+    and its attention ranges equal the brute-force forest mask."""
+    from decision_js_amd import engine
+    rng = np.random.default_rng(0)
+    trees = [_tree(rng, 1000, t, b) for t, b in [(40, [5, 9, 1]), (0, [7]), (13, []), (1, [1, 1, 30])]]
+    pk = engine.pack_forest(trees)
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest(trees)
+    assert np.array_equal(pk["ids"], ids) and np.array_equal(pk["pos"], pos) and np.array_equal(pk["meta"], meta)
+    assert np.array_equal(pk["leaves"], leaves) and np.array_equal(pk["leaf_ids"][:len(leaf_ids)], leaf_ids) and pk["n_ids"] == n_ids
+    assert np.array_equal(ref.ranges_mask(pk["rng"], len(ids)), ref.forest_mask(meta))
+
+
+@pytest.mark.parametrize("which", ["q8", "q4"])
+def test_decoder_forest_vs_oracle(pkg, models, which):
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models[which])
+    eng = DecoderEngine.load(models[which])
+    try:
+        rng = np.random.default_rng(1)
+        V = model.c["vocab"]
+        trees = [_tree(rng, V, 384, [24, 31, 17]), _tree(rng, V, 0, [96]), _tree(rng, V, 130, [1, 65])]
+        L = model.c["layers"]
+        got = eng.run(trees, debug_layers=[L - 1])
+        want, dbg = _oracle_forest(model, trees, debug=(L - 1,))
+        worst = max(abs(a - b) for gt, wt in zip(got["scores"], want) for gq, wq in zip(gt, wt)
+                    for a, b in zip(ref.softmax(gq), ref.softmax(wq)))
+        hid = rel_l2(got["debug"][L - 1], dbg[L - 1])
+        print(f"{which}: max prob gap {worst:.2e}, final hidden rel L2 {hid:.2e}")
+        assert worst < PROB_TOL and hid < HIDDEN_TOL
+    finally:
+        eng.destroy()
+
+
+def test_varlen_batch_equals_single_runs(pkg, models):
+    """Config-4 style: many sequences of random length packed into one forward give the answers each gives
+    alone (packing is exact), and agree with the oracle."""
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models["q8"])
+    eng = DecoderEngine.load(models["q8"])
+    try:
+        rng = np.random.default_rng(2)
+        V = model.c["vocab"]
+        lens = rng.integers(128, 769, 9)
+        trees = [_tree(rng, V, 0, [int(n)]) for n in lens]
+        batch = eng.run(trees)["scores"]
+        for k in (0, 4, 8):
+            alone = eng.run([trees[k]])["scores"][0]
+            for a, b in zip(ref.softmax(alone[0]), ref.softmax(batch[k][0])):
+                assert abs(a - b) < 2e-4
+        want, _ = _oracle_forest(model, trees[:3])
+        for gt, wt in zip(batch[:3], want):
+            assert max(abs(a - b) for a, b in zip(ref.softmax(gt[0]), ref.softmax(wt[0]))) < PROB_TOL
+    finally:
+        eng.destroy()
+
+
+def test_shared_state_equals_forest(pkg, models):
+    """Config-5 style: a 1024-token state prefilled once and its K/V reused by 8 questions of 32 tokens gives
+    the forest's answers (the model is causal, so both are exact), and the oracle's."""
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models["shared"])
+    eng = DecoderEngine.load(models["shared"])
+    try:
+        rng = np.random.default_rng(3)
+        V = model.c["vocab"]
+        tree = _tree(rng, V, 1024, [32] * 8)
+        forest = eng.run([tree])["scores"][0]
+        st = eng.prefill(tree["trunk"])
+        shared = eng.run_shared(st, tree["branches"], tree["groups"])
+        shared2 = eng.run_shared(st, tree["branches"], tree["groups"])  # replay of the captured graph
+        want, _ = _oracle_forest(model, [tree])
+        for f, s, s2, w in zip(forest, shared, shared2, want[0]):
+            pf, ps, pw = ref.softmax(f), ref.softmax(s), ref.softmax(w)
+            assert max(abs(a - b) for a, b in zip(pf, ps)) < 2e-4
+            assert s == s2
+            assert max(abs(a - b) for a, b in zip(ps, pw)) < PROB_TOL
+        st.free()
+    finally:
+        eng.destroy()
+
+
+def test_graph_replay_is_bit_identical(pkg, models):
+    from decision_js_amd.engine import DecoderEngine
+    eng = DecoderEngine.load(models["q8"])
+    try:
+        rng = np.random.default_rng(4)
+        V = 4096
+        a = [_tree(rng, V, 100, [20, 20, 20])]
+        b = [_tree(rng, V, 100, [20, 20, 20])]  # same shapes, other ids: replays a's graph
+        ra1, rb, ra2 = eng.run(a)["logits"], eng.run(b)["logits"], eng.run(a)["logits"]
+        eng.graphs = False
+        ra_eager = eng.run(a)["logits"]
+        assert np.array_equal(ra1, ra2) and np.array_equal(ra1, ra_eager) and not np.array_equal(ra1, rb)
+    finally:
+        eng.destroy()
+
+
+def test_encoder_vs_oracle(pkg, models):
+    from decision_js_amd.encoder import EncoderEngine
+    model = ref.Model(models["enc"])
+    eng = EncoderEngine.load(models["enc"])
+    try:
+        rng = np.random.default_rng(5)
+        V = model.c["vocab"]
+        seqs = [[int(x) for x in rng.integers(0, V, n)] for n in [256] + [24] * 3 + [8] * 7]
+        got = eng.embed(seqs)["embeddings"]
+        want = ref.encoder_forward(model, seqs, acc=np.float64)
+        err = max(rel_l2(g, w) for g, w in zip(got, want))
+        print(f"encoder: worst embedding rel L2 {err:.2e}")
+        assert err < HIDDEN_TOL
+        # config-1 ticket: every question scores all 7 options, cos(option, state + question)
+        for q in range(3):
+            z_got = ref.cosine_scores(got[0], got[1 + q], got[4:])
+            z_want = ref.cosine_scores(want[0], want[1 + q], want[4:])
+            assert max(abs(a - b) for a, b in zip(ref.softmax(z_got), ref.softmax(z_want))) < PROB_TOL
+    finally:
+        eng.destroy()
+
+
+def _questions(rng, V):
+    ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+    opt = lambda: [int(rng.integers(0, V))]  # noqa: E731
+    return {
+        "topic": {"type": "choice", "instructions": "What is the topic?", "criteria": {"billing": None, "delivery": None, "bug": None},
+                  "ids": ids(30), "options": [opt(), opt(), opt() + opt()]},
+        "churn": {"type": "noul", "instructions": "Leaving?", "ids": ids(20), "options": [opt() + opt(), opt()]},
+        "urgency": {"type": "score", "instructions": "How urgent?", "criteria": ["low", "medium", "high", "max", "now"],
+                    "ids": ids(25), "options": [opt() for _ in range(5)]},
+    }
+
+
+def test_decision_api(pkg, models):
+    from decision_js_amd.d1 import Decision
+    from decision_js_amd.questions import QuestionError
+    rng = np.random.default_rng(6)
+    V = 4096
+    d = Decision.load(models["q8"])
+    try:
+        state = [int(x) for x in rng.integers(0, V, 200)]
+        qs = _questions(rng, V)
+        r = d.system_one(state, qs)
+        assert set(r["answers"]) == {"topic", "churn", "urgency"}
+        assert r["usage"]["input_tokens"] == 200 + 30 + 20 + 25
+        assert r["answers"]["topic"]["choice"] in ("billing", "delivery", "bug")
+        p = d.probabilities(state, list(qs.values()))
+        assert abs(r["answers"]["churn"]["noul"] - p[1][0]) < 1e-12
+        assert abs(r["answers"]["urgency"]["score"] - sum(i * x for i, x in enumerate(p[2]))) < 1e-12
+        # the oracle agrees
+        tree = {"trunk": state, "branches": [q["ids"] for q in qs.values()], "groups": [q["options"] for q in qs.values()]}
+        want, _ = _oracle_forest(ref.Model(models["q8"]), [tree])
+        for gp, wq in zip(p, want[0]):
+            assert max(abs(a - b) for a, b in zip(gp, ref.softmax(wq))) < PROB_TOL
+        # batch of requests packed under a budget equals one-by-one
+        reqs = [([int(x) for x in rng.integers(0, V, n)], qs) for n in (50, 300, 10)]
+        d.tokens_per_pass = 400
+        seen = []
+        batch = d.system_one_batch(reqs, on_progress=lambda a, b: seen.append((a, b)))
+        assert seen[-1] == (3, 3) and len(seen) >= 2
+        for (s, q), b in zip(reqs, batch):
+            one = d.system_one(s, q)
+            assert abs(one["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 2e-4
+        # a malformed question throws, and the queue keeps working
+        with pytest.raises(QuestionError, match="decision.js: a choice needs criteria"):
+            d.system_one(state, {"bad": {"type": "choice", "instructions": "x", "criteria": {"a": 1}}})
+        assert d.system_one(state, qs)["answers"]["topic"]["choice"] == r["answers"]["topic"]["choice"]
+        # share_state: the state prefilled once, reused; same answers
+        d.share_state = True
+        rs = d.system_one(state, qs)
+        rs2 = d.system_one(state, qs)
+        for n in qs:
+            a, b = r["answers"][n], rs["answers"][n]
+            key = "noul" if n == "churn" else "confidence"
+            assert abs(a[key] - b[key]) < 2e-4 and rs2["answers"][n] == rs["answers"][n]
+    finally:
+        d.destroy()
+
+
+def test_decision_api_encoder(pkg, models):
+    from decision_js_amd.d1 import Decision
+    rng = np.random.default_rng(7)
+    V = 4096
+    d = Decision.load(models["enc"])
+    try:
+        state = [int(x) for x in rng.integers(0, V, 256)]
+        options = [[int(x) for x in rng.integers(0, V, 8)] for _ in range(7)]
+        qs = {f"q{i}": {"type": "choice", "instructions": "?", "criteria": {f"o{k}": None for k in range(7)},
+                        "ids": [int(x) for x in rng.integers(0, V, 24)], "option_ids": options} for i in range(3)}
+        r = d.system_one(state, qs)
+        assert r["usage"]["input_tokens"] == 256 + 3 * 24 + 7 * 8
+        r2 = d.system_one(state, qs)  # every text cached: nothing left to embed
+        assert r2["usage"]["input_tokens"] == 0 and r2["answers"] == r["answers"]
+    finally:
+        d.destroy()
