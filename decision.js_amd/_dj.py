@@ -51,6 +51,7 @@ SIGNATURES = {
     "dj_weight_bytes": [_P],
     "dj_rec_begin": [_P, _U64, C.POINTER(_P), C.POINTER(_I)],
     "dj_upload": [_P, _P, _P, _SZ],
+    "dj_buf_copy": [_P, _P, _P, _SZ],
     "dj_rec_snapshot": [_P, _P, _SZ, _P],
     "dj_rec_finish": [_P],
     "dj_graph_clear": [_P],
@@ -131,6 +132,13 @@ class DevBuf:
         if arr.nbytes > self.nbytes:
             raise ValueError(f"decision.js: {arr.nbytes} bytes do not fit a {self.nbytes}-byte buffer")
         check(lib().dj_upload(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes))
+
+    def copy_from(self, src: "DevBuf", nbytes: int = None):
+        """Asynchronous device->device copy on the context's stream (dj_buf_copy)."""
+        n = src.nbytes if nbytes is None else nbytes
+        if n > self.nbytes or n > src.nbytes:
+            raise ValueError("decision.js: device copy larger than a buffer")
+        check(lib().dj_buf_copy(self.ctx.h, self.ptr, src.ptr, n))
 
     def read(self, dtype, shape) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)

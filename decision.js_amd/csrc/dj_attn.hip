@@ -15,6 +15,7 @@
 //                                each 32-key MFMA step is permuted to match, and V^T is read to match)
 // Scores, the running max (m0 = -1e30) and the row sums are f32; the output is f16(acc / l), as the reference.
 #include <math.h>
+#include <stdio.h>
 #include "dj_internal.h"
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
@@ -188,5 +189,7 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
     int st = dj_launch_attention(rec->ctx->stream, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O);
     if (st) return st;
   }
-  return dj_op_end(rec, "attention");
+  char shape[48];
+  snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
+  return dj_op_end(rec, "attention", shape);
 }

@@ -11,13 +11,16 @@
 // blocks were interleaved at load, so a lane holds a gate value and its up value side by side
 // (MATMUL_SWIGLU, kernels.ts:591-599; GELU_MUL, eg2-kernels.ts:165-177).
 #include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 #include "dj_internal.h"
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
 template <int BITS> struct RawB;
-template <> struct RawB<8> { uint4 v; };
-template <> struct RawB<4> { uint2 v; };
+template <> struct RawB<8> { u32x4 v; };
+template <> struct RawB<4> { u32x2 v; };
 
 __device__ __forceinline__ h2 pair_q(uint32_t p, h2 bias, h2 sc) {
   h2 v = __builtin_bit_cast(h2, p | 0x64006400u);
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
   constexpr int ACH = BM * 8 / NT;
   static_assert((BM * 8) % NT == 0, "A stage must split evenly over the threads");
   constexpr int CB = BITS == 8 ? 1024 : 512;
-  __shared__ uint4 As[2][BM * 8];
+  __shared__ u32x4 As[2][BM * 8];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -97,73 +100,74 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  uint4 areg[ACH];
-  auto gload_a = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + i * NT, r = c >> 3, ch = c & 7;
-      const int gm = min(m0 + r, M - 1);
-      areg[i] = *(const uint4 *)(X + (size_t)gm * K + kt * 64 + ch * 8);
-    }
-  };
-  auto sstore_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + i * NT, r = c >> 3, ch = c & 7;
-      As[buf][r * 8 + (ch ^ (r & 7))] = areg[i];
-    }
-  };
+  // Software pipeline, unrolled by two so that both register sets are named (no dynamic indexing, which
+  // would put them in scratch): A(k) is loaded two k-steps ahead into registers and stored to LDS one step
+  // ahead (double-buffered LDS); B(k) (codes + scales) is loaded into registers two steps ahead.
   const int nb0 = (n0 >> 4) + wn * FN;
-  RawB<BITS> braw[FN], bnext[FN];
-  uint32_t sraw[FN], snext[FN];
-  auto gload_b = [&](int kt, RawB<BITS> *br, uint32_t *sr) {
+  const uint16_t *xrow[ACH];
+  int aoff[ACH];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const size_t blk = (size_t)(nb0 + j) * KT + kt;
-      if constexpr (BITS == 8)
-        br[j].v = *(const uint4 *)(Wc + blk * CB + lane * 16);
-      else
-        br[j].v = *(const uint2 *)(Wc + blk * CB + lane * 8);
-      sr[j] = Ws[blk * 16 + (lane & 15)];
-    }
-  };
+  for (int i = 0; i < ACH; ++i) {
+    const int c = tid + i * NT, r = c >> 3, ch = c & 7;
+    xrow[i] = X + (size_t)min(m0 + r, M - 1) * K + ch * 8;
+    aoff[i] = r * 8 + (ch ^ (r & 7));
+  }
+  u32x4 a0[ACH], a1[ACH];
+  RawB<BITS> b0[FN], b1[FN];
+  uint32_t s0[FN], s1[FN];
 
-  gload_a(0);
-  sstore_a(0);
-  gload_b(0, braw, sraw);
+#define DJ_LOAD_A(dst, kt)                                                     \
+  _Pragma("unroll") for (int i = 0; i < ACH; ++i) dst[i] = *(const u32x4 *)(xrow[i] + (kt) * 64);
+#define DJ_STORE_A(src, buf) _Pragma("unroll") for (int i = 0; i < ACH; ++i) As[buf][aoff[i]] = src[i];
+#define DJ_LOAD_B(dst, sdst, kt)                                               \
+  _Pragma("unroll") for (int j = 0; j < FN; ++j) {                             \
+    const size_t blk = (size_t)(nb0 + j) * KT + (kt);                          \
+    if constexpr (BITS == 8)                                                   \
+      dst[j].v = *(const u32x4 *)(Wc + blk * CB + lane * 16);                  \
+    else                                                                       \
+      dst[j].v = *(const u32x2 *)(Wc + blk * CB + lane * 8);                   \
+    sdst[j] = Ws[blk * 16 + (lane & 15)];                                      \
+  }
+#define DJ_COMPUTE(buf, bb, ss)                                                        \
+  _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                      \
+    h8 bf[FN];                                                                         \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(bb[j], s, ss[j]); \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                   \
+      const int r = wm * FM * 16 + i * 16 + (lane & 15);                               \
+      const int ch = s * 4 + (lane >> 4);                                              \
+      const h8 af = __builtin_bit_cast(h8, As[buf][r * 8 + (ch ^ (r & 7))]);           \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]); \
+    }                                                                                  \
+  }
+
+  DJ_LOAD_A(a0, 0);
+  DJ_LOAD_B(b0, s0, 0);
+  if (KT > 1) {
+    DJ_LOAD_A(a1, 1);
+    DJ_LOAD_B(b1, s1, 1);
+  }
+  DJ_STORE_A(a0, 0);
   __syncthreads();
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      gload_a(kt + 1);
-      gload_b(kt + 1, bnext, snext);
-    }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      h8 bf[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(braw[j], s, sraw[j]);
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * FM * 16 + i * 16 + (lane & 15);
-        const int ch = s * 4 + (lane >> 4);
-        const h8 af = __builtin_bit_cast(h8, As[cur][r * 8 + (ch ^ (r & 7))]);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]);
-      }
-    }
-    if (more) {
-      sstore_a(cur ^ 1);
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        braw[j] = bnext[j];
-        sraw[j] = snext[j];
-      }
-    }
+  for (int kt = 0; kt < KT; kt += 2) {
+    // step kt: LDS 0 = A(kt), b0 = B(kt); a1 = A(kt+1) in flight
+    if (kt + 2 < KT) DJ_LOAD_A(a0, kt + 2);
+    DJ_COMPUTE(0, b0, s0);
+    if (kt + 1 < KT) DJ_STORE_A(a1, 1);
+    if (kt + 2 < KT) DJ_LOAD_B(b0, s0, kt + 2);
+    __syncthreads();
+    if (kt + 1 >= KT) break;
+    // step kt+1: LDS 1 = A(kt+1), b1 = B(kt+1); a0 = A(kt+2) in flight
+    if (kt + 3 < KT) DJ_LOAD_A(a1, kt + 3);
+    DJ_COMPUTE(1, b1, s1);
+    if (kt + 2 < KT) DJ_STORE_A(a0, 0);
+    if (kt + 3 < KT) DJ_LOAD_B(b1, s1, kt + 3);
     __syncthreads();
   }
+#undef DJ_LOAD_A
+#undef DJ_STORE_A
+#undef DJ_LOAD_B
+#undef DJ_COMPUTE
 
   // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
   const int rbase = m0 + wm * FM * 16 + (lane >> 4) * 4;
@@ -205,23 +209,62 @@ static void launch_cfg(hipStream_t s, const uint16_t *X, const dj_weight *w, uin
       X, w->codes, (const uint32_t *)w->scales, Y, M, w->N, w->K, act, tiles_m, tiles_n);
 }
 
+// Tile configurations: (waves along M, waves along N, 16-row fragments per wave, 16-column fragments per wave).
+struct GemmCfg {
+  const char *tag;
+  int wm, wn, fm, fn;
+  int bm() const { return wm * fm * 16; }
+  int bn() const { return wn * fn * 16; }
+};
+static const GemmCfg kCfgs[] = {
+    {"128x128", 2, 2, 4, 4}, {"128x64", 2, 2, 4, 2}, {"64x128", 2, 2, 2, 4}, {"64x64", 2, 2, 2, 2},
+    {"32x128", 1, 4, 2, 2},  {"128x32", 4, 1, 2, 2}, {"128x16", 4, 1, 2, 1},
+};
+static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+template <int BITS, bool GLU>
+static void launch_index(int i, hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act) {
+  switch (i) {
+    case 0: launch_cfg<BITS, 2, 2, 4, 4, GLU>(s, X, w, Y, M, act); break;
+    case 1: launch_cfg<BITS, 2, 2, 4, 2, GLU>(s, X, w, Y, M, act); break;
+    case 2: launch_cfg<BITS, 2, 2, 2, 4, GLU>(s, X, w, Y, M, act); break;
+    case 3: launch_cfg<BITS, 2, 2, 2, 2, GLU>(s, X, w, Y, M, act); break;
+    case 4: launch_cfg<BITS, 1, 4, 2, 2, GLU>(s, X, w, Y, M, act); break;
+    case 5: launch_cfg<BITS, 4, 1, 2, 2, GLU>(s, X, w, Y, M, act); break;
+    default: launch_cfg<BITS, 4, 1, 2, 1, false>(s, X, w, Y, M, act); break;
+  }
+}
+
+static bool cfg_fits(const GemmCfg &c, int N, bool glu) {
+  return N % c.bn() == 0 && (!glu || c.fn % 2 == 0);
+}
+
+// The tile: DJ_GEMM_TILE=<tag> forces one (tuning sweeps). Otherwise the order below, measured on MI355X
+// over the configurations' shapes (M 32 to 86016, N 1024 to 9216, K 1024 to 3072): 32x128 was the fastest
+// or within 5% everywhere (4 waves side by side on one A tile; more workgroups per CU hide load latency).
+static int pick_cfg(int M, int N, bool glu) {
+  const char *force = getenv("DJ_GEMM_TILE");
+  if (force)
+    for (int i = 0; i < kNumCfgs; ++i)
+      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, glu)) return i;
+  static const int order[] = {4, 3, 5, 6};  // 32x128, 64x64, 128x32, 128x16
+  for (int i : order)
+    if (cfg_fits(kCfgs[i], N, glu)) return i;
+  (void)M;
+  return -1;
+}
+
 template <int BITS, bool GLU>
 static int launch_bits(hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name) {
-  const int N = w->N;
-  if (N % 128 == 0 && M >= 2048) {
-    launch_cfg<BITS, 2, 2, 8, 4, GLU>(s, X, w, Y, M, act);
-    *name = BITS == 8 ? (GLU ? "matmul_glu_q8_256x128" : "matmul_q8_256x128") : (GLU ? "matmul_glu_q4_256x128" : "matmul_q4_256x128");
-  } else if (N % 128 == 0) {
-    launch_cfg<BITS, 2, 2, 4, 4, GLU>(s, X, w, Y, M, act);
-    *name = BITS == 8 ? (GLU ? "matmul_glu_q8_128x128" : "matmul_q8_128x128") : (GLU ? "matmul_glu_q4_128x128" : "matmul_q4_128x128");
-  } else if (N % 32 == 0) {
-    launch_cfg<BITS, 4, 1, 2, 2, GLU>(s, X, w, Y, M, act);
-    *name = BITS == 8 ? (GLU ? "matmul_glu_q8_128x32" : "matmul_q8_128x32") : (GLU ? "matmul_glu_q4_128x32" : "matmul_q4_128x32");
-  } else {
-    if (GLU) return dj_fail(DJ_EINVAL, "decision.js: gated matmul needs N %% 32 == 0 (N = %d)", N);
-    launch_cfg<BITS, 4, 1, 2, 1, false>(s, X, w, Y, M, act);
-    *name = BITS == 8 ? "matmul_q8_128x16" : "matmul_q4_128x16";
-  }
+  static const char *const names[2][2][kNumCfgs] = {
+      {{"matmul_q4_128x128", "matmul_q4_128x64", "matmul_q4_64x128", "matmul_q4_64x64", "matmul_q4_32x128", "matmul_q4_128x32", "matmul_q4_128x16"},
+       {"matmul_glu_q4_128x128", "matmul_glu_q4_128x64", "matmul_glu_q4_64x128", "matmul_glu_q4_64x64", "matmul_glu_q4_32x128", "matmul_glu_q4_128x32", "-"}},
+      {{"matmul_q8_128x128", "matmul_q8_128x64", "matmul_q8_64x128", "matmul_q8_64x64", "matmul_q8_32x128", "matmul_q8_128x32", "matmul_q8_128x16"},
+       {"matmul_glu_q8_128x128", "matmul_glu_q8_128x64", "matmul_glu_q8_64x128", "matmul_glu_q8_64x64", "matmul_glu_q8_32x128", "matmul_glu_q8_128x32", "-"}}};
+  const int i = pick_cfg(M, w->N, GLU);
+  if (i < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", w->N, GLU ? " (gated: N % 32 == 0)" : "");
+  launch_index<BITS, GLU>(i, s, X, w, Y, M, act);
+  *name = names[BITS == 8][GLU][i];
   return DJ_OK;
 }
 
@@ -240,7 +283,9 @@ extern "C" int dj_matmul(dj_rec *rec, const uint16_t *X, const dj_weight *w, uin
     int st = dj_launch_gemm(rec->ctx->stream, X, w, Y, M, -1, &name);
     if (st) return st;
   }
-  return dj_op_end(rec, name);
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  return dj_op_end(rec, name, shape);
 }
 
 extern "C" int dj_matmul_glu(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *H, int M, int act) {
@@ -252,5 +297,7 @@ extern "C" int dj_matmul_glu(dj_rec *rec, const uint16_t *X, const dj_weight *w,
     int st = dj_launch_gemm(rec->ctx->stream, X, w, H, M, act, &name);
     if (st) return st;
   }
-  return dj_op_end(rec, name);
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  return dj_op_end(rec, name, shape);
 }

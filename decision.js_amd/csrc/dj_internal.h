@@ -11,6 +11,10 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+// native vector types for registers that must stay in registers (HIP's uint4 is a struct that can keep
+// arrays of it out of SROA and in scratch memory)
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- errors
 int dj_fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -45,7 +49,7 @@ struct dj_graph_entry {
 };
 
 struct dj_prof_slot {
-  const char *name;
+  std::string name;
   hipEvent_t a, b;
 };
 
@@ -86,8 +90,9 @@ struct dj_rec {
 // Opens an op: validates the recorder, honours replay (ops ignored) and fault injection, and starts a
 // profiling slot. Returns 1 if the op must be skipped (replay), 0 to launch, or a negative status.
 int dj_op_begin(dj_rec *rec, const char *name);
-// Closes an op after its kernel launches: checks the launch and ends the profiling slot.
-int dj_op_end(dj_rec *rec, const char *name);
+// Closes an op after its kernel launches: checks the launch and ends the profiling slot. `detail`
+// (optional) is appended to the profile key, e.g. the GEMM shape.
+int dj_op_end(dj_rec *rec, const char *name, const char *detail = nullptr);
 
 #define DJ_OP_BEGIN(rec, name)                   \
   do {                                           \

@@ -134,6 +134,11 @@ extern "C" int dj_buf_read(dj_ctx *c, void *host, const void *dev, size_t bytes)
   return DJ_OK;
 }
 
+extern "C" int dj_buf_copy(dj_ctx *c, void *dst, const void *src, size_t bytes) {
+  DJ_REQUIRE(c && (dst || !bytes) && (src || !bytes), "decision.js: dj_buf_copy: null argument");
+  return dj_launch_copy(c->stream, dst, src, bytes);
+}
+
 extern "C" int dj_upload(dj_ctx *c, void *dev, const void *host, size_t bytes) {
   DJ_REQUIRE(c && (dev || !bytes) && (host || !bytes), "decision.js: dj_upload: null argument");
   DJ_REQUIRE(!c->active || !c->active->capturing,
@@ -323,7 +328,7 @@ int dj_op_begin(dj_rec *rec, const char *name) {
   return 0;
 }
 
-int dj_op_end(dj_rec *rec, const char *name) {
+int dj_op_end(dj_rec *rec, const char *name, const char *detail) {
   dj_ctx *c = rec->ctx;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -332,7 +337,7 @@ int dj_op_end(dj_rec *rec, const char *name) {
   }
   if (c->profiling && !rec->capturing && !c->prof_pending.empty()) {
     dj_prof_slot &s = c->prof_pending.back();
-    s.name = name;  // the launcher may refine the name (e.g. the GEMM tile)
+    s.name = detail ? std::string(name) + detail : std::string(name);  // the launcher may refine the name
     (void)hipEventRecord(s.b, c->stream);
   }
   return DJ_OK;

@@ -258,22 +258,42 @@ class DecoderEngine(GpuEngine):
         self.stats["tokens"] += T
         return got
 
+    INPUTS = ("ids", "pos", "rng", "leaves", "leaf_ids")
+
     def run(self, trees, debug_layers=()):
         """Option scores for every question of every tree: [tree][question][option] (max over the option's
         token group), plus {layer: hidden state x} for the requested debug layers (D13BEngine.run)."""
-        debug_layers = tuple(sorted(set(debug_layers)))
         pk = pack_forest(trees)
-        T, L, n_ids = pk["T"], pk["L"], pk["n_ids"]
-        if T == 0:
+        if pk["T"] == 0:
             return {"scores": [[] for _ in trees], "debug": {}}
+        return self._forward(pk, trees, debug_layers, None)
+
+    def stage(self, trees):
+        """Packs `trees` and keeps the packed inputs in device memory, so that run_staged starts from inputs
+        already resident in HBM (the benchmark's timed region)."""
+        pk = pack_forest(trees)
+        return {"pk": pk, "trees": trees, "bufs": {k: self.ctx.array(pk[k]) for k in self.INPUTS}}
+
+    def run_staged(self, st):
+        """run() on a stage()d batch: device-to-device copies of its inputs, then the same forward."""
+        return self._forward(st["pk"], st["trees"], (), st["bufs"])
+
+    def free_staged(self, st):
+        for b in st["bufs"].values():
+            b.free()
+
+    def _forward(self, pk, trees, debug_layers, staged):
+        debug_layers = tuple(sorted(set(debug_layers)))
+        T, L, n_ids = pk["T"], pk["L"], pk["n_ids"]
         self.ensure(T, L, n_ids)
         B = self._bufs
-        B["ids"].upload(pk["ids"])
-        B["pos"].upload(pk["pos"])
-        B["rng"].upload(pk["rng"])
-        if L:
-            B["leaves"].upload(pk["leaves"])
-            B["leaf_ids"].upload(pk["leaf_ids"])
+        for k in self.INPUTS:
+            if k in ("leaves", "leaf_ids") and not L:
+                continue
+            if staged is not None:
+                B[k].copy_from(staged[k])
+            else:
+                B[k].upload(pk[k])
         rec = self.ctx.recorder(self._key("run", T, L, n_ids, tuple(debug_layers)))
         snaps = {}
         if not rec.replay:

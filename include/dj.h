@@ -99,6 +99,9 @@ int dj_rec_begin(dj_ctx *ctx, uint64_t graph_key, dj_rec **out, int *replay);
  * leaves...). `host` is copied into pinned staging memory at once, so it may be reused on return.
  * Replaces: storage(view) (gpu.ts:148-152). Not allowed while capturing a graph: upload first. */
 int dj_upload(dj_ctx *ctx, void *dev, const void *host, size_t bytes);
+/* Asynchronous device->device copy on the context's stream (a kernel: it may be recorded into a graph).
+ * Both pointers 16-byte aligned. Used to move inputs already resident in HBM into an engine's buffers. */
+int dj_buf_copy(dj_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
 /* Copies `bytes` of device memory into `host` once the forward has run (filled by dj_rec_finish).
  * Replaces: snapshot(buf, bytes, type) (gpu.ts:237-244). */
 int dj_rec_snapshot(dj_rec *rec, const void *dev, size_t bytes, void *host);
