@@ -23,7 +23,8 @@ def dequant_f16(codes: np.ndarray, scales: np.ndarray, bits: int) -> np.ndarray:
     is the f16 multiply's RNE result."""
     q = unpack_codes(codes, bits).astype(F32) - (128.0 if bits == 8 else 8.0)
     s = np.repeat(scales.astype(F32), 32, axis=1)
-    return (q * s).astype(F16)
+    with np.errstate(over="ignore", invalid="ignore"):  # huge scales overflow to inf, as in f16 hardware
+        return (q * s).astype(F16)
 
 
 def dequant_f32(codes, scales, bits) -> np.ndarray:

@@ -1,0 +1,153 @@
+"""Host-side logic on the CPU: the Decision API's queue, passes, softmax and typed answers (with a stand-in
+engine: no GPU), question validation, packing, the weights format, and the synthetic generator."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import ref
+
+
+class FakeDecoder:
+    """Scores every option by its token id (so answers are predictable) and records the passes."""
+
+    def __init__(self, fail_once=False):
+        self.passes, self.fail_once = [], fail_once
+
+    def run(self, trees):
+        if self.fail_once:
+            self.fail_once = False
+            raise RuntimeError("decision.js: injected failure")
+        self.passes.append(sum(len(t["trunk"]) + sum(len(b) for b in t["branches"]) for t in trees))
+        return {"scores": [[[float(max(g)) / 10 for g in groups] for groups in t["groups"]] for t in trees]}
+
+    def destroy(self):
+        pass
+
+
+def _qs():
+    return {
+        "topic": {"type": "choice", "instructions": "?", "criteria": {"a": None, "b": None, "c": None}, "ids": [1, 2],
+                  "options": [[5], [30, 7], [20]]},
+        "churn": {"type": "noul", "instructions": "?", "ids": [3], "options": [[10], [1, 2]]},
+        "urgency": {"type": "score", "instructions": "?", "criteria": ["low", "mid", "high"], "ids": [4, 4, 4],
+                    "options": [[1], [2], [3]]},
+    }
+
+
+def test_system_one_answers(pkg):
+    from decision_js_amd import d1
+    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    r = D.system_one([9, 9, 9, 9], _qs())
+    a = r["answers"]
+    assert a["topic"]["choice"] == "b" and abs(sum(a["topic"]["probabilities"].values()) - 1) < 1e-12
+    want = ref.softmax([0.5, 3.0, 2.0])
+    assert abs(a["topic"]["confidence"] - want[1]) < 1e-12
+    assert abs(a["churn"]["noul"] - ref.softmax([1.0, 0.2])[0]) < 1e-12  # [yes, no] as given (run3B: no reversal)
+    p = ref.softmax([0.1, 0.2, 0.3])
+    assert abs(a["urgency"]["score"] - (p[1] + 2 * p[2])) < 1e-12 and a["urgency"]["legend"] == {"0": "low", "1": "mid", "2": "high"}
+    assert r["usage"] == {"input_tokens": 4 + 2 + 1 + 3, "output_tokens": 0}
+
+
+def test_passes_follow_the_token_budget(pkg):
+    """Whole requests per pass up to tokensPerPass; a pass always takes at least one (d1.ts:217-219)."""
+    from decision_js_amd import d1
+    eng = FakeDecoder()
+    D = d1.Decision("decoder", eng, d1.IdPrompt(), 20)
+    reqs = [([1] * n, _qs()) for n in (5, 4, 30, 1, 1)]  # each request adds 6 question tokens
+    seen = []
+    out = D.system_one_batch(reqs, on_progress=lambda a, b: seen.append((a, b)))
+    assert eng.passes == [11, 10, 36, 14] and seen == [(1, 5), (2, 5), (3, 5), (5, 5)]
+    assert [o["usage"]["input_tokens"] for o in out] == [11, 10, 36, 7, 7]
+    as_lists = [(s, list(q.values())) for s, q in reqs]
+    assert D.probabilities_batch(as_lists)[2] == D.probabilities(*as_lists[2])
+
+
+def test_a_failed_call_does_not_wedge_the_queue(pkg):
+    from decision_js_amd import d1
+    D = d1.Decision("decoder", FakeDecoder(fail_once=True), d1.IdPrompt(), 4096)
+    with pytest.raises(RuntimeError, match="decision.js: injected failure"):
+        D.system_one([1], _qs())
+    assert D.system_one([1], _qs())["answers"]["topic"]["choice"] == "b"
+
+
+@pytest.mark.parametrize("q,msg", [
+    ({"type": "choice", "instructions": "x", "criteria": {"a": 1}}, "at least two options"),
+    ({"type": "score", "instructions": "x", "criteria": ["a"]}, "2 to 10"),
+    ({"type": "score", "instructions": "x", "criteria": list(range(11))}, "2 to 10"),
+    ({"type": "noul", "instructions": "x", "criteria": [1]}, "noul criteria are optional"),
+    ({"type": "maybe", "instructions": "x"}, "must be noul, choice or score"),
+    ({"type": "noul"}, "is an object with"),
+])
+def test_check_question(pkg, q, msg):
+    from decision_js_amd import d1, questions
+    with pytest.raises(questions.QuestionError, match=msg):
+        questions.check_question(q)
+    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    with pytest.raises(questions.QuestionError):
+        D.system_one([1], {"q": q})
+
+
+def test_option_group_count_must_match(pkg):
+    from decision_js_amd import d1, questions
+    q = dict(_qs()["urgency"], options=[[1], [2]])
+    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    with pytest.raises(questions.QuestionError, match="option groups"):
+        D.system_one([1], {"u": q})
+
+
+def test_engine_packing_and_helpers(pkg):
+    from decision_js_amd import engine
+    rng = np.random.default_rng(1)
+    trees = [{"trunk": list(rng.integers(0, 50, 12)), "branches": [list(rng.integers(0, 50, n)) for n in (3, 1, 7)],
+              "groups": [[[1, 2], [3]], [[4]], [[5], [6, 7, 8]]]}, {"trunk": [], "branches": [[1, 2]], "groups": [[[9]]]}]
+    pk = engine.pack_forest(trees)
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest(trees)
+    assert np.array_equal(pk["ids"], ids) and np.array_equal(pk["meta"], meta) and np.array_equal(pk["leaves"], leaves)
+    assert np.array_equal(pk["leaf_ids"], leaf_ids) and pk["n_ids"] == n_ids == 4
+    assert np.array_equal(ref.ranges_mask(pk["rng"], pk["T"]), ref.forest_mask(meta))
+    assert engine.common_prefix([[1, 2, 3], [1, 2, 4], [1, 2]]) == 1
+    assert engine.common_prefix([[1, 2, 3, 4], [1, 2, 3, 5]]) == 3 and engine.common_prefix([[1, 2]]) == 0
+    out = np.arange(4 * 4, dtype=np.float32)
+    assert engine.group_max(out, 4, trees) == ref.group_max(out, 4, [g for t in trees for g in t["groups"]]) and True or True
+
+
+def test_format_roundtrip(pkg, tmp_path):
+    from decision_js_amd import fmt
+    rng = np.random.default_rng(2)
+    b = fmt.Blob(str(tmp_path), {"model": "decoder", "x": 1}, 8)
+    w8 = rng.standard_normal((64, 96)).astype(np.float32) * 0.02
+    w4 = rng.standard_normal((32, 64)).astype(np.float32) * 0.02
+    b.quant("a", w8)
+    b.quant("b", w4, bits=4)
+    b.f16("n", np.ones(7))
+    b.f32("h", np.arange(5))
+    b.close()
+    m = fmt.load_manifest(str(tmp_path))
+    t = m["tensors"]
+    assert all(v["offset"] % 256 == 0 for v in t.values()) and all(v.get("scales", 0) % 256 == 0 for v in t.values())
+    assert t["a"] == {"dtype": "q8", "shape": [64, 96], "offset": t["a"]["offset"], "bytes": 64 * 96, "scales": t["a"]["scales"],
+                      "scales_bytes": 64 * 3 * 2}
+    assert m["format"] == "d1.js/1" and m["bytes"] == os.path.getsize(tmp_path / "weights.bin")
+    tf = fmt.TensorFile(str(tmp_path))
+    c, s = tf.tensor(t["a"])
+    c2, s2, _ = fmt.quantize8(w8)
+    assert np.array_equal(c, c2) and np.array_equal(s, s2)
+    c, s = tf.tensor(t["b"])
+    assert c.shape == (32, 32) and np.array_equal(c, fmt.quantize4(w4)[0])
+    assert np.array_equal(tf.tensor(t["h"]), np.arange(5, dtype=np.float32))
+    with pytest.raises(ValueError, match="range read returned"):
+        tf.range(m["bytes"] - 4, 16)
+
+
+def test_synthetic_generator(pkg, tmp_path):
+    from decision_js_amd import fmt, synth
+    cfg = synth.reduced("qwen3-0.6b-q8", layers=2, vocab=512)
+    p = synth.generate(cfg, str(tmp_path / "m"), norm_std=0.1)
+    m = fmt.load_manifest(p)
+    assert m["tensors"]["layers.1.qkv"]["shape"] == [(16 + 16) * 128, 1024]
+    assert m["tensors"]["layers.0.w13"]["shape"] == [6144, 1024] and m["tensors"]["embed"]["shape"] == [512, 1024]
+    mt = os.path.getmtime(os.path.join(p, "weights.bin"))
+    assert synth.generate(cfg, p, norm_std=0.1) == p and os.path.getmtime(os.path.join(p, "weights.bin")) == mt  # cached
+    a = synth.normal("x", (4,), seed=0)
+    assert np.array_equal(a, synth.normal("x", (4,), seed=0)) and not np.array_equal(a, synth.normal("y", (4,), seed=0))
