@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libdj.so")
 
 DJ_OK, DJ_EINVAL, DJ_EHIP, DJ_ENOMEM, DJ_ESTATE, DJ_EINJECT = range(6)
 W_PLAIN, W_MFMA, W_MFMA_GLU = 0, 1, 2
+W_DIRECT = 16  # flag: f16 weights dequantized once at load (the reference's directWeights)
 ACT_SILU, ACT_GELU_TANH = 0, 1
 ROPE_POW_NEG, ROPE_INV_POW = 0, 1
 

@@ -25,9 +25,14 @@ FLAGS = [
 ]
 
 
+# MFMA kernels keep their accumulators in ordinary VGPRs (gfx950 allows it): with AGPRs the register allocator
+# shuffled the accumulators between AGPRs on every K iteration of the GEMM loop.
+PER_FILE = {"dj_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"], "dj_attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def compile_one(src: str) -> str:
     obj = os.path.join(HERE, "_build", src.replace(".hip", ".o"))
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *PER_FILE.get(src, []), "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so: harmless, filtered
     noise = "'-packed-fp32-ops' is not a recognized feature"

@@ -1,14 +1,24 @@
-// q8/q4 block-dequant GEMM on gfx950 f16 MFMA (v_mfma_f32_16x16x32_f16), f32 accumulation:
-//   Y[M, N] = X[M, K] . W^T, X f16 row-major, W quantized in blocks of 32 along K with an f16 scale each.
-// The weight is repacked at load (dj_runtime.hip) so that one wave reads the B operand of two MFMA k-steps
-// as one 16-byte (q8) or 8-byte (q4) load per lane, already in lane order. Codes become f16 in registers by
-// the exponent trick (0x6400 | code is 1024 + code exactly), minus the zero point, times the scale: the
-// same single RNE rounding as the reference's f16 dequantization (kernels.ts:20, 296, 541), so the GEMM
-// multiplies by bit-identical f16 weights. X tiles go through LDS (double buffered, XOR-swizzled 16-byte
-// chunks); each wave dequantizes only its own columns.
+// GEMM on gfx950 f16 MFMA (v_mfma_f32_16x16x32_f16), f32 accumulation:
+//   Y[M, N] = X[M, K] . W^T, X f16 row-major, W one of
+//     q8 / q4  quantized in blocks of 32 along K with an f16 scale each (kept quantized in HBM), or
+//     f16      the same weights dequantized once at load ("direct weights", the reference's directWeights
+//              option, gpu.ts:16-20, 114-133) — bit-identical f16 values, twice the bytes of q8.
+// Weights are repacked at load (dj_runtime.hip) so one wave reads the B operand of two MFMA k-steps with one
+// 16-byte (q8), 8-byte (q4) or two 16-byte (f16) loads per lane, already in lane order. Quantized codes become
+// f16 in registers by the exponent trick: 0x6400 | code is exactly 1024 + code; minus (1024 + zero point),
+// times the group scale — one RNE rounding, the reference's f16 dequantization (kernels.ts:20, 296, 541).
+//
+// Per workgroup: WM x WN waves, each computing FM x FN 16x16 fragments. X tiles (64 K per step) go through
+// double-buffered, XOR-swizzled LDS, loaded one step ahead; B goes straight to registers two steps ahead.
+// The K loop is unrolled by two so both register sets have names (no dynamic indexing -> no scratch).
+//
+// Split-K (grid y = S): each split stores its f32 partial tile in its own workspace slice; the last split to
+// arrive at a tile (per-tile counter) adds the slices in split order (deterministic), resets the counter (so
+// the counters need clearing only once, at context creation, and a captured graph holds no memset), then
+// runs the epilogue.
 //
 // Epilogues: plain f16 store, or the gated MLP (SiLU / tanh-GELU) on a [w1; w3] weight whose 16-column
-// blocks were interleaved at load, so a lane holds a gate value and its up value side by side
+// blocks were interleaved at load so a lane holds a gate value and its up value side by side
 // (MATMUL_SWIGLU, kernels.ts:591-599; GELU_MUL, eg2-kernels.ts:165-177).
 #include <math.h>
 #include <stdio.h>
@@ -18,39 +28,44 @@
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
+// Per-lane raw B of one 64-K step for one 16-column fragment.
 template <int BITS> struct RawB;
-template <> struct RawB<8> { u32x4 v; };
-template <> struct RawB<4> { u32x2 v; };
+template <> struct RawB<8> { u32x4 v; };         // 16 codes: [k-step 0: 8][k-step 1: 8]
+template <> struct RawB<4> { u32x2 v; };         // 16 nibbles
+template <> struct RawB<16> { u32x4 v0, v1; };   // 16 f16 weights
 
-__device__ __forceinline__ h2 pair_q(uint32_t p, h2 bias, h2 sc) {
-  h2 v = __builtin_bit_cast(h2, p | 0x64006400u);
-  return (v - bias) * sc;
+__device__ __forceinline__ h2 fma_free_dequant(uint32_t p, h2 bias, h2 sc) {
+  const h2 v = __builtin_bit_cast(h2, p);
+  return (v - bias) * sc;  // exact subtraction, then the one rounding of the f16 multiply
 }
 
-// 8 f16 weights of k-step s from the lane's raw codes.
+// The 8 f16 weights of k-step s.
 template <int BITS>
 __device__ __forceinline__ h8 dequant(const RawB<BITS> &r, int s, uint32_t sp) {
-  const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)(s ? (sp >> 16) : (sp & 0xffffu)));
-  const h2 sc = {sv, sv};
-  h8 out;
-  if constexpr (BITS == 8) {
-    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + zero point 128
-    const uint32_t lo = s ? r.v.z : r.v.x, hi = s ? r.v.w : r.v.y;
-    const h2 p0 = pair_q((lo & 0xffu) | ((lo & 0xff00u) << 8), bias, sc);
-    const h2 p1 = pair_q(((lo >> 16) & 0xffu) | ((lo >> 8) & 0xff0000u), bias, sc);
-    const h2 p2 = pair_q((hi & 0xffu) | ((hi & 0xff00u) << 8), bias, sc);
-    const h2 p3 = pair_q(((hi >> 16) & 0xffu) | ((hi >> 8) & 0xff0000u), bias, sc);
-    out = (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  if constexpr (BITS == 16) {
+    return __builtin_bit_cast(h8, s ? r.v1 : r.v0);
   } else {
-    const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + zero point 8
-    const uint32_t w = s ? r.v.y : r.v.x;
-    const h2 p0 = pair_q(w & 0x000f000fu, bias, sc);
-    const h2 p1 = pair_q((w >> 4) & 0x000f000fu, bias, sc);
-    const h2 p2 = pair_q((w >> 8) & 0x000f000fu, bias, sc);
-    const h2 p3 = pair_q((w >> 12) & 0x000f000fu, bias, sc);
-    out = (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    const _Float16 sv = __builtin_bit_cast(_Float16, (uint16_t)(s ? (sp >> 16) : (sp & 0xffffu)));
+    const h2 sc = {sv, sv};
+    if constexpr (BITS == 8) {
+      const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};  // 1024 + zero point 128
+      const uint32_t lo = s ? r.v.z : r.v.x, hi = s ? r.v.w : r.v.y;
+      // v_perm_b32: bytes (code_a, 0x64, code_b, 0x64) = the f16 pair (1024 + code_a, 1024 + code_b)
+      const h2 p0 = fma_free_dequant(__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u), bias, sc);
+      const h2 p1 = fma_free_dequant(__builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u), bias, sc);
+      const h2 p2 = fma_free_dequant(__builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u), bias, sc);
+      const h2 p3 = fma_free_dequant(__builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u), bias, sc);
+      return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    } else {
+      const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};  // 1024 + zero point 8
+      const uint32_t w = s ? r.v.y : r.v.x;
+      const h2 p0 = fma_free_dequant((w & 0x000f000fu) | 0x64006400u, bias, sc);
+      const h2 p1 = fma_free_dequant(((w >> 4) & 0x000f000fu) | 0x64006400u, bias, sc);
+      const h2 p2 = fma_free_dequant(((w >> 8) & 0x000f000fu) | 0x64006400u, bias, sc);
+      const h2 p3 = fma_free_dequant(((w >> 12) & 0x000f000fu) | 0x64006400u, bias, sc);
+      return (h8){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    }
   }
-  return out;
 }
 
 // Block id -> output tile. Workgroups are dealt round-robin to the 8 XCDs (each with its own L2), so give
@@ -76,23 +91,34 @@ __device__ __forceinline__ float act_gelu_tanh(float x) {
   return 0.5f * x * (1.0f + (e - 1.0f) / (e + 1.0f));
 }
 
+struct GemmArgs {
+  const uint16_t *X;
+  const uint8_t *Wc;
+  const uint32_t *Ws;
+  uint16_t *Y;
+  float *ws;          // split-K workspace [S, M, N] f32
+  uint32_t *counter;  // split-K arrivals per tile, zero between launches
+  int M, N, K, act, tiles_m, tiles_n, splits, ksteps;  // ksteps: 64-K steps per split
+};
+
 template <int BITS, int WM, int WN, int FM, int FN, bool GLU>
-__global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict__ X, const uint8_t *__restrict__ Wc,
-                                                      const uint32_t *__restrict__ Ws, uint16_t *__restrict__ Y, int M,
-                                                      int N, int K, int act, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   constexpr int NT = WM * WN * 64;
   constexpr int BM = WM * FM * 16, BN = WN * FN * 16;
   constexpr int ACH = BM * 8 / NT;
-  static_assert((BM * 8) % NT == 0, "A stage must split evenly over the threads");
-  constexpr int CB = BITS == 8 ? 1024 : 512;
+  static_assert((BM * 8) % NT == 0, "an A stage must split evenly over the threads");
+  constexpr int CB = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;  // bytes per 16x64 weight block
   __shared__ u32x4 As[2][BM * 8];
+  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
-  map_tile(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  map_tile(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int KT = K >> 6;
+  const int M = g.M, K = g.K, KT = g.K >> 6;
+  const int kbeg = blockIdx.y * g.ksteps;       // this split's first 64-K step
+  const int KS = g.ksteps;                       // steps in this split
 
   f4 acc[FM][FN];
 #pragma unroll
@@ -100,69 +126,89 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  // Software pipeline, unrolled by two so that both register sets are named (no dynamic indexing, which
-  // would put them in scratch): A(k) is loaded two k-steps ahead into registers and stored to LDS one step
-  // ahead (double-buffered LDS); B(k) (codes + scales) is loaded into registers two steps ahead.
   const int nb0 = (n0 >> 4) + wn * FN;
   const uint16_t *xrow[ACH];
   int aoff[ACH];
 #pragma unroll
   for (int i = 0; i < ACH; ++i) {
     const int c = tid + i * NT, r = c >> 3, ch = c & 7;
-    xrow[i] = X + (size_t)min(m0 + r, M - 1) * K + ch * 8;
+    xrow[i] = g.X + (size_t)min(m0 + r, M - 1) * K + (size_t)kbeg * 64 + ch * 8;
     aoff[i] = r * 8 + (ch ^ (r & 7));
   }
-  u32x4 a0[ACH], a1[ACH];
+  u32x4 a[ACH];
   RawB<BITS> b0[FN], b1[FN];
   uint32_t s0[FN], s1[FN];
 
-#define DJ_LOAD_A(dst, kt)                                                     \
-  _Pragma("unroll") for (int i = 0; i < ACH; ++i) dst[i] = *(const u32x4 *)(xrow[i] + (kt) * 64);
-#define DJ_STORE_A(src, buf) _Pragma("unroll") for (int i = 0; i < ACH; ++i) As[buf][aoff[i]] = src[i];
-#define DJ_LOAD_B(dst, sdst, kt)                                               \
-  _Pragma("unroll") for (int j = 0; j < FN; ++j) {                             \
-    const size_t blk = (size_t)(nb0 + j) * KT + (kt);                          \
-    if constexpr (BITS == 8)                                                   \
-      dst[j].v = *(const u32x4 *)(Wc + blk * CB + lane * 16);                  \
-    else                                                                       \
-      dst[j].v = *(const u32x2 *)(Wc + blk * CB + lane * 8);                   \
-    sdst[j] = Ws[blk * 16 + (lane & 15)];                                      \
+#define DJ_LOAD_A(kt) _Pragma("unroll") for (int i = 0; i < ACH; ++i) a[i] = *(const u32x4 *)(xrow[i] + (kt) * 64);
+#define DJ_STORE_A(buf) _Pragma("unroll") for (int i = 0; i < ACH; ++i) As[buf][aoff[i]] = a[i];
+#define DJ_LOAD_B(dst, sdst, kt)                                              \
+  _Pragma("unroll") for (int j = 0; j < FN; ++j) {                            \
+    const size_t blk = (size_t)(nb0 + j) * KT + kbeg + (kt);                  \
+    if constexpr (BITS == 8) {                                                \
+      dst[j].v = *(const u32x4 *)(g.Wc + blk * CB + lane * 16);               \
+      sdst[j] = g.Ws[blk * 16 + (lane & 15)];                                 \
+    } else if constexpr (BITS == 4) {                                         \
+      dst[j].v = *(const u32x2 *)(g.Wc + blk * CB + lane * 8);                \
+      sdst[j] = g.Ws[blk * 16 + (lane & 15)];                                 \
+    } else {                                                                  \
+      dst[j].v0 = *(const u32x4 *)(g.Wc + blk * CB + lane * 32);              \
+      dst[j].v1 = *(const u32x4 *)(g.Wc + blk * CB + lane * 32 + 16);         \
+      sdst[j] = 0;                                                            \
+    }                                                                         \
   }
-#define DJ_COMPUTE(buf, bb, ss)                                                        \
-  _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                      \
-    h8 bf[FN];                                                                         \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(bb[j], s, ss[j]); \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                   \
-      const int r = wm * FM * 16 + i * 16 + (lane & 15);                               \
-      const int ch = s * 4 + (lane >> 4);                                              \
-      const h8 af = __builtin_bit_cast(h8, As[buf][r * 8 + (ch ^ (r & 7))]);           \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]); \
-    }                                                                                  \
+#define DJ_COMPUTE(buf, bb, ss)                                                                  \
+  _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                                \
+    h8 bf[FN];                                                                                   \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(bb[j], s, ss[j]);       \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                             \
+      const int r = wm * FM * 16 + i * 16 + (lane & 15);                                         \
+      const int ch = s * 4 + (lane >> 4);                                                        \
+      const h8 af = __builtin_bit_cast(h8, As[buf][r * 8 + (ch ^ (r & 7))]);                     \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]);   \
+    }                                                                                            \
   }
 
-  DJ_LOAD_A(a0, 0);
+  DJ_LOAD_A(0);
   DJ_LOAD_B(b0, s0, 0);
-  if (KT > 1) {
-    DJ_LOAD_A(a1, 1);
-    DJ_LOAD_B(b1, s1, 1);
-  }
-  DJ_STORE_A(a0, 0);
+  if (KS > 1) DJ_LOAD_B(b1, s1, 1);
+  DJ_STORE_A(0);
   __syncthreads();
-
-  for (int kt = 0; kt < KT; kt += 2) {
-    // step kt: LDS 0 = A(kt), b0 = B(kt); a1 = A(kt+1) in flight
-    if (kt + 2 < KT) DJ_LOAD_A(a0, kt + 2);
+  // Steady state without conditionals (branches inside the loop split the accumulators' live ranges and
+  // made the compiler copy them between AGPRs and VGPRs every iteration); the last 1-3 steps are peeled.
+  // At the top of each iteration: LDS 0 = A(kt), b0 = B(kt), b1 = B(kt+1).
+  int kt = 0;
+  for (; kt + 3 < KS; kt += 2) {
+    DJ_LOAD_A(kt + 1);
     DJ_COMPUTE(0, b0, s0);
-    if (kt + 1 < KT) DJ_STORE_A(a1, 1);
-    if (kt + 2 < KT) DJ_LOAD_B(b0, s0, kt + 2);
+    DJ_LOAD_B(b0, s0, kt + 2);
+    DJ_STORE_A(1);
     __syncthreads();
-    if (kt + 1 >= KT) break;
-    // step kt+1: LDS 1 = A(kt+1), b1 = B(kt+1); a0 = A(kt+2) in flight
-    if (kt + 3 < KT) DJ_LOAD_A(a1, kt + 3);
+    DJ_LOAD_A(kt + 2);
     DJ_COMPUTE(1, b1, s1);
-    if (kt + 2 < KT) DJ_STORE_A(a0, 0);
-    if (kt + 3 < KT) DJ_LOAD_B(b1, s1, kt + 3);
+    DJ_LOAD_B(b1, s1, kt + 3);
+    DJ_STORE_A(0);
     __syncthreads();
+  }
+  const int rem = KS - kt;
+  if (rem == 3) {
+    DJ_LOAD_A(kt + 1);
+    DJ_COMPUTE(0, b0, s0);
+    DJ_LOAD_B(b0, s0, kt + 2);
+    DJ_STORE_A(1);
+    __syncthreads();
+    DJ_LOAD_A(kt + 2);
+    DJ_COMPUTE(1, b1, s1);
+    DJ_STORE_A(0);
+    __syncthreads();
+    DJ_COMPUTE(0, b0, s0);
+  } else if (rem == 2) {
+    DJ_LOAD_A(kt + 1);
+    DJ_COMPUTE(0, b0, s0);
+    DJ_STORE_A(1);
+    __syncthreads();
+    DJ_COMPUTE(1, b1, s1);
+  } else {
+    DJ_COMPUTE(0, b0, s0);
   }
 #undef DJ_LOAD_A
 #undef DJ_STORE_A
@@ -171,6 +217,52 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
 
   // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
   const int rbase = m0 + wm * FM * 16 + (lane >> 4) * 4;
+  const int N = g.N;
+  if (g.splits > 1) {
+    // each split stores its partial tile in its own f32 slice; the last to arrive adds the slices in split
+    // order (deterministic: the same bits whichever split arrives last) and resets the tile's counter
+    const size_t slice = (size_t)M * N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * FN * 16 + j * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = rbase + i * 16 + r;
+          if (m < M) g.ws[blockIdx.y * slice + (size_t)m * N + n] = acc[i][j][r];
+        }
+      }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = atomicAdd(g.counter + blockIdx.x, 1u);
+      last_flag = prev == (uint32_t)(g.splits - 1);
+    }
+    __syncthreads();
+    if (!last_flag) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int n = n0 + wn * FN * 16 + j * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = rbase + i * 16 + r;
+          if (m < M) {
+            float sum = 0.0f;
+            for (int k = 0; k < g.splits; ++k)
+              sum += k == (int)blockIdx.y ? acc[i][j][r]
+                                          : __hip_atomic_load(g.ws + k * slice + (size_t)m * N + n, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT);
+            acc[i][j][r] = sum;
+          }
+        }
+      }
+    if (tid == 0) __hip_atomic_store(g.counter + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   if constexpr (!GLU) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -180,7 +272,7 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = rbase + i * 16 + r;
-          if (m < M) Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
+          if (m < M) g.Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
         }
       }
   } else {
@@ -194,22 +286,16 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(const uint16_t *__restrict
         for (int r = 0; r < 4; ++r) {
           const int m = rbase + i * 16 + r;
           const float a = (float)(_Float16)acc[i][j][r], b = (float)(_Float16)acc[i][j + 1][r];
-          const float h = (act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b;
-          if (m < M) Y[(size_t)m * I + col] = __builtin_bit_cast(uint16_t, (_Float16)h);
+          const float h = (g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b;
+          if (m < M) g.Y[(size_t)m * I + col] = __builtin_bit_cast(uint16_t, (_Float16)h);
         }
       }
   }
 }
 
-template <int BITS, int WM, int WN, int FM, int FN, bool GLU>
-static void launch_cfg(hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act) {
-  constexpr int BM = WM * FM * 16, BN = WN * FN * 16;
-  const int tiles_m = dj_cdiv(M, BM), tiles_n = w->N / BN;
-  k_gemm<BITS, WM, WN, FM, FN, GLU><<<tiles_m * tiles_n, WM * WN * 64, 0, s>>>(
-      X, w->codes, (const uint32_t *)w->scales, Y, M, w->N, w->K, act, tiles_m, tiles_n);
-}
+// ---------------------------------------------------------------- dispatch
 
-// Tile configurations: (waves along M, waves along N, 16-row fragments per wave, 16-column fragments per wave).
+// Tile configurations: waves along M and N, 16x16 fragments per wave along M and N.
 struct GemmCfg {
   const char *tag;
   int wm, wn, fm, fn;
@@ -217,87 +303,140 @@ struct GemmCfg {
   int bn() const { return wn * fn * 16; }
 };
 static const GemmCfg kCfgs[] = {
-    {"128x128", 2, 2, 4, 4}, {"128x64", 2, 2, 4, 2}, {"64x128", 2, 2, 2, 4}, {"64x64", 2, 2, 2, 2},
-    {"32x128", 1, 4, 2, 2},  {"128x32", 4, 1, 2, 2}, {"128x16", 4, 1, 2, 1},
+    {"256x128", 2, 2, 8, 4}, {"128x128", 2, 2, 4, 4}, {"128x64", 2, 2, 4, 2}, {"64x128", 2, 2, 2, 4},
+    {"64x64", 2, 2, 2, 2},   {"32x128", 1, 4, 2, 2},  {"128x32", 4, 1, 2, 2}, {"128x16", 4, 1, 2, 1},
 };
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
+template <int BITS, int WM, int WN, int FM, int FN, bool GLU>
+static void launch_cfg(hipStream_t s, GemmArgs a) {
+  dim3 grid(a.tiles_m * a.tiles_n, a.splits);
+  k_gemm<BITS, WM, WN, FM, FN, GLU><<<grid, WM * WN * 64, 0, s>>>(a);
+}
+
 template <int BITS, bool GLU>
-static void launch_index(int i, hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act) {
+static void launch_index(int i, hipStream_t s, GemmArgs a) {
   switch (i) {
-    case 0: launch_cfg<BITS, 2, 2, 4, 4, GLU>(s, X, w, Y, M, act); break;
-    case 1: launch_cfg<BITS, 2, 2, 4, 2, GLU>(s, X, w, Y, M, act); break;
-    case 2: launch_cfg<BITS, 2, 2, 2, 4, GLU>(s, X, w, Y, M, act); break;
-    case 3: launch_cfg<BITS, 2, 2, 2, 2, GLU>(s, X, w, Y, M, act); break;
-    case 4: launch_cfg<BITS, 1, 4, 2, 2, GLU>(s, X, w, Y, M, act); break;
-    case 5: launch_cfg<BITS, 4, 1, 2, 2, GLU>(s, X, w, Y, M, act); break;
-    default: launch_cfg<BITS, 4, 1, 2, 1, false>(s, X, w, Y, M, act); break;
+    case 0: launch_cfg<BITS, 2, 2, 8, 4, GLU>(s, a); break;
+    case 1: launch_cfg<BITS, 2, 2, 4, 4, GLU>(s, a); break;
+    case 2: launch_cfg<BITS, 2, 2, 4, 2, GLU>(s, a); break;
+    case 3: launch_cfg<BITS, 2, 2, 2, 4, GLU>(s, a); break;
+    case 4: launch_cfg<BITS, 2, 2, 2, 2, GLU>(s, a); break;
+    case 5: launch_cfg<BITS, 1, 4, 2, 2, GLU>(s, a); break;
+    case 6: launch_cfg<BITS, 4, 1, 2, 2, GLU>(s, a); break;
+    default: launch_cfg<BITS, 4, 1, 2, 1, false>(s, a); break;
   }
 }
 
-static bool cfg_fits(const GemmCfg &c, int N, bool glu) {
-  return N % c.bn() == 0 && (!glu || c.fn % 2 == 0);
-}
+static bool cfg_fits(const GemmCfg &c, int N, bool glu) { return N % c.bn() == 0 && (!glu || c.fn % 2 == 0); }
 
-// The tile: DJ_GEMM_TILE=<tag> forces one (tuning sweeps). Otherwise the order below, measured on MI355X
-// over the configurations' shapes (M 32 to 86016, N 1024 to 9216, K 1024 to 3072): 32x128 was the fastest
-// or within 5% everywhere (4 waves side by side on one A tile; more workgroups per CU hide load latency).
-static int pick_cfg(int M, int N, bool glu) {
+// Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
+// sweeps on MI355X over the configurations' shapes: the largest of 128x128, 128x64, 64x64, 32x128 whose grid
+// still gives every CU a workgroup (within 15% of the best everywhere measured). Split-K only when even the
+// smallest tile leaves most CUs idle (skinny M): its device-scope fence writes back the XCD's L2, which costs
+// more than it saves once the grid covers the chip.
+static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, int &splits) {
   const char *force = getenv("DJ_GEMM_TILE");
+  const char *fs = getenv("DJ_GEMM_SPLITK");
+  cfg = -1;
+  splits = 1;
   if (force)
     for (int i = 0; i < kNumCfgs; ++i)
-      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, glu)) return i;
-  static const int order[] = {4, 3, 5, 6};  // 32x128, 64x64, 128x32, 128x16
-  for (int i : order)
-    if (cfg_fits(kCfgs[i], N, glu)) return i;
-  (void)M;
-  return -1;
+      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, glu)) cfg = i;
+  auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
+  if (cfg < 0) {
+    static const int order[] = {1, 2, 4, 5, 6, 7};  // 128x128, 128x64, 64x64, 32x128, 128x32, 128x16
+    for (int i : order)
+      if (cfg_fits(kCfgs[i], N, glu) && tiles(i) >= cus) { cfg = i; break; }
+    if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups
+      long best = -1;
+      for (int i : order)
+        if (cfg_fits(kCfgs[i], N, glu) && tiles(i) > best) { cfg = i; best = tiles(i); }
+    }
+  }
+  if (cfg < 0) return;
+  const int KT = K / 64;
+  if (fs) {
+    splits = atoi(fs);
+  } else {
+    const long t = tiles(cfg);
+    while (t * splits * 4 < cus && KT % (splits * 2) == 0 && KT / (splits * 2) >= 4) splits *= 2;
+  }
+  if (splits < 1 || KT % splits || !ws_ok) splits = 1;
 }
 
+// launcher state: the split-K workspace lives in the context
+int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
+
 template <int BITS, bool GLU>
-static int launch_bits(hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name) {
-  static const char *const names[2][2][kNumCfgs] = {
-      {{"matmul_q4_128x128", "matmul_q4_128x64", "matmul_q4_64x128", "matmul_q4_64x64", "matmul_q4_32x128", "matmul_q4_128x32", "matmul_q4_128x16"},
-       {"matmul_glu_q4_128x128", "matmul_glu_q4_128x64", "matmul_glu_q4_64x128", "matmul_glu_q4_64x64", "matmul_glu_q4_32x128", "matmul_glu_q4_128x32", "-"}},
-      {{"matmul_q8_128x128", "matmul_q8_128x64", "matmul_q8_64x128", "matmul_q8_64x64", "matmul_q8_32x128", "matmul_q8_128x32", "matmul_q8_128x16"},
-       {"matmul_glu_q8_128x128", "matmul_glu_q8_128x64", "matmul_glu_q8_64x128", "matmul_glu_q8_64x64", "matmul_glu_q8_32x128", "matmul_glu_q8_128x32", "-"}}};
-  const int i = pick_cfg(M, w->N, GLU);
-  if (i < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", w->N, GLU ? " (gated: N % 32 == 0)" : "");
-  launch_index<BITS, GLU>(i, s, X, w, Y, M, act);
-  *name = names[BITS == 8][GLU][i];
+static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name,
+                       int *splits_out) {
+  static const char *const names[3][2][kNumCfgs] = {
+      {{"matmul_q4_256x128", "matmul_q4_128x128", "matmul_q4_128x64", "matmul_q4_64x128", "matmul_q4_64x64", "matmul_q4_32x128", "matmul_q4_128x32", "matmul_q4_128x16"},
+       {"matmul_glu_q4_256x128", "matmul_glu_q4_128x128", "matmul_glu_q4_128x64", "matmul_glu_q4_64x128", "matmul_glu_q4_64x64", "matmul_glu_q4_32x128", "matmul_glu_q4_128x32", "-"}},
+      {{"matmul_q8_256x128", "matmul_q8_128x128", "matmul_q8_128x64", "matmul_q8_64x128", "matmul_q8_64x64", "matmul_q8_32x128", "matmul_q8_128x32", "matmul_q8_128x16"},
+       {"matmul_glu_q8_256x128", "matmul_glu_q8_128x128", "matmul_glu_q8_128x64", "matmul_glu_q8_64x128", "matmul_glu_q8_64x64", "matmul_glu_q8_32x128", "matmul_glu_q8_128x32", "-"}},
+      {{"matmul_f16_256x128", "matmul_f16_128x128", "matmul_f16_128x64", "matmul_f16_64x128", "matmul_f16_64x64", "matmul_f16_32x128", "matmul_f16_128x32", "matmul_f16_128x16"},
+       {"matmul_glu_f16_256x128", "matmul_glu_f16_128x128", "matmul_glu_f16_128x64", "matmul_glu_f16_64x128", "matmul_glu_f16_64x64", "matmul_glu_f16_32x128", "matmul_glu_f16_128x32", "-"}}};
+  const int N = w->N, K = w->K;
+  float *ws = nullptr;
+  uint32_t *cnt = nullptr;
+  int cfg, splits;
+  pick(M, N, K, GLU, c->cus, 1, cfg, splits);
+  if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, 1 << 16, &ws, &cnt) != DJ_OK) splits = 1;
+  if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
+  GemmArgs a;
+  a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws; a.counter = cnt;
+  a.M = M; a.N = N; a.K = K; a.act = act;
+  a.tiles_m = dj_cdiv(M, kCfgs[cfg].bm());
+  a.tiles_n = N / kCfgs[cfg].bn();
+  a.splits = splits;
+  a.ksteps = (K / 64) / splits;
+  if (splits > 1 && (long)a.tiles_m * a.tiles_n > (1 << 16)) {  // more tiles than counters: no split
+    a.splits = 1;
+    a.ksteps = K / 64;
+  }
+  launch_index<BITS, GLU>(cfg, c->stream, a);
+  *name = names[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
+  *splits_out = a.splits;
   return DJ_OK;
 }
 
-int dj_launch_gemm(hipStream_t s, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act, const char **name) {
+int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act, const char **name,
+                   int *splits) {
   const bool glu = glu_act >= 0;
-  if (w->bits == 8) return glu ? launch_bits<8, true>(s, X, w, Y, M, glu_act, name) : launch_bits<8, false>(s, X, w, Y, M, 0, name);
-  return glu ? launch_bits<4, true>(s, X, w, Y, M, glu_act, name) : launch_bits<4, false>(s, X, w, Y, M, 0, name);
+  const int bits = (w->layout & DJ_W_DIRECT) ? 16 : w->bits;
+  if (bits == 8) return glu ? launch_bits<8, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<8, false>(c, X, w, Y, M, 0, name, splits);
+  if (bits == 4) return glu ? launch_bits<4, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<4, false>(c, X, w, Y, M, 0, name, splits);
+  return glu ? launch_bits<16, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<16, false>(c, X, w, Y, M, 0, name, splits);
 }
 
 extern "C" int dj_matmul(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M) {
-  DJ_REQUIRE(w && w->layout == DJ_W_MFMA, "decision.js: matmul needs an MFMA-tiled weight (DJ_W_MFMA)");
+  DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA, "decision.js: matmul needs an MFMA-tiled weight (DJ_W_MFMA)");
   DJ_REQUIRE(X && Y && M >= 0, "decision.js: matmul: bad arguments");
   DJ_OP_BEGIN(rec, "matmul");
   const char *name = "matmul";
+  int splits = 1;
   if (M > 0) {
-    int st = dj_launch_gemm(rec->ctx->stream, X, w, Y, M, -1, &name);
+    int st = dj_launch_gemm(rec->ctx, X, w, Y, M, -1, &name, &splits);
     if (st) return st;
   }
   char shape[48];
-  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
   return dj_op_end(rec, name, shape);
 }
 
 extern "C" int dj_matmul_glu(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *H, int M, int act) {
-  DJ_REQUIRE(w && w->layout == DJ_W_MFMA_GLU, "decision.js: matmul_glu needs a fused w1|w3 weight (DJ_W_MFMA_GLU)");
+  DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA_GLU, "decision.js: matmul_glu needs a fused w1|w3 weight (DJ_W_MFMA_GLU)");
   DJ_REQUIRE(X && H && M >= 0 && (act == DJ_ACT_SILU || act == DJ_ACT_GELU_TANH), "decision.js: matmul_glu: bad arguments");
   DJ_OP_BEGIN(rec, "matmul_glu");
   const char *name = "matmul_glu";
+  int splits = 1;
   if (M > 0) {
-    int st = dj_launch_gemm(rec->ctx->stream, X, w, H, M, act, &name);
+    int st = dj_launch_gemm(rec->ctx, X, w, H, M, act, &name, &splits);
     if (st) return st;
   }
   char shape[48];
-  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
   return dj_op_end(rec, name, shape);
 }

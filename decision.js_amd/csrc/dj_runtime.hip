@@ -50,7 +50,24 @@ extern "C" int dj_init(int ordinal, dj_ctx **out) {
   DJ_HIP(hipEventCreate(&c->t1));
   const char *f = getenv("DJ_FAULT_INJECT");
   if (f) c->fault_op = f;
+  // split-K workspace: 64 MiB of f32 partials + 64 Ki tile counters, cleared here once (never by a memset
+  // inside a forward, which a captured graph could replay wrongly)
+  const size_t ws_floats = (size_t)16 << 20, ws_cnt = (size_t)1 << 16;
+  if (hipMalloc((void **)&c->gemm_ws, ws_floats * 4) == hipSuccess &&
+      hipMalloc((void **)&c->gemm_cnt, ws_cnt * 4) == hipSuccess &&
+      hipMemset(c->gemm_ws, 0, ws_floats * 4) == hipSuccess && hipMemset(c->gemm_cnt, 0, ws_cnt * 4) == hipSuccess &&
+      hipDeviceSynchronize() == hipSuccess) {
+    c->gemm_ws_floats = ws_floats;
+    c->gemm_cnt_n = ws_cnt;
+  }
   *out = c;
+  return DJ_OK;
+}
+
+int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt) {
+  if (!c->gemm_ws || need_floats > c->gemm_ws_floats || need_counters > c->gemm_cnt_n) return DJ_ENOMEM;
+  *ws = c->gemm_ws;
+  *cnt = c->gemm_cnt;
   return DJ_OK;
 }
 
@@ -83,6 +100,8 @@ extern "C" int dj_destroy(dj_ctx *c) {
     delete w;
   }
   for (auto &kv : c->buffers) (void)hipFree(kv.first);
+  if (c->gemm_ws) (void)hipFree(c->gemm_ws);
+  if (c->gemm_cnt) (void)hipFree(c->gemm_cnt);
   if (c->pinned) (void)hipHostFree(c->pinned);
   for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
   (void)hipEventDestroy(c->t0);
@@ -175,20 +194,58 @@ extern "C" int dj_upload(dj_ctx *c, void *dev, const void *host, size_t bytes) {
 //  q4:  512 bytes per block, lane l at byte 8l: one u32 per k-step; code j at bits 4(j/2) + 16(j%2)
 //       (so ((w >> 4i) & 0x000F000F) is the f16 pair (j = 2i, 2i+1) once or'ed with 0x6400).
 // Scales: block (nb, kb) holds 16 u32, lane l % 16 reads (scale[n][2kb] | scale[n][2kb+1] << 16).
+// DJ_W_DIRECT: 2048 bytes per block, lane l at byte 32l: the 16 dequantized f16 weights of the same k
+// positions ([s0 j0..7][s1 j0..7]); no scales.
 // DJ_W_MFMA_GLU: physical row block p maps to w1 block p/2 (p even) or w3 block p/2 (p odd).
 static inline int src_row_block(int p, int N, int layout) {
-  if (layout != DJ_W_MFMA_GLU) return p;
+  if ((layout & ~DJ_W_DIRECT) != DJ_W_MFMA_GLU) return p;
   int half = N / 32;  // row blocks per half
   return (p & 1) ? half + (p >> 1) : (p >> 1);
+}
+
+// IEEE binary32 -> binary16, round to nearest even (the f16 conversions of the GPU and of numpy).
+static uint16_t f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u, a = x & 0x7fffffffu;
+  if (a >= 0x7f800000u) return (uint16_t)(sign | (a > 0x7f800000u ? 0x7e00u : 0x7c00u));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a < 0x33000000u) return (uint16_t)sign;
+  const int e = (int)(a >> 23) - 127;
+  const uint32_t m = (a & 0x7fffffu) | 0x800000u;
+  const int shift = e < -14 ? -1 - e : 13;  // significand bits dropped
+  const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1), half = 1u << (shift - 1);
+  uint32_t h = e < -14 ? q : (((uint32_t)(e + 15) << 10) + (q & 0x3ffu));
+  if (rem > half || (rem == half && (q & 1u))) h += 1;
+  return (uint16_t)(sign | h);
+}
+
+static float f16_to_f32(uint16_t h) {
+  const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31, f = h & 1023;
+  float v;
+  if (e == 0) {
+    v = ldexpf((float)f, -24);
+  } else if (e == 31) {
+    v = f ? NAN : INFINITY;
+  } else {
+    v = ldexpf((float)(f | 1024), (int)e - 25);
+  }
+  uint32_t x;
+  memcpy(&x, &v, 4);
+  x |= s;
+  memcpy(&v, &x, 4);
+  return v;
 }
 
 static int repack_mfma(const uint8_t *codes, const uint16_t *scales, int N, int K, int bits, int layout,
                        std::vector<uint8_t> &oc, std::vector<uint32_t> &os) {
   const int NB = N / 16, KB = K / 64, G = K / 32;
-  const size_t blk = bits == 8 ? 1024 : 512;
+  const bool direct = (layout & DJ_W_DIRECT) != 0;
+  const size_t blk = direct ? 2048 : bits == 8 ? 1024 : 512;
   oc.assign((size_t)NB * KB * blk, 0);
-  os.assign((size_t)NB * KB * 16, 0);
+  os.assign(direct ? 16 : (size_t)NB * KB * 16, 0);
   const size_t row_bytes = (size_t)K * bits / 8;
+  const float zp = bits == 8 ? 128.0f : 8.0f;
   for (int p = 0; p < NB; ++p) {
     const int sb = src_row_block(p, N, layout);
     for (int kb = 0; kb < KB; ++kb) {
@@ -198,7 +255,17 @@ static int repack_mfma(const uint8_t *codes, const uint16_t *scales, int N, int 
         const uint8_t *row = codes + (size_t)n * row_bytes;
         for (int s = 0; s < 2; ++s) {
           const int k0 = kb * 64 + s * 32 + g * 8;
-          if (bits == 8) {
+          if (direct) {
+            // (f16(code) - f16(zp)) * scale, rounded once: exact f32 product of two f16 values, then RNE
+            const float sc = f16_to_f32(scales[(size_t)n * G + k0 / 32]);
+            uint16_t hv[8];
+            for (int j = 0; j < 8; ++j) {
+              const int k = k0 + j;
+              const uint32_t c = bits == 8 ? row[k] : (row[k >> 1] >> ((k & 1) * 4)) & 15u;
+              hv[j] = f32_to_f16(((float)c - zp) * sc);
+            }
+            memcpy(dst + l * 32 + s * 16, hv, 16);
+          } else if (bits == 8) {
             memcpy(dst + l * 16 + s * 8, row + k0, 8);
           } else {
             uint32_t w = 0;
@@ -211,7 +278,7 @@ static int repack_mfma(const uint8_t *codes, const uint16_t *scales, int N, int 
           }
         }
       }
-      for (int i = 0; i < 16; ++i) {
+      for (int i = 0; i < 16 && !direct; ++i) {
         const int n = sb * 16 + i;
         os[((size_t)p * KB + kb) * 16 + i] =
             (uint32_t)scales[(size_t)n * G + 2 * kb] | ((uint32_t)scales[(size_t)n * G + 2 * kb + 1] << 16);
@@ -226,10 +293,12 @@ extern "C" int dj_weight_q(dj_ctx *c, const void *codes, const void *scales, int
   DJ_REQUIRE(c && codes && scales && out, "decision.js: dj_weight_q: null argument");
   DJ_REQUIRE(bits == 8 || bits == 4, "decision.js: weights must be q8 or q4, got %d bits", bits);
   DJ_REQUIRE(N > 0 && K > 0 && K % 32 == 0, "decision.js: weight [%d, %d]: K must be a multiple of 32", N, K);
-  DJ_REQUIRE(layout >= DJ_W_PLAIN && layout <= DJ_W_MFMA_GLU, "decision.js: unknown weight layout %d", layout);
+  const int base = layout & ~DJ_W_DIRECT;
+  DJ_REQUIRE(base >= DJ_W_PLAIN && base <= DJ_W_MFMA_GLU && (base != DJ_W_PLAIN || layout == DJ_W_PLAIN),
+             "decision.js: unknown weight layout %d", layout);
   if (layout != DJ_W_PLAIN) {
     DJ_REQUIRE(N % 16 == 0 && K % 64 == 0, "decision.js: MFMA weight [%d, %d] needs N %% 16 == 0 and K %% 64 == 0", N, K);
-    DJ_REQUIRE(layout != DJ_W_MFMA_GLU || N % 32 == 0, "decision.js: fused w1|w3 [%d, %d] needs N %% 32 == 0", N, K);
+    DJ_REQUIRE(base != DJ_W_MFMA_GLU || N % 32 == 0, "decision.js: fused w1|w3 [%d, %d] needs N %% 32 == 0", N, K);
   }
   dj_weight *w = new dj_weight();
   w->N = N; w->K = K; w->bits = bits; w->layout = layout;

@@ -71,8 +71,11 @@ int dj_buf_read(dj_ctx *ctx, void *host, const void *dev, size_t bytes);
 enum {
   DJ_W_PLAIN = 0,   /* kept in the file's layout: rows gathered (GATHER_Q8/Q4) and read as LM head (LEAF_LOGITS) */
   DJ_W_MFMA = 1,    /* repacked for the q8/q4 block-dequant MFMA GEMM (dj_matmul) */
-  DJ_W_MFMA_GLU = 2 /* as DJ_W_MFMA for a fused [w1; w3] (N = 2I), 16-column blocks of w1 and w3 interleaved
-                       so one output tile holds a gate column and its up column (dj_matmul_glu) */
+  DJ_W_MFMA_GLU = 2, /* as DJ_W_MFMA for a fused [w1; w3] (N = 2I), 16-column blocks of w1 and w3 interleaved
+                        so one output tile holds a gate column and its up column (dj_matmul_glu) */
+  DJ_W_DIRECT = 16   /* flag on DJ_W_MFMA / DJ_W_MFMA_GLU: dequantize once at load into f16 MFMA blocks (the
+                        reference's directWeights option, gpu.ts:16-20, 114-133): bit-identical f16 weights,
+                        2 bytes per weight, no dequantization in the GEMM */
 };
 
 /* A quantized weight [N, K] from the weights.bin encodings of export_common.py:4-7, 64-97:

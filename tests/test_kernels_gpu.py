@@ -100,13 +100,14 @@ def test_sandwich(pkg, ctx, with_y, with_w2):
     (77, 1040, 128, 8), (2304, 256, 512, 8), (5, 1024, 1536, 8),
     (512, 2560, 2048, 4), (300, 2048, 11008, 4), (2100, 512, 256, 4), (33, 48, 64, 4),
 ])
-def test_matmul(pkg, ctx, M, N, K, bits):
+@pytest.mark.parametrize("direct", [False, True])
+def test_matmul(pkg, ctx, M, N, K, bits, direct):
     dj = _dj()
     rng = np.random.default_rng(M * 7 + N + K + bits)
     codes, scales = quant(rng, N, K, bits)
     W16 = ref.dequant_f16(codes, scales, bits)
     X = rand_f16(rng, (M, K))
-    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA | (dj.W_DIRECT if direct else 0))
     dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
     run(ctx, lambda r: r.matmul(dX, W, dY, M))
     got = dY.read(np.float16, (M, N))
@@ -116,8 +117,8 @@ def test_matmul(pkg, ctx, M, N, K, bits):
     assert worst <= 1.0
 
 
-@pytest.mark.parametrize("bits", [8, 4])
-def test_matmul_weights_bit_exact(pkg, ctx, bits):
+@pytest.mark.parametrize("bits,direct", [(8, False), (4, False), (8, True), (4, True)])
+def test_matmul_weights_bit_exact(pkg, ctx, bits, direct):
     """X = identity: Y = W16^T exactly (one nonzero product per output), so the in-register dequantization
     must give the reference's f16 weights bit for bit."""
     dj = _dj()
@@ -125,7 +126,7 @@ def test_matmul_weights_bit_exact(pkg, ctx, bits):
     N, K = 384, 256
     codes, scales = quant(rng, N, K, bits, std=0.5)
     X = np.eye(K, dtype=np.float16)
-    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA | (dj.W_DIRECT if direct else 0))
     dX, dY = ctx.array(X), ctx.alloc(K * N * 2)
     run(ctx, lambda r: r.matmul(dX, W, dY, K))
     got = dY.read(np.uint16, (K, N))
@@ -133,13 +134,14 @@ def test_matmul_weights_bit_exact(pkg, ctx, bits):
 
 
 @pytest.mark.parametrize("M,I,K,bits,act", [(384, 3072, 1024, 8, 0), (70, 1152, 768, 8, 1), (2200, 1024, 512, 4, 0), (19, 64, 128, 8, 1)])
-def test_matmul_glu(pkg, ctx, M, I, K, bits, act):
+@pytest.mark.parametrize("direct", [False, True])
+def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
     dj = _dj()
     rng = np.random.default_rng(M + I + K + act)
     codes, scales = quant(rng, 2 * I, K, bits)
     W16 = ref.dequant_f16(codes, scales, bits)
     X = rand_f16(rng, (M, K), std=2.0)
-    W = ctx.weight_q(codes, scales, 2 * I, K, bits, dj.W_MFMA_GLU)
+    W = ctx.weight_q(codes, scales, 2 * I, K, bits, dj.W_MFMA_GLU | (dj.W_DIRECT if direct else 0))
     dX, dH = ctx.array(X), ctx.alloc(M * I * 2)
     run(ctx, lambda r: r.matmul_glu(dX, W, dH, M, act))
     got = dH.read(np.float16, (M, I))
@@ -159,6 +161,34 @@ def test_matmul_glu(pkg, ctx, M, I, K, bits, act):
     assert f is not None
     print(f"matmul_glu {M}x{I}x{K} q{bits} act{act}: worst/bound {worst:.3f}")
     assert worst <= 1.0
+
+
+@pytest.mark.parametrize("tile,splits,glu", [("128x128", 4, False), ("64x64", 2, False), ("128x128", 2, True),
+                                              ("256x128", 1, False), ("32x128", 8, False)])
+def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, glu):
+    """Every tile shape and the split-K path (f32 atomics into a workspace that the last split clears) agree
+    with the oracle; run twice to check the workspace and counters are left clean."""
+    dj = _dj()
+    monkeypatch.setenv("DJ_GEMM_TILE", tile)
+    monkeypatch.setenv("DJ_GEMM_SPLITK", str(splits))
+    rng = np.random.default_rng(splits)
+    M, N, K = 300, 1024, 2048
+    codes, scales = quant(rng, N, K, 8)
+    W16 = ref.dequant_f16(codes, scales, 8)
+    W = ctx.weight_q(codes, scales, N, K, 8, dj.W_MFMA_GLU if glu else dj.W_MFMA)
+    for rep in range(2):
+        X = rand_f16(rng, (M, K))
+        dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+        if glu:
+            run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
+            ab = ref.matmul(X, W16, np.float64)
+            want = ref.silu_mul(ab[:, :N // 2], ab[:, N // 2:], np.float64)
+            got = dY.read(np.float16, (M, N // 2))
+            assert np.abs(got.astype(np.float64) - want.astype(np.float64)).max() < 2e-2
+        else:
+            run(ctx, lambda r: r.matmul(dX, W, dY, M))
+            want = ref.matmul(X, W16, np.float64)
+            assert f16_close(dY.read(np.float16, (M, N)), want, ulps=1.0, atol=2e-5) <= 1.0
 
 
 # ---------------------------------------------------------------- q/k norm + rope

