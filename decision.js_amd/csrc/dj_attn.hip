@@ -20,6 +20,25 @@
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
 
+// Global -> register staging of one K/V tile (64 keys) of the flattened tile sequence: tiles of source A first,
+// then of source B. Rows past the range end are clamped to its last row (read, then masked).
+#define DJ_ATTN_LOAD(j)                                                                                      \
+  {                                                                                                          \
+    const bool sb_ = (j) >= ntA;                                                                             \
+    const uint16_t *kb_ = sb_ ? kbB : kbA, *vb_ = sb_ ? vbB : vbA;                                           \
+    const int st_ = sb_ ? B.stride : A.stride, hi_ = sb_ ? hiB : hiA;                                        \
+    const int k0_ = sb_ ? loB + ((j) - ntA) * 64 : loA + (j) * 64;                                           \
+    _Pragma("unroll") for (int i = 0; i < KC; ++i) {                                                         \
+      const int c = tid + 256 * i, r = c / CH, ch = c % CH;                                                  \
+      kr[i] = *(const u32x4 *)(kb_ + (size_t)min(k0_ + r, hi_ - 1) * st_ + ch * 8);                          \
+    }                                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < VI; ++i) {                                                         \
+      const int it = tid + 256 * i, r0 = 2 * (it & 31), ch = it >> 5;                                        \
+      vr[2 * i] = *(const u32x4 *)(vb_ + (size_t)min(k0_ + r0, hi_ - 1) * st_ + ch * 8);                     \
+      vr[2 * i + 1] = *(const u32x4 *)(vb_ + (size_t)min(k0_ + r0 + 1, hi_ - 1) * st_ + ch * 8);             \
+    }                                                                                                        \
+  }
+
 template <int D>
 __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
@@ -27,9 +46,12 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
   constexpr int NS = D / 32;   // MFMA k-steps over the head dim
   constexpr int NDB = D / 16;  // 16-row blocks of O^T
   constexpr int CH = D / 8;    // 16-byte chunks per K row
+  constexpr int KC = CH / 4;   // K chunks staged per thread and tile
+  constexpr int VI = CH / 8;   // V chunk pairs (two adjacent keys) staged per thread and tile
   constexpr int SW = CH >= 16 ? 15 : 7;
   constexpr int VS = 68;       // V^T row stride in halves: 64 keys + 4 (conflict-free 8-byte reads)
-  __shared__ uint4 Ks[64 * CH];
+  constexpr float LOG2E = 1.4426950408889634f;
+  __shared__ u32x4 Ks[64 * CH];
   __shared__ uint32_t Vt[D * VS / 2];
   __shared__ int bounds[4];
 
@@ -48,6 +70,11 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
     if (r.z < r.w) { atomicMin(&bounds[2], r.z); atomicMax(&bounds[3], r.w); }
   }
   __syncthreads();
+  const int loA = max(bounds[0], 0), hiA = min(bounds[1], A.rows);
+  const int loB = max(bounds[2], 0), hiB = min(bounds[3], B.rows);
+  const int ntA = hiA > loA ? (hiA - loA + 63) / 64 : 0, ntB = hiB > loB ? (hiB - loB + 63) / 64 : 0;
+  const uint16_t *kbA = A.base + A.k_col + (size_t)kvh * D, *vbA = A.base + A.v_col + (size_t)kvh * D;
+  const uint16_t *kbB = B.base + B.k_col + (size_t)kvh * D, *vbB = B.base + B.v_col + (size_t)kvh * D;
 
   const int qi = q0 + wave * 16 + c16;
   const int qc = min(qi, T - 1);
@@ -55,43 +82,54 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
 #pragma unroll
   for (int s = 0; s < NS; ++s) qf[s] = *(const h8 *)(Q + (size_t)qc * q_stride + (size_t)h * D + s * 32 + g * 8);
   const int4 rq = rng[qc];
+  // the wave's own key span per source (a tile outside it is skipped by the wave; queries past T see nothing)
+  int wlo[2] = {qi < T && rq.x < rq.y ? rq.x : INT_MAX, qi < T && rq.z < rq.w ? rq.z : INT_MAX};
+  int whi[2] = {qi < T && rq.x < rq.y ? rq.y : INT_MIN, qi < T && rq.z < rq.w ? rq.w : INT_MIN};
+#pragma unroll
+  for (int x = 1; x < 16; x <<= 1)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      wlo[s] = min(wlo[s], __shfl_xor(wlo[s], x, 64));
+      whi[s] = max(whi[s], __shfl_xor(whi[s], x, 64));
+    }
+  wlo[0] = __builtin_amdgcn_readfirstlane(wlo[0]); whi[0] = __builtin_amdgcn_readfirstlane(whi[0]);
+  wlo[1] = __builtin_amdgcn_readfirstlane(wlo[1]); whi[1] = __builtin_amdgcn_readfirstlane(whi[1]);
 
   f4 o[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) o[i] = (f4){0.f, 0.f, 0.f, 0.f};
-  float m = -1e30f, lsum = 0.f;
+  float m = -1e30f, lsum = 0.f;  // running max in log2 units of the scaled scores
+  const float sl = scale * LOG2E;
   const uint16_t *vt16 = (const uint16_t *)Vt;
 
-  for (int src = 0; src < 2; ++src) {
-    const dj_kv_src S = src ? B : A;
-    const int lo = max(bounds[2 * src], 0), hi = min(bounds[2 * src + 1], S.rows);
-    const int qlo = src ? rq.z : rq.x, qhi = src ? rq.w : rq.y;
-    const uint16_t *kbase = S.base + S.k_col + (size_t)kvh * D;
-    const uint16_t *vbase = S.base + S.v_col + (size_t)kvh * D;
-    for (int k0 = lo; k0 < hi; k0 += 64) {
-      // K tile, row-major, chunk ch of row r at (ch ^ (r & SW))
-      for (int c = tid; c < 64 * CH; c += 256) {
-        const int r = c / CH, ch = c % CH;
-        const int row = min(k0 + r, hi - 1);
-        Ks[r * CH + (ch ^ (r & SW))] = *(const uint4 *)(kbase + (size_t)row * S.stride + ch * 8);
-      }
-      // V tile transposed: Vt[d][key], two keys per 32-bit store
-      for (int it = tid; it < 32 * CH; it += 256) {
-        const int kp = it & 31, ch = it >> 5, r0 = 2 * kp;
-        const int row0 = min(k0 + r0, hi - 1), row1 = min(k0 + r0 + 1, hi - 1);
-        // integer lanes, not vector elements: a bit_cast of an f16 vector element read element 0 only
-        const uint4 v0 = *(const uint4 *)(vbase + (size_t)row0 * S.stride + ch * 8);
-        const uint4 v1 = *(const uint4 *)(vbase + (size_t)row1 * S.stride + ch * 8);
-        const uint32_t a[4] = {v0.x, v0.y, v0.z, v0.w}, b[4] = {v1.x, v1.y, v1.z, v1.w};
-        uint32_t *dst = Vt + (((ch * 8) * VS + r0) >> 1);
+  u32x4 kr[KC], vr[2 * VI];
+  const int ntiles = ntA + ntB;
+  if (ntiles > 0) DJ_ATTN_LOAD(0);
+  for (int j = 0; j < ntiles; ++j) {
+    // registers -> LDS: K row-major (chunk ch of row r at ch ^ (r & SW)), V transposed (Vt[d][key])
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          dst[(2 * w) * (VS / 2)] = (a[w] & 0xffffu) | (b[w] << 16);          // d = 8ch + 2w: (key r0, key r0+1)
-          dst[(2 * w + 1) * (VS / 2)] = (a[w] >> 16) | (b[w] & 0xffff0000u);  // d = 8ch + 2w + 1
-        }
+    for (int i = 0; i < KC; ++i) {
+      const int c = tid + 256 * i, r = c / CH, ch = c % CH;
+      Ks[r * CH + (ch ^ (r & SW))] = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int it = tid + 256 * i, r0 = 2 * (it & 31), ch = it >> 5;
+      uint32_t *dst = Vt + (((ch * 8) * VS + r0) >> 1);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t a = vr[2 * i][w], b = vr[2 * i + 1][w];
+        dst[(2 * w) * (VS / 2)] = (a & 0xffffu) | (b << 16);          // d = 8ch + 2w: (key r0, key r0+1)
+        dst[(2 * w + 1) * (VS / 2)] = (a >> 16) | (b & 0xffff0000u);  // d = 8ch + 2w + 1
       }
-      __syncthreads();
+    }
+    __syncthreads();
+    if (j + 1 < ntiles) DJ_ATTN_LOAD(j + 1);  // in flight while this tile is computed
 
+    const bool sb = j >= ntA;
+    const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64, hi = sb ? hiB : hiA;
+    const int qlo = sb ? rq.z : rq.x, qhi = sb ? rq.w : rq.y;
+    if (k0 < whi[sb] && k0 + 64 > wlo[sb]) {
       f4 sc[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
@@ -110,21 +148,21 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
         for (int r = 0; r < 4; ++r) {
           const int kk = k0 + 16 * b + 4 * g + r;
           const bool ok = kk >= qlo && kk < qhi && kk < hi;
-          const float v = ok ? sc[b][r] * scale : -INFINITY;
+          const float v = ok ? sc[b][r] * sl : -INFINITY;
           sc[b][r] = v;
           tmax = fmaxf(tmax, v);
         }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float mn = fmaxf(m, tmax);
-      const float corr = expf(m - mn);
+      const float corr = __builtin_amdgcn_exp2f(m - mn);
       float ps = 0.f;
       h8 pf[2];
 #pragma unroll
       for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = sc[b][r] == -INFINITY ? 0.f : expf(sc[b][r] - mn);
+          const float p = __builtin_amdgcn_exp2f(sc[b][r] - mn);  // exp2(-inf) = 0 for masked keys
           ps += p;
           pf[b >> 1][(b & 1) * 4 + r] = (_Float16)p;
         }
@@ -137,17 +175,17 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
           const uint16_t *vrow = vt16 + (size_t)(16 * db + c16) * VS + 32 * t + 4 * g;
-          const uint2 lo8 = *(const uint2 *)vrow, hi8 = *(const uint2 *)(vrow + 16);
-          const h8 vf = __builtin_bit_cast(h8, (uint4){lo8.x, lo8.y, hi8.x, hi8.y});
+          const u32x2 lo8 = *(const u32x2 *)vrow, hi8 = *(const u32x2 *)(vrow + 16);
+          const h8 vf = __builtin_bit_cast(h8, (u32x4){lo8.x, lo8.y, hi8.x, hi8.y});
           o[db] = MFMA16(vf, pf[t], o[db]);
         }
-      __syncthreads();
     }
+    __syncthreads();
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < T) {
-    const float inv = 1.0f / lsum;
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     uint16_t *orow = O + (size_t)qi * heads * D + (size_t)h * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {

@@ -61,19 +61,20 @@ extern "C" int dj_gather_q(dj_rec *rec, const uint32_t *ids, int T, const dj_wei
 }
 
 // ---------------------------------------------------------------- residual + RMSNorm (kernels.ts:23-46)
-// One wave per row, 8 halves per lane per step; up to MAXC steps stay in registers.
-#define MAXC 8
+// One wave per row, 8 halves per lane per chunk; NC = ceil(H / 512) chunks per lane stay in registers
+// between the sum of squares and the scaling (NC = 0: rows too long for that, re-read from memory).
+template <int NC>
 __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, float eps, uint16_t *__restrict__ X,
                                                      const uint16_t *__restrict__ Y, const uint16_t *__restrict__ W,
                                                      uint16_t *__restrict__ O) {
   const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (row >= T) return;
   const size_t base = (size_t)row * H;
-  h8 xs[MAXC];
+  constexpr int R = NC > 0 ? NC : 1;
+  h8 xs[R];
   float ss = 0.f;
-  int c = 0;
-  for (int k = lane * 8; k < H; k += WAVE * 8, ++c) {
-    h8 x = *(const h8 *)(X + base + k);
+  auto step = [&](int k, h8 &x) {
+    x = *(const h8 *)(X + base + k);
     if (add) {
       const h8 y = *(const h8 *)(Y + base + k);
 #pragma unroll
@@ -87,52 +88,91 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, floa
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += (float)x[j] * (float)x[j];
     }
-    if (c < MAXC) xs[c] = x;
-  }
-  ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-  c = 0;
-  for (int k = lane * 8; k < H; k += WAVE * 8, ++c) {
-    const h8 x = c < MAXC ? xs[c] : *(const h8 *)(X + base + k);
+  };
+  auto scale_out = [&](int k, const h8 &x, float inv) {
     const h8 w = *(const h8 *)(W + k);
     h8 o;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)x[j] * inv * (float)w[j]);
     *(h8 *)(O + base + k) = o;
+  };
+  if (NC > 0) {
+#pragma unroll
+    for (int c = 0; c < R; ++c)
+      if (lane * 8 + c * WAVE * 8 < H) step(lane * 8 + c * WAVE * 8, xs[c]);
+  } else {
+    for (int k = lane * 8; k < H; k += WAVE * 8) step(k, xs[0]);
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(ss) / (float)H + eps);
+  if (NC > 0) {
+#pragma unroll
+    for (int c = 0; c < R; ++c)
+      if (lane * 8 + c * WAVE * 8 < H) scale_out(lane * 8 + c * WAVE * 8, xs[c], inv);
+  } else {
+    for (int k = lane * 8; k < H; k += WAVE * 8) scale_out(k, *(const h8 *)(X + base + k), inv);
   }
 }
+
+// Chunks of 8 halves per lane for a row of H (H % 8 == 0): 1..8 in registers, 0 = re-read.
+static int row_chunks(int H) {
+  const int nc = dj_cdiv(H / 8, WAVE);
+  return nc <= 8 ? nc : 0;
+}
+
+#define DJ_ROW_DISPATCH(KERNEL, H, grid, stream, ...)                          \
+  switch (row_chunks(H)) {                                                     \
+    case 1: KERNEL<1><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 2: KERNEL<2><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 3: KERNEL<3><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 4: KERNEL<4><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 5: KERNEL<5><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 6: KERNEL<6><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 7: KERNEL<7><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 8: KERNEL<8><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    default: KERNEL<0><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;          \
+  }
 
 extern "C" int dj_add_rmsnorm(dj_rec *rec, int T, int H, int add, float eps, uint16_t *X, const uint16_t *Y,
                               const uint16_t *W, uint16_t *O) {
   DJ_REQUIRE(X && W && O && (Y || !add) && T >= 0 && H > 0 && H % 8 == 0,
              "decision.js: add_rmsnorm: bad arguments (H = %d must be a multiple of 8)", H);
   DJ_OP_BEGIN(rec, "add_rmsnorm");
-  if (T > 0) k_add_rmsnorm<<<dj_cdiv(T, 4), 256, 0, rec->ctx->stream>>>(T, H, add, eps, X, Y, W, O);
+  if (T > 0) DJ_ROW_DISPATCH(k_add_rmsnorm, H, dj_cdiv(T, 4), rec->ctx->stream, T, H, add, eps, X, Y, W, O);
   return dj_op_end(rec, "add_rmsnorm");
 }
 
 // ---------------------------------------------------------------- sandwich (eg2-kernels.ts:15-48)
+// Same row layout as add_rmsnorm: the residual chunks stay in registers across the two reductions.
+template <int NC>
 __global__ __launch_bounds__(256) void k_sandwich(int T, int H, float eps, float scale, uint16_t *__restrict__ X,
                                                   const uint16_t *__restrict__ Y, const uint16_t *__restrict__ W1,
                                                   const uint16_t *__restrict__ W2, uint16_t *__restrict__ O) {
   const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (row >= T) return;
   const size_t base = (size_t)row * H;
+  constexpr int R = NC > 0 ? NC : 1;
+  h8 xs[R], ys[R];
+  auto live = [&](int c) { return lane * 8 + c * WAVE * 8 < H; };
   float iy = 0.f;
   if (Y) {
     float ss = 0.f;
-    for (int k = lane * 8; k < H; k += WAVE * 8) {
-      const h8 y = *(const h8 *)(Y + base + k);
+    auto sq = [&](const h8 &y) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += (float)y[j] * (float)y[j];
+    };
+    if (NC > 0) {
+#pragma unroll
+      for (int c = 0; c < R; ++c)
+        if (live(c)) { ys[c] = *(const h8 *)(Y + base + lane * 8 + c * WAVE * 8); sq(ys[c]); }
+    } else {
+      for (int k = lane * 8; k < H; k += WAVE * 8) sq(*(const h8 *)(Y + base + k));
     }
     iy = 1.0f / sqrtf(wave_sum(ss) / (float)H + eps);
   }
   float ss2 = 0.f;
-  for (int k = lane * 8; k < H; k += WAVE * 8) {
-    h8 x = *(const h8 *)(X + base + k);
+  auto mix = [&](int k, const h8 &y, h8 &x) {
+    x = *(const h8 *)(X + base + k);
     if (Y) {
-      const h8 y = *(const h8 *)(Y + base + k);
       const h8 w1 = *(const h8 *)(W1 + k);
 #pragma unroll
       for (int j = 0; j < 8; ++j) x[j] = (_Float16)(((float)x[j] + (float)y[j] * iy * (float)w1[j]) * scale);
@@ -143,16 +183,33 @@ __global__ __launch_bounds__(256) void k_sandwich(int T, int H, float eps, float
     *(h8 *)(X + base + k) = x;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss2 += (float)x[j] * (float)x[j];  // the stored residual, as the next block reads it
+  };
+  if (NC > 0) {
+#pragma unroll
+    for (int c = 0; c < R; ++c)
+      if (live(c)) mix(lane * 8 + c * WAVE * 8, ys[c], xs[c]);
+  } else {
+    for (int k = lane * 8; k < H; k += WAVE * 8) {
+      h8 y = {};
+      if (Y) y = *(const h8 *)(Y + base + k);
+      mix(k, y, xs[0]);
+    }
   }
   if (!W2) return;
   const float ix = 1.0f / sqrtf(wave_sum(ss2) / (float)H + eps);
-  for (int k = lane * 8; k < H; k += WAVE * 8) {
-    const h8 x = *(const h8 *)(X + base + k);
+  auto out = [&](int k, const h8 &x) {
     const h8 w2 = *(const h8 *)(W2 + k);
     h8 o;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)x[j] * ix * (float)w2[j]);
     *(h8 *)(O + base + k) = o;
+  };
+  if (NC > 0) {
+#pragma unroll
+    for (int c = 0; c < R; ++c)
+      if (live(c)) out(lane * 8 + c * WAVE * 8, xs[c]);
+  } else {
+    for (int k = lane * 8; k < H; k += WAVE * 8) out(k, *(const h8 *)(X + base + k));
   }
 }
 
@@ -160,82 +217,107 @@ extern "C" int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, ui
                            const uint16_t *W1, const uint16_t *W2, uint16_t *O) {
   DJ_REQUIRE(X && (W1 || !Y) && (O || !W2) && T >= 0 && H > 0 && H % 8 == 0, "decision.js: sandwich: bad arguments");
   DJ_OP_BEGIN(rec, "sandwich");
-  if (T > 0) k_sandwich<<<dj_cdiv(T, 4), 256, 0, rec->ctx->stream>>>(T, H, eps, scale, X, Y, W1, W2, O);
+  if (T > 0) DJ_ROW_DISPATCH(k_sandwich, H, dj_cdiv(T, 4), rec->ctx->stream, T, H, eps, scale, X, Y, W1, W2, O);
   return dj_op_end(rec, "sandwich");
 }
 
 // ---------------------------------------------------------------- q/k(/v) norm + RoPE
-// One wave per (token, head). Lane i owns rotation pairs (d, d + rot/2) for d = i, i + 64, ... < rot/2 and
-// the unrotated dims rot + i, rot + i + 64, ... < D.
+// One workgroup per token; LPH lanes per head (a power of two). Lane s < rot/8 owns the four rotation pairs
+// (d, d + rot/2), d = 4s..4s+3; the next (D - rot)/8 lanes own 8 unrotated dims each. A lane's frequencies and
+// sin/cos depend only on its d and the token, so they are computed once and reused for every head the lane
+// visits. Frequency: theta^(-2d/rot) (POW_NEG) or 1 / theta^(2d/rot) (INV_POW), angle = f32(pos * f), as the
+// reference kernels compute them.
+template <int LPH>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, int D, int stride, uint16_t *__restrict__ Z,
                                                       const uint16_t *__restrict__ qn, const uint16_t *__restrict__ kn,
                                                       int vnorm, const int32_t *__restrict__ pos, int pos_stride, float eps,
                                                       float theta, int rot, int mode) {
+  const int t = blockIdx.x;
   const int per = heads + kv + (vnorm ? kv : 0);
-  const long item = (long)blockIdx.x * 4 + threadIdx.x / WAVE;
-  const int lane = threadIdx.x % WAVE;
-  if (item >= (long)T * per) return;
-  const int t = (int)(item / per), h = (int)(item % per);
-  const bool isQ = h < heads, isK = !isQ && h < heads + kv;
-  const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
-  const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
-  uint16_t *z = Z + (size_t)t * stride + (size_t)h * D;
-  const int half = rot / 2;
-  float a[4], b[4], e[8];
-  float ss = 0.f;
-  int np = 0, ne = 0;
-  for (int d = lane; d < half; d += WAVE, ++np) {
-    a[np] = hf(z[d]);
-    b[np] = hf(z[d + half]);
-    ss += a[np] * a[np] + b[np] * b[np];
-  }
-  for (int d = rot + lane; d < D; d += WAVE, ++ne) {
-    e[ne] = hf(z[d]);
-    ss += e[ne] * e[ne];
-  }
-  float inv = 1.f;
-  if (norm) inv = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
-  np = 0;
-  ne = 0;
-  const float ps = (float)pos[(size_t)t * pos_stride];
-  for (int d = lane; d < half; d += WAVE, ++np) {
-    float x = a[np] * inv, y = b[np] * inv;
-    if (nw) {
-      x *= hf(nw[d]);
-      y *= hf(nw[d + half]);
-    }
-    if (isQ || isK) {
-      const float ex = (float)(2 * d) / (float)rot;
+  const int sub = threadIdx.x % LPH, grp = threadIdx.x / LPH;
+  const int half = rot / 2, npl = rot / 8, ntl = (D - rot) / 8;
+  const bool pl = sub < npl, tl = !pl && sub < npl + ntl;
+  const int d0 = pl ? 4 * sub : rot + 8 * (sub - npl);  // first owned dim
+  float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+  if (pl) {
+    const float ps = (float)pos[(size_t)t * pos_stride];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ex = (float)(2 * (d0 + i)) / (float)rot;
       const float f = mode == DJ_ROPE_POW_NEG ? powf(theta, -ex) : 1.0f / powf(theta, ex);
-      const float ang = ps * f;
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      const float x2 = x * cs - y * sn, y2 = y * cs + x * sn;
-      x = x2;
-      y = y2;
+      sincosf(ps * f, &sn[i], &cs[i]);
     }
-    z[d] = h2u((_Float16)x);
-    z[d + half] = h2u((_Float16)y);
   }
-  for (int d = rot + lane; d < D; d += WAVE, ++ne) {
-    float x = e[ne] * inv;
-    if (nw) x *= hf(nw[d]);
-    z[d] = h2u((_Float16)x);
+  for (int hh = grp; hh < per; hh += 256 / LPH) {
+    const bool isQ = hh < heads, isK = !isQ && hh < heads + kv;
+    const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
+    const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
+    uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
+    float v[8];
+    if (pl) {
+      const h4 x = *(const h4 *)(z + d0), y = *(const h4 *)(z + half + d0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { v[i] = (float)x[i]; v[4 + i] = (float)y[i]; }
+    } else if (tl) {
+      const h8 e = *(const h8 *)(z + d0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (float)e[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+#pragma unroll
+    for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
+    const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
+    if (pl) {
+      h4 xo, yo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = v[i] * inv, y = v[4 + i] * inv;
+        if (nw) {
+          x *= hf(nw[d0 + i]);
+          y *= hf(nw[half + d0 + i]);
+        }
+        if (isQ || isK) {
+          const float x2 = x * cs[i] - y * sn[i], y2 = y * cs[i] + x * sn[i];
+          x = x2;
+          y = y2;
+        }
+        xo[i] = (_Float16)x;
+        yo[i] = (_Float16)y;
+      }
+      *(h4 *)(z + d0) = xo;
+      *(h4 *)(z + half + d0) = yo;
+    } else if (tl) {
+      h8 eo;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? v[i] * inv * hf(nw[d0 + i]) : v[i] * inv);
+      *(h8 *)(z + d0) = eo;
+    }
   }
 }
 
 extern "C" int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
                                const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta,
                                int rot, int mode) {
-  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 && rot > 0 && rot <= D && rot % 2 == 0 &&
-                 rot / 2 <= 4 * WAVE && D - rot <= 8 * WAVE && stride >= (heads + 2 * kv) * D,
+  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && rot > 0 && rot <= D && rot % 8 == 0 &&
+                 (D - rot) % 8 == 0 && D / 8 <= 64 && stride % 8 == 0 && stride >= (heads + 2 * kv) * D,
              "decision.js: qk_norm_rope: unsupported shape (D %d, rot %d, stride %d)", D, rot, stride);
   DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: qk_norm_rope: unknown rope mode");
   DJ_OP_BEGIN(rec, "qk_norm_rope");
-  const long items = (long)T * (heads + kv + (vnorm ? kv : 0));
-  if (items > 0)
-    k_qk_norm_rope<<<dj_cdiv(items, 4), 256, 0, rec->ctx->stream>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos,
-                                                                    pos_stride, eps, theta, rot, mode);
+  if (T > 0) {
+    const int lanes = D / 8;  // rot/8 pair lanes + (D - rot)/8 tail lanes
+    hipStream_t s = rec->ctx->stream;
+    if (lanes <= 16)
+      k_qk_norm_rope<16><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
+    else if (lanes <= 32)
+      k_qk_norm_rope<32><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
+    else
+      k_qk_norm_rope<64><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
+  }
   return dj_op_end(rec, "qk_norm_rope");
 }
 

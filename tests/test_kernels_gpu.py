@@ -79,10 +79,11 @@ def test_add_rmsnorm(pkg, ctx, H, add):
     assert f16_close(dO.read(np.float16, (T, H)), O, ulps=1.0) <= 1.0
 
 
-@pytest.mark.parametrize("with_y,with_w2", [(True, True), (True, False), (False, True)])
-def test_sandwich(pkg, ctx, with_y, with_w2):
+@pytest.mark.parametrize("with_y,with_w2,H", [(True, True, 768), (True, False, 768), (False, True, 768),
+                                              (True, True, 2560), (True, True, 4160), (False, True, 4160)])
+def test_sandwich(pkg, ctx, with_y, with_w2, H):
     rng = np.random.default_rng(7)
-    T, H = 50, 768
+    T = 50
     X, Y = rand_f16(rng, (T, H)), rand_f16(rng, (T, H))
     w1, w2 = (1 + rng.standard_normal(H) * 0.1).astype(np.float16), (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
     dX, dY, d1, d2, dO = ctx.array(X), ctx.array(Y), ctx.array(w1), ctx.array(w2), ctx.alloc(T * H * 2)
@@ -196,6 +197,7 @@ def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, gl
 @pytest.mark.parametrize("heads,kv,D,qk,vnorm,mode,rot", [
     (16, 8, 128, True, False, 0, None), (16, 2, 128, False, False, 0, None), (12, 2, 128, True, False, 0, None),
     (3, 1, 256, True, True, 1, None), (8, 2, 256, True, False, 0, 64), (4, 4, 64, True, False, 0, None),
+    (6, 2, 128, True, False, 1, 96), (5, 5, 512, False, True, 0, 256),
 ])
 def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
     rng = np.random.default_rng(heads * D + kv)
@@ -203,6 +205,7 @@ def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
     stride = (heads + 2 * kv) * D
     Z = rand_f16(rng, (T, stride))
     pos = rng.integers(0, 1100, T).astype(np.int32)
+    pos[:4] = [0, 1, 65535, 131071]  # the position range of a full tokens-per-pass budget
     qn, kn = (1 + rng.standard_normal(D) * 0.1).astype(np.float16), (1 + rng.standard_normal(D) * 0.1).astype(np.float16)
     dZ, dpos, dq, dk = ctx.array(Z), ctx.array(pos), ctx.array(qn), ctx.array(kn)
     theta = 1e6 if mode == 0 else 1e4
@@ -210,9 +213,20 @@ def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
                                       1e-6, theta, rot, mode))
     want = ref.qk_norm_rope(Z, heads, kv, D, pos, qn if qk else None, kn if qk else None, vnorm, 1e-6, theta, rot, mode, np.float64)
     got = dZ.read(np.float16, (T, stride))
-    worst = f16_close(got, want, ulps=2.0, atol=2e-4)
+    worst = f16_close(got[4:], want[4:], ulps=2.0, atol=2e-4)
     print(f"qk_norm_rope h{heads} kv{kv} D{D}: worst/bound {worst:.3f}")
     assert worst <= 1.0
+    assert f16_close(got[:2], want[:2], ulps=2.0, atol=2e-4) <= 1.0
+    # at positions near 2^17 one ulp of an f32 frequency moves the f32 angle by pos * 2^-24 rad, so any two
+    # correct implementations (this kernel, the oracle, the reference's pow) differ by |x| * that much
+    r = D if rot is None else rot
+    big = np.abs(got[2:4].astype(np.float64) - want[2:4])
+    assert big.max() <= 8 * 131071 * 2.0 ** -24 * max(1.0, np.abs(want[2:4]).max()) + 4e-3
+    # rotation keeps each pair's length: |(x, y)| before and after RoPE agree for the q and k heads
+    g = got[2:4, :(heads + kv) * D].astype(np.float64).reshape(2, heads + kv, D)
+    w = want[2:4, :(heads + kv) * D].reshape(2, heads + kv, D)
+    ln = lambda a: np.hypot(a[..., :r // 2], a[..., r // 2:r])
+    assert np.abs(ln(g) - ln(w)).max() <= 4e-3 * max(1.0, ln(w).max())
 
 
 # ---------------------------------------------------------------- attention
