@@ -3,14 +3,18 @@
 //     q8 / q4  quantized in blocks of 32 along K with an f16 scale each (kept quantized in HBM), or
 //     f16      the same weights dequantized once at load ("direct weights", the reference's directWeights
 //              option, gpu.ts:16-20, 114-133) — bit-identical f16 values, twice the bytes of q8.
-// Weights are repacked at load (dj_runtime.hip) so one wave reads the B operand of two MFMA k-steps with one
-// 16-byte (q8), 8-byte (q4) or two 16-byte (f16) loads per lane, already in lane order. Quantized codes become
-// f16 in registers by the exponent trick: 0x6400 | code is exactly 1024 + code; minus (1024 + zero point),
-// times the group scale — one RNE rounding, the reference's f16 dequantization (kernels.ts:20, 296, 541).
+// Weights are repacked at load (dj_runtime.hip) into 16-column x 64-K blocks in MFMA lane order (1 KB q8,
+// 512 B q4, 2 KB f16) with 16 scale words per block. Quantized codes become f16 in registers by the exponent
+// trick: 0x6400 | code is exactly 1024 + code; minus (1024 + zero point), times the group scale — one RNE
+// rounding, the reference's f16 dequantization (kernels.ts:20, 296, 541).
 //
-// Per workgroup: WM x WN waves, each computing FM x FN 16x16 fragments. X tiles (64 K per step) go through
-// double-buffered, XOR-swizzled LDS, loaded one step ahead; B goes straight to registers two steps ahead.
-// The K loop is unrolled by two so both register sets have names (no dynamic indexing -> no scratch).
+// Per workgroup: WM x WN waves, each computing FM x FN 16x16 fragments. Operands reach LDS without passing
+// through registers: global_load_lds (16 bytes per lane; 4 for scales) fills a ring of NS stages, each one
+// 64-K step of the tile (X rows XOR-swizzled in 16-byte chunks, weight blocks and scales as stored), NS - 1
+// steps ahead of the MFMAs, so several steps of HBM/L2 latency are in flight per wave. Every vector-memory
+// instruction in the loop is one of these, the same number per step (tail steps re-load the last step), so
+// "this step has landed" is an exact s_waitcnt vmcnt count; a bare s_barrier (no fence, which would drain
+// every outstanding load) then publishes the stage to the other waves.
 //
 // Split-K (grid y = S): each split stores its f32 partial tile in its own workspace slice; the last split to
 // arrive at a tile (per-tile counter) adds the slices in split order (deterministic), resets the counter (so
@@ -101,24 +105,76 @@ struct GemmArgs {
   int M, N, K, act, tiles_m, tiles_n, splits, ksteps;  // ksteps: 64-K steps per split
 };
 
-template <int BITS, int WM, int WN, int FM, int FN, bool GLU>
+// The LDS-fill DMAs and the "step landed" wait are inline assembly on purpose: the compiler models an LDS read
+// after a global_load_lds it issued as depending on every such load still in flight and waits vmcnt(0) before
+// it, which would drain the whole ring each step. Hidden from it, the ring's ordering is the explicit vmcnt
+// below; the compiler's own vmcnt waits for other loads only get stricter from ops it cannot see (in-order
+// completion). "memory" keeps LDS reads from moving across the fill or the barrier. s_nop: one wait state
+// between an SALU write of M0 and the LDS DMA that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is named as clobbered on purpose: the asm writes it
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// this wave's vector-memory ops older than the newest n are complete and its LDS reads have returned, then
+// the workgroup barrier
+template <int n>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(n) : "memory");
+}
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// Ring of LDS stages, each holding one 64-K step of the tile: A (BM rows x 128 bytes, XOR-swizzled 16-byte
+// chunks), the NB weight blocks of B in their global lane order, and (quantized B) each block's 16 scale words.
+template <int BITS, int WM, int WN, int FM, int FN, int RING>
+struct GemmShape {
+  static constexpr int NW = WM * WN, NT = NW * 64;
+  static constexpr int BM = WM * FM * 16, BN = WN * FN * 16, NB = BN / 16;
+  static constexpr int CB = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;  // bytes per 16x64 weight block
+  static constexpr int A_BYTES = BM * 128;
+  static constexpr int B_BYTES = (NB * CB + 1023) / 1024 * 1024;      // whole 1 KB DMA rows
+  static constexpr int S_BYTES = BITS == 16 ? 0 : NW * 256;           // one 256-byte DMA row per wave
+  static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+  // ring depth (NS - 1 steps in flight): RING, or 0 = the deepest of 4 / 3 that fits. Shallower rings leave
+  // LDS for more workgroups per CU, which on MI355X hides more latency than a deeper ring does.
+  static constexpr int NS = RING ? RING : 4 * STAGE <= 160 * 1024 ? 4 : 3;
+  static constexpr int IA = A_BYTES / 1024 / NW;                      // 16-byte-per-lane DMAs per wave and step
+  static constexpr int TB = B_BYTES / 1024, IB = (TB + NW - 1) / NW;
+  static constexpr int IS = BITS == 16 ? 0 : 1;                       // 4-byte-per-lane DMA (scales)
+  static constexpr int I = IA + IB + IS;                              // vector-memory ops per wave and step
+  static_assert(A_BYTES % (1024 * NW) == 0, "A stage must split into whole 1 KB rows per wave");
+  static_assert(NB <= 4 * NW, "scale rows cover 4 blocks per wave");
+  static_assert((NS - 2) * I < 64, "vmcnt range");
+  static_assert(NS * STAGE <= 160 * 1024, "LDS");
+};
+
+template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
 __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int BM = WM * FM * 16, BN = WN * FN * 16;
-  constexpr int ACH = BM * 8 / NT;
-  static_assert((BM * 8) % NT == 0, "an A stage must split evenly over the threads");
-  constexpr int CB = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;  // bytes per 16x64 weight block
-  __shared__ u32x4 As[2][BM * 8];
+  using S = GemmShape<BITS, WM, WN, FM, FN, RING>;
+  constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
+  constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
   __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
   int tm, tn;
   map_tile(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = tn * (WN * FN * 16);
   const int M = g.M, K = g.K, KT = g.K >> 6;
-  const int kbeg = blockIdx.y * g.ksteps;       // this split's first 64-K step
-  const int KS = g.ksteps;                       // steps in this split
+  const int kbeg = blockIdx.y * g.ksteps;  // this split's first 64-K step
+  const int KS = g.ksteps;
 
   f4 acc[FM][FN];
 #pragma unroll
@@ -126,94 +182,87 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
 
-  const int nb0 = (n0 >> 4) + wn * FN;
-  const uint16_t *xrow[ACH];
-  int aoff[ACH];
+  // Per-lane DMA sources at step 0 of the split (a step adds 128 bytes to A, one block to B and scales).
+  // A row q (1 KB = 8 rows of the tile): lane L fills LDS chunk L of it = row 8q + L/8, physical chunk L%8,
+  // which holds logical chunk (L%8) ^ (row % 8).
+  const uint16_t *asrc[S::IA];
 #pragma unroll
-  for (int i = 0; i < ACH; ++i) {
-    const int c = tid + i * NT, r = c >> 3, ch = c & 7;
-    xrow[i] = g.X + (size_t)min(m0 + r, M - 1) * K + (size_t)kbeg * 64 + ch * 8;
-    aoff[i] = r * 8 + (ch ^ (r & 7));
+  for (int i = 0; i < S::IA; ++i) {
+    const int q = wave * S::IA + i, r = 8 * q + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    asrc[i] = g.X + (size_t)min(m0 + r, M - 1) * K + (size_t)kbeg * 64 + c * 8;
   }
-  u32x4 a[ACH];
-  RawB<BITS> b0[FN], b1[FN];
-  uint32_t s0[FN], s1[FN];
-
-#define DJ_LOAD_A(kt) _Pragma("unroll") for (int i = 0; i < ACH; ++i) a[i] = *(const u32x4 *)(xrow[i] + (kt) * 64);
-#define DJ_STORE_A(buf) _Pragma("unroll") for (int i = 0; i < ACH; ++i) As[buf][aoff[i]] = a[i];
-#define DJ_LOAD_B(dst, sdst, kt)                                              \
-  _Pragma("unroll") for (int j = 0; j < FN; ++j) {                            \
-    const size_t blk = (size_t)(nb0 + j) * KT + kbeg + (kt);                  \
-    if constexpr (BITS == 8) {                                                \
-      dst[j].v = *(const u32x4 *)(g.Wc + blk * CB + lane * 16);               \
-      sdst[j] = g.Ws[blk * 16 + (lane & 15)];                                 \
-    } else if constexpr (BITS == 4) {                                         \
-      dst[j].v = *(const u32x2 *)(g.Wc + blk * CB + lane * 8);                \
-      sdst[j] = g.Ws[blk * 16 + (lane & 15)];                                 \
-    } else {                                                                  \
-      dst[j].v0 = *(const u32x4 *)(g.Wc + blk * CB + lane * 32);              \
-      dst[j].v1 = *(const u32x4 *)(g.Wc + blk * CB + lane * 32 + 16);         \
-      sdst[j] = 0;                                                            \
-    }                                                                         \
+  const int nb0 = n0 >> 4;  // the tile's first weight block row
+  const uint8_t *bsrc[S::IB];
+  int bdst[S::IB];
+#pragma unroll
+  for (int i = 0; i < S::IB; ++i) {
+    const int q = min(wave + NW * i, S::TB - 1);  // waves past the last row repeat it (same bytes, same place)
+    int j, off;
+    if constexpr (BITS == 8) { j = q; off = lane * 16; }
+    else if constexpr (BITS == 4) { j = min(2 * q + (lane >> 5), NB - 1); off = (lane & 31) * 16; }
+    else { j = q >> 1; off = (q & 1) * 1024 + lane * 16; }
+    bsrc[i] = g.Wc + ((size_t)(nb0 + j) * KT + kbeg) * CB + off;
+    bdst[i] = __builtin_amdgcn_readfirstlane(A_BYTES + q * 1024);
   }
-#define DJ_COMPUTE(buf, bb, ss)                                                                  \
-  _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                                \
-    h8 bf[FN];                                                                                   \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(bb[j], s, ss[j]);       \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i) {                                             \
-      const int r = wm * FM * 16 + i * 16 + (lane & 15);                                         \
-      const int ch = s * 4 + (lane >> 4);                                                        \
-      const h8 af = __builtin_bit_cast(h8, As[buf][r * 8 + (ch ^ (r & 7))]);                     \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]);   \
-    }                                                                                            \
+  const uint32_t *ssrc = nullptr;
+  if constexpr (S::IS) {
+    const int j = min(wave * 4 + (lane >> 4), NB - 1);
+    ssrc = g.Ws + ((size_t)(nb0 + j) * KT + kbeg) * 16 + (lane & 15);
   }
 
-  DJ_LOAD_A(0);
-  DJ_LOAD_B(b0, s0, 0);
-  if (KS > 1) DJ_LOAD_B(b1, s1, 1);
-  DJ_STORE_A(0);
-  __syncthreads();
-  // Steady state without conditionals (branches inside the loop split the accumulators' live ranges and
-  // made the compiler copy them between AGPRs and VGPRs every iteration); the last 1-3 steps are peeled.
-  // At the top of each iteration: LDS 0 = A(kt), b0 = B(kt), b1 = B(kt+1).
-  int kt = 0;
-  for (; kt + 3 < KS; kt += 2) {
-    DJ_LOAD_A(kt + 1);
-    DJ_COMPUTE(0, b0, s0);
-    DJ_LOAD_B(b0, s0, kt + 2);
-    DJ_STORE_A(1);
-    __syncthreads();
-    DJ_LOAD_A(kt + 2);
-    DJ_COMPUTE(1, b1, s1);
-    DJ_LOAD_B(b1, s1, kt + 3);
-    DJ_STORE_A(0);
-    __syncthreads();
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](int kt, int slot) {
+    const uint32_t st = lds0 + slot * STAGE;
+#pragma unroll
+    for (int i = 0; i < S::IA; ++i) dma16(asrc[i] + kt * 64, st + (wv * S::IA + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < S::IB; ++i) dma16(bsrc[i] + (size_t)kt * CB, st + bdst[i]);
+    if constexpr (S::IS) dma4(ssrc + kt * 16, st + A_BYTES + B_BYTES + wv * 256);
+  };
+
+  // prologue: steps 0 .. NS-2 in flight (clamped to the last step: a short split re-reads it, harmlessly)
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p) issue(min(p, KS - 1), p);
+
+  for (int kt = 0; kt < KS; ++kt) {
+    // this wave's DMAs of step kt are done once at most the NS-2 later steps' remain outstanding; after the
+    // barrier every wave's are, and every wave has finished reading step kt-1's stage, which is refilled next
+    wait_vm_barrier<(NS - 2) * S::I>();
+    const int slot = kt % NS;
+    issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
+
+    const uint8_t *st = smem + slot * STAGE;
+    const u32x4 *As = (const u32x4 *)st;
+    RawB<BITS> rb[FN];
+    uint32_t sp[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int jb = wn * FN + j;
+      if constexpr (BITS == 8) rb[j].v = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 16);
+      else if constexpr (BITS == 4) rb[j].v = *(const u32x2 *)(st + A_BYTES + jb * CB + lane * 8);
+      else {
+        rb[j].v0 = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 32);
+        rb[j].v1 = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 32 + 16);
+      }
+      sp[j] = S::IS ? *(const uint32_t *)(st + A_BYTES + B_BYTES + jb * 64 + (lane & 15) * 4) : 0u;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      h8 bf[FN];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(rb[j], s, sp[j]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * FM * 16 + i * 16 + (lane & 15);
+        const int ch = s * 4 + (lane >> 4);
+        const h8 af = __builtin_bit_cast(h8, As[r * 8 + (ch ^ (r & 7))]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]);
+      }
+    }
   }
-  const int rem = KS - kt;
-  if (rem == 3) {
-    DJ_LOAD_A(kt + 1);
-    DJ_COMPUTE(0, b0, s0);
-    DJ_LOAD_B(b0, s0, kt + 2);
-    DJ_STORE_A(1);
-    __syncthreads();
-    DJ_LOAD_A(kt + 2);
-    DJ_COMPUTE(1, b1, s1);
-    DJ_STORE_A(0);
-    __syncthreads();
-    DJ_COMPUTE(0, b0, s0);
-  } else if (rem == 2) {
-    DJ_LOAD_A(kt + 1);
-    DJ_COMPUTE(0, b0, s0);
-    DJ_STORE_A(1);
-    __syncthreads();
-    DJ_COMPUTE(1, b1, s1);
-  } else {
-    DJ_COMPUTE(0, b0, s0);
-  }
-#undef DJ_LOAD_A
-#undef DJ_STORE_A
-#undef DJ_LOAD_B
-#undef DJ_COMPUTE
+  wait_vm<0>();  // the clamped tail DMAs land before the wave moves on
 
   // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
   const int rbase = m0 + wm * FM * 16 + (lane >> 4) * 4;
@@ -277,11 +326,12 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
       }
   } else {
     const int I = N >> 1;
+    const int wb0 = nb0 + wn * FN;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; j += 2) {
-        const int col = ((nb0 + j) >> 1) * 16 + (lane & 15);  // physical block p even -> w1 block p / 2
+        const int col = ((wb0 + j) >> 1) * 16 + (lane & 15);  // physical block p even -> w1 block p / 2
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = rbase + i * 16 + r;
@@ -295,46 +345,55 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
 
 // ---------------------------------------------------------------- dispatch
 
-// Tile configurations: waves along M and N, 16x16 fragments per wave along M and N.
+// Tile configurations: waves along M and N, 16x16 fragments per wave along M and N, K groups.
 struct GemmCfg {
   const char *tag;
-  int wm, wn, fm, fn;
+  int wm, wn, fm, fn, ring;
   int bm() const { return wm * fm * 16; }
   int bn() const { return wn * fn * 16; }
 };
-static const GemmCfg kCfgs[] = {
-    {"256x128", 2, 2, 8, 4}, {"128x128", 2, 2, 4, 4}, {"128x64", 2, 2, 4, 2}, {"64x128", 2, 2, 2, 4},
-    {"64x64", 2, 2, 2, 2},   {"32x128", 1, 4, 2, 2},  {"128x32", 4, 1, 2, 2}, {"128x16", 4, 1, 2, 1},
-};
+// tag "<BM>x<BN>[s<ring>]": waves along M and N, 16x16 fragments per wave along M and N, LDS ring depth
+#define DJ_GEMM_CFGS(X)                                                                                    \
+  X(0, "256x128", 2, 2, 8, 4, 0) X(1, "128x128", 2, 2, 4, 4, 0) X(2, "128x64", 2, 2, 4, 2, 0)              \
+  X(3, "64x128", 2, 2, 2, 4, 0) X(4, "64x64", 2, 2, 2, 2, 0) X(5, "32x128", 1, 4, 2, 2, 0)                 \
+  X(6, "128x32", 4, 1, 2, 2, 0) X(7, "128x16", 4, 1, 2, 1, 0) X(8, "32x64", 1, 4, 2, 1, 0)                 \
+  X(9, "64x32", 2, 2, 2, 1, 0) X(10, "128x128s2", 2, 2, 4, 4, 2) X(11, "128x128s3", 2, 2, 4, 4, 3)         \
+  X(12, "256x128s2", 2, 2, 8, 4, 2) X(13, "128x256", 2, 2, 4, 8, 0) X(14, "128x256s2", 2, 2, 4, 8, 2)      \
+  X(15, "64x64s2", 2, 2, 2, 2, 2) X(16, "32x128s2", 1, 4, 2, 2, 2) X(17, "64x128s2", 2, 2, 2, 4, 2)        \
+  X(18, "128x64s2", 2, 2, 4, 2, 2)
+#define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
+static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int BITS, int WM, int WN, int FM, int FN, bool GLU>
+template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
 static void launch_cfg(hipStream_t s, GemmArgs a) {
-  dim3 grid(a.tiles_m * a.tiles_n, a.splits);
-  k_gemm<BITS, WM, WN, FM, FN, GLU><<<grid, WM * WN * 64, 0, s>>>(a);
+  if constexpr (GLU && FN % 2 != 0) {
+    return;  // never picked: a gated tile needs gate/up fragment pairs
+  } else {
+    dim3 grid(a.tiles_m * a.tiles_n, a.splits);
+    k_gemm<BITS, WM, WN, FM, FN, RING, GLU><<<grid, WM * WN * 64, 0, s>>>(a);
+  }
 }
 
 template <int BITS, bool GLU>
 static void launch_index(int i, hipStream_t s, GemmArgs a) {
-  switch (i) {
-    case 0: launch_cfg<BITS, 2, 2, 8, 4, GLU>(s, a); break;
-    case 1: launch_cfg<BITS, 2, 2, 4, 4, GLU>(s, a); break;
-    case 2: launch_cfg<BITS, 2, 2, 4, 2, GLU>(s, a); break;
-    case 3: launch_cfg<BITS, 2, 2, 2, 4, GLU>(s, a); break;
-    case 4: launch_cfg<BITS, 2, 2, 2, 2, GLU>(s, a); break;
-    case 5: launch_cfg<BITS, 1, 4, 2, 2, GLU>(s, a); break;
-    case 6: launch_cfg<BITS, 4, 1, 2, 2, GLU>(s, a); break;
-    default: launch_cfg<BITS, 4, 1, 2, 1, false>(s, a); break;
-  }
+#define DJ_CFG_CASE(i, tag, wm, wn, fm, fn, ring) \
+  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, GLU>(s, a); break;
+  switch (i) { DJ_GEMM_CFGS(DJ_CFG_CASE) }
+#undef DJ_CFG_CASE
 }
 
-static bool cfg_fits(const GemmCfg &c, int N, bool glu) { return N % c.bn() == 0 && (!glu || c.fn % 2 == 0); }
+static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
+  (void)K;
+  return N % c.bn() == 0 && (!glu || c.fn % 2 == 0);
+}
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
-// sweeps on MI355X over the configurations' shapes: the largest of 128x128, 128x64, 64x64, 32x128 whose grid
-// still gives every CU a workgroup (within 15% of the best everywhere measured). Split-K only when even the
-// smallest tile leaves most CUs idle (skinny M): its device-scope fence writes back the XCD's L2, which costs
-// more than it saves once the grid covers the chip.
+// sweeps on MI355X (q8 and f16; M from 1152 to 86016; the decoders' N and K):
+//   128x128, 2-deep ring   when it gives >= 3 tiles per CU (large M: 845-990 TFLOP/s, 3 workgroups per CU),
+//   128x64, 2-deep ring    when that gives >= 2 tiles per CU (M ~ 1-2K on wide N),
+//   32x64                  when that gives >= 2 tiles per CU (narrow N),
+//   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
 static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, int &splits) {
   const char *force = getenv("DJ_GEMM_TILE");
   const char *fs = getenv("DJ_GEMM_SPLITK");
@@ -342,16 +401,17 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
   splits = 1;
   if (force)
     for (int i = 0; i < kNumCfgs; ++i)
-      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, glu)) cfg = i;
+      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) cfg = i;
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
-    static const int order[] = {1, 2, 4, 5, 6, 7};  // 128x128, 128x64, 64x64, 32x128, 128x32, 128x16
-    for (int i : order)
-      if (cfg_fits(kCfgs[i], N, glu) && tiles(i) >= cus) { cfg = i; break; }
+    static const struct { int cfg, per_cu; } rules[] = {{10, 3}, {18, 2}, {8, 2}};
+    for (const auto &r : rules)
+      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && tiles(r.cfg) >= (long)r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups
+      static const int small[] = {8, 5, 4, 7, 9, 15, 16};  // 32x64, 32x128, 64x64, 128x16, 64x32, ...
       long best = -1;
-      for (int i : order)
-        if (cfg_fits(kCfgs[i], N, glu) && tiles(i) > best) { cfg = i; best = tiles(i); }
+      for (int i : small)
+        if (cfg_fits(kCfgs[i], N, K, glu) && tiles(i) > best) { cfg = i; best = tiles(i); }
     }
   }
   if (cfg < 0) return;
@@ -365,19 +425,23 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
   if (splits < 1 || KT % splits || !ws_ok) splits = 1;
 }
 
+// Profile labels "matmul[_glu]_<q4|q8|f16>_<tile>", built when the library loads.
+static const struct GemmNames {
+  char v[3][2][kNumCfgs][40];
+  GemmNames() {
+    for (int b = 0; b < 3; ++b)
+      for (int glu = 0; glu < 2; ++glu)
+        for (int i = 0; i < kNumCfgs; ++i)
+          snprintf(v[b][glu][i], 40, "matmul%s_%s_%s", glu ? "_glu" : "", b == 0 ? "q4" : b == 1 ? "q8" : "f16", kCfgs[i].tag);
+  }
+} kNames;
+
 // launcher state: the split-K workspace lives in the context
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
 
 template <int BITS, bool GLU>
 static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name,
                        int *splits_out) {
-  static const char *const names[3][2][kNumCfgs] = {
-      {{"matmul_q4_256x128", "matmul_q4_128x128", "matmul_q4_128x64", "matmul_q4_64x128", "matmul_q4_64x64", "matmul_q4_32x128", "matmul_q4_128x32", "matmul_q4_128x16"},
-       {"matmul_glu_q4_256x128", "matmul_glu_q4_128x128", "matmul_glu_q4_128x64", "matmul_glu_q4_64x128", "matmul_glu_q4_64x64", "matmul_glu_q4_32x128", "matmul_glu_q4_128x32", "-"}},
-      {{"matmul_q8_256x128", "matmul_q8_128x128", "matmul_q8_128x64", "matmul_q8_64x128", "matmul_q8_64x64", "matmul_q8_32x128", "matmul_q8_128x32", "matmul_q8_128x16"},
-       {"matmul_glu_q8_256x128", "matmul_glu_q8_128x128", "matmul_glu_q8_128x64", "matmul_glu_q8_64x128", "matmul_glu_q8_64x64", "matmul_glu_q8_32x128", "matmul_glu_q8_128x32", "-"}},
-      {{"matmul_f16_256x128", "matmul_f16_128x128", "matmul_f16_128x64", "matmul_f16_64x128", "matmul_f16_64x64", "matmul_f16_32x128", "matmul_f16_128x32", "matmul_f16_128x16"},
-       {"matmul_glu_f16_256x128", "matmul_glu_f16_128x128", "matmul_glu_f16_128x64", "matmul_glu_f16_64x128", "matmul_glu_f16_64x64", "matmul_glu_f16_32x128", "matmul_glu_f16_128x32", "-"}}};
   const int N = w->N, K = w->K;
   float *ws = nullptr;
   uint32_t *cnt = nullptr;
@@ -385,6 +449,7 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   pick(M, N, K, GLU, c->cus, 1, cfg, splits);
   if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, 1 << 16, &ws, &cnt) != DJ_OK) splits = 1;
   if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
+  const char *label = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
   GemmArgs a;
   a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws; a.counter = cnt;
   a.M = M; a.N = N; a.K = K; a.act = act;
@@ -397,7 +462,7 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
     a.ksteps = K / 64;
   }
   launch_index<BITS, GLU>(cfg, c->stream, a);
-  *name = names[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
+  *name = label;
   *splits_out = a.splits;
   return DJ_OK;
 }
