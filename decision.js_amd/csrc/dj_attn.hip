@@ -19,125 +19,146 @@
 #include "dj_internal.h"
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
+typedef short s4 __attribute__((ext_vector_type(4)));
 
-// Global -> register staging of one K/V tile (64 keys) of the flattened tile sequence: tiles of source A first,
-// then of source B. Rows past the range end are clamped to its last row (read, then masked).
-#define DJ_ATTN_LOAD(j)                                                                                      \
-  {                                                                                                          \
-    const bool sb_ = (j) >= ntA;                                                                             \
-    const uint16_t *kb_ = sb_ ? kbB : kbA, *vb_ = sb_ ? vbB : vbA;                                           \
-    const int st_ = sb_ ? B.stride : A.stride, hi_ = sb_ ? hiB : hiA;                                        \
-    const int k0_ = sb_ ? loB + ((j) - ntA) * 64 : loA + (j) * 64;                                           \
-    _Pragma("unroll") for (int i = 0; i < KC; ++i) {                                                         \
-      const int c = tid + 256 * i, r = c / CH, ch = c % CH;                                                  \
-      kr[i] = *(const u32x4 *)(kb_ + (size_t)min(k0_ + r, hi_ - 1) * st_ + ch * 8);                          \
-    }                                                                                                        \
-    _Pragma("unroll") for (int i = 0; i < VI; ++i) {                                                         \
-      const int it = tid + 256 * i, r0 = 2 * (it & 31), ch = it >> 5;                                        \
-      vr[2 * i] = *(const u32x4 *)(vb_ + (size_t)min(k0_ + r0, hi_ - 1) * st_ + ch * 8);                     \
-      vr[2 * i + 1] = *(const u32x4 *)(vb_ + (size_t)min(k0_ + r0 + 1, hi_ - 1) * st_ + ch * 8);             \
-    }                                                                                                        \
-  }
+// LDS layout of one ring stage: K tile then V tile, 64 keys x D halves each, row-major (2D bytes per key) with
+// 16-byte chunks XOR-swizzled per row. K: chunk c of key r at c ^ (r & KSW) (conflict-free 16-byte MFMA reads of
+// 16 keys x one chunk). V: chunk c at c ^ vswz(r), chosen so the transposing reads below (4 keys x 2 chunks per
+// 16 lanes) hit distinct banks.
+template <int D>
+struct AttnShape {
+  static constexpr int CH = D / 8;                              // 16-byte chunks per key row
+  static constexpr int KSW = CH >= 16 ? 15 : 7;
+  static constexpr int TILE = 64 * 2 * D;                       // bytes of K (or V) per 64-key tile
+  static constexpr int STAGE = 2 * TILE;
+  static constexpr int NS = 4 * STAGE <= 128 * 1024 ? 4 : 2;    // D 64/128: 3 tiles in flight; D 256: 1
+  static constexpr int IK = TILE / 1024 / 4;                    // 1 KB DMAs per wave per tile, K (and V)
+  static constexpr int I = 2 * IK;                              // vector-memory ops per wave per tile
+  static_assert((NS - 2) * I < 64, "vmcnt range");
+  __device__ static int vswz(int r) { return D >= 128 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); }
+};
 
 template <int D>
 __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
                                               uint16_t *__restrict__ O) {
-  constexpr int NS = D / 32;   // MFMA k-steps over the head dim
+  using S = AttnShape<D>;
+  constexpr int NS_ = D / 32;  // MFMA k-steps over the head dim
   constexpr int NDB = D / 16;  // 16-row blocks of O^T
-  constexpr int CH = D / 8;    // 16-byte chunks per K row
-  constexpr int KC = CH / 4;   // K chunks staged per thread and tile
-  constexpr int VI = CH / 8;   // V chunk pairs (two adjacent keys) staged per thread and tile
-  constexpr int SW = CH >= 16 ? 15 : 7;
-  constexpr int VS = 68;       // V^T row stride in halves: 64 keys + 4 (conflict-free 8-byte reads)
+  constexpr int CH = S::CH, KSW = S::KSW, TILE = S::TILE, STAGE = S::STAGE, NS = S::NS;
   constexpr float LOG2E = 1.4426950408889634f;
-  __shared__ u32x4 Ks[64 * CH];
-  __shared__ uint32_t Vt[D * VS / 2];
-  __shared__ int bounds[4];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int h = blockIdx.y, q0 = blockIdx.x * 64;
   const int kvh = h / (heads / kv);
 
-  if (tid == 0) {
-    bounds[0] = INT_MAX; bounds[1] = INT_MIN; bounds[2] = INT_MAX; bounds[3] = INT_MIN;
-  }
-  __syncthreads();
-  if (tid < 64 && q0 + tid < T) {
-    const int4 r = rng[q0 + tid];
-    if (r.x < r.y) { atomicMin(&bounds[0], r.x); atomicMax(&bounds[1], r.y); }
-    if (r.z < r.w) { atomicMin(&bounds[2], r.z); atomicMax(&bounds[3], r.w); }
-  }
-  __syncthreads();
-  const int loA = max(bounds[0], 0), hiA = min(bounds[1], A.rows);
-  const int loB = max(bounds[2], 0), hiB = min(bounds[3], B.rows);
-  const int ntA = hiA > loA ? (hiA - loA + 63) / 64 : 0, ntB = hiB > loB ? (hiB - loB + 63) / 64 : 0;
-  const uint16_t *kbA = A.base + A.k_col + (size_t)kvh * D, *vbA = A.base + A.v_col + (size_t)kvh * D;
-  const uint16_t *kbB = B.base + B.k_col + (size_t)kvh * D, *vbB = B.base + B.v_col + (size_t)kvh * D;
-
+  // Q fragments first: nothing below depends on them until the first MFMA
   const int qi = q0 + wave * 16 + c16;
   const int qc = min(qi, T - 1);
-  h8 qf[NS];
+  h8 qf[NS_];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) qf[s] = *(const h8 *)(Q + (size_t)qc * q_stride + (size_t)h * D + s * 32 + g * 8);
-  const int4 rq = rng[qc];
-  // the wave's own key span per source (a tile outside it is skipped by the wave; queries past T see nothing)
+  for (int s = 0; s < NS_; ++s) qf[s] = *(const h8 *)(Q + (size_t)qc * q_stride + (size_t)h * D + s * 32 + g * 8);
+
+  // The block's key span per source: lane l reads query q0 + l's ranges, the wave reduces them (every wave
+  // does the same, so no LDS and no barrier before the first K/V loads).
+  const bool lv = q0 + lane < T;
+  const int4 rl = rng[min(q0 + lane, T - 1)];
+  int blo[2] = {lv && rl.x < rl.y ? rl.x : INT_MAX, lv && rl.z < rl.w ? rl.z : INT_MAX};
+  int bhi[2] = {lv && rl.x < rl.y ? rl.y : INT_MIN, lv && rl.z < rl.w ? rl.w : INT_MIN};
+  // this lane's query ranges, and the wave's own span (a tile outside it is skipped by the wave)
+  const int src_lane = wave * 16 + c16;
+  const int4 rq = {__shfl(rl.x, src_lane, 64), __shfl(rl.y, src_lane, 64), __shfl(rl.z, src_lane, 64),
+                   __shfl(rl.w, src_lane, 64)};
   int wlo[2] = {qi < T && rq.x < rq.y ? rq.x : INT_MAX, qi < T && rq.z < rq.w ? rq.z : INT_MAX};
   int whi[2] = {qi < T && rq.x < rq.y ? rq.y : INT_MIN, qi < T && rq.z < rq.w ? rq.w : INT_MIN};
 #pragma unroll
-  for (int x = 1; x < 16; x <<= 1)
+  for (int x = 1; x < 64; x <<= 1)
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      wlo[s] = min(wlo[s], __shfl_xor(wlo[s], x, 64));
-      whi[s] = max(whi[s], __shfl_xor(whi[s], x, 64));
+      blo[s] = min(blo[s], __shfl_xor(blo[s], x, 64));
+      bhi[s] = max(bhi[s], __shfl_xor(bhi[s], x, 64));
+      if (x < 16) {
+        wlo[s] = min(wlo[s], __shfl_xor(wlo[s], x, 64));
+        whi[s] = max(whi[s], __shfl_xor(whi[s], x, 64));
+      }
     }
-  wlo[0] = __builtin_amdgcn_readfirstlane(wlo[0]); whi[0] = __builtin_amdgcn_readfirstlane(whi[0]);
-  wlo[1] = __builtin_amdgcn_readfirstlane(wlo[1]); whi[1] = __builtin_amdgcn_readfirstlane(whi[1]);
+  const int loA = max(__builtin_amdgcn_readfirstlane(blo[0]), 0), hiA = min(__builtin_amdgcn_readfirstlane(bhi[0]), A.rows);
+  const int loB = max(__builtin_amdgcn_readfirstlane(blo[1]), 0), hiB = min(__builtin_amdgcn_readfirstlane(bhi[1]), B.rows);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    wlo[s] = __builtin_amdgcn_readfirstlane(wlo[s]);
+    whi[s] = __builtin_amdgcn_readfirstlane(whi[s]);
+  }
+  const int ntA = hiA > loA ? (hiA - loA + 63) / 64 : 0, ntB = hiB > loB ? (hiB - loB + 63) / 64 : 0;
+  const int ntiles = ntA + ntB;
+
+  // Per-lane DMA source offsets inside a tile: 1 KB DMA q of this wave covers LDS bytes [q KB, q KB + 1 KB) of
+  // the K (or V) tile; lane L fills 16 bytes at key row r, physical chunk p, i.e. logical chunk p ^ swizzle(r).
+  int krow[S::IK], kch[S::IK], vch[S::IK];
+#pragma unroll
+  for (int i = 0; i < S::IK; ++i) {
+    const int off = (wave * S::IK + i) * 1024 + lane * 16;
+    krow[i] = off / (2 * D);
+    const int p = (off % (2 * D)) / 16;
+    kch[i] = p ^ (krow[i] & KSW);
+    vch[i] = p ^ S::vswz(krow[i]);
+  }
+  // The Q fragments must have landed before the first DMA is issued: the compiler's own wait for them, placed
+  // at their first use inside the loop, would count only its own loads and drain the DMA ring every tile. An
+  // empty asm that reads them pins that wait here (volatile asm keeps its order with the DMA asm below).
+#pragma unroll
+  for (int s = 0; s < NS_; ++s) asm volatile("" : "+v"(qf[s]));
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  auto issue = [&](int j, int slot) {
+    const bool sb = j >= ntA;
+    const uint16_t *base = sb ? B.base : A.base;
+    const int stride = sb ? B.stride : A.stride, hi = sb ? hiB : hiA;
+    const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64;
+    const uint16_t *kb = base + (sb ? B.k_col : A.k_col) + (size_t)kvh * D;
+    const uint16_t *vb = base + (sb ? B.v_col : A.v_col) + (size_t)kvh * D;
+    const uint32_t st = lds0 + slot * STAGE;
+#pragma unroll
+    for (int i = 0; i < S::IK; ++i) {
+      const size_t row = (size_t)min(k0 + krow[i], hi - 1) * stride;  // rows past the range: its last row
+      dma16(kb + row + kch[i] * 8, st + (wv * S::IK + i) * 1024);
+      dma16(vb + row + vch[i] * 8, st + TILE + (wv * S::IK + i) * 1024);
+    }
+  };
+  if (ntiles > 0) {
+#pragma unroll
+    for (int p = 0; p < NS - 1; ++p) issue(min(p, ntiles - 1), p);  // a short range re-loads its last tile
+  }
 
   f4 o[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) o[i] = (f4){0.f, 0.f, 0.f, 0.f};
   float m = -1e30f, lsum = 0.f;  // running max in log2 units of the scaled scores
   const float sl = scale * LOG2E;
-  const uint16_t *vt16 = (const uint16_t *)Vt;
 
-  u32x4 kr[KC], vr[2 * VI];
-  const int ntiles = ntA + ntB;
-  if (ntiles > 0) DJ_ATTN_LOAD(0);
   for (int j = 0; j < ntiles; ++j) {
-    // registers -> LDS: K row-major (chunk ch of row r at ch ^ (r & SW)), V transposed (Vt[d][key])
-#pragma unroll
-    for (int i = 0; i < KC; ++i) {
-      const int c = tid + 256 * i, r = c / CH, ch = c % CH;
-      Ks[r * CH + (ch ^ (r & SW))] = kr[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      const int it = tid + 256 * i, r0 = 2 * (it & 31), ch = it >> 5;
-      uint32_t *dst = Vt + (((ch * 8) * VS + r0) >> 1);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t a = vr[2 * i][w], b = vr[2 * i + 1][w];
-        dst[(2 * w) * (VS / 2)] = (a & 0xffffu) | (b << 16);          // d = 8ch + 2w: (key r0, key r0+1)
-        dst[(2 * w + 1) * (VS / 2)] = (a >> 16) | (b & 0xffff0000u);  // d = 8ch + 2w + 1
-      }
-    }
-    __syncthreads();
-    if (j + 1 < ntiles) DJ_ATTN_LOAD(j + 1);  // in flight while this tile is computed
+    // tile j landed for this wave once at most the NS-2 later tiles' DMAs remain; after the barrier for every
+    // wave, and every wave is done with tile j-1's stage, which is refilled next
+    wait_vm_barrier<(NS - 2) * S::I>();
+    issue(min(j + NS - 1, ntiles - 1), (j + NS - 1) % NS);
 
+    const uint8_t *st = smem + (j % NS) * STAGE;
+    const u32x4 *Ks = (const u32x4 *)st;
     const bool sb = j >= ntA;
     const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64, hi = sb ? hiB : hiA;
     const int qlo = sb ? rq.z : rq.x, qhi = sb ? rq.w : rq.y;
     if (k0 < whi[sb] && k0 + 64 > wlo[sb]) {
+      // S^T[key, q] = K . Q^T: A = 16 keys x 32 dims of K, B = the query fragment
       f4 sc[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         sc[b] = (f4){0.f, 0.f, 0.f, 0.f};
         const int r = 16 * b + c16;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          const h8 kf = __builtin_bit_cast(h8, Ks[r * CH + ((4 * s + g) ^ (r & SW))]);
+        for (int s = 0; s < NS_; ++s) {
+          const h8 kf = __builtin_bit_cast(h8, Ks[r * CH + ((4 * s + g) ^ (r & KSW))]);
           sc[b] = MFMA16(kf, qf[s], sc[b]);
         }
       }
@@ -170,18 +191,28 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
       m = mn;
 #pragma unroll
       for (int db = 0; db < NDB; ++db) o[db] *= corr;
+      // O^T[d, q] += V^T . P^T. A = V^T (16 dims x keys {32t + 4g + 0..3, 32t + 16 + 4g + 0..3}, the key order
+      // of the S^T accumulator that became P^T) read by two transposing loads: within 16 lanes, lane i points
+      // at key 32t + 4g + i/4, dims 16db + 4(i%4)..+3, and receives dim 16db + i of keys 32t + 4g + 0..3.
+      const uint8_t *vt = st + TILE;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
+        const int key = 32 * t + 4 * g + (c16 >> 2);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const uint16_t *vrow = vt16 + (size_t)(16 * db + c16) * VS + 32 * t + 4 * g;
-          const u32x2 lo8 = *(const u32x2 *)vrow, hi8 = *(const u32x2 *)(vrow + 16);
-          const h8 vf = __builtin_bit_cast(h8, (u32x4){lo8.x, lo8.y, hi8.x, hi8.y});
+          const int c = 2 * db + ((c16 & 3) >> 1), half8 = (c16 & 1) * 8;
+          const uint8_t *p0 = vt + key * (2 * D) + ((c ^ S::vswz(key)) * 16) + half8;
+          const uint8_t *p1 = vt + (key + 16) * (2 * D) + ((c ^ S::vswz(key + 16)) * 16) + half8;
+          const h4 lo = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p0));
+          const h4 hi4 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p1));
+          const h8 vf = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
           o[db] = MFMA16(vf, pf[t], o[db]);
         }
+      }
     }
-    __syncthreads();
   }
+  wait_vm<0>();  // the clamped tail DMAs land before the wave ends
+
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
   if (qi < T) {

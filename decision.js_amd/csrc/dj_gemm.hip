@@ -105,36 +105,6 @@ struct GemmArgs {
   int M, N, K, act, tiles_m, tiles_n, splits, ksteps;  // ksteps: 64-K steps per split
 };
 
-// The LDS-fill DMAs and the "step landed" wait are inline assembly on purpose: the compiler models an LDS read
-// after a global_load_lds it issued as depending on every such load still in flight and waits vmcnt(0) before
-// it, which would drain the whole ring each step. Hidden from it, the ring's ordering is the explicit vmcnt
-// below; the compiler's own vmcnt waits for other loads only get stricter from ops it cannot see (in-order
-// completion). "memory" keeps LDS reads from moving across the fill or the barrier. s_nop: one wait state
-// between an SALU write of M0 and the LDS DMA that reads it.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"  // M0 is named as clobbered on purpose: the asm writes it
-__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// this wave's vector-memory ops older than the newest n are complete and its LDS reads have returned, then
-// the workgroup barrier
-template <int n>
-__device__ __forceinline__ void wait_vm_barrier() {
-  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(n) : "memory");
-}
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
 // Ring of LDS stages, each holding one 64-K step of the tile: A (BM rows x 128 bytes, XOR-swizzled 16-byte
 // chunks), the NB weight blocks of B in their global lane order, and (quantized B) each block's 16 scale words.
 template <int BITS, int WM, int WN, int FM, int FN, int RING>

@@ -115,3 +115,35 @@ int dj_launch_attention(hipStream_t s, int T, int heads, int kv, int D, const ui
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);
 
 static inline int dj_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------- LDS fill by DMA (device side)
+// global_load_lds (16 or 4 bytes per lane, written to LDS at M0 + 16 * lane or 4 * lane) and the "stage
+// landed" wait are inline assembly on purpose: the compiler models an LDS read after a global_load_lds it
+// issued as depending on every such load still in flight and waits vmcnt(0) before it, which would drain a
+// whole prefetch ring each step. Hidden from it, the ring's ordering is the explicit vmcnt
+// below; the compiler's own vmcnt waits for other loads only get stricter from ops it cannot see (in-order
+// completion). "memory" keeps LDS reads from moving across the fill or the barrier. s_nop: one wait state
+// between an SALU write of M0 and the LDS DMA that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is named as clobbered on purpose: the asm writes it
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// this wave's vector-memory ops older than the newest n are complete and its LDS reads have returned, then
+// the workgroup barrier
+template <int n>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(n >= 0 && n < 64, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(n) : "memory");
+}
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}

@@ -222,79 +222,87 @@ extern "C" int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, ui
 }
 
 // ---------------------------------------------------------------- q/k(/v) norm + RoPE
-// One workgroup per token; LPH lanes per head (a power of two). Lane s < rot/8 owns the four rotation pairs
-// (d, d + rot/2), d = 4s..4s+3; the next (D - rot)/8 lanes own 8 unrotated dims each. A lane's frequencies and
-// sin/cos depend only on its d and the token, so they are computed once and reused for every head the lane
-// visits. Frequency: theta^(-2d/rot) (POW_NEG) or 1 / theta^(2d/rot) (INV_POW), angle = f32(pos * f), as the
-// reference kernels compute them.
+// One workgroup per token; LPH lanes per head (a power of two). Lane s < rot/16 owns the 8 rotation pairs
+// (d, d + rot/2), d = 8s..8s+7 (two 16-byte loads); the next (D - rot)/8 lanes own 8 unrotated dims each.
+// cos/sin of the token's rot/2 angles are computed once into LDS. Frequency theta^(-2d/rot) (POW_NEG) or
+// 1 / theta^(2d/rot) (INV_POW) as exp2(e log2 theta) — the definition of WGSL pow the reference kernels use
+// (kernels.ts:106, eg2-kernels.ts:86) — and angle = f32(pos * f).
 template <int LPH>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, int D, int stride, uint16_t *__restrict__ Z,
                                                       const uint16_t *__restrict__ qn, const uint16_t *__restrict__ kn,
                                                       int vnorm, const int32_t *__restrict__ pos, int pos_stride, float eps,
                                                       float theta, int rot, int mode) {
+  __shared__ float2 tab[256];  // (cos, sin) of rotation pair i < rot / 2
   const int t = blockIdx.x;
   const int per = heads + kv + (vnorm ? kv : 0);
   const int sub = threadIdx.x % LPH, grp = threadIdx.x / LPH;
-  const int half = rot / 2, npl = rot / 8, ntl = (D - rot) / 8;
+  const int half = rot / 2, npl = rot / 16, ntl = (D - rot) / 8;
   const bool pl = sub < npl, tl = !pl && sub < npl + ntl;
-  const int d0 = pl ? 4 * sub : rot + 8 * (sub - npl);  // first owned dim
-  float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-  if (pl) {
-    const float ps = (float)pos[(size_t)t * pos_stride];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ex = (float)(2 * (d0 + i)) / (float)rot;
-      const float f = mode == DJ_ROPE_POW_NEG ? powf(theta, -ex) : 1.0f / powf(theta, ex);
-      sincosf(ps * f, &sn[i], &cs[i]);
-    }
+  const int d0 = pl ? 8 * sub : rot + 8 * (sub - npl);  // first owned dim
+  constexpr int HPP = 256 / LPH;                        // heads per pass
+  // this lane's values of its first head, loaded before the table is built
+  int hh = grp;
+  h8 x = {}, y = {};
+  if (hh < per && (pl || tl)) {
+    const uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
+    x = *(const h8 *)(z + d0);
+    if (pl) y = *(const h8 *)(z + half + d0);
   }
-  for (int hh = grp; hh < per; hh += 256 / LPH) {
+  if ((int)threadIdx.x < half) {
+    const float ps = (float)pos[(size_t)t * pos_stride];
+    const float e = (float)(2 * threadIdx.x) / (float)rot;
+    const float l2t = log2f(theta);
+    const float f = mode == DJ_ROPE_POW_NEG ? exp2f(-e * l2t) : 1.0f / exp2f(e * l2t);
+    float sn, cs;
+    sincosf(ps * f, &sn, &cs);
+    tab[threadIdx.x] = make_float2(cs, sn);
+  }
+  __syncthreads();
+  for (; hh < per; hh += HPP) {
+    uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
+    if (hh != grp && (pl || tl)) {
+      x = *(const h8 *)(z + d0);
+      if (pl) y = *(const h8 *)(z + half + d0);
+    }
     const bool isQ = hh < heads, isK = !isQ && hh < heads + kv;
     const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
     const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
-    uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
-    float v[8];
-    if (pl) {
-      const h4 x = *(const h4 *)(z + d0), y = *(const h4 *)(z + half + d0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { v[i] = (float)x[i]; v[4 + i] = (float)y[i]; }
-    } else if (tl) {
-      const h8 e = *(const h8 *)(z + d0);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = (float)e[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = 0.f;
-    }
     float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+    for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i] + (float)y[i] * (float)y[i];
 #pragma unroll
     for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
     const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
     if (pl) {
-      h4 xo, yo;
+      h8 wx, wy;
+      if (nw) {
+        wx = *(const h8 *)(nw + d0);
+        wy = *(const h8 *)(nw + half + d0);
+      }
+      h8 xo, yo;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float x = v[i] * inv, y = v[4 + i] * inv;
+      for (int i = 0; i < 8; ++i) {
+        float a = (float)x[i] * inv, b = (float)y[i] * inv;
         if (nw) {
-          x *= hf(nw[d0 + i]);
-          y *= hf(nw[half + d0 + i]);
+          a *= (float)wx[i];
+          b *= (float)wy[i];
         }
         if (isQ || isK) {
-          const float x2 = x * cs[i] - y * sn[i], y2 = y * cs[i] + x * sn[i];
-          x = x2;
-          y = y2;
+          const float2 r = tab[d0 + i];
+          const float a2 = a * r.x - b * r.y, b2 = b * r.x + a * r.y;
+          a = a2;
+          b = b2;
         }
-        xo[i] = (_Float16)x;
-        yo[i] = (_Float16)y;
+        xo[i] = (_Float16)a;
+        yo[i] = (_Float16)b;
       }
-      *(h4 *)(z + d0) = xo;
-      *(h4 *)(z + half + d0) = yo;
+      *(h8 *)(z + d0) = xo;
+      *(h8 *)(z + half + d0) = yo;
     } else if (tl) {
       h8 eo;
+      const h8 we = nw ? *(const h8 *)(nw + d0) : h8{};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? v[i] * inv * hf(nw[d0 + i]) : v[i] * inv);
+      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? (float)x[i] * inv * (float)we[i] : (float)x[i] * inv);
       *(h8 *)(z + d0) = eo;
     }
   }
@@ -303,20 +311,22 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
 extern "C" int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
                                const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta,
                                int rot, int mode) {
-  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && rot > 0 && rot <= D && rot % 8 == 0 &&
-                 (D - rot) % 8 == 0 && D / 8 <= 64 && stride % 8 == 0 && stride >= (heads + 2 * kv) * D,
+  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 && rot > 0 && rot <= D && rot % 16 == 0 &&
+                 (D - rot) % 8 == 0 && stride % 8 == 0 && stride >= (heads + 2 * kv) * D,
              "decision.js: qk_norm_rope: unsupported shape (D %d, rot %d, stride %d)", D, rot, stride);
   DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: qk_norm_rope: unknown rope mode");
   DJ_OP_BEGIN(rec, "qk_norm_rope");
   if (T > 0) {
-    const int lanes = D / 8;  // rot/8 pair lanes + (D - rot)/8 tail lanes
+    const int lanes = rot / 16 + (D - rot) / 8;
     hipStream_t s = rec->ctx->stream;
-    if (lanes <= 16)
-      k_qk_norm_rope<16><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
-    else if (lanes <= 32)
-      k_qk_norm_rope<32><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
-    else
-      k_qk_norm_rope<64><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode);
+#define DJ_ROPE_LAUNCH(L) \
+  k_qk_norm_rope<L><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode)
+    if (lanes <= 4) DJ_ROPE_LAUNCH(4);
+    else if (lanes <= 8) DJ_ROPE_LAUNCH(8);
+    else if (lanes <= 16) DJ_ROPE_LAUNCH(16);
+    else if (lanes <= 32) DJ_ROPE_LAUNCH(32);
+    else DJ_ROPE_LAUNCH(64);
+#undef DJ_ROPE_LAUNCH
   }
   return dj_op_end(rec, "qk_norm_rope");
 }
