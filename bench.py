@@ -9,8 +9,11 @@ ticket. Its packed inputs are staged in HBM before the timed region; a step copi
 buffers (device to device), runs the forward (a replayed HIP graph) and reads the 10 logits back.
 
 The JSON line also carries:
-  roofline      the dominant kernel (by GPU time in a profiled pass of the same tickets) against f16 dense
-                MFMA peak: algorithmic FLOPs per launch / its mean launch time (HIP events on the stream)
+  roofline      the dominant kernel (by GPU time in a profiled pass of the same tickets, HIP events around
+                every op) against f16 dense MFMA peak: algorithmic FLOPs per launch (2 M N K) / its launch
+                time, timed alone — the model's own weight, 50 launches in one HIP graph replayed between two
+                HIP events on the engine's stream; traffic = HBM bytes per launch from the FETCH_SIZE and
+                WRITE_SIZE counters (profiles/traffic.json, when it names the same kernel)
   cpu_baseline  the oracle (oracle/ref.py, numpy on the host cores) on one ticket of the same workload
 """
 import argparse
@@ -74,18 +77,45 @@ def model_flops_bytes(c, T, seqs_len):
 
 
 def roofline_from_profile(table):
-    """The dominant kernel by total GPU time and its achieved TFLOP/s from the shape in its profile key."""
+    """The dominant kernel by total GPU time in the profiled pass: (name, shape (M, N, K) or None, event ms)."""
     name, (ms, n) = max(table.items(), key=lambda kv: kv[1][0])
     m = re.search(r"\[(\d+)x(\d+)x(\d+)\]", name)
-    if not m:
-        return name, None
-    M, N, K = map(int, m.groups())
-    flops = 2.0 * M * N * K
-    avg_ms = ms / n
-    achieved = flops / (avg_ms * 1e-3) / 1e12
-    return name, {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                  "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
-                  "kernel": name, "launch_ms": round(avg_ms, 5), "flops_per_launch": flops}
+    return name, (tuple(map(int, m.groups())) if m else None), ms / n
+
+
+def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
+    """That GEMM alone: the model's own weight of this shape, `reps` launches captured in one HIP graph and
+    replayed `rounds` times between two HIP events on the engine's stream. Back-to-back launches in a graph
+    leave no per-launch event overhead, so this is the kernel's own duration (what rocprofv3 reports)."""
+    from decision_js_amd import _dj
+    M, N, K = shape
+    glu = name.startswith("matmul_glu")
+    want = _dj.W_MFMA_GLU if glu else _dj.W_MFMA
+    w = next((w for w in eng.w.values() if isinstance(w, _dj.Weight) and w.N == N and w.K == K
+              and (w.layout & ~_dj.W_DIRECT) == want), None)
+    if w is None:
+        return None
+    ctx = eng.ctx
+    rng = np.random.default_rng(5)
+    X = ctx.array((rng.standard_normal((M, K)) * 0.5).astype(np.float16))
+    Y = ctx.alloc(M * (N // 2 if glu else N) * 2)
+    key = 0x6A5EB0000 + (M * 131 + N * 7 + K) % 65521
+
+    def run():
+        rec = ctx.recorder(key)
+        if not rec.replay:
+            for _ in range(reps):
+                rec.matmul_glu(X, w, Y, M) if glu else rec.matmul(X, w, Y, M)
+        rec.finish()
+
+    run()
+    ctx.timer_begin()
+    for _ in range(rounds):
+        run()
+    ms = ctx.timer_end() / (rounds * reps)
+    X.free()
+    Y.free()
+    return ms
 
 
 def cpu_baseline(model_dir, ticket, budget_s):
@@ -175,7 +205,19 @@ def main():
     total = sum(v[0] for v in table.values())
     for k, (ms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:12]:
         log(f"  {k:48s} {ms / args.profile_steps:8.4f} ms/ticket  {100 * ms / total:5.1f}%  ({cnt // args.profile_steps}/ticket, {1e3 * ms / cnt:7.2f} us each)")
-    name, roof = roofline_from_profile(table)
+    name, shape, ev_ms = roofline_from_profile(table)
+    roof = None
+    if shape and name.startswith("matmul"):
+        k_ms = isolated_gemm_ms(eng, name, shape)
+        if k_ms:
+            M, N, K = shape
+            fl = 2.0 * M * N * K
+            achieved = fl / (k_ms * 1e-3) / 1e12
+            roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None, "kernel": name,
+                    "launch_ms": round(k_ms, 5), "launch_ms_events": round(ev_ms, 5), "flops_per_launch": fl}
+            log(f"dominant kernel {name}: {1e3 * k_ms:.2f} us per launch alone (graph of 50), {1e3 * ev_ms:.2f} us "
+                f"between per-op events; {achieved:.0f} TFLOP/s")
     flops, wbytes = model_flops_bytes(cfg, T, [384, 384, 384])
     t_roof_ms = max(flops / (MFMA_F16_PEAK_TFLOPS * 1e12), wbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     if args.calib_mb:
@@ -184,11 +226,15 @@ def main():
         eng.ctx.timer_begin()
         dst.copy_from(src)
         log(f"calibration copy {args.calib_mb} MiB: {eng.ctx.timer_end():.3f} ms")
-    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
-    if roof and os.path.exists(traffic_file):
-        tr = json.load(open(traffic_file))
-        if tr.get("kernel_key") == name:
-            roof["traffic"] = tr.get("bytes_per_launch")
+    # HBM bytes per launch of this kernel from the committed counter summary that names it (FETCH_SIZE and
+    # WRITE_SIZE, each scaled by its reading for a copy of known size)
+    if roof:
+        import glob
+        for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "traffic_*.json"))):
+            tr = json.load(open(f))
+            if tr.get("kernel_key") == name:
+                roof["traffic"] = tr.get("bytes_per_launch")
+                roof["traffic_source"] = os.path.relpath(f, ROOT)
 
     cpu = None
     if not args.no_cpu:
@@ -202,7 +248,7 @@ def main():
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
         "config": {"workload": f"configs[1]: {args.config} causal decoder, seeded N(0,0.02) weights; ticket = 3 questions x 384 random-id "
                                "tokens packed in one forward (T=1152), answer sets of 2/3/5 ids at each last token",
-                   "model": args.config, "tokens_per_ticket": T, "graphs": not args.no_graphs},
+                   "tokens_per_ticket": T, "graphs": not args.no_graphs},
         "roofline": roof,
         "forward_roofline": {"t_roof_ms": round(t_roof_ms, 4), "frac_of_roofline": round(t_roof_ms / (gpu_ms / args.steps), 4),
                              "flops_per_ticket": flops, "weight_bytes": wbytes},
