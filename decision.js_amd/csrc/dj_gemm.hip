@@ -125,7 +125,7 @@ struct GemmShape {
   static constexpr int I = IA + IB + IS;                              // vector-memory ops per wave and step
   static_assert(A_BYTES % (1024 * NW) == 0, "A stage must split into whole 1 KB rows per wave");
   static_assert(NB <= 4 * NW, "scale rows cover 4 blocks per wave");
-  static_assert((NS - 2) * I < 64, "vmcnt range");
+  static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
 };
 
@@ -191,47 +191,76 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
     if constexpr (S::IS) dma4(ssrc + kt * 16, st + A_BYTES + B_BYTES + wv * 256);
   };
 
+  // Fragments of one step in registers: A (FM x 2 k-halves of 16 rows x 32 K), raw B and scale words.
+#define DJ_READ(step, A_, R_, P_)                                                                        \
+  {                                                                                                      \
+    const uint8_t *st_ = smem + ((step) % NS) * STAGE;                                                   \
+    const u32x4 *As_ = (const u32x4 *)st_;                                                               \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i) _Pragma("unroll") for (int s = 0; s < 2; ++s) {       \
+      const int r = wm * FM * 16 + i * 16 + (lane & 15), ch = s * 4 + (lane >> 4);                       \
+      A_[i][s] = __builtin_bit_cast(h8, As_[r * 8 + (ch ^ (r & 7))]);                                    \
+    }                                                                                                    \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) {                                                     \
+      const int jb = wn * FN + j;                                                                        \
+      if constexpr (BITS == 8) R_[j].v = *(const u32x4 *)(st_ + A_BYTES + jb * CB + lane * 16);          \
+      else if constexpr (BITS == 4) R_[j].v = *(const u32x2 *)(st_ + A_BYTES + jb * CB + lane * 8);      \
+      else {                                                                                             \
+        R_[j].v0 = *(const u32x4 *)(st_ + A_BYTES + jb * CB + lane * 32);                                \
+        R_[j].v1 = *(const u32x4 *)(st_ + A_BYTES + jb * CB + lane * 32 + 16);                           \
+      }                                                                                                  \
+      P_[j] = S::IS ? *(const uint32_t *)(st_ + A_BYTES + B_BYTES + jb * 64 + (lane & 15) * 4) : 0u;     \
+    }                                                                                                    \
+  }
+#define DJ_MMA(A_, R_, P_)                                                                               \
+  _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                                        \
+    h8 bf[FN];                                                                                           \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(R_[j], s, P_[j]);               \
+    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                       \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(A_[i][s], bf[j], acc[i][j]);     \
+  }
+
   // prologue: steps 0 .. NS-2 in flight (clamped to the last step: a short split re-reads it, harmlessly)
 #pragma unroll
   for (int p = 0; p < NS - 1; ++p) issue(min(p, KS - 1), p);
 
-  for (int kt = 0; kt < KS; ++kt) {
-    // this wave's DMAs of step kt are done once at most the NS-2 later steps' remain outstanding; after the
-    // barrier every wave's are, and every wave has finished reading step kt-1's stage, which is refilled next
+  if constexpr (NS == 2) {
+    // two stages: read a step's fragments right after its barrier, then compute it
+    for (int kt = 0; kt < KS; ++kt) {
+      // this wave's DMAs of step kt are done once at most the NS-2 later steps' remain outstanding; after the
+      // barrier every wave's are, and every wave has finished reading step kt-1's stage, which is refilled next
+      wait_vm_barrier<(NS - 2) * S::I>();
+      issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
+      h8 fa[FM][2];
+      RawB<BITS> fr[FN];
+      uint32_t fp[FN];
+      DJ_READ(kt, fa, fr, fp);
+      DJ_MMA(fa, fr, fp);
+    }
+  } else {
+    // three or more stages: step k+1's fragments are read into the other register set while step k's MFMAs
+    // run, so LDS latency overlaps the matrix work. At half-step k: step k+1 has landed (NS-3 later steps may
+    // still be in flight), and after the barrier every wave is done with step k-1 (read at k-2, used at
+    // k-1), whose stage takes step k+NS-1.
+    h8 a0[FM][2], a1[FM][2];
+    RawB<BITS> r0[FN], r1[FN];
+    uint32_t p0[FN], p1[FN];
     wait_vm_barrier<(NS - 2) * S::I>();
-    const int slot = kt % NS;
-    issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
-
-    const uint8_t *st = smem + slot * STAGE;
-    const u32x4 *As = (const u32x4 *)st;
-    RawB<BITS> rb[FN];
-    uint32_t sp[FN];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int jb = wn * FN + j;
-      if constexpr (BITS == 8) rb[j].v = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 16);
-      else if constexpr (BITS == 4) rb[j].v = *(const u32x2 *)(st + A_BYTES + jb * CB + lane * 8);
-      else {
-        rb[j].v0 = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 32);
-        rb[j].v1 = *(const u32x4 *)(st + A_BYTES + jb * CB + lane * 32 + 16);
-      }
-      sp[j] = S::IS ? *(const uint32_t *)(st + A_BYTES + B_BYTES + jb * 64 + (lane & 15) * 4) : 0u;
+    DJ_READ(0, a0, r0, p0);
+    int kt = 0;
+    for (; kt + 2 <= KS; kt += 2) {
+      wait_vm_barrier<(NS - 3) * S::I>();
+      issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
+      DJ_READ(kt + 1, a1, r1, p1);
+      DJ_MMA(a0, r0, p0);
+      wait_vm_barrier<(NS - 3) * S::I>();
+      issue(min(kt + NS, KS - 1), (kt + NS) % NS);
+      DJ_READ(kt + 2, a0, r0, p0);  // kt + 2 == KS: the stage holds a re-loaded last step, read and unused
+      DJ_MMA(a1, r1, p1);
     }
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      h8 bf[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(rb[j], s, sp[j]);
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * FM * 16 + i * 16 + (lane & 15);
-        const int ch = s * 4 + (lane >> 4);
-        const h8 af = __builtin_bit_cast(h8, As[r * 8 + (ch ^ (r & 7))]);
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(af, bf[j], acc[i][j]);
-      }
-    }
+    if (kt < KS) DJ_MMA(a0, r0, p0);  // odd step count: the last step's fragments are in set 0
   }
+#undef DJ_READ
+#undef DJ_MMA
   wait_vm<0>();  // the clamped tail DMAs land before the wave moves on
 
   // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
@@ -313,6 +342,132 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------- skinny M (GEMV-style, M <= 64)
+// Below a few dozen rows the product is bound by streaming the weights, and a tile grid has too few
+// workgroups to keep HBM busy. Measured (graph replay, q8): 0.85 TB/s at M = 1 and 0.4-0.6 TB/s at M = 32
+// on 1536-2048-wide weights, 2-3x the tiled kernel; the limit is that each workgroup re-reads X from L2
+// (M / 8.5 times the weight bytes at 16 columns per workgroup). Here a workgroup owns CB 16-column weight blocks (CB = 2 for a gated weight:
+// its gate and up blocks) and all of K; its KW waves take the 64-K steps round-robin. A wave loads BATCH
+// steps at once — weight blocks (16 bytes per lane, already in MFMA lane order), scale words and the X
+// fragments (L2-resident) — straight into registers, then runs their MFMAs; with up to 16 waves per
+// workgroup that keeps enough weight bytes in flight. The waves' partial tiles are added through LDS in wave
+// order (deterministic), and wave 0 runs the same epilogue as the tiled kernel.
+template <int BITS, int MT, int CB, bool GLU>
+__global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
+  constexpr int CBYTES = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;
+  // steps per load batch: about 80 VGPRs of staging (X fragments 8 MT, weight blocks 4 or 8 and a scale word
+  // per block and step), so 16 waves per workgroup (128 VGPRs each) fit without spilling
+  constexpr int PER_STEP = 8 * MT + (BITS == 16 ? 8 : 5) * CB;
+  constexpr int BATCH = 80 / PER_STEP < 1 ? 1 : 80 / PER_STEP > 8 ? 8 : 80 / PER_STEP;
+  __shared__ f4 red[15 * MT * CB * 64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, KW = blockDim.x >> 6;
+  const int nb0 = blockIdx.x * CB;
+  const int M = g.M, K = g.K, KT = K >> 6;
+
+  f4 acc[MT][CB];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
+  const uint16_t *xr[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) xr[i] = g.X + (size_t)min(16 * i + (lane & 15), M - 1) * K + (lane >> 4) * 8;
+
+  for (int kb = wave; kb < KT; kb += KW * BATCH) {
+    h8 a[BATCH][MT][2];
+    RawB<BITS> b[BATCH][CB];
+    uint32_t sp[BATCH][CB];
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      const int kt = min(kb + q * KW, KT - 1);  // past the end: re-load the last step (not accumulated)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int s = 0; s < 2; ++s) a[q][i][s] = *(const h8 *)(xr[i] + kt * 64 + s * 32);
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const size_t blk = (size_t)(nb0 + j) * KT + kt;
+        if constexpr (BITS == 8) b[q][j].v = *(const u32x4 *)(g.Wc + blk * CBYTES + lane * 16);
+        else if constexpr (BITS == 4) b[q][j].v = *(const u32x2 *)(g.Wc + blk * CBYTES + lane * 8);
+        else {
+          b[q][j].v0 = *(const u32x4 *)(g.Wc + blk * CBYTES + lane * 32);
+          b[q][j].v1 = *(const u32x4 *)(g.Wc + blk * CBYTES + lane * 32 + 16);
+        }
+        sp[q][j] = BITS == 16 ? 0u : g.Ws[blk * 16 + (lane & 15)];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < BATCH; ++q) {
+      if (kb + q * KW < KT) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int j = 0; j < CB; ++j) {
+            const h8 bf = dequant<BITS>(b[q][j], s, sp[q][j]);
+#pragma unroll
+            for (int i = 0; i < MT; ++i) acc[i][j] = MFMA16(a[q][i][s], bf, acc[i][j]);
+          }
+      }
+    }
+  }
+
+  // partial tiles of waves 1.. through LDS, added by wave 0 in wave order
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) red[(((wave - 1) * MT + i) * CB + j) * 64 + lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+  for (int w = 1; w < KW; ++w)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) acc[i][j] += red[(((w - 1) * MT + i) * CB + j) * 64 + lane];
+
+  // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
+  const int N = g.N;
+  if constexpr (!GLU) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        const int n = (nb0 + j) * 16 + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * i + (lane >> 4) * 4 + r;
+          if (m < M) g.Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
+        }
+      }
+  } else {
+    static_assert(!GLU || CB == 2, "a gated weight pairs gate and up blocks");
+    const int I = N >> 1, col = (nb0 >> 1) * 16 + (lane & 15);  // block pair (2p, 2p + 1) -> w1/w3 block p
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + (lane >> 4) * 4 + r;
+        const float a = (float)(_Float16)acc[i][0][r], b = (float)(_Float16)acc[i][1][r];
+        const float h = (g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b;
+        if (m < M) g.Y[(size_t)m * I + col] = __builtin_bit_cast(uint16_t, (_Float16)h);
+      }
+  }
+}
+
+// Waves per workgroup for the skinny kernel: about two steps each, 4..15 waves (the LDS reduction holds 15
+// partial tiles).
+static int gemv_waves(int KT) { return KT / 2 < 4 ? 4 : KT / 2 > 15 ? 15 : KT / 2; }
+
+template <int BITS, bool GLU>
+static void launch_gemv(hipStream_t s, GemmArgs a) {
+  constexpr int CB = GLU ? 2 : 1;
+  const dim3 grid(a.N / 16 / CB), block(64 * gemv_waves(a.K / 64));
+  if (a.M <= 16) k_gemv<BITS, 1, CB, GLU><<<grid, block, 0, s>>>(a);
+  else if (a.M <= 32) k_gemv<BITS, 2, CB, GLU><<<grid, block, 0, s>>>(a);
+  else k_gemv<BITS, 4, CB, GLU><<<grid, block, 0, s>>>(a);
+}
+
 // ---------------------------------------------------------------- dispatch
 
 // Tile configurations: waves along M and N, 16x16 fragments per wave along M and N, K groups.
@@ -322,7 +477,9 @@ struct GemmCfg {
   int bm() const { return wm * fm * 16; }
   int bn() const { return wn * fn * 16; }
 };
-// tag "<BM>x<BN>[s<ring>]": waves along M and N, 16x16 fragments per wave along M and N, LDS ring depth
+// tag "<BM>x<BN>[s<ring>]": waves along M and N, 16x16 fragments per wave along M and N, LDS ring depth;
+// "n": one wave row (every wave spans all BM rows and owns distinct columns, so no two waves dequantize the
+// same weight fragment)
 #define DJ_GEMM_CFGS(X)                                                                                    \
   X(0, "256x128", 2, 2, 8, 4, 0) X(1, "128x128", 2, 2, 4, 4, 0) X(2, "128x64", 2, 2, 4, 2, 0)              \
   X(3, "64x128", 2, 2, 2, 4, 0) X(4, "64x64", 2, 2, 2, 2, 0) X(5, "32x128", 1, 4, 2, 2, 0)                 \
@@ -330,7 +487,8 @@ struct GemmCfg {
   X(9, "64x32", 2, 2, 2, 1, 0) X(10, "128x128s2", 2, 2, 4, 4, 2) X(11, "128x128s3", 2, 2, 4, 4, 3)         \
   X(12, "256x128s2", 2, 2, 8, 4, 2) X(13, "128x256", 2, 2, 4, 8, 0) X(14, "128x256s2", 2, 2, 4, 8, 2)      \
   X(15, "64x64s2", 2, 2, 2, 2, 2) X(16, "32x128s2", 1, 4, 2, 2, 2) X(17, "64x128s2", 2, 2, 2, 4, 2)        \
-  X(18, "128x64s2", 2, 2, 4, 2, 2)
+  X(18, "128x64s2", 2, 2, 4, 2, 2) X(19, "128x128n", 1, 4, 8, 2, 2) X(20, "128x128n3", 1, 4, 8, 2, 3)        \
+  X(21, "64x128n", 1, 4, 4, 2, 2) X(22, "128x256n", 1, 4, 8, 4, 2) X(23, "64x256n", 1, 4, 4, 4, 2)
 #define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -359,10 +517,12 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
 }
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
-// sweeps on MI355X (q8 and f16; M from 1152 to 86016; the decoders' N and K):
-//   128x128, 2-deep ring   when it gives >= 3 tiles per CU (large M: 845-990 TFLOP/s, 3 workgroups per CU),
-//   128x64, 2-deep ring    when that gives >= 2 tiles per CU (M ~ 1-2K on wide N),
-//   32x64                  when that gives >= 2 tiles per CU (narrow N),
+// sweeps on MI355X with warm clocks (q8; M 1152-86016; the decoders' N and K), first rule that fits:
+//   128x128n    when it gives >= 1.5 tiles per CU (large M: 925-1040 TFLOP/s; also the 1152-row GLU), or
+//               >= 0.5 per CU when K >= 4096 (few long tiles beat many short ones: 3B's w2),
+//   64x128n     when it gives >= 2 tiles per CU (1152-row qkv),
+//   32x64       when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows),
+//   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
 static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, int &splits) {
   const char *force = getenv("DJ_GEMM_TILE");
@@ -374,9 +534,10 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
       if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) cfg = i;
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
-    static const struct { int cfg, per_cu; } rules[] = {{10, 3}, {18, 2}, {8, 2}};
+    static const struct { int cfg; double per_cu; int min_k; } rules[] = {
+        {19, 1.5, 0}, {19, 0.5, 4096}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
     for (const auto &r : rules)
-      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && tiles(r.cfg) >= (long)r.per_cu * cus) { cfg = r.cfg; break; }
+      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups
       static const int small[] = {8, 5, 4, 7, 9, 15, 16};  // 32x64, 32x128, 64x64, 128x16, 64x32, ...
       long best = -1;
@@ -406,6 +567,10 @@ static const struct GemmNames {
   }
 } kNames;
 
+static const char *const kGemvNames[3][2] = {{"matmul_q4_gemv", "matmul_glu_q4_gemv"},
+                                             {"matmul_q8_gemv", "matmul_glu_q8_gemv"},
+                                             {"matmul_f16_gemv", "matmul_glu_f16_gemv"}};
+
 // launcher state: the split-K workspace lives in the context
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
 
@@ -413,6 +578,19 @@ template <int BITS, bool GLU>
 static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name,
                        int *splits_out) {
   const int N = w->N, K = w->K;
+  const char *force = getenv("DJ_GEMM_TILE");
+  // skinny M on weights up to 4096 outputs wide: 2-3x faster than any tile (measured); wider weights give the
+  // tiled kernel enough workgroups and it wins there
+  const bool skinny = M <= 64 && N % (GLU ? 32 : 16) == 0 && (force ? !strcmp(force, "gemv") : N <= 4096);
+  if (skinny) {
+    GemmArgs a{};
+    a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y;
+    a.M = M; a.N = N; a.K = K; a.act = act;
+    launch_gemv<BITS, GLU>(c->stream, a);
+    *name = kGemvNames[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU];
+    *splits_out = 1;
+    return DJ_OK;
+  }
   float *ws = nullptr;
   uint32_t *cnt = nullptr;
   int cfg, splits;

@@ -100,6 +100,9 @@ def test_sandwich(pkg, ctx, with_y, with_w2, H):
     (384, 4096, 1024, 8), (384, 1024, 3072, 8), (1152, 6144, 1024, 8),  # the minimum slice's shapes
     (77, 1040, 128, 8), (2304, 256, 512, 8), (5, 1024, 1536, 8),
     (512, 2560, 2048, 4), (300, 2048, 11008, 4), (2100, 512, 256, 4), (33, 48, 64, 4),
+    # skinny M (the GEMV-style kernel): one row, a single K step, 16/17/32/64 rows, long K in several batches
+    (1, 2048, 1536, 8), (8, 1536, 64, 8), (16, 1536, 4608, 8), (17, 2048, 1536, 4), (32, 1536, 1536, 8),
+    (64, 2560, 2048, 4), (32, 2048, 11008, 4),
 ])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul(pkg, ctx, M, N, K, bits, direct):
@@ -134,7 +137,8 @@ def test_matmul_weights_bit_exact(pkg, ctx, bits, direct):
     assert np.array_equal(got, np.ascontiguousarray(ref.dequant_f16(codes, scales, bits).T).view(np.uint16))
 
 
-@pytest.mark.parametrize("M,I,K,bits,act", [(384, 3072, 1024, 8, 0), (70, 1152, 768, 8, 1), (2200, 1024, 512, 4, 0), (19, 64, 128, 8, 1)])
+@pytest.mark.parametrize("M,I,K,bits,act", [(384, 3072, 1024, 8, 0), (70, 1152, 768, 8, 1), (2200, 1024, 512, 4, 0), (19, 64, 128, 8, 1),
+                                             (32, 4608, 1536, 8, 0), (1, 1024, 2048, 4, 0), (64, 1152, 768, 8, 1)])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
     dj = _dj()
