@@ -265,6 +265,29 @@ def test_attention_forest(pkg, ctx, heads, kv, D):
     assert err < 4e-3
 
 
+def test_attention_large_grid(pkg, ctx):
+    """A varlen batch of causal sequences large enough (>= 512 workgroups) for the two-stage K/V ring, and
+    long enough that the lazy max-rescaling and the unmasked-tile path both run many times."""
+    dj = _dj()
+    rng = np.random.default_rng(41)
+    heads, kv, D = 16, 8, 128
+    meta, rng4 = _forest_case(rng, [(300, []), (450, []), (128, []), (700, []), (512, []), (300, [])])
+    T = meta.shape[0]
+    assert (T + 63) // 64 * heads >= 512
+    mask = ref.forest_mask(meta)
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride), std=1.5)  # sharper softmax: the running max moves often
+    dZ, drng, dO = ctx.array(Z), ctx.array(rng4), ctx.alloc(T * heads * D * 2)
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    scale = 1.0 / math.sqrt(D)
+    run(ctx, lambda r: r.attention(T, heads, kv, D, dZ, stride, src, src, drng, scale, dO))
+    got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+    want = ref.attention(Z, heads, kv, D, mask, scale, np.float64).astype(np.float64)
+    err = np.abs(got - want).max()
+    print(f"attention large grid T{T}: max abs err {err:.2e}")
+    assert err < 4e-3
+
+
 @pytest.mark.parametrize("D", [128, 256])
 def test_attention_bidirectional_and_windows(pkg, ctx, D):
     dj = _dj()
