@@ -57,8 +57,8 @@ class Decision:
     @classmethod
     def load(cls, base: str, opts: dict = None):
         """A model in the decision.js format at `base` (manifest.json + weights.bin). opts: device,
-        on_progress, share_state, tokens_per_pass, graphs, prompt. The kind comes from manifest.config.model
-        (d1.ts:63-64)."""
+        on_progress, share_state, tokens_per_pass, graphs, prompt, direct_weights (LoadOptions.directWeights,
+        gpu.ts:20). The kind comes from manifest.config.model (d1.ts:63-64)."""
         opts = dict(opts or {})
         from .fmt import load_manifest
         model = load_manifest(base if base.endswith("/") else base + "/")["config"].get("model")

@@ -28,8 +28,8 @@ def default_layout(name: str, info: dict) -> int:
 
 def load_weights(base: str, opts: dict = None, layout=default_layout):
     """The manifest and every tensor of `base` on the device: (ctx, manifest, weights). opts: device (an
-    existing _dj.Context), on_progress(loaded, total). Quantized tensors become _dj.Weight, f16/f32 ones
-    DevBuf (with the host array kept as .host). Mirrors loadWeights (gpu.ts:57-88): range reads, a length
+    existing _dj.Context), on_progress(loaded, total), direct_weights (bool). Quantized tensors become
+    _dj.Weight, f16/f32 ones DevBuf (with the host array kept as .host). Mirrors loadWeights (gpu.ts:57-88): range reads, a length
     check per read, and a refusal when a tensor exceeds what the device can hold."""
     opts = opts or {}
     if not base.endswith("/"):
@@ -41,12 +41,20 @@ def load_weights(base: str, opts: dict = None, layout=default_layout):
     largest = max(t["bytes"] for t in m["tensors"].values())
     if largest > total_mem:
         raise _dj.DJError(_dj.DJ_ENOMEM, f"decision.js: this GPU holds {total_mem / 1e6:.0f} MB, this model needs a {largest / 1e6:.0f} MB tensor")
+    # directWeights (gpu.ts:16-20, 114-133): the linears dequantized once at load to f16 (the same values the
+    # in-kernel dequantization gives, bit for bit). true / false as given; unset keeps them quantized — the
+    # reference turns it on below 1.5 GB to win WebGPU speed, while these kernels dequantize in registers at
+    # the same speed and half the bytes (the option stays a drop-in switch, not a different result).
+    direct = bool(opts.get("direct_weights", opts.get("directWeights", False)))
     w, loaded = {}, 0
     for name, info in m["tensors"].items():
         if info["dtype"] in ("q4", "q8"):
             codes, scales = tf.tensor(info)
             N, K = info["shape"]
-            w[name] = ctx.weight_q(codes, scales, N, K, 8 if info["dtype"] == "q8" else 4, layout(name, info))
+            lay = layout(name, info)
+            if direct and lay != _dj.W_PLAIN:
+                lay |= _dj.W_DIRECT
+            w[name] = ctx.weight_q(codes, scales, N, K, 8 if info["dtype"] == "q8" else 4, lay)
             loaded += info["bytes"] + info["scales_bytes"]
         else:
             arr = np.array(tf.tensor(info))

@@ -99,6 +99,25 @@ def test_decoder_forest_vs_oracle(pkg, models, which):
         eng.destroy()
 
 
+@pytest.mark.parametrize("which", ["q8", "q4"])
+def test_direct_weights_are_bit_identical(pkg, models, which):
+    """directWeights (gpu.ts:16-20): the linears dequantized once at load give the same f16 weights, the same
+    tiles and the same accumulation order as in-register dequantization — so the same logits, bit for bit —
+    at a varlen length (tiled GEMMs) and a 32-token one (the skinny kernel)."""
+    from decision_js_amd.engine import DecoderEngine
+    rng = np.random.default_rng(8)
+    trees = [_tree(rng, 4096, 0, [300]), _tree(rng, 4096, 0, [200, 180])]
+    short = [_tree(rng, 4096, 0, [32])]
+    out = []
+    for direct in (False, True):
+        eng = DecoderEngine.load(models[which], {"direct_weights": direct})
+        try:
+            out.append((eng.run(trees)["logits"], eng.run(short)["logits"]))
+        finally:
+            eng.destroy()
+    assert np.array_equal(out[0][0], out[1][0]) and np.array_equal(out[0][1], out[1][1])
+
+
 def test_varlen_batch_equals_single_runs(pkg, models):
     """Config-4 style: many sequences of random length packed into one forward give the answers each gives
     alone (packing is exact), and agree with the oracle."""
