@@ -3,7 +3,8 @@
     python decision.js_amd/csrc/build.py [--jobs N]
 
 Each .hip source is compiled by hipcc to an object in decision.js_amd/csrc/_build/, then linked into
-decision.js_amd/lib/libdj.so. No cmake: the sources are few and the flags are the ones below.
+decision.js_amd/lib/libdj.so; the Node host's N-API binding (decision.js_amd/node/dj_napi.cc) is built next to
+it as dj_napi.node. No cmake: the sources are few and the flags are the ones below.
 """
 import argparse
 import concurrent.futures as cf
@@ -54,7 +55,30 @@ def build(jobs: int = 4) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_node_addon()
     return LIB
+
+
+NODE_ADDON = os.path.join(PKG, "lib", "dj_napi.node")
+NODE_INCLUDE = "/usr/include/node"
+
+
+def build_node_addon() -> str:
+    """The N-API binding of the C ABI for the Node host (decision.js_amd/node/), next to libdj.so: plain g++
+    against the system's Node headers (N-API 8), linked to libdj.so with an $ORIGIN rpath. Skipped, with a
+    note, where Node's headers are absent."""
+    if not os.path.exists(os.path.join(NODE_INCLUDE, "node_api.h")):
+        sys.stderr.write("build.py: no Node headers at /usr/include/node: the Node binding is not built\n")
+        return ""
+    tmp = NODE_ADDON + ".tmp"
+    cmd = ["g++", "-shared", "-fPIC", "-O2", "-std=c++17", "-Wall", "-DNODE_GYP_MODULE_NAME=dj_napi",
+           "-I" + NODE_INCLUDE, "-I" + os.path.join(ROOT, "include"), os.path.join(PKG, "node", "dj_napi.cc"),
+           "-L" + os.path.dirname(LIB), "-ldj", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on the Node binding:\n{r.stderr}")
+    os.replace(tmp, NODE_ADDON)
+    return NODE_ADDON
 
 
 if __name__ == "__main__":

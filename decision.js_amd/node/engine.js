@@ -1,0 +1,290 @@
+"use strict";
+/* The causal decoder engine on the Node host (D13BEngine, d1-3b-engine.ts; shared state after d3-engine.ts):
+ * forest packing on the host, the per-layer op sequence on a Recorder of the native library, answer-set
+ * logits at each branch's last token. The same steps as decision_js_amd/engine.py, which the tests hold the
+ * two hosts to (identical logits through the same library). */
+const { Context, kvSrc, lib } = require("./dj");
+const { loadWeights } = require("./format");
+
+/** Device layout of a quantized tensor: the embedding (gathered, read as the LM head) stays plain, fused
+ * gated-MLP inputs are interleaved for the GLU epilogue, other linears are repacked for the MFMA GEMM
+ * (directWeights: dequantized once to f16 — gpu.ts:16-20, 114-133). */
+function layoutFor(direct) {
+  return (name) => {
+    const L = lib();
+    if (name === "embed" || name.startsWith("head.dense")) return L.W_PLAIN;
+    const base = name.endsWith("w13") || name.endsWith(".gu") ? L.W_MFMA_GLU : L.W_MFMA;
+    return direct ? base | L.W_DIRECT : base;
+  };
+}
+
+/** Forest packing of D13BEngine.run (d1-3b-engine.ts:46-72): each tree's trunk once, each branch
+ * continuing it; per token ids (u32), pos (branch positions continue after the trunk), and the attention key
+ * ranges (a0, a1, b0, b1) equal to the forest mask of kernels.ts:135 — a trunk token i sees
+ * [start, start+i+1), a branch token the trunk [start, start+P) and its branch up to itself; leaves = each
+ * branch's last token; leafIds = the flattened option groups, zero-padded to nIds. */
+function packForest(trees) {
+  let T = 0;
+  for (const t of trees) T += t.trunk.length + t.branches.reduce((a, b) => a + b.length, 0);
+  const ids = new Uint32Array(T), pos = new Int32Array(T), rng = new Int32Array(T * 4);
+  const leaves = [], leafGroups = [];
+  let off = 0;
+  for (const tr of trees) {
+    const start = off, P = tr.trunk.length;
+    for (let i = 0; i < P; ++i, ++off) {
+      ids[off] = tr.trunk[i];
+      pos[off] = i;
+      rng[4 * off] = start;
+      rng[4 * off + 1] = start + i + 1;
+    }
+    tr.branches.forEach((br, b) => {
+      const b0 = off;
+      for (let o = 0; o < br.length; ++o, ++off) {
+        ids[off] = br[o];
+        pos[off] = P + o;
+        rng.set([start, start + P, b0, off + 1], 4 * off);
+      }
+      leaves.push(off - 1);
+      leafGroups.push([].concat(...tr.groups[b]));
+    });
+  }
+  const L = leaves.length;
+  const nIds = leafGroups.reduce((a, g) => Math.max(a, g.length), 0);
+  const leafIds = new Uint32Array(Math.max(L * nIds, 1));
+  leafGroups.forEach((g, k) => leafIds.set(g, k * nIds));
+  return { ids, pos, rng, leaves: Uint32Array.from(leaves), leafIds, nIds, T, L };
+}
+
+/** Readout of d1-3b-engine.ts:112-121: each option scores the max over its token group. */
+function groupMax(out, nIds, trees) {
+  const scores = [];
+  let leaf = 0;
+  for (const tr of trees) {
+    const perQ = [];
+    for (const groups of tr.groups) {
+      let j = 0;
+      const s = [];
+      for (const g of groups) {
+        let best = -Infinity;
+        for (let k = 0; k < g.length; ++k) best = Math.max(best, out[leaf * nIds + j + k]);
+        s.push(best);
+        j += g.length;
+      }
+      perQ.push(s);
+      ++leaf;
+    }
+    scores.push(perQ);
+  }
+  return scores;
+}
+
+// FNV-1a over a string, 64-bit: the key of a captured forward graph
+function hashKey(s) {
+  let h = 0xcbf29ce484222325n;
+  for (let i = 0; i < s.length; ++i) h = BigInt.asUintN(64, (h ^ BigInt(s.charCodeAt(i))) * 0x100000001b3n);
+  return h | 1n;
+}
+
+let engineSerial = 0, stateSerial = 0;
+
+class GpuEngine {
+  constructor(ctx, m, w, opts) {
+    this.ctx = ctx;
+    this.m = m;
+    this.w = w;
+    this.opts = opts || {};
+    this.graphs = this.opts.graphs === undefined ? true : !!this.opts.graphs;
+    this.stats = { forwards: 0, tokens: 0 };
+    this.bufs = {};
+    this.gen = 0;
+    this.serial = ++engineSerial;
+    this.ownsCtx = !this.opts.device;
+  }
+  /** Frees every weight and buffer (gpu.ts:108-110). */
+  destroy() {
+    for (const b of Object.values(this.bufs)) b.free();
+    this.bufs = {};
+    for (const v of Object.values(this.w)) v.free();
+    this.w = {};
+    if (this.ownsCtx) this.ctx.close();
+  }
+  alloc(spec) {
+    for (const b of Object.values(this.bufs)) b.free();
+    this.bufs = {};
+    for (const [k, n] of Object.entries(spec)) this.bufs[k] = this.ctx.alloc(n);
+    this.gen += 1;
+    this.ctx.graphClear();
+  }
+  key(...parts) {
+    return this.graphs ? hashKey(JSON.stringify([this.serial, this.gen].concat(parts))) : 0n;
+  }
+}
+
+class SharedState {
+  constructor(P, cache, ids) {
+    this.P = P;
+    this.cache = cache;
+    this.ids = ids;
+    this.serial = ++stateSerial;
+  }
+  free() {
+    this.cache.free();
+  }
+}
+
+const INPUTS = ["ids", "pos", "rng", "leaves", "leafIds"];
+
+class DecoderEngine extends GpuEngine {
+  static async load(base, opts) {
+    opts = opts || {};
+    const direct = !!(opts.directWeights || opts.direct_weights);
+    const { ctx, m, w } = await loadWeights(base, opts, layoutFor(direct));
+    const model = m.config.model;
+    if (model !== "decoder" && model !== "d1-3b") throw new Error(`decision.js: ${base} is not a causal decoder (${model})`);
+    if ((m.config.layer_types || []).some((t) => t !== "full_attention")) {
+      throw new Error("decision.js: only attention layers are supported (LFM2 conv layers are not on this path)");
+    }
+    return new DecoderEngine(ctx, m, w, opts);
+  }
+
+  constructor(ctx, m, w, opts) {
+    super(ctx, m, w, opts);
+    const c = m.config;
+    Object.assign(this, { H: c.hidden, I: c.intermediate, h: c.heads, kv: c.kv_heads, D: c.head_dim, eps: c.eps, theta: c.rope_theta });
+    this.layers = c.layers !== undefined ? c.layers : (c.layer_types || []).length;
+    this.stride = (this.h + 2 * this.kv) * this.D;
+    this.capacity = 0;
+    this.leafCapacity = 0;
+  }
+
+  /** Activation buffers, grown and never shrunk, capacity rounded to 64 rows (d1-3b-engine.ts:33-42). */
+  ensure(T, L = 0, nIds = 0) {
+    if (T <= this.capacity && L * Math.max(nIds, 1) <= this.leafCapacity) return;
+    let cap = Math.max(T, this.capacity, 256);
+    cap = Math.ceil(cap / 64) * 64;
+    const lcap = Math.max(L * Math.max(nIds, 1), this.leafCapacity, 1024);
+    const { H, I } = this;
+    this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * this.stride * 2, y: cap * this.h * this.D * 2,
+      h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, leaves: lcap * 4, leafIds: lcap * 4, out: lcap * 4 });
+    this.capacity = cap;
+    this.leafCapacity = lcap;
+  }
+
+  /** The per-layer loop (d1-3b-engine.ts:88-105) on the recorder. */
+  recordLayers(rec, T, B, kvA, kvStore) {
+    const w = this.w, L = lib();
+    const { H, h, kv, D, eps } = this;
+    const z = B.z.ptr;
+    const src = kvSrc(z, T, this.stride, h * D, (h + kv) * D);
+    const ptr = (name) => (w[name] ? w[name].ptr : 0n);
+    rec.gatherQ(B.ids.ptr, T, w.embed, B.x.ptr);
+    rec.addRmsnorm(T, H, false, eps, B.x.ptr, B.o.ptr, ptr("layers.0.operator_norm"), B.normed.ptr);
+    for (let i = 0; i < this.layers; ++i) {
+      const p = `layers.${i}.`;
+      rec.matmul(B.normed.ptr, w[p + "qkv"], z, T);
+      rec.qkNormRope(T, h, kv, D, this.stride, z, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1, eps, this.theta, D, L.ROPE_POW_NEG);
+      if (kvStore) rec.kvStore(T, kv, D, z, this.stride, h * D, kvStore.at(i * T * 2 * kv * D * 2), 0);
+      rec.attention(T, h, kv, D, z, this.stride, kvA ? kvA(i) : src, src, B.rng.ptr, 1 / Math.sqrt(D), B.y.ptr);
+      rec.matmul(B.y.ptr, w[p + "o_proj"], B.o.ptr, T);
+      rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(p + "ffn_norm"), B.normed.ptr);
+      rec.matmulGlu(B.normed.ptr, w[p + "w13"], B.h.ptr, T, L.ACT_SILU);
+      rec.matmul(B.h.ptr, w[p + "w2"], B.o.ptr, T);
+      const nxt = i + 1 < this.layers ? `layers.${i + 1}.operator_norm` : "final_norm";
+      rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(nxt), B.normed.ptr);
+    }
+  }
+
+  async finish(rec, T) {
+    const got = await rec.finish();
+    this.stats.forwards += 1;
+    this.stats.tokens += T;
+    return got;
+  }
+
+  /** Option scores for every question of every tree: [tree][question][option], plus the raw logits. */
+  async run(trees) {
+    const pk = packForest(trees);
+    if (pk.T === 0) return { scores: trees.map(() => []), logits: new Float32Array(0) };
+    const { T, L, nIds } = pk;
+    this.ensure(T, L, nIds);
+    const B = this.bufs;
+    B.ids.upload(pk.ids);
+    B.pos.upload(pk.pos);
+    B.rng.upload(pk.rng);
+    if (L) {
+      B.leaves.upload(pk.leaves);
+      B.leafIds.upload(pk.leafIds);
+    }
+    const rec = this.ctx.recorder(this.key("run", T, L, nIds));
+    if (!rec.replay) {
+      this.recordLayers(rec, T, B, null, null);
+      if (L && nIds) rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
+    }
+    const oi = L && nIds ? rec.snapshot(B.out.ptr, Float32Array, L * nIds) : -1;
+    const got = await this.finish(rec, T);
+    const out = oi >= 0 ? got[oi] : new Float32Array(0);
+    return { scores: groupMax(out, nIds, trees), logits: out };
+  }
+
+  /** Runs the state alone (causal) and keeps every layer's K/V rows on the device. */
+  async prefill(trunk) {
+    const P = trunk.length;
+    if (P === 0) throw new Error("decision.js: an empty state has nothing to prefill");
+    this.ensure(P);
+    const B = this.bufs;
+    const pos = new Int32Array(P), rng = new Int32Array(P * 4);
+    for (let i = 0; i < P; ++i) {
+      pos[i] = i;
+      rng[4 * i + 1] = i + 1;
+    }
+    B.ids.upload(Uint32Array.from(trunk));
+    B.pos.upload(pos);
+    B.rng.upload(rng);
+    const cache = this.ctx.alloc(this.layers * P * 2 * this.kv * this.D * 2);
+    const rec = this.ctx.recorder(0n); // the cache pointer is new each time: no graph
+    this.recordLayers(rec, P, B, null, cache);
+    await this.finish(rec, P);
+    return new SharedState(P, cache, trunk.slice());
+  }
+
+  /** Scores of each branch continuing a prefilled state (its K/V reused; positions continue after it). */
+  async runShared(state, branches, groups) {
+    const P = state.P;
+    const T = branches.reduce((a, b) => a + b.length, 0);
+    if (T === 0) return branches.map(() => []);
+    const ids = new Uint32Array(T), pos = new Int32Array(T), rng = new Int32Array(T * 4);
+    const leaves = [], leafGroups = [];
+    let off = 0;
+    branches.forEach((br, b) => {
+      const b0 = off;
+      for (let o = 0; o < br.length; ++o, ++off) {
+        ids[off] = br[o];
+        pos[off] = P + o;
+        rng.set([0, P, b0, off + 1], 4 * off);
+      }
+      leaves.push(off - 1);
+      leafGroups.push([].concat(...groups[b]));
+    });
+    const L = leaves.length, nIds = leafGroups.reduce((a, g) => Math.max(a, g.length), 0);
+    const leafIds = new Uint32Array(L * nIds);
+    leafGroups.forEach((g, k) => leafIds.set(g, k * nIds));
+    this.ensure(T, L, nIds);
+    const B = this.bufs;
+    B.ids.upload(ids);
+    B.pos.upload(pos);
+    B.rng.upload(rng);
+    B.leaves.upload(Uint32Array.from(leaves));
+    B.leafIds.upload(leafIds);
+    const width = 2 * this.kv * this.D;
+    const rec = this.ctx.recorder(this.key("shared", state.serial, T, L, nIds));
+    if (!rec.replay) {
+      this.recordLayers(rec, T, B, (i) => kvSrc(state.cache.at(i * P * width * 2), P, width, 0, this.kv * this.D), null);
+      rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
+    }
+    const oi = rec.snapshot(B.out.ptr, Float32Array, L * nIds);
+    const out = (await this.finish(rec, T))[oi];
+    return groupMax(out, nIds, [{ groups }])[0];
+  }
+}
+
+module.exports = { packForest, groupMax, hashKey, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };

@@ -1,0 +1,176 @@
+"""The Node host (decision.js_amd/node/: the Decision API in JavaScript over the N-API binding of the C ABI)
+against the Python host and the oracle. CPU: the binding exports one function per entry point of
+include/dj.h; forest packing, group-max readout, question answers and errors, and pass splitting equal the
+Python host's; loading without a GPU fails with the library's error. GPU: systemOne / probabilities /
+systemOneBatch / shareState through Node give the Python host's probabilities and bit-identical logits (the
+same library, op sequence and packing)."""
+import json
+import os
+import re
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from _pkg import ROOT, load_pkg
+
+NODE = shutil.which("node")
+ADDON = os.path.join(ROOT, "decision.js_amd", "lib", "dj_napi.node")
+pytestmark = pytest.mark.skipif(NODE is None, reason="node is not installed")
+
+
+def node(req, timeout=120):
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "check.js")], input=json.dumps(req),
+                       capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"node failed: {r.stderr}")
+    return json.loads(r.stdout)
+
+
+def camel(name):
+    head, *rest = name.split("_")
+    return head + "".join(p.capitalize() for p in rest)
+
+
+def test_binding_exports_every_entry_point():
+    if not os.path.exists(ADDON):
+        pytest.skip("the Node binding is not built (no Node headers)")
+    header = open(os.path.join(ROOT, "include", "dj.h")).read()
+    fns = sorted(set(re.findall(r"^\w[\w\s\*]*?\b(dj_\w+)\(", header, re.M)))
+    got = set(node({"cmd": "exports"}))
+    missing = [f for f in fns if camel(f[3:]) not in got]
+    assert not missing, f"entry points without a Node binding: {missing}"
+    assert {"recFinishAsync", "W_MFMA", "W_DIRECT", "ABI_VERSION"} <= got
+
+
+def _trees(rng, V=5000):
+    out = []
+    for trunk, branches in [(40, [5, 9, 1]), (0, [7]), (13, []), (1, [1, 1, 30]), (200, [24, 31, 17])]:
+        groups = []
+        for b in range(len(branches)):
+            n = (2, 3, 5)[b % 3]
+            ids = rng.choice(V, size=2 * n, replace=False)
+            groups.append([[int(ids[2 * i])] if i % 2 else [int(ids[2 * i]), int(ids[2 * i + 1])] for i in range(n)])
+        out.append({"trunk": [int(x) for x in rng.integers(0, V, trunk)],
+                    "branches": [[int(x) for x in rng.integers(0, V, b)] for b in branches], "groups": groups})
+    return out
+
+
+def test_packing_and_readout_match_python_host():
+    load_pkg()
+    from decision_js_amd import engine
+    rng = np.random.default_rng(0)
+    trees = _trees(rng)
+    js = node({"cmd": "pack", "trees": trees})
+    py = engine.pack_forest(trees)
+    assert js["T"] == py["T"] and js["L"] == py["L"] and js["nIds"] == py["n_ids"]
+    for k_js, k_py in [("ids", "ids"), ("pos", "pos"), ("rng", "rng"), ("leaves", "leaves"), ("leafIds", "leaf_ids")]:
+        assert np.array_equal(np.asarray(js[k_js]), np.asarray(py[k_py]).reshape(-1)), k_js
+    out = rng.standard_normal(py["L"] * py["n_ids"]).astype(np.float32)
+    got = node({"cmd": "groupmax", "out": [float(x) for x in out], "nIds": py["n_ids"], "trees": trees})
+    assert got == engine.group_max(out, py["n_ids"], trees)
+
+
+def test_questions_match_python_host():
+    load_pkg()
+    from decision_js_amd import questions as Q
+    items = [
+        ({"type": "noul", "instructions": "?"}, [0.7, 0.3]),
+        ({"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}}, [0.2, 0.5, 0.3]),
+        ({"type": "score", "instructions": "?", "criteria": ["lo", "mid", "hi"]}, [0.1, 0.3, 0.6]),
+        ({"type": "choice", "instructions": "?", "criteria": {"a": ""}}, [1.0]),
+        ({"type": "score", "instructions": "?", "criteria": ["x"]}, [1.0]),
+        ({"type": "maybe", "instructions": "?"}, [1.0]),
+        ({"instructions": "?"}, [1.0]),
+        ({"type": "noul", "instructions": "?", "criteria": ["yes", "no"]}, [0.5, 0.5]),
+    ]
+    js = node({"cmd": "answer", "items": items})
+    for (q, p), j in zip(items, js):
+        try:
+            want = Q.answer(Q.check_question(q), p)
+        except Q.QuestionError as e:
+            assert j == {"error": str(e)}
+            continue
+        assert j == want
+
+
+def test_pass_splitting_matches_python_host():
+    load_pkg()
+    from decision_js_amd.d1 import Decision
+    d = Decision.__new__(Decision)
+    for sizes, budget in [([50, 300, 10, 500, 20], 400), ([1000], 10), ([5] * 9, 12), ([], 100)]:
+        d.tokens_per_pass = budget
+        assert node({"cmd": "passes", "sizes": sizes, "budget": budget}) == [list(p) for p in d._passes(sizes)]
+
+
+def test_load_without_gpu_throws_the_library_error(tmp_path):
+    if not os.path.exists(ADDON):
+        pytest.skip("the Node binding is not built (no Node headers)")
+    load_pkg()
+    from decision_js_amd import synth
+    try:
+        import torch
+        if torch.cuda.is_available():
+            pytest.skip("a GPU is present: the no-device path is not reachable")
+    except ImportError:
+        pass
+    mdir = synth.generate(synth.reduced("qwen3-0.6b-q8", layers=1, vocab=512), str(tmp_path / "m"), seed=0)
+    got = node({"cmd": "load", "model": mdir})
+    assert got["error"].startswith("decision.js: no HIP device")
+
+
+@pytest.mark.gpu
+def test_node_decision_matches_python_host(tmp_path):
+    """The same model, state and questions through the Node host and the Python host: identical logits (bit for
+    bit) and probabilities; a malformed question throws the reference's message without wedging the queue;
+    a batch under a token budget reports progress; shareState answers agree."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    from decision_js_amd.engine import DecoderEngine
+    mdir = synth.generate(synth.reduced("qwen3-0.6b-q8", layers=3, vocab=4096), str(tmp_path / "m"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(6)
+    V = 4096
+    ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+    opt = lambda: [int(rng.integers(0, V))]  # noqa: E731
+    qs = {
+        "topic": {"type": "choice", "instructions": "?", "criteria": {"billing": "", "delivery": "", "bug": ""},
+                  "ids": ids(30), "options": [opt(), opt(), opt() + opt()]},
+        "churn": {"type": "noul", "instructions": "?", "ids": ids(20), "options": [opt() + opt(), opt()]},
+        "urgency": {"type": "score", "instructions": "?", "criteria": ["1", "2", "3", "4", "5"], "ids": ids(25),
+                    "options": [opt() for _ in range(5)]},
+    }
+    state = ids(200)
+    batch = [[ids(n), qs] for n in (50, 300, 10)]
+    trees = [{"trunk": state, "branches": [q["ids"] for q in qs.values()], "groups": [q["options"] for q in qs.values()]}]
+    js = node({"cmd": "decide", "model": mdir, "state": state, "questions": qs, "batch": batch, "budget": 400,
+               "shared": True, "trees": trees}, timeout=300)
+    d = Decision.load(mdir)
+    try:
+        py_one = d.system_one(state, qs)
+        py_probs = d.probabilities(state, list(qs.values()))
+        d.tokens_per_pass = 400
+        py_batch = d.system_one_batch([tuple(b) for b in batch])
+    finally:
+        d.destroy()
+    eng = DecoderEngine.load(mdir)
+    try:
+        py_logits = eng.run(trees)["logits"]
+    finally:
+        eng.destroy()
+    assert np.array_equal(np.asarray(js["logits"], dtype=np.float32), py_logits)
+    for a, b in zip(js["probs"], py_probs):
+        assert np.allclose(a, b, rtol=0, atol=1e-12)
+    assert js["one"]["usage"] == py_one["usage"] == {"input_tokens": 275, "output_tokens": 0}
+    assert js["one"]["answers"]["topic"]["choice"] == py_one["answers"]["topic"]["choice"]
+    assert abs(js["one"]["answers"]["churn"]["noul"] - py_one["answers"]["churn"]["noul"]) < 1e-12
+    assert js["again"] == js["one"] and js["afterError"] == js["one"]
+    assert js["badError"] == "decision.js: a choice needs criteria {name: description} with at least two options"
+    assert js["progress"][-1] == [3, 3] and len(js["progress"]) >= 2
+    for a, b in zip(js["batch"], py_batch):
+        assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-12
+    for n in qs:
+        key = "noul" if n == "churn" else "confidence"
+        assert abs(js["shared"]["answers"][n][key] - js["one"]["answers"][n][key]) < 5e-4
+    assert js["shared2"] == js["shared"]
