@@ -65,12 +65,12 @@ def make_tickets(n, V, seq_len=384, seed=1, answer_seed=3, sizes=(2, 3, 5)):
     return tickets
 
 
-def model_flops_bytes(c, T, seqs_len):
+def model_flops_bytes(c, T, seqs_len, causal=True):
     """Appendix-B algorithmic work of one forward: 2 T sum(N K) over the linears plus 4 D h (allowed
     query-key pairs) per layer; bytes = quantized linear weights + gathered embedding rows."""
     H, I, h, kv, D, L = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["layers"]
     nk = (h + 2 * kv) * D * H + H * h * D + 2 * I * H + H * I
-    pairs = sum(n * (n + 1) // 2 for n in seqs_len)
+    pairs = sum(n * (n + 1) // 2 if causal else n * n for n in seqs_len)
     flops = 2 * T * nk * L + 4 * D * h * pairs * L
     qbytes = 1.0625 if c.get("bits", 8) == 8 else 0.5625
     return flops, nk * L * qbytes + T * H * qbytes
@@ -138,8 +138,177 @@ def cpu_baseline(model_dir, ticket, budget_s):
         if el > budget_s or done >= 3:
             break
     return {"value": round(3 * done / el, 4), "unit": "decisions/s", "cores": int(cores), "kind": "port",
-            "sample": f"{done} ticket(s) of the same workload (3 x 384 tokens, all {model.c['layers']} layers) through "
+            "sample": f"{done} ticket(s) of the same workload ({len(ticket)} x {len(ticket[0]['branches'][0])} tokens, all {model.c['layers']} layers) through "
                       f"oracle/ref.decoder_forward (numpy f32, CPU restatement of the reference path); {el:.1f} s"}
+
+
+def _line(metric, value, unit, steps, warmup, ms, dtype, workload, roofline, extra=None):
+    out = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+           "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
+           "data": "synthetic", "config": {"workload": workload}, "roofline": roofline, "cpu_baseline": None}
+    out.update(extra or {})
+    return out
+
+
+def _forward_fraction(cfg, T, seqs, ms, causal=True):
+    """Appendix-B roofline of a forward: achieved TFLOP/s (and weight GB/s) over the measured time."""
+    flops, wbytes = model_flops_bytes(cfg, T, seqs, causal)
+    t_mfma, t_hbm = flops / (MFMA_F16_PEAK_TFLOPS * 1e12), wbytes / (HBM_PEAK_GBS * 1e9)
+    s = ms * 1e-3
+    if t_mfma >= t_hbm:
+        a = flops / s / 1e12
+        return {"bound": "mfma", "achieved": round(a, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(a / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None, "scope": "whole forward (Appendix B flops)"}
+    a = wbytes / s / 1e9
+    return {"bound": "hbm", "achieved": round(a, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(a / HBM_PEAK_GBS, 4),
+            "traffic": None, "scope": "whole forward (quantized weight bytes)"}
+
+
+def run_workload(args):
+    """The BASELINE configs other than the metric's, one JSON line each (not the driver's bench line):
+    batch   configs[3]: 192 sequences of U[128, 768] random ids (lengths seed 2) on the 0.6B q8 decoder, packed
+            varlen into one forward; a step is that forward (192 decisions)
+    shared  configs[4]: a 1024-id state prefilled once (K/V kept) and 8 questions of 32 ids against it on the
+            ~0.8B q8 decoder; a step is prefill + 8 questions (8 decisions); also one question alone
+    encoder configs[0]: 11 texts (1 x 256, 3 x 24, 7 x 8 ids) embedded in one forward of the EG2-shaped encoder,
+            every question scoring all 7 options by cosine; a step is one ticket (3 decisions)"""
+    from decision_js_amd import synth
+    from decision_js_amd.engine import DecoderEngine
+    steps, warmup = args.steps, args.warmup
+    if args.workload == "batch":
+        cfg = synth.CONFIGS["qwen3-0.6b-q8"]
+        mdir = os.path.join(args.model_dir, "qwen3-0.6b-q8")
+        synth.generate(cfg, mdir, seed=0, threads=16)
+        eng = DecoderEngine.load(mdir, {"graphs": not args.no_graphs})
+        lens_rng = np.random.Generator(np.random.PCG64(2))
+        ids_rng = np.random.Generator(np.random.PCG64(1))
+        ans_rng = np.random.Generator(np.random.PCG64(3))
+        V = cfg["vocab"]
+        lens = [int(x) for x in lens_rng.integers(128, 769, 192)]
+        trees = [{"trunk": [], "branches": [[int(x) for x in ids_rng.integers(0, V, n)]],
+                  "groups": [[[int(a)] for a in ans_rng.choice(V, size=(2, 3, 5)[k % 3], replace=False)]]} for k, n in enumerate(lens)]
+        st = eng.stage(trees)
+        T = sum(lens)
+        log(f"batch: 192 sequences, T = {T}")
+        for _ in range(warmup):
+            eng.run_staged(st)
+        eng.ctx.timer_begin()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            eng.run_staged(st)
+        wall = time.perf_counter() - t0
+        gpu_ms = eng.ctx.timer_end() / steps
+        ms = 1e3 * wall / steps
+        roof = _forward_fraction(cfg, T, lens, gpu_ms)
+        eng.graphs = False
+        eng.ctx.profile_reset()
+        eng.ctx.profile(True)
+        eng.run_staged(st)
+        eng.ctx.profile(False)
+        table = eng.ctx.profile_table()
+        eng.graphs = not args.no_graphs
+        total = sum(v[0] for v in table.values())
+        for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:8]:
+            log(f"  {k:48s} {kms:8.3f} ms/forward  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:8.1f} us each)")
+        gemm_ms = sum(v[0] for k, v in table.items() if k.startswith("matmul"))
+        gemm_flops = 2.0 * T * sum(n * k for n, k in _linear_shapes(cfg)) * cfg["layers"]
+        roof["gemm_tflops"] = round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1)
+        roof["gemm_frac"] = round(roof["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+        log(f"forward {gpu_ms:.2f} ms (GPU), {192 * steps / wall:.1f} decisions/s; GEMMs {roof['gemm_tflops']} TFLOP/s "
+            f"({100 * roof['gemm_frac']:.1f}% of dense f16 peak)")
+        out = _line("decisions/sec (config-4 batch: 192 sequences, one varlen forward) on 1 MI355X", 192 * steps / wall,
+                    "decisions/s", steps, warmup, ms, "f16",
+                    f"configs[3]: qwen3-0.6b-q8, 192 sequences of U[128,768] random ids (T={T}) in one forward", roof,
+                    {"gpu_ms_per_step": round(gpu_ms, 3)})
+        eng.free_staged(st)
+        eng.destroy()
+    elif args.workload == "shared":
+        cfg = synth.CONFIGS["d3lite-0.8b-q8"]
+        mdir = os.path.join(args.model_dir, "d3lite-0.8b-q8")
+        synth.generate(cfg, mdir, seed=0, threads=16)
+        eng = DecoderEngine.load(mdir, {"graphs": not args.no_graphs})
+        ids_rng = np.random.Generator(np.random.PCG64(1))
+        ans_rng = np.random.Generator(np.random.PCG64(3))
+        V = cfg["vocab"]
+        state = [int(x) for x in ids_rng.integers(0, V, 1024)]
+        branches = [[int(x) for x in ids_rng.integers(0, V, 32)] for _ in range(8)]
+        groups = [[[int(a)] for a in ans_rng.choice(V, size=(2, 3, 5)[k % 3], replace=False)] for k in range(8)]
+
+        def unit():
+            stt = eng.prefill(state)
+            eng.run_shared(stt, branches, groups)
+            stt.free()
+
+        for _ in range(warmup):
+            unit()
+        eng.ctx.timer_begin()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            unit()
+        wall = time.perf_counter() - t0
+        gpu_ms = eng.ctx.timer_end() / steps
+        ms = 1e3 * wall / steps
+        # one question alone against a kept state: the weight-streaming (GEMV) regime
+        stt = eng.prefill(state)
+        for _ in range(warmup):
+            eng.run_shared(stt, branches[:1], groups[:1])
+        eng.ctx.timer_begin()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            eng.run_shared(stt, branches[:1], groups[:1])
+        q_wall = (time.perf_counter() - t1) / steps
+        q_gpu = eng.ctx.timer_end() / steps
+        stt.free()
+        roof = _forward_fraction(cfg, 1024 + 256, [1024] + [32] * 8, gpu_ms)
+        q_roof = _forward_fraction(cfg, 32, [32], q_gpu)
+        log(f"shared: prefill 1024 + 8 x 32 questions {gpu_ms:.3f} ms (GPU); one question alone {q_gpu:.3f} ms "
+            f"({q_roof['achieved']} {q_roof['unit']}, {100 * q_roof['frac']:.1f}% of peak)")
+        out = _line("decisions/sec (config-5: prefill 1024-token state + 8 questions x 32 tokens) on 1 MI355X", 8 * steps / wall,
+                    "decisions/s", steps, warmup, ms, "f16",
+                    "configs[4]: d3lite-0.8b-q8 (20 layers), 1024-id state prefilled once, 8 questions of 32 ids on its kept K/V",
+                    roof, {"gpu_ms_per_step": round(gpu_ms, 3), "question_alone_ms": round(1e3 * q_wall, 4),
+                           "question_alone_gpu_ms": round(q_gpu, 4), "question_alone_roofline": q_roof})
+        eng.destroy()
+    else:
+        from decision_js_amd.encoder import EncoderEngine, cosine_logits
+        cfg = synth.CONFIGS["eg2-encoder-q8"]
+        mdir = os.path.join(args.model_dir, "eg2-encoder-q8")
+        synth.generate(cfg, mdir, seed=0, threads=16)
+        eng = EncoderEngine.load(mdir, {"graphs": not args.no_graphs})
+        ids_rng = np.random.Generator(np.random.PCG64(1))
+        V = cfg["vocab"]
+        lens = [256] + [24] * 3 + [8] * 7
+        tickets = [[[int(x) for x in ids_rng.integers(0, V, n)] for n in lens] for _ in range(warmup + steps)]
+
+        def unit(texts):
+            e = eng.embed(texts)["embeddings"]
+            for q in range(3):
+                cosine_logits(e[0], e[1 + q], e[4:])
+
+        for t in tickets[:warmup]:
+            unit(t)
+        eng.ctx.timer_begin()
+        t0 = time.perf_counter()
+        for t in tickets[warmup:]:
+            unit(t)
+        wall = time.perf_counter() - t0
+        gpu_ms = eng.ctx.timer_end() / steps
+        ms = 1e3 * wall / steps
+        T = sum(lens)
+        roof = _forward_fraction(cfg, T, lens, gpu_ms, causal=False)
+        log(f"encoder: ticket of 11 texts (T={T}) {ms:.3f} ms wall, {gpu_ms:.3f} ms GPU")
+        out = _line("decisions/sec (config-1 encoder tickets: 11 texts, 3 questions x 7 options) on 1 MI355X", 3 * steps / wall,
+                    "decisions/s", steps, warmup, ms, "f16",
+                    "configs[0]: eg2-encoder-q8 (24 layers), 1 x 256 + 3 x 24 + 7 x 8 random ids embedded in one forward, cosine over 7 options",
+                    roof, {"gpu_ms_per_step": round(gpu_ms, 4)})
+        eng.destroy()
+    print(json.dumps(out), flush=True)
+
+
+def _linear_shapes(c):
+    """(N, K) of one decoder layer's linears: qkv, o_proj, w13, w2."""
+    H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
+    return [((h + 2 * kv) * D, H), (H, h * D), (2 * I, H), (H, I)]
 
 
 def main():
@@ -154,6 +323,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calib-mb", type=int, default=0, help="also run a plain device copy of this many MiB (counter calibration)")
+    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder"],
+                    help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
+                         "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
+    ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the path shards by "
@@ -163,6 +336,8 @@ def main():
     pkg = load_pkg()
     from decision_js_amd import synth
     from decision_js_amd.engine import DecoderEngine
+    if args.workload != "ticket":
+        return run_workload(args)
 
     cfg = synth.CONFIGS[args.config]
     mdir = os.path.join(args.model_dir, args.config)
@@ -173,7 +348,7 @@ def main():
     log(f"device {eng.ctx.info()}; weights on device")
 
     n = args.warmup + args.steps
-    tickets = make_tickets(n, cfg["vocab"])
+    tickets = make_tickets(n, cfg["vocab"], seq_len=args.seq_len)
     staged = [eng.stage(t) for t in tickets]
     T = sum(len(b) for tr in tickets[0] for b in tr["branches"])
 
@@ -218,7 +393,7 @@ def main():
                     "launch_ms": round(k_ms, 5), "launch_ms_events": round(ev_ms, 5), "flops_per_launch": fl}
             log(f"dominant kernel {name}: {1e3 * k_ms:.2f} us per launch alone (graph of 50), {1e3 * ev_ms:.2f} us "
                 f"between per-op events; {achieved:.0f} TFLOP/s")
-    flops, wbytes = model_flops_bytes(cfg, T, [384, 384, 384])
+    flops, wbytes = model_flops_bytes(cfg, T, [args.seq_len] * 3)
     t_roof_ms = max(flops / (MFMA_F16_PEAK_TFLOPS * 1e12), wbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     if args.calib_mb:
         src, dst = eng.ctx.alloc(args.calib_mb << 20), eng.ctx.alloc(args.calib_mb << 20)
@@ -246,8 +421,9 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "p50_ms_per_ticket": round(p50, 4),
         "gpu_ms_per_ticket": round(gpu_ms / args.steps, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-        "config": {"workload": f"configs[1]: {args.config} causal decoder, seeded N(0,0.02) weights; ticket = 3 questions x 384 random-id "
-                               "tokens packed in one forward (T=1152), answer sets of 2/3/5 ids at each last token",
+        "config": {"workload": f"{'configs[1]' if args.config == 'qwen3-0.6b-q8' and args.seq_len == 384 else 'configs[2]' if args.config == 'qwen2.5-3b-q4' else 'custom'}: "
+                               f"{args.config} causal decoder, seeded N(0,0.02) weights; ticket = 3 questions x {args.seq_len} random-id "
+                               f"tokens packed in one forward (T={3 * args.seq_len}), answer sets of 2/3/5 ids at each last token",
                    "tokens_per_ticket": T, "graphs": not args.no_graphs},
         "roofline": roof,
         "forward_roofline": {"t_roof_ms": round(t_roof_ms, 4), "frac_of_roofline": round(t_roof_ms / (gpu_ms / args.steps), 4),
