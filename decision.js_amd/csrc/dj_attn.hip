@@ -15,6 +15,7 @@
 //                                each 32-key MFMA step is permuted to match, and V^T is read to match)
 // Scores, the running max (m0 = -1e30) and the row sums are f32; the output is f16(acc / l), as the reference.
 #include <math.h>
+#include <algorithm>
 #include <stdio.h>
 #include "dj_internal.h"
 
@@ -42,7 +43,7 @@ struct AttnShape {
 template <int D, int RING>
 __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
-                                              uint16_t *__restrict__ O) {
+                                              uint16_t *__restrict__ O, int splits, float *__restrict__ part) {
   using S = AttnShape<D, RING>;
   constexpr int NS_ = D / 32;  // MFMA k-steps over the head dim
   constexpr int NDB = D / 16;  // 16-row blocks of O^T
@@ -101,6 +102,10 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
   }
   const int ntA = hiA > loA ? (hiA - loA + 63) / 64 : 0, ntB = hiB > loB ? (hiB - loB + 63) / 64 : 0;
   const int ntiles = ntA + ntB;
+  // split-KV (grid z = splits, small grids): this workgroup takes tiles [j0, j1) of the block's sequence
+  const int split = blockIdx.z;
+  const int j0 = (int)((long)ntiles * split / splits), j1 = (int)((long)ntiles * (split + 1) / splits);
+  const int nloc = j1 - j0;
 
   // Per-lane DMA source offsets inside a tile: 1 KB DMA q of this wave covers LDS bytes [q KB, q KB + 1 KB) of
   // the K (or V) tile; lane L fills 16 bytes at key row r, physical chunk p, i.e. logical chunk p ^ swizzle(r).
@@ -135,9 +140,9 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
       dma16(vb + row + vch[i] * 8, st + TILE + (wv * S::IK + i) * 1024);
     }
   };
-  if (ntiles > 0) {
+  if (nloc > 0) {
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue(min(p, ntiles - 1), p);  // a short range re-loads its last tile
+    for (int p = 0; p < NS - 1; ++p) issue(j0 + min(p, nloc - 1), p);  // a short range re-loads its last tile
   }
 
   f4 o[NDB];
@@ -146,13 +151,14 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
   float m = -1e30f, lsum = 0.f;  // running max in log2 units of the scaled scores
   const float sl = scale * LOG2E;
 
-  for (int j = 0; j < ntiles; ++j) {
-    // tile j landed for this wave once at most the NS-2 later tiles' DMAs remain; after the barrier for every
-    // wave, and every wave is done with tile j-1's stage, which is refilled next
+  for (int jj = 0; jj < nloc; ++jj) {
+    // tile jj landed for this wave once at most the NS-2 later tiles' DMAs remain; after the barrier for every
+    // wave, and every wave is done with tile jj-1's stage, which is refilled next
     wait_vm_barrier<(NS - 2) * S::I>();
-    issue(min(j + NS - 1, ntiles - 1), (j + NS - 1) % NS);
+    issue(j0 + min(jj + NS - 1, nloc - 1), (jj + NS - 1) % NS);
+    const int j = j0 + jj;
 
-    const uint8_t *st = smem + (j % NS) * STAGE;
+    const uint8_t *st = smem + (jj % NS) * STAGE;
     const u32x4 *Ks = (const u32x4 *)st;
     const bool sb = j >= ntA;
     const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64, hi = sb ? hiB : hiA;
@@ -242,6 +248,21 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
 
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+  if (splits > 1) {
+    // partial of this split: unnormalized f32 O^T and (m, l) per query and head, merged by k_attn_combine
+    if (qi < T) {
+      const size_t row = ((size_t)split * T + qi) * heads + h;
+      float *po = part + row * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) *(f4 *)(po + 16 * db + 4 * g) = o[db];
+      if (g == 0) {
+        float *pml = part + (size_t)splits * T * heads * D + row * 2;
+        pml[0] = m;
+        pml[1] = lsum;
+      }
+    }
+    return;
+  }
   if (qi < T) {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     uint16_t *orow = O + (size_t)qi * heads * D + (size_t)h * D;
@@ -255,18 +276,61 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
   }
 }
 
-int dj_launch_attention(hipStream_t s, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
+// Merge of the split-KV partials of one (query, head): M = max m_s, L = sum l_s 2^(m_s - M),
+// O = sum O_s 2^(m_s - M) / L, in split order (deterministic). A split that saw no key has l = 0.
+__global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int D, int splits, const float *__restrict__ part,
+                                                      uint16_t *__restrict__ O) {
+  const int q = blockIdx.x, h = blockIdx.y;
+  const float *ml = part + (size_t)splits * T * heads * D;
+  float M = -1e30f;
+  for (int s = 0; s < splits; ++s) {
+    const float *e = ml + (((size_t)s * T + q) * heads + h) * 2;
+    if (e[1] > 0.f) M = fmaxf(M, e[0]);
+  }
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float L = 0.f, acc = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const size_t row = ((size_t)s * T + q) * heads + h;
+      const float l = ml[row * 2 + 1];
+      if (l > 0.f) {
+        const float w = __builtin_amdgcn_exp2f(ml[row * 2] - M);
+        L += l * w;
+        acc += part[row * D + d] * w;
+      }
+    }
+    O[((size_t)q * heads + h) * D + d] = __builtin_bit_cast(uint16_t, (_Float16)(L > 0.f ? acc / L : 0.f));
+  }
+}
+
+int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O) {
-  dim3 grid(dj_cdiv(T, 64), heads);
+  hipStream_t s = c->stream;
+  const int qblocks = dj_cdiv(T, 64);
+  const long grid = (long)qblocks * heads;
   const int4 *r4 = (const int4 *)rng;
+  // Small grids (a short question against a long state: one query block per head) split each block's key
+  // tiles over up to 16 workgroups, partials in the context's workspace (free between kernels of the
+  // stream), merged by k_attn_combine. Large grids run whole.
+  int splits = 1;
+  float *part = nullptr;
+  if (grid < c->cus) {
+    const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
+    splits = (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * c->cus, grid));
+    while (splits > 1 && (size_t)splits * T * heads * (D + 2) > c->gemm_ws_floats) --splits;
+    if (splits > 1) part = c->gemm_ws;
+    else splits = 1;
+    if (!part) splits = 1;
+  }
+  const dim3 g3(qblocks, heads, splits);
   // two-stage ring: two workgroups fit per CU and hide each other's latency. Measured on MI355X (D 128,
   // causal): 13.6 vs 18.0 us with a 4-stage ring (one workgroup per CU) at T = 1152, 504 vs 719 us at 86016
   switch (D) {
-    case 64: k_attn<64, 2><<<grid, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O); break;
-    case 128: k_attn<128, 2><<<grid, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O); break;
-    case 256: k_attn<256, 2><<<grid, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O); break;
+    case 64: k_attn<64, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
+    case 128: k_attn<128, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
+    case 256: k_attn<256, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
     default: return dj_fail(DJ_EINVAL, "decision.js: attention head dim %d (64, 128 or 256)", D);
   }
+  if (splits > 1) k_attn_combine<<<dim3(T, heads), 128, 0, s>>>(T, heads, D, splits, part, O);
   return DJ_OK;
 }
 
@@ -284,7 +348,7 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_OP_BEGIN(rec, "attention");
   if (T > 0) {
-    int st = dj_launch_attention(rec->ctx->stream, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O);
+    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O);
     if (st) return st;
   }
   char shape[48];

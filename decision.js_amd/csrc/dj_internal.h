@@ -110,7 +110,7 @@ int dj_op_end(dj_rec *rec, const char *name, const char *detail = nullptr);
 int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
                    const char **name, int *splits);
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
-int dj_launch_attention(hipStream_t s, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
+int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
                         dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, uint16_t *O);
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);
 
