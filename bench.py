@@ -314,7 +314,7 @@ def _linear_shapes(c):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="qwen3-0.6b-q8")
     ap.add_argument("--model-dir", default=os.environ.get("DJ_MODEL_DIR", "/tmp/dj_models"))

@@ -7,8 +7,10 @@
 // trunk + branch ranges of attention256 (d3-kernels.ts:207-223), and a kept prefix KV (source A = the
 // cache) in the shared-state mode.
 //
-// A workgroup takes 64 queries of one head (4 waves x 16). K/V tiles of 64 keys of the block's union range
-// are staged in LDS: K row-major (XOR-swizzled 16-byte chunks), V transposed. Per wave and tile:
+// A workgroup takes 64 queries of one head (4 waves x 16; with KG = 2 key groups, 8 waves, each group scoring
+// one half of every key tile with its own running max and sum, merged through LDS at the end). K/V tiles of
+// 64 keys of the block's union range are staged in LDS: K row-major (XOR-swizzled 16-byte chunks), V
+// transposed. Per wave and tile:
 //   S^T[key, q] = K . Q^T       (A = K from LDS, B = Q held in registers; the accumulator puts query
 //                                l % 16 in lane l, so the softmax row reduction is 2 shuffles)
 //   O^T[d, q]  += V^T . P^T     (P^T is the S^T accumulator itself, rounded to f16; the key order inside
@@ -17,6 +19,7 @@
 #include <math.h>
 #include <algorithm>
 #include <stdio.h>
+#include <stdlib.h>
 #include "dj_internal.h"
 
 #define MFMA16(a, b, c) __builtin_amdgcn_mfma_f32_16x16x32_f16((a), (b), (c), 0, 0, 0)
@@ -26,7 +29,7 @@ typedef short s4 __attribute__((ext_vector_type(4)));
 // 16-byte chunks XOR-swizzled per row. K: chunk c of key r at c ^ (r & KSW) (conflict-free 16-byte MFMA reads of
 // 16 keys x one chunk). V: chunk c at c ^ vswz(r), chosen so the transposing reads below (4 keys x 2 chunks per
 // 16 lanes) hit distinct banks.
-template <int D, int RING>
+template <int D, int RING, int KG>
 struct AttnShape {
   static constexpr int CH = D / 8;                              // 16-byte chunks per key row
   static constexpr int KSW = CH >= 16 ? 15 : 7;
@@ -34,17 +37,21 @@ struct AttnShape {
   static constexpr int STAGE = 2 * TILE;
   // ring depth: RING, or 0 = 4 stages where they fit in 128 KB, else 2
   static constexpr int NS = RING ? RING : 4 * STAGE <= 128 * 1024 ? 4 : 2;
-  static constexpr int IK = TILE / 1024 / 4;                    // 1 KB DMAs per wave per tile, K (and V)
+  static constexpr int IK = TILE / 1024 / (4 * KG);             // 1 KB DMAs per wave per tile, K (and V)
+  static_assert(TILE % (1024 * 4 * KG) == 0, "a tile must split into whole 1 KB DMAs per wave");
   static constexpr int I = 2 * IK;                              // vector-memory ops per wave per tile
   static_assert((NS - 2) * I < 64, "vmcnt range");
   __device__ static int vswz(int r) { return D >= 128 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); }
 };
 
-template <int D, int RING>
-__global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
+template <int D, int RING, int KG>
+__global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
                                               uint16_t *__restrict__ O, int splits, float *__restrict__ part) {
-  using S = AttnShape<D, RING>;
+  using S = AttnShape<D, RING, KG>;
+  constexpr int KW = 64 / KG;          // keys of each tile this wave scores (KG key groups split a tile)
+  constexpr int NB = KW / 16;          // 16-key blocks of S^T per wave and tile
+  constexpr int NT = KW / 32;          // 32-key MFMA steps of P V per wave and tile
   constexpr int NS_ = D / 32;  // MFMA k-steps over the head dim
   constexpr int NDB = D / 16;  // 16-row blocks of O^T
   constexpr int CH = S::CH, KSW = S::KSW, TILE = S::TILE, STAGE = S::STAGE, NS = S::NS;
@@ -53,11 +60,12 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
+  const int kg = KG > 1 ? wave >> 2 : 0, wq = wave & 3;  // key group; which 16 queries of the block
   const int h = blockIdx.y, q0 = blockIdx.x * 64;
   const int kvh = h / (heads / kv);
 
   // Q fragments first: nothing below depends on them until the first MFMA
-  const int qi = q0 + wave * 16 + c16;
+  const int qi = q0 + wq * 16 + c16;
   const int qc = min(qi, T - 1);
   h8 qf[NS_];
 #pragma unroll
@@ -70,7 +78,7 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
   int blo[2] = {lv && rl.x < rl.y ? rl.x : INT_MAX, lv && rl.z < rl.w ? rl.z : INT_MAX};
   int bhi[2] = {lv && rl.x < rl.y ? rl.y : INT_MIN, lv && rl.z < rl.w ? rl.w : INT_MIN};
   // this lane's query ranges, and the wave's own span (a tile outside it is skipped by the wave)
-  const int src_lane = wave * 16 + c16;
+  const int src_lane = wq * 16 + c16;
   const int4 rq = {__shfl(rl.x, src_lane, 64), __shfl(rl.y, src_lane, 64), __shfl(rl.z, src_lane, 64),
                    __shfl(rl.w, src_lane, 64)};
   int wlo[2] = {qi < T && rq.x < rq.y ? rq.x : INT_MAX, qi < T && rq.z < rq.w ? rq.z : INT_MAX};
@@ -163,40 +171,41 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
     const bool sb = j >= ntA;
     const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64, hi = sb ? hiB : hiA;
     const int qlo = sb ? rq.z : rq.x, qhi = sb ? rq.w : rq.y;
-    if (k0 < whi[sb] && k0 + 64 > wlo[sb]) {
+    const int kb0 = k0 + KW * kg;  // this wave's keys of the tile: [kb0, kb0 + KW)
+    if (kb0 < whi[sb] && kb0 + KW > wlo[sb]) {
       // S^T[key, q] = K . Q^T: A = 16 keys x 32 dims of K, B = the query fragment
-      f4 sc[4];
+      f4 sc[NB];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        sc[b] = (f4){0.f, 0.f, 0.f, 0.f};
-        const int r = 16 * b + c16;
+      for (int bb = 0; bb < NB; ++bb) {
+        sc[bb] = (f4){0.f, 0.f, 0.f, 0.f};
+        const int r = 16 * (NB * kg + bb) + c16;
 #pragma unroll
         for (int s = 0; s < NS_; ++s) {
           const h8 kf = __builtin_bit_cast(h8, Ks[r * CH + ((4 * s + g) ^ (r & KSW))]);
-          sc[b] = MFMA16(kf, qf[s], sc[b]);
+          sc[bb] = MFMA16(kf, qf[s], sc[bb]);
         }
       }
       // Tiles that every query of the wave sees whole (all but the diagonal ones of a causal block) skip the
       // per-key mask.
-      const bool whole = k0 >= wl2[sb] && k0 + 64 <= wh2[sb] && k0 + 64 <= hi;
+      const bool whole = kb0 >= wl2[sb] && kb0 + KW <= wh2[sb] && kb0 + KW <= hi;
       float tmax = -INFINITY;
       if (whole) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            sc[b][r] *= sl;
-            tmax = fmaxf(tmax, sc[b][r]);
+            sc[bb][r] *= sl;
+            tmax = fmaxf(tmax, sc[bb][r]);
           }
       } else {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int kk = k0 + 16 * b + 4 * g + r;
+            const int kk = kb0 + 16 * bb + 4 * g + r;
             const bool ok = kk >= qlo && kk < qhi && kk < hi;
-            const float v = ok ? sc[b][r] * sl : -INFINITY;
-            sc[b][r] = v;
+            const float v = ok ? sc[bb][r] * sl : -INFINITY;
+            sc[bb][r] = v;
             tmax = fmaxf(tmax, v);
           }
       }
@@ -214,14 +223,14 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
         m = mn;
       }
       float ps = 0.f;
-      h8 pf[2];
+      h8 pf[NT];
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
+      for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(sc[b][r] - m);  // exp2(-inf) = 0 for masked keys
+          const float p = __builtin_amdgcn_exp2f(sc[bb][r] - m);  // exp2(-inf) = 0 for masked keys
           ps += p;
-          pf[b >> 1][(b & 1) * 4 + r] = (_Float16)p;
+          pf[bb >> 1][(bb & 1) * 4 + r] = (_Float16)p;
         }
       lsum += ps;
       // O^T[d, q] += V^T . P^T. A = V^T (16 dims x keys {32t + 4g + 0..3, 32t + 16 + 4g + 0..3}, the key order
@@ -229,7 +238,8 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
       // at key 32t + 4g + i/4, dims 16db + 4(i%4)..+3, and receives dim 16db + i of keys 32t + 4g + 0..3.
       const uint8_t *vt = st + TILE;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int tt = 0; tt < NT; ++tt) {
+        const int t = NT * kg + tt;
         const int key = 32 * t + 4 * g + (c16 >> 2);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
@@ -239,12 +249,35 @@ __global__ __launch_bounds__(256) void k_attn(int T, int heads, int kv, const ui
           const h4 lo = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p0));
           const h4 hi4 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p1));
           const h8 vf = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          o[db] = MFMA16(vf, pf[t], o[db]);
+          o[db] = MFMA16(vf, pf[tt], o[db]);
         }
       }
     }
   }
   wait_vm<0>();  // the clamped tail DMAs land before the wave ends
+
+  if constexpr (KG > 1) {
+    // key group 1 hands its (m, l, O) to group 0 through LDS (the ring is free: every DMA has landed and every
+    // wave is past its last read), which merges them: M = max, both rescaled to it
+    f4 *xo = (f4 *)smem;
+    float *xml = (float *)(smem + 4 * NDB * 64 * sizeof(f4));
+    __syncthreads();
+    if (kg == 1) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) xo[(wq * NDB + db) * 64 + lane] = o[db];
+      xml[(wq * 64 + lane) * 2] = m;
+      xml[(wq * 64 + lane) * 2 + 1] = lsum;
+    }
+    __syncthreads();
+    if (kg == 1) return;
+    const float m1 = xml[(wq * 64 + lane) * 2], l1 = xml[(wq * 64 + lane) * 2 + 1];
+    const float mm = fmaxf(m, m1);
+    const float c0 = __builtin_amdgcn_exp2f(m - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = o[db] * c0 + xo[(wq * NDB + db) * 64 + lane] * c1;
+    lsum = lsum * c0 + l1 * c1;
+    m = mm;
+  }
 
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
@@ -311,25 +344,38 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
   // Small grids (a short question against a long state: one query block per head) split each block's key
   // tiles over up to 16 workgroups, partials in the context's workspace (free between kernels of the
   // stream), merged by k_attn_combine. Large grids run whole.
+  // DJ_ATTN_SPLITS=<n> forces the split count (tuning sweeps)
   int splits = 1;
   float *part = nullptr;
-  if (grid < c->cus) {
+  const char *force = getenv("DJ_ATTN_SPLITS");
+  if (force || grid < c->cus) {
     const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
-    splits = (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * c->cus, grid));
+    splits = force ? atoi(force) : (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * c->cus, grid));
+    splits = std::max(1, std::min(splits, 64));
     while (splits > 1 && (size_t)splits * T * heads * (D + 2) > c->gemm_ws_floats) --splits;
-    if (splits > 1) part = c->gemm_ws;
+    if (splits > 1 && c->gemm_ws) part = c->gemm_ws;
     else splits = 1;
-    if (!part) splits = 1;
   }
   const dim3 g3(qblocks, heads, splits);
   // two-stage ring: two workgroups fit per CU and hide each other's latency. Measured on MI355X (D 128,
   // causal): 13.6 vs 18.0 us with a 4-stage ring (one workgroup per CU) at T = 1152, 504 vs 719 us at 86016
+  // key groups per workgroup: two (8 waves, each scoring half of every key tile, merged in LDS) for D 256,
+  // where they measured 35.1 vs 37.6 us (2 x 1024 causal, 8 heads); one below (D 128: 30.3 vs 32.7 us at
+  // 1 x 1152, 42.5 vs 46.8 at 16 x 384). DJ_ATTN_KG=1|2 forces it (tuning sweeps).
+  const char *kgs = getenv("DJ_ATTN_KG");
+  const int kg = kgs ? atoi(kgs) : D >= 256 ? 2 : 1;
+#define DJ_ATTN_CASE(DD)                                                                                              \
+  case DD:                                                                                                            \
+    if (kg == 1) k_attn<DD, 2, 1><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);    \
+    else k_attn<DD, 2, 2><<<g3, 512, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);            \
+    break;
   switch (D) {
-    case 64: k_attn<64, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
-    case 128: k_attn<128, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
-    case 256: k_attn<256, 2><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); break;
+    DJ_ATTN_CASE(64)
+    DJ_ATTN_CASE(128)
+    DJ_ATTN_CASE(256)
     default: return dj_fail(DJ_EINVAL, "decision.js: attention head dim %d (64, 128 or 256)", D);
   }
+#undef DJ_ATTN_CASE
   if (splits > 1) k_attn_combine<<<dim3(T, heads), 128, 0, s>>>(T, heads, D, splits, part, O);
   return DJ_OK;
 }

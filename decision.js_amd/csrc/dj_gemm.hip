@@ -12,14 +12,15 @@
 // through registers: global_load_lds (16 bytes per lane; 4 for scales) fills a ring of NS stages, each one
 // 64-K step of the tile (X rows XOR-swizzled in 16-byte chunks, weight blocks and scales as stored), NS - 1
 // steps ahead of the MFMAs, so several steps of HBM/L2 latency are in flight per wave. Every vector-memory
-// instruction in the loop is one of these, the same number per step (tail steps re-load the last step), so
-// "this step has landed" is an exact s_waitcnt vmcnt count; a bare s_barrier (no fence, which would drain
-// every outstanding load) then publishes the stage to the other waves.
+// instruction in the loop is one of these, the same number per step, so "this step has landed" is an exact
+// s_waitcnt vmcnt count (smaller in the tail, where no further steps are issued); a bare s_barrier (no fence,
+// which would drain every outstanding load) then publishes the stage to the other waves.
 //
-// Split-K (grid y = S): each split stores its f32 partial tile in its own workspace slice; the last split to
-// arrive at a tile (per-tile counter) adds the slices in split order (deterministic), resets the counter (so
-// the counters need clearing only once, at context creation, and a captured graph holds no memset), then
-// runs the epilogue.
+// Split-K (grid y = S): each split stores its f32 partial tile in its own workspace slice with plain stores;
+// k_splitk_sum, the next kernel on the stream, adds the slices in split order (deterministic) and runs the
+// epilogue. No workgroup waits for another: on MI355X a device-scope release from each workgroup writes back
+// its XCD's L2, which measured 130-290 ns per workgroup, serialized, and made a fenced last-arriver reduction
+// slower than no split at all; a kernel boundary publishes the slices once.
 //
 // Epilogues: plain f16 store, or the gated MLP (SiLU / tanh-GELU) on a [w1; w3] weight whose 16-column
 // blocks were interleaved at load so a lane holds a gate value and its up value side by side
@@ -100,8 +101,7 @@ struct GemmArgs {
   const uint8_t *Wc;
   const uint32_t *Ws;
   uint16_t *Y;
-  float *ws;          // split-K workspace [S, M, N] f32
-  uint32_t *counter;  // split-K arrivals per tile, zero between launches
+  float *ws;          // split-K workspace [S, M, N] f32 (N physical columns: a gated weight's interleaved blocks)
   int M, N, K, act, tiles_m, tiles_n, splits, ksteps;  // ksteps: 64-K steps per split
 };
 
@@ -118,16 +118,30 @@ struct GemmShape {
   static constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
   // ring depth (NS - 1 steps in flight): RING, or 0 = the deepest of 4 / 3 that fits. Shallower rings leave
   // LDS for more workgroups per CU, which on MI355X hides more latency than a deeper ring does.
-  static constexpr int NS = RING ? RING : 4 * STAGE <= 160 * 1024 ? 4 : 3;
-  static constexpr int IA = A_BYTES / 1024 / NW;                      // 16-byte-per-lane DMAs per wave and step
+  // (a RING deeper than LDS holds, e.g. for the twice-as-large f16 weight blocks, is cut to what fits)
+  static constexpr int NS_FIT = 160 * 1024 / STAGE;
+  static constexpr int NS = RING ? (RING < NS_FIT ? RING : NS_FIT) : 4 * STAGE <= 160 * 1024 ? 4 : 3;
+  static constexpr int TA = A_BYTES / 1024, IA = (TA + NW - 1) / NW; // 16-byte-per-lane DMAs per wave and step
   static constexpr int TB = B_BYTES / 1024, IB = (TB + NW - 1) / NW;
   static constexpr int IS = BITS == 16 ? 0 : 1;                       // 4-byte-per-lane DMA (scales)
   static constexpr int I = IA + IB + IS;                              // vector-memory ops per wave and step
-  static_assert(A_BYTES % (1024 * NW) == 0, "A stage must split into whole 1 KB rows per wave");
+  static_assert(A_BYTES % 1024 == 0, "A stage must split into whole 1 KB rows");
   static_assert(NB <= 4 * NW, "scale rows cover 4 blocks per wave");
   static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
 };
+
+// wait_vm_barrier with at most n (clamped to [0, MAXN]) steps of I DMAs each left in flight; n is
+// wave-uniform, so this is a scalar branch to one immediate
+template <int I, int MAXN>
+__device__ __forceinline__ void wait_steps_barrier(int n) {
+  if constexpr (MAXN <= 0) {
+    wait_vm_barrier<0>();
+  } else {
+    if (n >= MAXN) wait_vm_barrier<MAXN * I>();
+    else wait_steps_barrier<I, MAXN - 1>(n);
+  }
+}
 
 template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
 __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
@@ -135,7 +149,6 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
-  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
@@ -155,11 +168,14 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   // Per-lane DMA sources at step 0 of the split (a step adds 128 bytes to A, one block to B and scales).
   // A row q (1 KB = 8 rows of the tile): lane L fills LDS chunk L of it = row 8q + L/8, physical chunk L%8,
   // which holds logical chunk (L%8) ^ (row % 8).
+  // Waves past the last row (BM not a multiple of 8 NW) repeat it: same bytes, same place.
   const uint16_t *asrc[S::IA];
+  int adst[S::IA];
 #pragma unroll
   for (int i = 0; i < S::IA; ++i) {
-    const int q = wave * S::IA + i, r = 8 * q + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    const int q = min(wave * S::IA + i, S::TA - 1), r = 8 * q + (lane >> 3), c = (lane & 7) ^ (r & 7);
     asrc[i] = g.X + (size_t)min(m0 + r, M - 1) * K + (size_t)kbeg * 64 + c * 8;
+    adst[i] = __builtin_amdgcn_readfirstlane(q * 1024);
   }
   const int nb0 = n0 >> 4;  // the tile's first weight block row
   const uint8_t *bsrc[S::IB];
@@ -185,7 +201,7 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   auto issue = [&](int kt, int slot) {
     const uint32_t st = lds0 + slot * STAGE;
 #pragma unroll
-    for (int i = 0; i < S::IA; ++i) dma16(asrc[i] + kt * 64, st + (wv * S::IA + i) * 1024);
+    for (int i = 0; i < S::IA; ++i) dma16(asrc[i] + kt * 64, st + adst[i]);
 #pragma unroll
     for (int i = 0; i < S::IB; ++i) dma16(bsrc[i] + (size_t)kt * CB, st + bdst[i]);
     if constexpr (S::IS) dma4(ssrc + kt * 16, st + A_BYTES + B_BYTES + wv * 256);
@@ -216,20 +232,24 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
     h8 bf[FN];                                                                                           \
     _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(R_[j], s, P_[j]);               \
     _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                       \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(A_[i][s], bf[j], acc[i][j]);     \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);     \
   }
 
-  // prologue: steps 0 .. NS-2 in flight (clamped to the last step: a short split re-reads it, harmlessly)
+  // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
+  // have been issued (min(NS - 2, KS - 1) for t = 0), so min(NS - 3, KS - 1 - t) later steps may still be in
+  // flight — the full ring depth until the tail, then exact counts (no re-loads of the last step to wait for).
+  // prologue: steps 0 .. NS-2 in flight
 #pragma unroll
-  for (int p = 0; p < NS - 1; ++p) issue(min(p, KS - 1), p);
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < KS) issue(p, p);
 
   if constexpr (NS == 2) {
     // two stages: read a step's fragments right after its barrier, then compute it
     for (int kt = 0; kt < KS; ++kt) {
-      // this wave's DMAs of step kt are done once at most the NS-2 later steps' remain outstanding; after the
-      // barrier every wave's are, and every wave has finished reading step kt-1's stage, which is refilled next
-      wait_vm_barrier<(NS - 2) * S::I>();
-      issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
+      // this wave's DMAs of step kt are done (nothing later is in flight); after the barrier every wave's
+      // are, and every wave has finished reading step kt-1's stage, which is refilled next
+      wait_vm_barrier<0>();
+      if (kt + 1 < KS) issue(kt + 1, (kt + 1) % NS);
       h8 fa[FM][2];
       RawB<BITS> fr[FN];
       uint32_t fp[FN];
@@ -238,23 +258,22 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
     }
   } else {
     // three or more stages: step k+1's fragments are read into the other register set while step k's MFMAs
-    // run, so LDS latency overlaps the matrix work. At half-step k: step k+1 has landed (NS-3 later steps may
-    // still be in flight), and after the barrier every wave is done with step k-1 (read at k-2, used at
-    // k-1), whose stage takes step k+NS-1.
+    // run, so LDS latency overlaps the matrix work. At half-step k: step k+1 has landed, and after the barrier
+    // every wave is done with step k-1 (read at k-2, used at k-1), whose stage takes step k+NS-1.
     h8 a0[FM][2], a1[FM][2];
     RawB<BITS> r0[FN], r1[FN];
     uint32_t p0[FN], p1[FN];
-    wait_vm_barrier<(NS - 2) * S::I>();
+    wait_steps_barrier<S::I, NS - 2>(min(NS - 2, KS - 1));
     DJ_READ(0, a0, r0, p0);
     int kt = 0;
     for (; kt + 2 <= KS; kt += 2) {
-      wait_vm_barrier<(NS - 3) * S::I>();
-      issue(min(kt + NS - 1, KS - 1), (kt + NS - 1) % NS);
+      wait_steps_barrier<S::I, NS - 3>(KS - 2 - kt);
+      if (kt + NS - 1 < KS) issue(kt + NS - 1, (kt + NS - 1) % NS);
       DJ_READ(kt + 1, a1, r1, p1);
       DJ_MMA(a0, r0, p0);
-      wait_vm_barrier<(NS - 3) * S::I>();
-      issue(min(kt + NS, KS - 1), (kt + NS) % NS);
-      DJ_READ(kt + 2, a0, r0, p0);  // kt + 2 == KS: the stage holds a re-loaded last step, read and unused
+      wait_steps_barrier<S::I, NS - 3>(KS - 3 - kt);
+      if (kt + NS < KS) issue(kt + NS, (kt + NS) % NS);
+      DJ_READ(kt + 2, a0, r0, p0);  // kt + 2 == KS: a stale stage, read and unused
       DJ_MMA(a1, r1, p1);
     }
     if (kt < KS) DJ_MMA(a0, r0, p0);  // odd step count: the last step's fragments are in set 0
@@ -263,52 +282,22 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
 #undef DJ_MMA
   wait_vm<0>();  // the clamped tail DMAs land before the wave moves on
 
-  // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
-  const int rbase = m0 + wm * FM * 16 + (lane >> 4) * 4;
+  // The MFMAs take the weight fragment as their first operand, so each accumulator holds a 16x16 block of
+  // Y^T: lane l has output row l%16 of the block and its 4 consecutive columns 4(l/16)..+3 — one 8-byte f16
+  // (16-byte f32) store instead of four scattered 2-byte ones.
+  const int mrow = m0 + wm * FM * 16 + (lane & 15), c4 = 4 * (lane >> 4);
   const int N = g.N;
   if (g.splits > 1) {
-    // each split stores its partial tile in its own f32 slice; the last to arrive adds the slices in split
-    // order (deterministic: the same bits whichever split arrives last) and resets the tile's counter
-    const size_t slice = (size_t)M * N;
+    // this split's partial tile, f32, into its slice; k_splitk_sum finishes the product
+    float *slice = g.ws + (size_t)blockIdx.y * M * N;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * FN * 16 + j * 16 + (lane & 15);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = rbase + i * 16 + r;
-          if (m < M) g.ws[blockIdx.y * slice + (size_t)m * N + n] = acc[i][j][r];
-        }
+        const int m = mrow + i * 16, n = n0 + wn * FN * 16 + j * 16 + c4;
+        if (m < M) *(f4 *)(slice + (size_t)m * N + n) = acc[i][j];
       }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev = atomicAdd(g.counter + blockIdx.x, 1u);
-      last_flag = prev == (uint32_t)(g.splits - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * FN * 16 + j * 16 + (lane & 15);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = rbase + i * 16 + r;
-          if (m < M) {
-            float sum = 0.0f;
-            for (int k = 0; k < g.splits; ++k)
-              sum += k == (int)blockIdx.y ? acc[i][j][r]
-                                          : __hip_atomic_load(g.ws + k * slice + (size_t)m * N + n, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT);
-            acc[i][j][r] = sum;
-          }
-        }
-      }
-    if (tid == 0) __hip_atomic_store(g.counter + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
   }
 
   if constexpr (!GLU) {
@@ -316,12 +305,11 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
-        const int n = n0 + wn * FN * 16 + j * 16 + (lane & 15);
+        const int m = mrow + i * 16, n = n0 + wn * FN * 16 + j * 16 + c4;
+        h4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = rbase + i * 16 + r;
-          if (m < M) g.Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
-        }
+        for (int r = 0; r < 4; ++r) v[r] = (_Float16)acc[i][j][r];
+        if (m < M) *(h4 *)(g.Y + (size_t)m * N + n) = v;
       }
   } else {
     const int I = N >> 1;
@@ -330,15 +318,53 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; j += 2) {
-        const int col = ((wb0 + j) >> 1) * 16 + (lane & 15);  // physical block p even -> w1 block p / 2
+        const int m = mrow + i * 16;
+        const int col = ((wb0 + j) >> 1) * 16 + c4;  // physical block p even -> w1 block p / 2
+        h4 v;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = rbase + i * 16 + r;
           const float a = (float)(_Float16)acc[i][j][r], b = (float)(_Float16)acc[i][j + 1][r];
-          const float h = (g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b;
-          if (m < M) g.Y[(size_t)m * I + col] = __builtin_bit_cast(uint16_t, (_Float16)h);
+          v[r] = (_Float16)((g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b);
         }
+        if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
       }
+  }
+}
+
+// Split-K finish: Y = epilogue(sum over splits of the f32 slices, in split order — the same bits whatever the
+// schedule). Plain: 4 outputs per thread. Gated: output column c = 16 q + o takes its gate from physical column
+// 32 q + o and its up value from 32 q + 16 + o (the load-time block interleave), each rounded to f16 first, as
+// the tiled epilogue does.
+template <bool GLU>
+__global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws, int splits, int M, int N, int act,
+                                                    uint16_t *__restrict__ Y) {
+  const int NO = GLU ? N / 2 : N;  // output columns
+  const long e = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= (long)M * NO) return;
+  const int m = (int)(e / NO), c = (int)(e % NO);
+  const size_t slice = (size_t)M * N;
+  if constexpr (!GLU) {
+    const float *p = ws + (size_t)m * N + c;
+    f4 s = *(const f4 *)p;
+    for (int k = 1; k < splits; ++k) s += *(const f4 *)(p + k * slice);
+    h4 v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = (_Float16)s[r];
+    *(h4 *)(Y + e) = v;
+  } else {
+    const float *p = ws + (size_t)m * N + (c >> 4) * 32 + (c & 15);
+    f4 a = *(const f4 *)p, b = *(const f4 *)(p + 16);
+    for (int k = 1; k < splits; ++k) {
+      a += *(const f4 *)(p + k * slice);
+      b += *(const f4 *)(p + k * slice + 16);
+    }
+    h4 v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = (float)(_Float16)a[r], u = (float)(_Float16)b[r];
+      v[r] = (_Float16)((act == DJ_ACT_SILU ? act_silu(x) : act_gelu_tanh(x)) * u);
+    }
+    *(h4 *)(Y + (size_t)m * NO + c) = v;
   }
 }
 
@@ -405,7 +431,7 @@ __global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
           for (int j = 0; j < CB; ++j) {
             const h8 bf = dequant<BITS>(b[q][j], s, sp[q][j]);
 #pragma unroll
-            for (int i = 0; i < MT; ++i) acc[i][j] = MFMA16(a[q][i][s], bf, acc[i][j]);
+            for (int i = 0; i < MT; ++i) acc[i][j] = MFMA16(bf, a[q][i][s], acc[i][j]);
           }
       }
     }
@@ -426,32 +452,34 @@ __global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < CB; ++j) acc[i][j] += red[(((w - 1) * MT + i) * CB + j) * 64 + lane];
 
-  // accumulator of 16x16 MFMA: lane l holds rows 4(l/16)..+3 of column l%16
-  const int N = g.N;
+  // accumulators hold blocks of Y^T (weight fragment first): lane l has row 16 i + l%16 and the 4 consecutive
+  // columns 4(l/16)..+3 of a 16-column block, one 8-byte store
+  const int N = g.N, c4 = 4 * (lane >> 4);
   if constexpr (!GLU) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < CB; ++j) {
-        const int n = (nb0 + j) * 16 + (lane & 15);
+        const int m = 16 * i + (lane & 15), n = (nb0 + j) * 16 + c4;
+        h4 v;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * i + (lane >> 4) * 4 + r;
-          if (m < M) g.Y[(size_t)m * N + n] = __builtin_bit_cast(uint16_t, (_Float16)acc[i][j][r]);
-        }
+        for (int r = 0; r < 4; ++r) v[r] = (_Float16)acc[i][j][r];
+        if (m < M) *(h4 *)(g.Y + (size_t)m * N + n) = v;
       }
   } else {
     static_assert(!GLU || CB == 2, "a gated weight pairs gate and up blocks");
-    const int I = N >> 1, col = (nb0 >> 1) * 16 + (lane & 15);  // block pair (2p, 2p + 1) -> w1/w3 block p
+    const int I = N >> 1, col = (nb0 >> 1) * 16 + c4;  // block pair (2p, 2p + 1) -> w1/w3 block p
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MT; ++i) {
+      const int m = 16 * i + (lane & 15);
+      h4 v;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = 16 * i + (lane >> 4) * 4 + r;
         const float a = (float)(_Float16)acc[i][0][r], b = (float)(_Float16)acc[i][1][r];
-        const float h = (g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b;
-        if (m < M) g.Y[(size_t)m * I + col] = __builtin_bit_cast(uint16_t, (_Float16)h);
+        v[r] = (_Float16)((g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b);
       }
+      if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
+    }
   }
 }
 
@@ -488,7 +516,14 @@ struct GemmCfg {
   X(12, "256x128s2", 2, 2, 8, 4, 2) X(13, "128x256", 2, 2, 4, 8, 0) X(14, "128x256s2", 2, 2, 4, 8, 2)      \
   X(15, "64x64s2", 2, 2, 2, 2, 2) X(16, "32x128s2", 1, 4, 2, 2, 2) X(17, "64x128s2", 2, 2, 2, 4, 2)        \
   X(18, "128x64s2", 2, 2, 4, 2, 2) X(19, "128x128n", 1, 4, 8, 2, 2) X(20, "128x128n3", 1, 4, 8, 2, 3)        \
-  X(21, "64x128n", 1, 4, 4, 2, 2) X(22, "128x256n", 1, 4, 8, 4, 2) X(23, "64x256n", 1, 4, 4, 4, 2)
+  X(21, "64x128n", 1, 4, 4, 2, 2) X(22, "128x256n", 1, 4, 8, 4, 2) X(23, "64x256n", 1, 4, 4, 4, 2)        \
+  X(24, "144x128n", 1, 4, 9, 2, 2) X(25, "144x64n", 1, 4, 9, 1, 2) X(26, "96x128n", 1, 4, 6, 2, 2)         \
+  X(27, "48x128n", 1, 4, 3, 2, 2) X(28, "144x128n4", 1, 4, 9, 2, 4) X(29, "144x128n5", 1, 4, 9, 2, 5)        \
+  X(30, "144x64n4", 1, 4, 9, 1, 4) X(31, "144x64n6", 1, 4, 9, 1, 6) X(32, "128x128n4", 1, 4, 8, 2, 4)        \
+  X(33, "128x128n6", 1, 4, 8, 2, 6) X(34, "64x128n4", 1, 4, 4, 2, 4) X(35, "64x128n6", 1, 4, 4, 2, 6)        \
+  X(36, "144x128w8", 1, 8, 9, 1, 2) X(37, "144x128w8r3", 1, 8, 9, 1, 3) X(38, "128x128w8", 2, 4, 4, 2, 2)     \
+  X(39, "64x128w8", 1, 8, 4, 1, 2) X(40, "32x64w8", 2, 4, 1, 1, 0) X(41, "128x256w8", 1, 8, 8, 2, 2)          \
+  X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)
 #define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -518,9 +553,12 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
 // sweeps on MI355X with warm clocks (q8; M 1152-86016; the decoders' N and K), first rule that fits:
-//   128x128n    when it gives >= 1.5 tiles per CU (large M: 925-1040 TFLOP/s; also the 1152-row GLU), or
-//               >= 0.5 per CU when K >= 4096 (few long tiles beat many short ones: 3B's w2),
-//   64x128n     when it gives >= 2 tiles per CU (1152-row qkv),
+//   128x256w8   when it gives >= 4 tiles per CU (large M: 890-980 TFLOP/s at 16384 rows, 1-10% over 128x128n),
+//   128x128n    when it gives >= 1.5 tiles per CU (the 1152-row GLU), or >= 0.5 per CU when K >= 4096 (few
+//               long tiles beat many short ones: 3B's w2),
+//   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
+//               against 17-18 for 64x128n),
+//   64x128n     when it gives >= 2 tiles per CU,
 //   32x64       when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows),
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
@@ -535,7 +573,7 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; } rules[] = {
-        {19, 1.5, 0}, {19, 0.5, 4096}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
+        {41, 4.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups
@@ -572,7 +610,7 @@ static const char *const kGemvNames[3][2] = {{"matmul_q4_gemv", "matmul_glu_q4_g
                                              {"matmul_f16_gemv", "matmul_glu_f16_gemv"}};
 
 // launcher state: the split-K workspace lives in the context
-int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
+int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws);
 
 template <int BITS, bool GLU>
 static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name,
@@ -592,24 +630,23 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
     return DJ_OK;
   }
   float *ws = nullptr;
-  uint32_t *cnt = nullptr;
   int cfg, splits;
   pick(M, N, K, GLU, c->cus, 1, cfg, splits);
-  if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, 1 << 16, &ws, &cnt) != DJ_OK) splits = 1;
+  if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, &ws) != DJ_OK) splits = 1;
   if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
   const char *label = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
   GemmArgs a;
-  a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws; a.counter = cnt;
+  a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws;
   a.M = M; a.N = N; a.K = K; a.act = act;
   a.tiles_m = dj_cdiv(M, kCfgs[cfg].bm());
   a.tiles_n = N / kCfgs[cfg].bn();
   a.splits = splits;
   a.ksteps = (K / 64) / splits;
-  if (splits > 1 && (long)a.tiles_m * a.tiles_n > (1 << 16)) {  // more tiles than counters: no split
-    a.splits = 1;
-    a.ksteps = K / 64;
-  }
   launch_index<BITS, GLU>(cfg, c->stream, a);
+  if (splits > 1) {
+    const long n4 = (long)M * (GLU ? N / 2 : N) / 4;
+    k_splitk_sum<GLU><<<(unsigned)dj_cdiv(n4, 256), 256, 0, c->stream>>>(ws, splits, M, N, act, Y);
+  }
   *name = label;
   *splits_out = a.splits;
   return DJ_OK;

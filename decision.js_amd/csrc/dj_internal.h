@@ -74,11 +74,10 @@ struct dj_ctx {
   std::unordered_map<std::string, std::pair<double, int64_t>> prof;
   std::vector<std::string> prof_order;
   std::string fault_op;  // DJ_FAULT_INJECT
-  // split-K GEMM workspace: f32 partial sums and per-tile arrival counters, zeroed once at creation and
-  // left zero by every GEMM that uses them
+  // split-K GEMM / split-KV attention workspace: f32 partials, written and read by consecutive kernels of
+  // the stream (free between ops)
   float *gemm_ws = nullptr;
-  uint32_t *gemm_cnt = nullptr;
-  size_t gemm_ws_floats = 0, gemm_cnt_n = 0;
+  size_t gemm_ws_floats = 0;
 };
 
 struct dj_rec {
@@ -109,7 +108,7 @@ int dj_op_end(dj_rec *rec, const char *name, const char *detail = nullptr);
 // ---------------------------------------------------------------- launchers (one per kernel family)
 int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
                    const char **name, int *splits);
-int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt);
+int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws);
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
                         dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, uint16_t *O);
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);

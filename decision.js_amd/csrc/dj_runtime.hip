@@ -50,24 +50,16 @@ extern "C" int dj_init(int ordinal, dj_ctx **out) {
   DJ_HIP(hipEventCreate(&c->t1));
   const char *f = getenv("DJ_FAULT_INJECT");
   if (f) c->fault_op = f;
-  // split-K workspace: 64 MiB of f32 partials + 64 Ki tile counters, cleared here once (never by a memset
-  // inside a forward, which a captured graph could replay wrongly)
-  const size_t ws_floats = (size_t)16 << 20, ws_cnt = (size_t)1 << 16;
-  if (hipMalloc((void **)&c->gemm_ws, ws_floats * 4) == hipSuccess &&
-      hipMalloc((void **)&c->gemm_cnt, ws_cnt * 4) == hipSuccess &&
-      hipMemset(c->gemm_ws, 0, ws_floats * 4) == hipSuccess && hipMemset(c->gemm_cnt, 0, ws_cnt * 4) == hipSuccess &&
-      hipDeviceSynchronize() == hipSuccess) {
-    c->gemm_ws_floats = ws_floats;
-    c->gemm_cnt_n = ws_cnt;
-  }
+  // split-K / split-KV workspace: 64 MiB of f32 partials (every slice is written before it is read)
+  const size_t ws_floats = (size_t)16 << 20;
+  if (hipMalloc((void **)&c->gemm_ws, ws_floats * 4) == hipSuccess) c->gemm_ws_floats = ws_floats;
   *out = c;
   return DJ_OK;
 }
 
-int dj_gemm_workspace(dj_ctx *c, size_t need_floats, size_t need_counters, float **ws, uint32_t **cnt) {
-  if (!c->gemm_ws || need_floats > c->gemm_ws_floats || need_counters > c->gemm_cnt_n) return DJ_ENOMEM;
+int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws) {
+  if (!c->gemm_ws || need_floats > c->gemm_ws_floats) return DJ_ENOMEM;
   *ws = c->gemm_ws;
-  *cnt = c->gemm_cnt;
   return DJ_OK;
 }
 
@@ -101,7 +93,6 @@ extern "C" int dj_destroy(dj_ctx *c) {
   }
   for (auto &kv : c->buffers) (void)hipFree(kv.first);
   if (c->gemm_ws) (void)hipFree(c->gemm_ws);
-  if (c->gemm_cnt) (void)hipFree(c->gemm_cnt);
   if (c->pinned) (void)hipHostFree(c->pinned);
   for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
   (void)hipEventDestroy(c->t0);
