@@ -311,28 +311,56 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
 
 // Merge of the split-KV partials of one (query, head): M = max m_s, L = sum l_s 2^(m_s - M),
 // O = sum O_s 2^(m_s - M) / L, in split order (deterministic). A split that saw no key has l = 0.
-__global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int D, int splits, const float *__restrict__ part,
+// One wave per (query, head): lane s loads split s's (m, l), lane l owns D / 64 consecutive dims, and every
+// partial of up to 16 splits is loaded before the first add, so the loads overlap; the sums then run in split
+// order on values broadcast from lane s.
+template <int DPL>
+__global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int splits, const float *__restrict__ part,
                                                       uint16_t *__restrict__ O) {
-  const int q = blockIdx.x, h = blockIdx.y;
-  const float *ml = part + (size_t)splits * T * heads * D;
-  float M = -1e30f;
-  for (int s = 0; s < splits; ++s) {
-    const float *e = ml + (((size_t)s * T + q) * heads + h) * 2;
-    if (e[1] > 0.f) M = fmaxf(M, e[0]);
+  constexpr int D = 64 * DPL, PRE = 16;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (pair >= T * heads) return;
+  const int q = pair / heads, h = pair % heads;
+  const size_t rs = (size_t)T * heads;  // rows per split
+  const size_t row0 = (size_t)q * heads + h;
+  const float *ml = part + (size_t)splits * rs * D;
+  float ms = -1e30f, ls = 0.f;
+  if (lane < splits) {
+    ms = ml[(lane * rs + row0) * 2];
+    ls = ml[(lane * rs + row0) * 2 + 1];
   }
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float L = 0.f, acc = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const size_t row = ((size_t)s * T + q) * heads + h;
-      const float l = ml[row * 2 + 1];
-      if (l > 0.f) {
-        const float w = __builtin_amdgcn_exp2f(ml[row * 2] - M);
-        L += l * w;
-        acc += part[row * D + d] * w;
-      }
+  float M = ls > 0.f ? ms : -1e30f;
+#pragma unroll
+  for (int x = 1; x < 64; x <<= 1) M = fmaxf(M, __shfl_xor(M, x, 64));
+  const float wl = ls > 0.f ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+  float pv[PRE][DPL];
+#pragma unroll
+  for (int k = 0; k < PRE; ++k)
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) pv[k][i] = k < splits ? part[(k * rs + row0) * D + lane * DPL + i] : 0.f;
+  float L = 0.f, acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int k = 0; k < PRE; ++k) {
+    const float l = __shfl(ls, k, 64), w = __shfl(wl, k, 64);
+    if (k < splits && l > 0.f) {
+      L += l * w;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) acc[i] += pv[k][i] * w;
     }
-    O[((size_t)q * heads + h) * D + d] = __builtin_bit_cast(uint16_t, (_Float16)(L > 0.f ? acc / L : 0.f));
   }
+  for (int k = PRE; k < splits; ++k) {
+    const float l = __shfl(ls, k, 64), w = __shfl(wl, k, 64);
+    if (l > 0.f) {
+      L += l * w;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) acc[i] += part[(k * rs + row0) * D + lane * DPL + i] * w;
+    }
+  }
+  uint16_t *o = O + row0 * D + lane * DPL;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) o[i] = __builtin_bit_cast(uint16_t, (_Float16)(L > 0.f ? acc[i] / L : 0.f));
 }
 
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
@@ -376,7 +404,12 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
     default: return dj_fail(DJ_EINVAL, "decision.js: attention head dim %d (64, 128 or 256)", D);
   }
 #undef DJ_ATTN_CASE
-  if (splits > 1) k_attn_combine<<<dim3(T, heads), 128, 0, s>>>(T, heads, D, splits, part, O);
+  if (splits > 1) {
+    const unsigned blocks = (unsigned)dj_cdiv((long)T * heads, 4);
+    if (D == 64) k_attn_combine<1><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
+    else if (D == 128) k_attn_combine<2><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
+    else k_attn_combine<4><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
+  }
   return DJ_OK;
 }
 

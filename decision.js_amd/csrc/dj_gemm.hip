@@ -26,6 +26,7 @@
 // blocks were interleaved at load so a lane holds a gate value and its up value side by side
 // (MATMUL_SWIGLU, kernels.ts:591-599; GELU_MUL, eg2-kernels.ts:165-177).
 #include <math.h>
+#include <algorithm>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -576,11 +577,18 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
         {41, 4.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
-    if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups
+    if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
+                    // the rows need (a 128-row tile on 32 rows does 4x the matrix work: 25 us against 9 for
+                    // 32x64 on M = 32, 1536 x 4608)
       static const int small[] = {8, 5, 4, 7, 9, 15, 16};  // 32x64, 32x128, 64x64, 128x16, 64x32, ...
+      const int need = std::max(32, (M + 15) / 16 * 16);
       long best = -1;
-      for (int i : small)
-        if (cfg_fits(kCfgs[i], N, K, glu) && tiles(i) > best) { cfg = i; best = tiles(i); }
+      for (int pass = 0; pass < 2 && cfg < 0; ++pass)
+        for (int i : small)
+          if (cfg_fits(kCfgs[i], N, K, glu) && (pass || kCfgs[i].bm() <= need) && tiles(i) > best) {
+            cfg = i;
+            best = tiles(i);
+          }
     }
   }
   if (cfg < 0) return;
@@ -617,9 +625,13 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
                        int *splits_out) {
   const int N = w->N, K = w->K;
   const char *force = getenv("DJ_GEMM_TILE");
-  // skinny M on weights up to 4096 outputs wide: 2-3x faster than any tile (measured); wider weights give the
-  // tiled kernel enough workgroups and it wins there
-  const bool skinny = M <= 64 && N % (GLU ? 32 : 16) == 0 && (force ? !strcmp(force, "gemv") : N <= 4096);
+  // skinny M: the GEMV-style kernel on weights up to 4096 outputs wide, and on any weight for M <= 16 (M = 1
+  // GLU 9216 x 1536: 6.8 us against 9.5-10.1 for tiles). At 17-64 rows wider weights give the tiled kernel
+  // enough workgroups (M = 32 GLU 9216 x 1536: 9.8-10.3 against 13.3 us), measured on MI355X. (Long K stays
+  // here: M = 32, 1536 x 4608 took 10.0 + 4.6 us tiled with split-K and its sum inside the 0.8B decoder's
+  // forward, against about 12 for this kernel.)
+  const bool skinny = M <= 64 && N % (GLU ? 32 : 16) == 0 &&
+                      (force ? !strcmp(force, "gemv") : M <= 16 || N <= 4096);
   if (skinny) {
     GemmArgs a{};
     a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y;
