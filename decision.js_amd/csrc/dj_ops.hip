@@ -89,17 +89,21 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, floa
       for (int j = 0; j < 8; ++j) ss += (float)x[j] * (float)x[j];
     }
   };
-  auto scale_out = [&](int k, const h8 &x, float inv) {
-    const h8 w = *(const h8 *)(W + k);
+  auto scale_out = [&](int k, const h8 &x, const h8 &w, float inv) {
     h8 o;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = (_Float16)((float)x[j] * inv * (float)w[j]);
     *(h8 *)(O + base + k) = o;
   };
+  // the norm weight chunks are loaded with the row, so the only memory latency after the reduction is the store
+  h8 ws[R];
   if (NC > 0) {
 #pragma unroll
     for (int c = 0; c < R; ++c)
-      if (lane * 8 + c * WAVE * 8 < H) step(lane * 8 + c * WAVE * 8, xs[c]);
+      if (lane * 8 + c * WAVE * 8 < H) {
+        ws[c] = *(const h8 *)(W + lane * 8 + c * WAVE * 8);
+        step(lane * 8 + c * WAVE * 8, xs[c]);
+      }
   } else {
     for (int k = lane * 8; k < H; k += WAVE * 8) step(k, xs[0]);
   }
@@ -107,9 +111,9 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, floa
   if (NC > 0) {
 #pragma unroll
     for (int c = 0; c < R; ++c)
-      if (lane * 8 + c * WAVE * 8 < H) scale_out(lane * 8 + c * WAVE * 8, xs[c], inv);
+      if (lane * 8 + c * WAVE * 8 < H) scale_out(lane * 8 + c * WAVE * 8, xs[c], ws[c], inv);
   } else {
-    for (int k = lane * 8; k < H; k += WAVE * 8) scale_out(k, *(const h8 *)(X + base + k), inv);
+    for (int k = lane * 8; k < H; k += WAVE * 8) scale_out(k, *(const h8 *)(X + base + k), *(const h8 *)(W + k), inv);
   }
 }
 
@@ -240,14 +244,23 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
   const bool pl = sub < npl, tl = !pl && sub < npl + ntl;
   const int d0 = pl ? 8 * sub : rot + 8 * (sub - npl);  // first owned dim
   constexpr int HPP = 256 / LPH;                        // heads per pass
-  // this lane's values of its first head, loaded before the table is built
+  // this lane's values of a head and the head's norm weights (q or k); the first head's are loaded before the
+  // table is built
+  h8 x = {}, y = {}, wx = {}, wy = {};
+  auto load = [&](int hh) {
+    if (pl || tl) {
+      const uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
+      x = *(const h8 *)(z + d0);
+      if (pl) y = *(const h8 *)(z + half + d0);
+      const uint16_t *nw = hh < heads ? qn : hh < heads + kv ? kn : nullptr;
+      if (nw) {
+        wx = *(const h8 *)(nw + d0);
+        if (pl) wy = *(const h8 *)(nw + half + d0);
+      }
+    }
+  };
   int hh = grp;
-  h8 x = {}, y = {};
-  if (hh < per && (pl || tl)) {
-    const uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
-    x = *(const h8 *)(z + d0);
-    if (pl) y = *(const h8 *)(z + half + d0);
-  }
+  if (hh < per) load(hh);
   if ((int)threadIdx.x < half) {
     const float ps = (float)pos[(size_t)t * pos_stride];
     const float e = (float)(2 * threadIdx.x) / (float)rot;
@@ -260,10 +273,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
   __syncthreads();
   for (; hh < per; hh += HPP) {
     uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
-    if (hh != grp && (pl || tl)) {
-      x = *(const h8 *)(z + d0);
-      if (pl) y = *(const h8 *)(z + half + d0);
-    }
+    if (hh != grp) load(hh);
     const bool isQ = hh < heads, isK = !isQ && hh < heads + kv;
     const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
     const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
@@ -274,11 +284,6 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
     for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
     const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
     if (pl) {
-      h8 wx, wy;
-      if (nw) {
-        wx = *(const h8 *)(nw + d0);
-        wy = *(const h8 *)(nw + half + d0);
-      }
       h8 xo, yo;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -300,9 +305,8 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
       *(h8 *)(z + half + d0) = yo;
     } else if (tl) {
       h8 eo;
-      const h8 we = nw ? *(const h8 *)(nw + d0) : h8{};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? (float)x[i] * inv * (float)we[i] : (float)x[i] * inv);
+      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? (float)x[i] * inv * (float)wx[i] : (float)x[i] * inv);
       *(h8 *)(z + d0) = eo;
     }
   }
