@@ -387,11 +387,12 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
   const dim3 g3(qblocks, heads, splits);
   // two-stage ring: two workgroups fit per CU and hide each other's latency. Measured on MI355X (D 128,
   // causal): 13.6 vs 18.0 us with a 4-stage ring (one workgroup per CU) at T = 1152, 504 vs 719 us at 86016
-  // key groups per workgroup: two (8 waves, each scoring half of every key tile, merged in LDS) for D 256,
-  // where they measured 35.1 vs 37.6 us (2 x 1024 causal, 8 heads); one below (D 128: 30.3 vs 32.7 us at
-  // 1 x 1152, 42.5 vs 46.8 at 16 x 384). DJ_ATTN_KG=1|2 forces it (tuning sweeps).
+  // key groups per workgroup: one. Two (8 waves, each scoring half of every key tile, merged in LDS) measured
+  // slower at D 128 (32.7 vs 30.3 us at 1 x 1152, 46.8 vs 42.5 at 16 x 384) and mixed at D 256 (35.1 vs 37.6
+  // us at 2 x 1024 causal, 8 heads, but 23.5 vs 20.5 us in the encoder's 384-token layer). DJ_ATTN_KG=2
+  // selects them (tuning sweeps; covered by the attention tests).
   const char *kgs = getenv("DJ_ATTN_KG");
-  const int kg = kgs ? atoi(kgs) : D >= 256 ? 2 : 1;
+  const int kg = kgs ? atoi(kgs) : 1;
 #define DJ_ATTN_CASE(DD)                                                                                              \
   case DD:                                                                                                            \
     if (kg == 1) k_attn<DD, 2, 1><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);    \

@@ -130,6 +130,13 @@ struct GemmShape {
   static_assert(NB <= 4 * NW, "scale rows cover 4 blocks per wave");
   static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
+  // waves per SIMD that LDS allows (workgroups per CU x waves per workgroup / 4 SIMDs): the register budget
+  // the compiler may use without costing occupancy. Left to itself it squeezes a 128x128 tile to 120 VGPRs
+  // to reach 4 waves per SIMD that LDS never grants, serializing the fragment reads (9-15% slower at 1536 x
+  // 2048 x 11008, measured).
+  static constexpr int WG_PER_CU = 160 * 1024 / (NS * STAGE);
+  static constexpr int WPE_RAW = WG_PER_CU * NW / 4;
+  static constexpr int WPE = WPE_RAW < 1 ? 1 : WPE_RAW > 8 ? 8 : WPE_RAW;
 };
 
 // wait_vm_barrier with at most n (clamped to [0, MAXN]) steps of I DMAs each left in flight; n is
@@ -145,7 +152,8 @@ __device__ __forceinline__ void wait_steps_barrier(int n) {
 }
 
 template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
-__global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
+__global__ __launch_bounds__(WM *WN * 64)
+__attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE))) void k_gemm(GemmArgs g) {
   using S = GemmShape<BITS, WM, WN, FM, FN, RING>;
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
@@ -232,8 +240,8 @@ __global__ __launch_bounds__(WM *WN * 64) void k_gemm(GemmArgs g) {
   _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                                        \
     h8 bf[FN];                                                                                           \
     _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(R_[j], s, P_[j]);               \
-    _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                       \
-      _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);     \
+    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                       \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);     \
   }
 
   // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
@@ -554,7 +562,8 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
 // sweeps on MI355X with warm clocks (q8; M 1152-86016; the decoders' N and K), first rule that fits:
-//   128x256w8   when it gives >= 4 tiles per CU (large M: 890-980 TFLOP/s at 16384 rows, 1-10% over 128x128n),
+//   128x256w8   when it gives >= 8 tiles per CU (large M: 950-980 TFLOP/s at 86016 rows, 3-8% over 128x128n;
+//               at 1536 rows the 3B GLU's 1032 tiles ran 3% slower than 128x128n),
 //   128x128n    when it gives >= 1.5 tiles per CU (the 1152-row GLU), or >= 0.5 per CU when K >= 4096 (few
 //               long tiles beat many short ones: 3B's w2),
 //   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
@@ -574,7 +583,7 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; } rules[] = {
-        {41, 4.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
+        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than

@@ -442,45 +442,73 @@ extern "C" int dj_readout(dj_rec *rec, int T, int P, int H, const uint16_t *X, c
 }
 
 // ---------------------------------------------------------------- mean pooling (eg2-kernels.ts:202-219)
+// One workgroup per (sequence, 64 columns): lane = column, the 4 waves take every 4th token (8 loads in
+// flight each), then wave 0 adds the 4 partial sums in wave order (deterministic) and divides.
 __global__ __launch_bounds__(256) void k_mean_pool(int T, int H, const uint16_t *__restrict__ X, const uint32_t *__restrict__ seqs,
                                                    float *__restrict__ out) {
-  const int s = blockIdx.x;
+  __shared__ float red[3][64];
+  const int s = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int k = blockIdx.y * 64 + lane;
   uint32_t a = seqs[2 * s], b = seqs[2 * s + 1];
   if (b > (uint32_t)T) b = T;
   if (a > b) a = b;
-  const float n = (float)(b - a);
-  for (int k = threadIdx.x; k < H; k += 256) {
-    float acc = 0.f;
-    for (uint32_t t = a; t < b; ++t) acc += hf(X[(size_t)t * H + k]);
-    out[(size_t)s * H + k] = acc / n;
+  float acc = 0.f;
+  if (k < H) {
+#pragma unroll 8
+    for (uint32_t t = a + wave; t < b; t += 4) acc += hf(X[(size_t)t * H + k]);
+  }
+  if (wave > 0) red[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && k < H) {
+    for (int w = 0; w < 3; ++w) acc += red[w][lane];
+    out[(size_t)s * H + k] = acc / (float)(b - a);
   }
 }
 
 extern "C" int dj_mean_pool(dj_rec *rec, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out) {
   DJ_REQUIRE(X && seqs && out && T > 0 && S >= 0 && H > 0, "decision.js: mean_pool: bad arguments");
   DJ_OP_BEGIN(rec, "mean_pool");
-  if (S > 0) k_mean_pool<<<S, 256, 0, rec->ctx->stream>>>(T, H, X, seqs, out);
+  if (S > 0) k_mean_pool<<<dim3(S, dj_cdiv(H, 64)), 256, 0, rec->ctx->stream>>>(T, H, X, seqs, out);
   return dj_op_end(rec, "mean_pool");
 }
 
 // ---------------------------------------------------------------- small f32 dense (pooled head)
+// One wave per output column: lane l takes 4 consecutive k (one 4-byte q8 / 2-byte q4 code load, one scale,
+// a float4 of each input row) every 256 k, rows in chunks of 16 kept in registers; lane partials are then
+// added by a butterfly (fixed order: deterministic).
 template <int BITS>
 __global__ __launch_bounds__(256) void k_dense_f32(int M, int N, int K, const float *__restrict__ in, const uint8_t *__restrict__ codes,
                                                    const uint16_t *__restrict__ scales, float *__restrict__ out) {
+  constexpr int MR = 16;
   const int n = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (n >= N) return;
   const float zp = BITS == 8 ? 128.f : 8.f;
-  for (int m0 = 0; m0 < M; m0 += 8) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int k = lane; k < K; k += WAVE) {
-      const uint32_t c = BITS == 8 ? codes[(size_t)n * K + k] : (codes[(size_t)n * (K / 2) + k / 2] >> ((k & 1) * 4)) & 15u;
-      const float w = ((float)c - zp) * hf(scales[(size_t)n * (K / 32) + k / 32]);
+  for (int m0 = 0; m0 < M; m0 += MR) {
+    float acc[MR];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (m0 + i < M) acc[i] += in[(size_t)(m0 + i) * K + k] * w;
+    for (int i = 0; i < MR; ++i) acc[i] = 0.f;
+#pragma unroll 2
+    for (int k = 4 * lane; k < K; k += 4 * WAVE) {
+      uint32_t c4;
+      if constexpr (BITS == 8) {
+        c4 = *(const uint32_t *)(codes + (size_t)n * K + k);
+      } else {
+        const uint32_t p = *(const uint16_t *)(codes + (size_t)n * (K / 2) + k / 2);  // nibbles k..k+3, low first
+        c4 = (p & 15u) | ((p >> 4 & 15u) << 8) | ((p >> 8 & 15u) << 16) | ((p >> 12 & 15u) << 24);
+      }
+      const float sc = hf(scales[(size_t)n * (K / 32) + k / 32]);
+      float w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = ((float)((c4 >> (8 * j)) & 255u) - zp) * sc;
+#pragma unroll
+      for (int i = 0; i < MR; ++i)
+        if (m0 + i < M) {
+          const float4 x = *(const float4 *)(in + (size_t)(m0 + i) * K + k);
+          acc[i] += x.x * w[0] + x.y * w[1] + x.z * w[2] + x.w * w[3];
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < MR; ++i) {
       const float v = wave_sum(acc[i]);
       if (lane == 0 && m0 + i < M) out[(size_t)(m0 + i) * N + n] = v;
     }
@@ -489,6 +517,7 @@ __global__ __launch_bounds__(256) void k_dense_f32(int M, int N, int K, const fl
 
 extern "C" int dj_dense_f32(dj_rec *rec, int M, const float *in, const dj_weight *w, float *out) {
   DJ_REQUIRE(w && w->layout == DJ_W_PLAIN, "decision.js: dense_f32 needs a plain weight");
+  DJ_REQUIRE(w->K % 32 == 0, "decision.js: dense_f32: K = %d must be a multiple of 32", w->K);
   DJ_REQUIRE(in && out && M >= 0, "decision.js: dense_f32: bad arguments");
   DJ_OP_BEGIN(rec, "dense_f32");
   if (M > 0) {

@@ -247,8 +247,12 @@ def _forest_case(rng, trunks_branches):
     return meta, ref.forest_ranges(meta)
 
 
+@pytest.mark.parametrize("kg", [1, 2])
 @pytest.mark.parametrize("heads,kv,D", [(16, 8, 128), (16, 2, 128), (12, 2, 128), (3, 1, 256), (4, 2, 64)])
-def test_attention_forest(pkg, ctx, heads, kv, D):
+def test_attention_forest(pkg, ctx, monkeypatch, heads, kv, D, kg):
+    """The forest mask through both workgroup forms: one key group (the default) and two (8 waves, each
+    scoring half of every key tile, merged through LDS)."""
+    monkeypatch.setenv("DJ_ATTN_KG", str(kg))
     dj = _dj()
     rng = np.random.default_rng(heads + kv + D)
     meta, rng4 = _forest_case(rng, [(100, [20, 37, 5]), (70, [64, 1]), (0, [90]), (130, [])])
@@ -268,9 +272,11 @@ def test_attention_forest(pkg, ctx, heads, kv, D):
     assert err < 4e-3
 
 
-def test_attention_large_grid(pkg, ctx):
+@pytest.mark.parametrize("kg", [1, 2])
+def test_attention_large_grid(pkg, ctx, monkeypatch, kg):
     """A varlen batch of causal sequences large enough (>= 512 workgroups) for the two-stage K/V ring, and
     long enough that the lazy max-rescaling and the unmasked-tile path both run many times."""
+    monkeypatch.setenv("DJ_ATTN_KG", str(kg))
     dj = _dj()
     rng = np.random.default_rng(41)
     heads, kv, D = 16, 8, 128
@@ -397,6 +403,38 @@ def test_readout_pool_dense(pkg, ctx):
     pooled = ref.mean_pool(X, ranges)
     assert np.allclose(dpool.read(np.float32, (3, H)), pooled, rtol=1e-5, atol=1e-6)
     assert np.allclose(dd.read(np.float32, (3, 96)), ref.dense_f32(pooled, c, s, 8), rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_pooled_head_long_sequences_and_many_rows(pkg, ctx, bits):
+    """mean_pool over a 256-token sequence (4 waves x 64 tokens each) and a 1-token one; dense_f32 with 20 rows
+    (two register chunks of 16) over K = 3072 (12 steps of 256 per lane) and its 768-wide second layer."""
+    dj = _dj()
+    rng = np.random.default_rng(bits + 90)
+    H = 768
+    lens = [256] + [24] * 3 + [8] * 7 + [1] * 9
+    T = sum(lens)
+    X = rand_f16(rng, (T, H))
+    starts = np.cumsum([0] + lens[:-1])
+    ranges = np.array([(a, a + n) for a, n in zip(starts, lens)], dtype=np.uint32)
+    M = len(lens)
+    c1, s1 = quant(rng, 3072, H, bits)
+    c2, s2 = quant(rng, H, 3072, bits)
+    W1, W2 = ctx.weight_q(c1, s1, 3072, H, bits, dj.W_PLAIN), ctx.weight_q(c2, s2, H, 3072, bits, dj.W_PLAIN)
+    dX, dr = ctx.array(X), ctx.array(ranges)
+    dpool, dh, de = ctx.alloc(M * H * 4), ctx.alloc(M * 3072 * 4), ctx.alloc(M * H * 4)
+
+    def body(r):
+        r.mean_pool(T, M, H, dX, dr, dpool)
+        r.dense_f32(M, dpool, W1, dh)
+        r.dense_f32(M, dh, W2, de)
+    run(ctx, body)
+    pooled = ref.mean_pool(X, ranges)
+    assert np.allclose(dpool.read(np.float32, (M, H)), pooled, rtol=1e-5, atol=1e-6)
+    h = ref.dense_f32(pooled, c1, s1, bits)
+    assert np.allclose(dh.read(np.float32, (M, 3072)), h, rtol=1e-4, atol=1e-5)
+    e = ref.dense_f32(h, c2, s2, bits)
+    assert np.allclose(de.read(np.float32, (M, H)), e, rtol=1e-4, atol=1e-4)
 
 
 # ---------------------------------------------------------------- recorder: snapshots, graphs, errors
