@@ -376,8 +376,11 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
   int splits = 1;
   float *part = nullptr;
   const char *force = getenv("DJ_ATTN_SPLITS");
-  if (force || grid < c->cus) {
-    const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
+  // Only long key sources are split: a 32-token question on a 1056-row kept state runs 14.1 us split against
+  // 25.0 whole, while the encoder's 384-token layer (at most 4 tiles per block) runs 21.4 split against 15.9
+  // whole, the merge costing as much as it saves (measured on MI355X).
+  const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
+  if (force || (grid < c->cus && max_tiles >= 16)) {
     splits = force ? atoi(force) : (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * c->cus, grid));
     splits = std::max(1, std::min(splits, 64));
     while (splits > 1 && (size_t)splits * T * heads * (D + 2) > c->gemm_ws_floats) --splits;

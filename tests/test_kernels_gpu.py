@@ -317,12 +317,17 @@ def test_attention_bidirectional_and_windows(pkg, ctx, D):
         assert np.abs(got - want).max() < 4e-3
 
 
-def test_attention_kept_prefix(pkg, ctx):
-    """Source A = a kept K/V cache (the shared state), source B = the current rows: same result as one pass."""
+@pytest.mark.parametrize("P,splits", [(300, None), (1100, None), (300, 4), (1100, 16), (1100, 1)])
+def test_attention_kept_prefix(pkg, ctx, monkeypatch, P, splits):
+    """Source A = a kept K/V cache (the shared state), source B = the current rows: same result as one pass.
+    A 1100-row cache is split over workgroups by default (partials merged by k_attn_combine); the split count
+    is also forced (4, 16) and turned off (1)."""
+    if splits is not None:
+        monkeypatch.setenv("DJ_ATTN_SPLITS", str(splits))
     dj = _dj()
-    rng = np.random.default_rng(5)
+    rng = np.random.default_rng(5 + P)
     heads, kv, D = 12, 2, 128
-    P, branches = 300, [32, 32, 17, 32]
+    branches = [32, 32, 17, 32]
     stride = (heads + 2 * kv) * D
     T = sum(branches)
     Zp = rand_f16(rng, (P, stride))
