@@ -137,6 +137,10 @@ struct GemmShape {
   static constexpr int WG_PER_CU = 160 * 1024 / (NS * STAGE);
   static constexpr int WPE_RAW = WG_PER_CU * NW / 4;
   static constexpr int WPE = WPE_RAW < 1 ? 1 : WPE_RAW > 8 ? 8 : WPE_RAW;
+  // MFMA loop order: weight fragment outermost where LDS holds occupancy to <= 3 waves per SIMD (up to 168
+  // VGPRs free: every A fragment of the step is read ahead, 110 vs 127 us at 1536 x 2048 x 11008 on
+  // 128x128n); row fragment outermost otherwise (the register-lean order: 128x256 on 8 waves keeps 4 waves
+  // per SIMD at 116 VGPRs, where the other order's 136 cost 14-17% at 86016 rows).
 };
 
 // wait_vm_barrier with at most n (clamped to [0, MAXN]) steps of I DMAs each left in flight; n is
@@ -240,8 +244,13 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
   _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                                        \
     h8 bf[FN];                                                                                           \
     _Pragma("unroll") for (int j = 0; j < FN; ++j) bf[j] = dequant<BITS>(R_[j], s, P_[j]);               \
-    _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                       \
-      _Pragma("unroll") for (int i = 0; i < FM; ++i) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);     \
+    if constexpr (S::WPE <= 3) {                                                                         \
+      _Pragma("unroll") for (int j = 0; j < FN; ++j)                                                     \
+        _Pragma("unroll") for (int i = 0; i < FM; ++i) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);   \
+    } else {                                                                                             \
+      _Pragma("unroll") for (int i = 0; i < FM; ++i)                                                     \
+        _Pragma("unroll") for (int j = 0; j < FN; ++j) acc[i][j] = MFMA16(bf[j], A_[i][s], acc[i][j]);   \
+    }                                                                                                    \
   }
 
   // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
