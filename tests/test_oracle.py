@@ -250,3 +250,121 @@ def test_leaf_logits_brute_force():
 def test_group_max_readout():
     out = np.array([1, 5, 2, 0, 0, 7, 8, 9, 0], dtype=np.float32)
     assert ref.group_max(out, 3, [[[10, 11], [12]], [[1], [2], [3]], [[4]]]) == [[5.0, 2.0], [0.0, 0.0, 7.0], [8.0]]
+
+
+# ---------------------------------------------------------------- the encoder's tail (eg2-kernels.ts, eg2-head.ts)
+
+def _check_sandwich(scale=0.5):
+    """SANDWICH against an element-by-element float64 loop: x' = f16((x + y / rms(y) * w1) * scale),
+    O = f16(x' / rms(x') * w2); rms(v) = sqrt(mean(v^2) + eps). Also rms-scale invariance in Y (Y and 4Y give
+    the same result) and the no-residual form x' = f16(x * scale)."""
+    rng = np.random.default_rng(17)
+    H, eps = 48, 1e-6
+    X = (rng.standard_normal((5, H)) * 2).astype(np.float16)
+    Y = rng.standard_normal((5, H)).astype(np.float16)
+    w1, w2 = [(1 + rng.standard_normal(H) * 0.2).astype(np.float16) for _ in range(2)]
+    Xn, O = ref.sandwich(X, Y, w1, w2, eps, scale, acc=np.float64)
+    for r in range(5):
+        y = [float(v) for v in Y[r]]
+        iy = 1.0 / math.sqrt(sum(v * v for v in y) / H + eps)
+        xs = [np.float16((float(X[r, k]) + y[k] * iy * float(w1[k])) * scale) for k in range(H)]
+        ix = 1.0 / math.sqrt(sum(float(v) * float(v) for v in xs) / H + eps)
+        for k in range(H):
+            assert abs(float(Xn[r, k]) - float(xs[k])) <= 2 ** -10 * abs(float(xs[k])) + 1e-7
+            want = float(xs[k]) * ix * float(w2[k])
+            assert abs(float(O[r, k]) - want) <= 2 ** -10 * abs(want) + 1e-7
+    Xn4, O4 = ref.sandwich(X, (Y.astype(np.float32) * 4).astype(np.float16), w1, w2, eps, scale, acc=np.float64)
+    assert np.abs(Xn4.astype(np.float64) - Xn.astype(np.float64)).max() <= 2 ** -9 * np.abs(Xn.astype(np.float64)).max()
+    Xs, none = ref.sandwich(X, None, None, None, eps, scale, acc=np.float64)
+    assert none is None and np.array_equal(Xs, (X.astype(np.float64) * scale).astype(np.float16))
+
+
+def test_sandwich_closed_form():
+    _check_sandwich()
+
+
+def test_planted_sandwich_mistake_is_caught(monkeypatch):
+    orig = ref.sandwich
+    # the layer scalar applied to the norm branch only, not to the residual sum
+    monkeypatch.setattr(ref, "sandwich", lambda X, Y, w1, w2, eps, scale, acc=np.float32:
+                        orig(X.astype(np.float64) / scale if Y is not None else X, Y, w1, w2, eps, scale, acc))
+    with pytest.raises(AssertionError):
+        _check_sandwich()
+
+
+def test_mean_pool_readout_dense_brute_force():
+    """mean_pool, readout and dense_f32 against explicit loops: the mean of each token range (a one-token
+    range is that row; constant rows pool to the constant), out[k] = X[row] . R[code], and out[m, n] =
+    sum_k in[m, k] * w[n, k] with w the dequantized weight — a 3 x 5 output from a 5 x 64 weight, so a
+    transposed operand cannot pass."""
+    rng = np.random.default_rng(23)
+    T, H = 20, 16
+    X = rng.standard_normal((T, H)).astype(np.float16)
+    X[12:15] = np.float16(0.75)
+    ranges = [(0, 7), (7, 8), (12, 15), (8, 20)]
+    pooled = ref.mean_pool(X, np.array(ranges, dtype=np.uint32))
+    for s, (a, b) in enumerate(ranges):
+        for k in range(H):
+            want = sum(float(X[t, k]) for t in range(a, b)) / (b - a)
+            assert abs(float(pooled[s, k]) - want) <= 1e-6 * (1 + abs(want))
+    assert np.array_equal(pooled[1], X[7].astype(np.float32)) and np.all(pooled[2] == np.float32(0.75))
+    R = rng.standard_normal((6, H)).astype(np.float32)
+    pairs = [(3, 5), (0, 0), (19, 2)]
+    got = ref.readout(X, R, pairs)
+    for i, (r, c) in enumerate(pairs):
+        assert abs(float(got[i]) - sum(float(X[r, k]) * float(R[c, k]) for k in range(H))) <= 1e-5
+    for bits in (8, 4):
+        w = (rng.standard_normal((5, 64)) * 0.05).astype(np.float32)
+        from decision_js_amd import fmt
+        codes, scales = (fmt.quantize8 if bits == 8 else fmt.quantize4)(w)[:2]
+        W = ref.dequant_f32(codes, scales, bits).astype(np.float64)
+        inp = rng.standard_normal((3, 64)).astype(np.float32)
+        out = ref.dense_f32(inp, codes, scales, bits)
+        assert out.shape == (3, 5) and out.dtype == np.float32
+        for m in range(3):
+            for n in range(5):
+                want = sum(float(inp[m, k]) * W[n, k] for k in range(64))
+                assert abs(float(out[m, n]) - want) <= 1e-5 * (1 + abs(want))
+
+
+def test_cosine_scores_closed_forms():
+    """cos(option, state + question): an option along the anchor scores 1 whatever its length, the opposite
+    direction -1, an orthogonal one 0; the anchor is the sum of the two embeddings, not either alone."""
+    s = np.array([1.0, 0.0, 0.0, 0.0], dtype=np.float32)
+    q = np.array([0.0, 1.0, 0.0, 0.0], dtype=np.float32)
+    opts = [np.array([3.0, 3.0, 0, 0], np.float32), np.array([-1.0, -1.0, 0, 0], np.float32),
+            np.array([0, 0, 2.0, 0], np.float32), np.array([1.0, 0, 0, 0], np.float32)]
+    got = ref.cosine_scores(s, q, opts)
+    assert abs(got[0] - 1) < 1e-12 and abs(got[1] + 1) < 1e-12 and abs(got[2]) < 1e-12
+    assert abs(got[3] - 1 / math.sqrt(2)) < 1e-12
+
+
+def test_encoder_texts_embed_independently(pkg, tmp_path):
+    """Texts packed into one encoder pass attend only within themselves: each text's embedding equals the
+    one it gets alone (a segment, window or position slip in the packing or the mask breaks this), and
+    embeddings are unit vectors."""
+    from decision_js_amd import synth
+    mdir = synth.generate(synth.reduced("eg2-encoder-q8", layers=1, vocab=512), str(tmp_path / "enc"), seed=0)
+    model = ref.Model(mdir)
+    rng = np.random.default_rng(29)
+    seqs = [[int(x) for x in rng.integers(0, 512, n)] for n in (37, 5, 1, 20)]
+    # float64 accumulation: numpy's blocking differs with the number of rows, and f32 sums in another order
+    # move the result by ~2e-5 (measured), which would hide nothing a mask slip does (O(1e-2) and up)
+    together = ref.encoder_forward(model, seqs, acc=np.float64)
+    assert np.allclose(np.linalg.norm(together.astype(np.float64), axis=1), 1, atol=1e-6)
+    for i, s in enumerate(seqs):
+        alone = ref.encoder_forward(model, [s], acc=np.float64)
+        assert np.abs(alone[0].astype(np.float64) - together[i].astype(np.float64)).max() < 1e-6
+
+
+def test_planted_encoder_mask_leak_is_caught(pkg, tmp_path, monkeypatch):
+    orig = ref.pack_encoder
+
+    def leaky(seqs, window=None):
+        ids, meta, full, slide, ranges = orig(seqs, window)
+        full = full.copy()
+        full[:, 0], full[:, 1] = 0, len(ids)  # every text attends to the whole batch
+        return ids, meta, full, slide, ranges
+    monkeypatch.setattr(ref, "pack_encoder", leaky)
+    with pytest.raises(AssertionError):
+        test_encoder_texts_embed_independently(pkg, tmp_path)
