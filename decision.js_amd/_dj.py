@@ -67,6 +67,8 @@ SIGNATURES = {
     "dj_matmul": [_P, _P, _P, _P, _I],
     "dj_matmul_glu": [_P, _P, _P, _P, _I, _I],
     "dj_qk_norm_rope": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _I, _F, _F, _I, _I],
+    "dj_rope_table": [_P, _I, _P, _I, _F, _I, _I, _P],
+    "dj_matmul_qkv_rope": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P],
     "dj_attention": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_kv_store": [_P, _I, _I, _I, _P, _I, _I, _P, _I],
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
@@ -272,6 +274,14 @@ class Recorder:
     def qk_norm_rope(self, T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot=None, mode=ROPE_POW_NEG):
         check(lib().dj_qk_norm_rope(self.h, T, heads, kv, D, stride, ptr(Z), ptr(qn), ptr(kn), 1 if vnorm else 0,
                                     ptr(pos), pos_stride, eps, theta, D if rot is None else rot, mode))
+
+    def rope_table(self, T, pos, pos_stride, theta, rot, tab, mode=ROPE_POW_NEG):
+        check(lib().dj_rope_table(self.h, T, ptr(pos), pos_stride, theta, rot, mode, ptr(tab)))
+
+    def matmul_qkv_rope(self, X, w: Weight, Z, M, heads, kv, D, qn, kn, vnorm, pos, pos_stride, eps, theta, tab, rot=None,
+                        mode=ROPE_POW_NEG):
+        check(lib().dj_matmul_qkv_rope(self.h, ptr(X), w.h, ptr(Z), M, heads, kv, D, ptr(qn), ptr(kn), 1 if vnorm else 0,
+                                       ptr(pos), pos_stride, eps, theta, D if rot is None else rot, mode, ptr(tab)))
 
     def attention(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))

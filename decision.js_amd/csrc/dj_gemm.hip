@@ -27,6 +27,7 @@
 // (MATMUL_SWIGLU, kernels.ts:591-599; GELU_MUL, eg2-kernels.ts:165-177).
 #include <math.h>
 #include <algorithm>
+#include <type_traits>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -104,6 +105,12 @@ struct GemmArgs {
   uint16_t *Y;
   float *ws;          // split-K workspace [S, M, N] f32 (N physical columns: a gated weight's interleaved blocks)
   int M, N, K, act, tiles_m, tiles_n, splits, ksteps;  // ksteps: 64-K steps per split
+  // q/k norm + RoPE epilogue (EPI 2; the tile is one 128-wide head): norm weights, the forward's per-token
+  // (cos, sin) table [M, rot / 2], heads layout
+  const uint16_t *qn, *kn;
+  const float2 *rtab;
+  int heads, kv, vnorm, rot;
+  float eps;
 };
 
 // Ring of LDS stages, each holding one 64-K step of the tile: A (BM rows x 128 bytes, XOR-swizzled 16-byte
@@ -155,10 +162,12 @@ __device__ __forceinline__ void wait_steps_barrier(int n) {
   }
 }
 
-template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
+// EPI: 0 plain store, 1 gated MLP, 2 QK_NORM_ROPE on a qkv weight (kernels.ts:86-112) before the store
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI>
 __global__ __launch_bounds__(WM *WN * 64)
 __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE))) void k_gemm(GemmArgs g) {
   using S = GemmShape<BITS, WM, WN, FM, FN, RING>;
+  constexpr bool GLU = EPI == 1;
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -316,6 +325,87 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
         if (m < M) *(f4 *)(slice + (size_t)m * N + n) = acc[i][j];
       }
     return;
+  }
+
+  if constexpr (EPI == 2) {
+    // The tile is one head of a qkv product (BN = D = 128, tile column n0 = head * 128). q and k heads (and v
+    // heads with vnorm): the f16-rounded tile goes to LDS (the ring is free: every DMA has landed), then
+    // LPH lanes per row run QK_NORM_ROPE's arithmetic (norm_rope_lane, shared with k_qk_norm_rope, cos/sin from
+    // the forward's table) and store the row. Other v heads take the plain store below.
+    // rows padded to 136 halves (272 bytes) so neighbouring rows start on different LDS banks
+    constexpr int RS = 136;
+    static_assert(BM * RS * 2 <= NS * STAGE, "the f16 tile fits the ring");
+    const int hh = n0 >> 7;
+    const bool isQ = hh < g.heads, isK = !isQ && hh < g.heads + g.kv;
+    if (isQ || isK || g.vnorm) {
+      uint16_t *tile = (uint16_t *)smem;
+      __syncthreads();  // every wave is past its last fragment read
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          h4 v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (_Float16)acc[i][j][r];
+          *(h4 *)(tile + (wm * FM * 16 + i * 16 + (lane & 15)) * RS + wn * FN * 16 + j * 16 + c4) = v;
+        }
+      __syncthreads();
+      const uint16_t *nw = isQ ? g.qn : isK ? g.kn : nullptr;
+      const bool norm = isQ ? g.qn != nullptr : isK ? g.kn != nullptr : true;
+      auto rows = [&](auto lph) {
+        constexpr int LPH = decltype(lph)::value, RPP = S::NT / LPH, PASSES = (BM + RPP - 1) / RPP;
+        const int rot = g.rot, half = rot / 2, npl = rot / 16, ntl = (128 - rot) / 8;
+        const int sub = tid % LPH;
+        const bool pl = sub < npl, tl = !pl && sub < npl + ntl;
+        const int d0 = pl ? 8 * sub : rot + 8 * (sub - npl);
+        h8 wx = {}, wy = {};
+        if (nw && (pl || tl)) {
+          wx = *(const h8 *)(nw + d0);
+          if (pl) wy = *(const h8 *)(nw + half + d0);
+        }
+        // every pass's row values and angles are loaded before the first is computed, so their latencies
+        // overlap (a lane group's rows are r0, r0 + RPP, ...; rows past BM or M are skipped as a group)
+        h8 xs[PASSES], ys[PASSES];
+        float2 cs[PASSES][8];
+#pragma unroll
+        for (int q = 0; q < PASSES; ++q) {
+          const int r = tid / LPH + q * RPP, m = m0 + r;
+          xs[q] = h8{};
+          ys[q] = h8{};
+          if (r < BM && m < M) {
+            if (pl || tl) xs[q] = *(const h8 *)(tile + r * RS + d0);
+            if (pl) ys[q] = *(const h8 *)(tile + r * RS + half + d0);
+            if (pl && (isQ || isK)) {
+              const float4 *c4p = (const float4 *)(g.rtab + (size_t)m * half + d0);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const float4 v = c4p[i];
+                cs[q][2 * i] = make_float2(v.x, v.y);
+                cs[q][2 * i + 1] = make_float2(v.z, v.w);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < PASSES; ++q) {
+          const int r = tid / LPH + q * RPP, m = m0 + r;
+          if (r >= BM || m >= M) continue;
+          const h8x2 o = norm_rope_lane<LPH>(xs[q], ys[q], wx, wy, nw != nullptr, norm, isQ || isK, pl, 128, g.eps,
+                                             [&](int i) { return cs[q][i]; });
+          uint16_t *z = g.Y + (size_t)m * N + (size_t)hh * 128;
+          if (pl) {
+            *(h8 *)(z + d0) = o.x;
+            *(h8 *)(z + half + d0) = o.y;
+          } else if (tl) {
+            *(h8 *)(z + d0) = o.x;
+          }
+        }
+      };
+      // the standalone kernel's lane counts: 8 lanes for a fully rotated head, 16 for a partial rotation
+      if (g.rot == 128) rows(std::integral_constant<int, 8>{});
+      else rows(std::integral_constant<int, 16>{});
+      return;
+    }
   }
 
   if constexpr (!GLU) {
@@ -546,27 +636,29 @@ struct GemmCfg {
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int BITS, int WM, int WN, int FM, int FN, int RING, bool GLU>
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI>
 static void launch_cfg(hipStream_t s, GemmArgs a) {
-  if constexpr (GLU && FN % 2 != 0) {
-    return;  // never picked: a gated tile needs gate/up fragment pairs
+  if constexpr ((EPI == 1 && FN % 2 != 0) || (EPI == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144))) {
+    return;  // never picked: a gated tile needs gate/up fragment pairs, a RoPE tile is one 128-wide head of at
+             // most 144 rows (its epilogue holds every row pass in registers)
   } else {
     dim3 grid(a.tiles_m * a.tiles_n, a.splits);
-    k_gemm<BITS, WM, WN, FM, FN, RING, GLU><<<grid, WM * WN * 64, 0, s>>>(a);
+    k_gemm<BITS, WM, WN, FM, FN, RING, EPI><<<grid, WM * WN * 64, 0, s>>>(a);
   }
 }
 
-template <int BITS, bool GLU>
+template <int BITS, int EPI>
 static void launch_index(int i, hipStream_t s, GemmArgs a) {
 #define DJ_CFG_CASE(i, tag, wm, wn, fm, fn, ring) \
-  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, GLU>(s, a); break;
+  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, EPI>(s, a); break;
   switch (i) { DJ_GEMM_CFGS(DJ_CFG_CASE) }
 #undef DJ_CFG_CASE
 }
 
-static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
+// epi: 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (the tile is one 128-wide head, <= 144 rows)
+static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
   (void)K;
-  return N % c.bn() == 0 && (!glu || c.fn % 2 == 0);
+  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144));
 }
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
@@ -581,7 +673,7 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, bool glu) {
 //   32x64       when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows),
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
-static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, int &splits) {
+static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int &splits) {
   const char *force = getenv("DJ_GEMM_TILE");
   const char *fs = getenv("DJ_GEMM_SPLITK");
   cfg = -1;
@@ -592,7 +684,8 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; } rules[] = {
-        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {21, 2.0, 0}, {8, 2.0, 0}, {16, 2.0, 0}};
+        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {24, 1.0, 0}, {21, 2.0, 0}, {8, 2.0, 0},
+        {16, 2.0, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
@@ -617,17 +710,18 @@ static void pick(int M, int N, int K, bool glu, int cus, int ws_ok, int &cfg, in
     const long t = tiles(cfg);
     while (t * splits * 4 < cus && KT % (splits * 2) == 0 && KT / (splits * 2) >= 4) splits *= 2;
   }
-  if (splits < 1 || KT % splits || !ws_ok) splits = 1;
+  if (splits < 1 || KT % splits || !ws_ok || glu == 2) splits = 1;
 }
 
-// Profile labels "matmul[_glu]_<q4|q8|f16>_<tile>", built when the library loads.
+// Profile labels "matmul[_glu|_rope]_<q4|q8|f16>_<tile>", built when the library loads.
 static const struct GemmNames {
-  char v[3][2][kNumCfgs][40];
+  char v[3][3][kNumCfgs][40];
   GemmNames() {
+    static const char *const epi[3] = {"", "_glu", "_rope"};
     for (int b = 0; b < 3; ++b)
-      for (int glu = 0; glu < 2; ++glu)
+      for (int e = 0; e < 3; ++e)
         for (int i = 0; i < kNumCfgs; ++i)
-          snprintf(v[b][glu][i], 40, "matmul%s_%s_%s", glu ? "_glu" : "", b == 0 ? "q4" : b == 1 ? "q8" : "f16", kCfgs[i].tag);
+          snprintf(v[b][e][i], 40, "matmul%s_%s_%s", epi[e], b == 0 ? "q4" : b == 1 ? "q8" : "f16", kCfgs[i].tag);
   }
 } kNames;
 
@@ -665,14 +759,14 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, &ws) != DJ_OK) splits = 1;
   if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
   const char *label = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
-  GemmArgs a;
+  GemmArgs a{};
   a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws;
   a.M = M; a.N = N; a.K = K; a.act = act;
   a.tiles_m = dj_cdiv(M, kCfgs[cfg].bm());
   a.tiles_n = N / kCfgs[cfg].bn();
   a.splits = splits;
   a.ksteps = (K / 64) / splits;
-  launch_index<BITS, GLU>(cfg, c->stream, a);
+  launch_index<BITS, GLU ? 1 : 0>(cfg, c->stream, a);
   if (splits > 1) {
     const long n4 = (long)M * (GLU ? N / 2 : N) / 4;
     k_splitk_sum<GLU><<<(unsigned)dj_cdiv(n4, 256), 256, 0, c->stream>>>(ws, splits, M, N, act, Y);
@@ -680,6 +774,65 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   *name = label;
   *splits_out = a.splits;
   return DJ_OK;
+}
+
+// The qkv product with QK_NORM_ROPE as its epilogue (one head per tile). Returns 1 with nothing launched where
+// that does not apply: skinny M (the GEMV kernel serves those rows), no 128-wide tile fits, or more than two
+// tiles per CU. The epilogue holds every row pass's values and angles in registers at once (256 VGPRs: one
+// wave per SIMD), which pays where the grid is about one wave of tiles and the saved kernel is a large share
+// (T = 1152: 3.00 against 3.10 ms per ticket), and costs where occupancy hides the loads (T = 86147: 118.6
+// against 108.2 ms per forward), measured on MI355X.
+template <int BITS>
+static int launch_rope_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Z, int M, GemmArgs a,
+                            const char **name) {
+  const int N = w->N, K = w->K;
+  if (M <= 64) return 1;
+  int cfg, splits;
+  pick(M, N, K, 2, c->cus, 0, cfg, splits);
+  if (cfg < 0 || (long)dj_cdiv(M, kCfgs[cfg].bm()) * (N / 128) > 2L * c->cus) return 1;
+  a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Z; a.ws = nullptr;
+  a.M = M; a.N = N; a.K = K; a.act = 0;
+  a.tiles_m = dj_cdiv(M, kCfgs[cfg].bm());
+  a.tiles_n = N / 128;
+  a.splits = 1;
+  a.ksteps = K / 64;
+  launch_index<BITS, 2>(cfg, c->stream, a);
+  *name = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][2][cfg];
+  return 0;
+}
+
+extern "C" int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Z, int M, int heads, int kv,
+                                  int D, const uint16_t *qn, const uint16_t *kn, int vnorm, const int32_t *pos,
+                                  int pos_stride, float eps, float theta, int rot, int mode, const float *tab) {
+  DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA, "decision.js: matmul_qkv_rope needs an MFMA-tiled weight (DJ_W_MFMA)");
+  DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: matmul_qkv_rope: unknown rope mode");
+  DJ_REQUIRE(X && Z && pos && tab && M >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 &&
+                 w->N == (heads + 2 * kv) * D && rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0,
+             "decision.js: matmul_qkv_rope: bad arguments (N %d for %d + 2 x %d heads of %d, rot %d)", w->N, heads, kv,
+             D, rot);
+  DJ_OP_BEGIN(rec, "matmul_qkv_rope");
+  const char *name = "matmul_qkv_rope";
+  if (M > 0) {
+    GemmArgs a{};
+    a.qn = qn; a.kn = kn; a.rtab = (const float2 *)tab;
+    a.heads = heads; a.kv = kv; a.vnorm = vnorm; a.rot = rot; a.eps = eps;
+    const int bits = (w->layout & DJ_W_DIRECT) ? 16 : w->bits;
+    int st = 1;
+    if (D == 128)
+      st = bits == 8 ? launch_rope_bits<8>(rec->ctx, X, w, Z, M, a, &name)
+           : bits == 4 ? launch_rope_bits<4>(rec->ctx, X, w, Z, M, a, &name)
+                       : launch_rope_bits<16>(rec->ctx, X, w, Z, M, a, &name);
+    if (st == 1) {  // the product, then the standalone kernel (its angles computed as the table's were)
+      int splits = 1;
+      st = dj_launch_gemm(rec->ctx, X, w, Z, M, -1, &name, &splits);
+      if (st) return st;
+      dj_launch_qk_norm_rope(rec->ctx->stream, M, heads, kv, D, w->N, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot,
+                             mode);
+    }
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  return dj_op_end(rec, name, shape);
 }
 
 int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act, const char **name,

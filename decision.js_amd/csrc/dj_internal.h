@@ -109,6 +109,10 @@ int dj_op_end(dj_rec *rec, const char *name, const char *detail = nullptr);
 int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
                    const char **name, int *splits);
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws);
+// QK_NORM_ROPE kernel launch (checked arguments)
+int dj_launch_qk_norm_rope(hipStream_t s, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
+                           const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta, int rot,
+                           int mode);
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
                         dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, uint16_t *O);
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);
@@ -145,4 +149,60 @@ __device__ __forceinline__ void wait_vm() {
 }
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+// ---------------------------------------------------------------- QK_NORM_ROPE pieces shared by its kernels
+// (the standalone k_qk_norm_rope, the once-per-forward table and the qkv GEMM epilogue), so every path does
+// the same arithmetic.
+// (cos, sin) of rotation pair j of a token at position pos: frequency theta^(-2j/rot) (POW_NEG) or
+// 1 / theta^(2j/rot) (INV_POW) as exp2(e log2 theta) — WGSL pow's definition (kernels.ts:106,
+// eg2-kernels.ts:86) — and angle = f32(pos * f).
+__device__ __forceinline__ float2 rope_cs(float ps, int j, int rot, float theta, int mode) {
+  const float e = (float)(2 * j) / (float)rot;
+  const float l2t = log2f(theta);
+  const float f = mode == DJ_ROPE_POW_NEG ? exp2f(-e * l2t) : 1.0f / exp2f(e * l2t);
+  float sn, cs;
+  sincosf(ps * f, &sn, &cs);
+  return make_float2(cs, sn);
+}
+// One lane's share of a head row: LPH consecutive lanes hold the row. A pair lane (pl) holds dims d0..d0+7 in
+// x and their partners d0 + rot/2.. in y; a tail lane (tl) holds 8 unrotated dims in x (y zero); others hold
+// zeros. Every lane of the group must call this (the row's sum of squares is a shuffle over LPH lanes).
+// x / rms(row) (when norm), times the norm weight w (when given), then the rotation by cs(i) = (cos, sin) of
+// pair d0 + i (when rope); results rounded to f16.
+struct h8x2 {
+  h8 x, y;
+};
+template <int LPH, typename CS>
+__device__ __forceinline__ h8x2 norm_rope_lane(h8 x, h8 y, h8 wx, h8 wy, bool has_w, bool norm, bool rope, bool pl, int D,
+                                               float eps, CS cs) {
+  h8 xo = {}, yo = {};
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i] + (float)y[i] * (float)y[i];
+#pragma unroll
+  for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
+  if (pl) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float a = (float)x[i] * inv, b = (float)y[i] * inv;
+      if (has_w) {
+        a *= (float)wx[i];
+        b *= (float)wy[i];
+      }
+      if (rope) {
+        const float2 r = cs(i);
+        const float a2 = a * r.x - b * r.y, b2 = b * r.x + a * r.y;
+        a = a2;
+        b = b2;
+      }
+      xo[i] = (_Float16)a;
+      yo[i] = (_Float16)b;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xo[i] = (_Float16)(has_w ? (float)x[i] * inv * (float)wx[i] : (float)x[i] * inv);
+  }
+  return {xo, yo};
 }

@@ -228,9 +228,7 @@ extern "C" int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, ui
 // ---------------------------------------------------------------- q/k(/v) norm + RoPE
 // One workgroup per token; LPH lanes per head (a power of two). Lane s < rot/16 owns the 8 rotation pairs
 // (d, d + rot/2), d = 8s..8s+7 (two 16-byte loads); the next (D - rot)/8 lanes own 8 unrotated dims each.
-// cos/sin of the token's rot/2 angles are computed once into LDS. Frequency theta^(-2d/rot) (POW_NEG) or
-// 1 / theta^(2d/rot) (INV_POW) as exp2(e log2 theta) — the definition of WGSL pow the reference kernels use
-// (kernels.ts:106, eg2-kernels.ts:86) — and angle = f32(pos * f).
+// cos/sin of the token's rot/2 angles are computed once into LDS (rope_cs).
 template <int LPH>
 __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, int D, int stride, uint16_t *__restrict__ Z,
                                                       const uint16_t *__restrict__ qn, const uint16_t *__restrict__ kn,
@@ -261,15 +259,7 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
   };
   int hh = grp;
   if (hh < per) load(hh);
-  if ((int)threadIdx.x < half) {
-    const float ps = (float)pos[(size_t)t * pos_stride];
-    const float e = (float)(2 * threadIdx.x) / (float)rot;
-    const float l2t = log2f(theta);
-    const float f = mode == DJ_ROPE_POW_NEG ? exp2f(-e * l2t) : 1.0f / exp2f(e * l2t);
-    float sn, cs;
-    sincosf(ps * f, &sn, &cs);
-    tab[threadIdx.x] = make_float2(cs, sn);
-  }
+  if ((int)threadIdx.x < half) tab[threadIdx.x] = rope_cs((float)pos[(size_t)t * pos_stride], threadIdx.x, rot, theta, mode);
   __syncthreads();
   for (; hh < per; hh += HPP) {
     uint16_t *z = Z + (size_t)t * stride + (size_t)hh * D;
@@ -277,62 +267,71 @@ __global__ __launch_bounds__(256) void k_qk_norm_rope(int T, int heads, int kv, 
     const bool isQ = hh < heads, isK = !isQ && hh < heads + kv;
     const uint16_t *nw = isQ ? qn : isK ? kn : nullptr;
     const bool norm = isQ ? qn != nullptr : isK ? kn != nullptr : true;  // v heads only come with vnorm
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i] + (float)y[i] * (float)y[i];
-#pragma unroll
-    for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, WAVE);
-    const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
+    const h8x2 o = norm_rope_lane<LPH>(x, y, wx, wy, nw != nullptr, norm, isQ || isK, pl, D, eps,
+                                       [&](int i) { return tab[d0 + i]; });
     if (pl) {
-      h8 xo, yo;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float a = (float)x[i] * inv, b = (float)y[i] * inv;
-        if (nw) {
-          a *= (float)wx[i];
-          b *= (float)wy[i];
-        }
-        if (isQ || isK) {
-          const float2 r = tab[d0 + i];
-          const float a2 = a * r.x - b * r.y, b2 = b * r.x + a * r.y;
-          a = a2;
-          b = b2;
-        }
-        xo[i] = (_Float16)a;
-        yo[i] = (_Float16)b;
-      }
-      *(h8 *)(z + d0) = xo;
-      *(h8 *)(z + half + d0) = yo;
+      *(h8 *)(z + d0) = o.x;
+      *(h8 *)(z + half + d0) = o.y;
     } else if (tl) {
-      h8 eo;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) eo[i] = (_Float16)(nw ? (float)x[i] * inv * (float)wx[i] : (float)x[i] * inv);
-      *(h8 *)(z + d0) = eo;
+      *(h8 *)(z + d0) = o.x;
     }
   }
+}
+
+static int qk_rope_check(int heads, int kv, int D, int stride, int rot) {
+  DJ_REQUIRE(heads > 0 && kv > 0 && D > 0 && D <= 512 && rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0 &&
+                 stride % 8 == 0 && stride >= (heads + 2 * kv) * D,
+             "decision.js: qk_norm_rope: unsupported shape (D %d, rot %d, stride %d)", D, rot, stride);
+  return DJ_OK;
+}
+
+int dj_launch_qk_norm_rope(hipStream_t s, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
+                           const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta, int rot,
+                           int mode) {
+  const int lanes = rot / 16 + (D - rot) / 8;
+#define DJ_ROPE_LAUNCH(L) \
+  k_qk_norm_rope<L><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode)
+  if (lanes <= 4) DJ_ROPE_LAUNCH(4);
+  else if (lanes <= 8) DJ_ROPE_LAUNCH(8);
+  else if (lanes <= 16) DJ_ROPE_LAUNCH(16);
+  else if (lanes <= 32) DJ_ROPE_LAUNCH(32);
+  else DJ_ROPE_LAUNCH(64);
+#undef DJ_ROPE_LAUNCH
+  return DJ_OK;
 }
 
 extern "C" int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
                                const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta,
                                int rot, int mode) {
-  DJ_REQUIRE(Z && pos && T >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 && rot > 0 && rot <= D && rot % 16 == 0 &&
-                 (D - rot) % 8 == 0 && stride % 8 == 0 && stride >= (heads + 2 * kv) * D,
-             "decision.js: qk_norm_rope: unsupported shape (D %d, rot %d, stride %d)", D, rot, stride);
+  DJ_REQUIRE(Z && pos && T >= 0, "decision.js: qk_norm_rope: bad arguments");
+  if (int st = qk_rope_check(heads, kv, D, stride, rot)) return st;
   DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: qk_norm_rope: unknown rope mode");
   DJ_OP_BEGIN(rec, "qk_norm_rope");
-  if (T > 0) {
-    const int lanes = rot / 16 + (D - rot) / 8;
-    hipStream_t s = rec->ctx->stream;
-#define DJ_ROPE_LAUNCH(L) \
-  k_qk_norm_rope<L><<<T, 256, 0, s>>>(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode)
-    if (lanes <= 4) DJ_ROPE_LAUNCH(4);
-    else if (lanes <= 8) DJ_ROPE_LAUNCH(8);
-    else if (lanes <= 16) DJ_ROPE_LAUNCH(16);
-    else if (lanes <= 32) DJ_ROPE_LAUNCH(32);
-    else DJ_ROPE_LAUNCH(64);
-#undef DJ_ROPE_LAUNCH
-  }
+  if (T > 0)
+    dj_launch_qk_norm_rope(rec->ctx->stream, T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot,
+                           mode);
   return dj_op_end(rec, "qk_norm_rope");
+}
+
+// ---------------------------------------------------------------- RoPE table (one per forward)
+__global__ __launch_bounds__(256) void k_rope_table(int T, const int32_t *__restrict__ pos, int pos_stride, float theta,
+                                                    int rot, int mode, float2 *__restrict__ tab) {
+  const int half = rot / 2;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)T * half) return;
+  const int t = (int)(i / half), j = (int)(i % half);
+  tab[i] = rope_cs((float)pos[(size_t)t * pos_stride], j, rot, theta, mode);
+}
+
+extern "C" int dj_rope_table(dj_rec *rec, int T, const int32_t *pos, int pos_stride, float theta, int rot, int mode,
+                             float *tab) {
+  DJ_REQUIRE(pos && tab && T >= 0 && rot > 0 && rot % 16 == 0 && rot <= 512, "decision.js: rope_table: bad arguments");
+  DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: rope_table: unknown rope mode");
+  DJ_OP_BEGIN(rec, "rope_table");
+  if (T > 0)
+    k_rope_table<<<dj_cdiv((long)T * (rot / 2), 256), 256, 0, rec->ctx->stream>>>(T, pos, pos_stride, theta, rot, mode,
+                                                                                 (float2 *)tab);
+  return dj_op_end(rec, "rope_table");
 }
 
 // ---------------------------------------------------------------- KV store (kept prefix of a shared state)

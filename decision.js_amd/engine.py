@@ -200,8 +200,9 @@ class SharedState:
 class DecoderEngine(GpuEngine):
     """A causal decoder (config model "decoder", or the reference's "d1-3b" naming on attention layers): many
     rows packed as a forest, answer-set logits at each branch's last token (D13BEngine, d1-3b-engine.ts).
-    Layers: qkv -> q/k RMSNorm (when the model has it) + RoPE -> attention -> o_proj -> residual + RMSNorm
-    -> w13 with the SwiGLU epilogue -> w2 -> residual + RMSNorm."""
+    Layers: qkv with q/k RMSNorm (when the model has it) + RoPE (one op: dj_matmul_qkv_rope on the forward's
+    RoPE table) -> attention -> o_proj -> residual + RMSNorm -> w13 with the SwiGLU epilogue -> w2 -> residual
+    + RMSNorm."""
 
     @classmethod
     def load(cls, base: str, opts: dict = None):
@@ -232,6 +233,7 @@ class DecoderEngine(GpuEngine):
         H, I = self.H, self.I
         self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * self.stride * 2,
                      "y": cap * self.h * self.D * 2, "h": cap * I * 2, "ids": cap * 4, "pos": cap * 4, "rng": cap * 16,
+                     "rope": cap * (self.D // 2) * 8,
                      "leaves": lcap * 4, "leaf_ids": lcap * 4, "out": lcap * 4})
         self.capacity, self.leaf_capacity = cap, lcap
 
@@ -243,10 +245,12 @@ class DecoderEngine(GpuEngine):
         src = _dj.kv_src(z, T, self.stride, h * D, (h + kv) * D)
         rec.gather_q(B["ids"], T, w["embed"], B["x"])
         rec.add_rmsnorm(T, H, False, eps, B["x"], B["o"], w["layers.0.operator_norm"], B["normed"])
+        # the RoPE angles of this forward, once; every layer's qkv product applies q/k norm + RoPE with them
+        rec.rope_table(T, B["pos"], 1, self.theta, D, B["rope"])
         for i in range(self.layers):
             p = f"layers.{i}."
-            rec.matmul(B["normed"], w[p + "qkv"], z, T)
-            rec.qk_norm_rope(T, h, kv, D, self.stride, z, w.get(p + "q_norm"), w.get(p + "k_norm"), False, B["pos"], 1, eps, self.theta)
+            rec.matmul_qkv_rope(B["normed"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"), w.get(p + "k_norm"), False,
+                                B["pos"], 1, eps, self.theta, B["rope"])
             if kv_store is not None:
                 rec.kv_store(T, kv, D, z, self.stride, h * D, kv_store.at(i * T * 2 * kv * D * 2), 0)
             a = src if kv_a is None else kv_a(i)

@@ -118,6 +118,10 @@ class Recorder {
   qkNormRope(T, heads, kv, D, stride, Z, qn, kn, vnorm, pos, posStride, eps, theta, rot, mode) {
     lib().qkNormRope(this.h, T, heads, kv, D, stride, Z, qn, kn, vnorm ? 1 : 0, pos, posStride, eps, theta, rot, mode);
   }
+  ropeTable(T, pos, posStride, theta, rot, tab, mode = lib().ROPE_POW_NEG) { lib().ropeTable(this.h, T, pos, posStride, theta, rot, mode, tab); }
+  matmulQkvRope(X, w, Z, M, heads, kv, D, qn, kn, vnorm, pos, posStride, eps, theta, tab, rot = D, mode = lib().ROPE_POW_NEG) {
+    lib().matmulQkvRope(this.h, X, w.h, Z, M, heads, kv, D, qn, kn, vnorm ? 1 : 0, pos, posStride, eps, theta, rot, mode, tab);
+  }
   attention(T, heads, kv, D, Q, qStride, A, B, rng, scale, O) {
     lib().attention(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, O);
   }

@@ -432,6 +432,15 @@ napi_value QkNormRope(napi_env env, napi_callback_info info) {
   END(dj_qk_norm_rope(R(0), I(1), I(2), I(3), I(4), I(5), P16(6), P16(7), P16(8), I(9), PI32(10), I(11), F(12), F(13),
                       I(14), I(15)));
 }
+napi_value RopeTable(napi_env env, napi_callback_info info) {
+  BEGIN(8);
+  END(dj_rope_table(R(0), I(1), PI32(2), I(3), F(4), I(5), I(6), PF32(7)));
+}
+napi_value MatmulQkvRope(napi_env env, napi_callback_info info) {
+  BEGIN(18);
+  END(dj_matmul_qkv_rope(R(0), P16(1), W(2), P16(3), I(4), I(5), I(6), I(7), P16(8), P16(9), I(10), PI32(11), I(12),
+                         F(13), F(14), I(15), I(16), PF32(17)));
+}
 napi_value Attention(napi_env env, napi_callback_info info) {
   BEGIN(12);
   const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
@@ -471,7 +480,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"graphClear", GraphClear}, {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
-      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"attention", Attention}, {"kvStore", KvStore},
+      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"kvStore", KvStore},
       {"leafLogits", LeafLogits}, {"readout", Readout}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
   };
   for (const auto &f : fns) {

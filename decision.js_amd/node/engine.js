@@ -165,7 +165,8 @@ class DecoderEngine extends GpuEngine {
     const lcap = Math.max(L * Math.max(nIds, 1), this.leafCapacity, 1024);
     const { H, I } = this;
     this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * this.stride * 2, y: cap * this.h * this.D * 2,
-      h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, leaves: lcap * 4, leafIds: lcap * 4, out: lcap * 4 });
+      h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, rope: cap * (this.D / 2) * 8, leaves: lcap * 4,
+      leafIds: lcap * 4, out: lcap * 4 });
     this.capacity = cap;
     this.leafCapacity = lcap;
   }
@@ -179,10 +180,12 @@ class DecoderEngine extends GpuEngine {
     const ptr = (name) => (w[name] ? w[name].ptr : 0n);
     rec.gatherQ(B.ids.ptr, T, w.embed, B.x.ptr);
     rec.addRmsnorm(T, H, false, eps, B.x.ptr, B.o.ptr, ptr("layers.0.operator_norm"), B.normed.ptr);
+    // the RoPE angles of this forward, once; every layer's qkv product applies q/k norm + RoPE with them
+    rec.ropeTable(T, B.pos.ptr, 1, this.theta, D, B.rope.ptr, L.ROPE_POW_NEG);
     for (let i = 0; i < this.layers; ++i) {
       const p = `layers.${i}.`;
-      rec.matmul(B.normed.ptr, w[p + "qkv"], z, T);
-      rec.qkNormRope(T, h, kv, D, this.stride, z, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1, eps, this.theta, D, L.ROPE_POW_NEG);
+      rec.matmulQkvRope(B.normed.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1, eps,
+        this.theta, B.rope.ptr, D, L.ROPE_POW_NEG);
       if (kvStore) rec.kvStore(T, kv, D, z, this.stride, h * D, kvStore.at(i * T * 2 * kv * D * 2), 0);
       rec.attention(T, h, kv, D, z, this.stride, kvA ? kvA(i) : src, src, B.rng.ptr, 1 / Math.sqrt(D), B.y.ptr);
       rec.matmul(B.y.ptr, w[p + "o_proj"], B.o.ptr, T);

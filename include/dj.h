@@ -177,6 +177,23 @@ int dj_qk_norm_rope(dj_rec *rec, int T, int heads, int kv, int D, int stride, ui
                     const uint16_t *qn_dev, const uint16_t *kn_dev, int vnorm, const int32_t *pos_dev,
                     int pos_stride, float eps, float theta, int rot, int rope_mode);
 
+/* The (cos, sin) pairs dj_qk_norm_rope computes for each token, kept for a whole forward:
+ * tab[t * rot/2 + i] = (cos a, sin a), a = f32(pos[t * pos_stride] * f_i), f_i as dj_qk_norm_rope (mode).
+ * tab_dev holds T * rot/2 float pairs. The reference recomputes these angles in every layer's QK_NORM_ROPE
+ * dispatch (kernels.ts:99-107); one table per forward feeds dj_matmul_qkv_rope in every layer. */
+int dj_rope_table(dj_rec *rec, int T, const int32_t *pos_dev, int pos_stride, float theta, int rot, int rope_mode,
+                  float *tab_dev);
+
+/* recorder().matmul(X, w_qkv, Z, M) (gpu.ts:202-226) followed by QK_NORM_ROPE (kernels.ts:86-112) on Z: the
+ * same results as dj_matmul then dj_qk_norm_rope(M, heads, kv, D, stride = w->N, Z, qn, kn, vnorm, pos,
+ * pos_stride, eps, theta, rot, rope_mode). tab_dev: dj_rope_table of the same positions, theta, rot and mode
+ * (M rows). For D = 128, M > 64 and at most two 128-row head tiles per CU the norm and rotation run in the
+ * product's epilogue on tab_dev's angles (one head per tile, one kernel instead of two); otherwise as the two
+ * kernels. */
+int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *Z_dev, int M, int heads,
+                       int kv, int D, const uint16_t *qn_dev, const uint16_t *kn_dev, int vnorm, const int32_t *pos_dev,
+                       int pos_stride, float eps, float theta, int rot, int rope_mode, const float *tab_dev);
+
 /* Key/value source of dj_attention: `rows` rows of `stride` halves; K of kv head j at column k_col + j*D,
  * V at v_col + j*D. Key indices outside [0, rows) are clamped (never read out of bounds). */
 typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_col; } dj_kv_src;

@@ -236,6 +236,54 @@ def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
     assert np.abs(ln(g) - ln(w)).max() <= 4e-3 * max(1.0, ln(w).max())
 
 
+@pytest.mark.parametrize("M,heads,kv,D,qk,vnorm,rot,bits", [
+    (300, 16, 8, 128, True, False, 128, 8),    # fused: one head per tile (144 / 128 / 64-row tiles)
+    (1152, 16, 8, 128, True, False, 128, 8),   # the bench's qkv shape
+    (8192, 16, 8, 128, True, False, 128, 8),   # more than two tiles per CU: the product, then the standalone kernel
+    (1536, 16, 2, 128, True, False, 128, 4),   # q4, GQA 8:1
+    (300, 12, 2, 128, False, True, 64, 8),     # partial rotation (16 lanes a row), no q/k weights, v norm
+    (200, 6, 2, 128, True, False, 96, 8),
+    (40, 16, 8, 128, True, False, 128, 8),     # skinny M: the product and the standalone kernel
+    (300, 8, 4, 64, True, False, 64, 8),       # D 64: no 128-wide head tile, two kernels
+])
+def test_matmul_qkv_rope_matches_two_ops(pkg, ctx, M, heads, kv, D, qk, vnorm, rot, bits):
+    """dj_matmul_qkv_rope (the forward's RoPE table, norm + rotation in the product's epilogue where it fits)
+    gives the same bits as dj_matmul followed by dj_qk_norm_rope (which computes its own angles); and the
+    table itself is the angles' cos and sin."""
+    dj = _dj()
+    rng = np.random.default_rng(M + heads + D + rot)
+    K = 1024
+    N = (heads + 2 * kv) * D
+    codes, scales = quant(rng, N, K, bits)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA)
+    X = rand_f16(rng, (M, K))
+    pos = rng.integers(0, 3000, M).astype(np.int32)
+    qn, kn = (1 + rng.standard_normal(D) * 0.1).astype(np.float16), (1 + rng.standard_normal(D) * 0.1).astype(np.float16)
+    dX, dpos, dq, dk = ctx.array(X), ctx.array(pos), ctx.array(qn), ctx.array(kn)
+    dZ1, dZ2, dtab = ctx.alloc(M * N * 2), ctx.alloc(M * N * 2), ctx.alloc(M * (rot // 2) * 8)
+    theta, eps = 1e6, 1e-6
+
+    def two(r):
+        r.matmul(dX, W, dZ1, M)
+        r.qk_norm_rope(M, heads, kv, D, N, dZ1, dq if qk else None, dk if qk else None, vnorm, dpos, 1, eps, theta, rot)
+
+    def fused(r):
+        r.rope_table(M, dpos, 1, theta, rot, dtab)
+        r.matmul_qkv_rope(dX, W, dZ2, M, heads, kv, D, dq if qk else None, dk if qk else None, vnorm, dpos, 1, eps, theta,
+                          dtab, rot)
+    run(ctx, two)
+    run(ctx, fused)
+    a, b = dZ1.read(np.uint16, (M, N)), dZ2.read(np.uint16, (M, N))
+    assert np.array_equal(a, b), f"{int((a != b).sum())} of {a.size} halves differ"
+    tab = dtab.read(np.float32, (M, rot // 2, 2)).astype(np.float64)
+    ang = pos[:, None].astype(np.float64) * ref.inv_freq(theta, rot, 0)[None, :]
+    assert np.abs(tab[..., 0] - np.cos(ang)).max() < 2e-3 and np.abs(tab[..., 1] - np.sin(ang)).max() < 2e-3
+    # and the fused result against the oracle (the product rounded to f16, then the op)
+    want = ref.qk_norm_rope(ref.matmul(X, ref.dequant_f16(codes, scales, bits), np.float64), heads, kv, D, pos,
+                            qn if qk else None, kn if qk else None, vnorm, eps, theta, rot, 0, np.float64)
+    assert f16_close(b.view(np.float16), want, ulps=4.0, atol=2e-3) <= 1.0
+
+
 # ---------------------------------------------------------------- attention
 
 def _forest_case(rng, trunks_branches):
