@@ -29,31 +29,70 @@ typedef short s4 __attribute__((ext_vector_type(4)));
 // 16-byte chunks XOR-swizzled per row. K: chunk c of key r at c ^ (r & KSW) (conflict-free 16-byte MFMA reads of
 // 16 keys x one chunk). V: chunk c at c ^ vswz(r), chosen so the transposing reads below (4 keys x 2 chunks per
 // 16 lanes) hit distinct banks.
-template <int D, int RING, int KG>
+template <int D, int RING, int KG, int HG>
 struct AttnShape {
+  static_assert(KG == 1 || HG == 1, "key groups and head groups are not combined");
+  static constexpr int NW = 4 * KG * HG;                        // waves per workgroup
   static constexpr int CH = D / 8;                              // 16-byte chunks per key row
   static constexpr int KSW = CH >= 16 ? 15 : 7;
   static constexpr int TILE = 64 * 2 * D;                       // bytes of K (or V) per 64-key tile
   static constexpr int STAGE = 2 * TILE;
   // ring depth: RING, or 0 = 4 stages where they fit in 128 KB, else 2
   static constexpr int NS = RING ? RING : 4 * STAGE <= 128 * 1024 ? 4 : 2;
-  static constexpr int IK = TILE / 1024 / (4 * KG);             // 1 KB DMAs per wave per tile, K (and V)
-  static_assert(TILE % (1024 * 4 * KG) == 0, "a tile must split into whole 1 KB DMAs per wave");
+  static constexpr int IK = TILE / 1024 / NW;                   // 1 KB DMAs per wave per tile, K (and V)
+  static_assert(TILE % (1024 * NW) == 0, "a tile must split into whole 1 KB DMAs per wave");
   static constexpr int I = 2 * IK;                              // vector-memory ops per wave per tile
   static_assert((NS - 2) * I < 64, "vmcnt range");
   __device__ static int vswz(int r) { return D >= 128 ? 2 * (r & 7) : 2 * ((r >> 1) & 3); }
 };
 
-template <int D, int RING, int KG>
-__global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
+// Max and sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lanes that hold one query's scores in an MFMA
+// accumulator) by gfx950's VALU lane swaps: permlane32_swap(v, v) leaves (v[l], v[l ^ 32]) in its two results,
+// permlane16_swap(v, v) (v[l], v[l ^ 16]). The sum adds the l ^ 16 partner first, then the l ^ 32 one.
+__device__ __forceinline__ float xmax4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xsum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Min / max over the 16 lanes of each row by DPP (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror:
+// each step combines disjoint lane sets), and over the whole wave by the two row-swapping permlanes after it.
+template <bool MAX>
+__device__ __forceinline__ int minmax(int a, int b) { return MAX ? max(a, b) : min(a, b); }
+template <bool MAX>
+__device__ __forceinline__ int row_reduce(int v) {
+  v = minmax<MAX>(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false));
+  v = minmax<MAX>(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false));
+  v = minmax<MAX>(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false));
+  return minmax<MAX>(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false));
+}
+template <bool MAX>
+__device__ __forceinline__ int wave_reduce(int v) {
+  v = row_reduce<MAX>(v);
+  const auto a = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  v = minmax<MAX>((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return minmax<MAX>((int)b[0], (int)b[1]);
+}
+
+template <int D, int RING, int KG, int HG>
+__global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
                                               uint16_t *__restrict__ O, int splits, float *__restrict__ part) {
-  using S = AttnShape<D, RING, KG>;
+  using S = AttnShape<D, RING, KG, HG>;
   constexpr int KW = 64 / KG;          // keys of each tile this wave scores (KG key groups split a tile)
   constexpr int NB = KW / 16;          // 16-key blocks of S^T per wave and tile
   constexpr int NT = KW / 32;          // 32-key MFMA steps of P V per wave and tile
   constexpr int NS_ = D / 32;  // MFMA k-steps over the head dim
   constexpr int NDB = D / 16;  // 16-row blocks of O^T
+  constexpr bool PRE_V = D <= 128;  // V^T fragments read ahead of the scores (register budget)
   constexpr int CH = S::CH, KSW = S::KSW, TILE = S::TILE, STAGE = S::STAGE, NS = S::NS;
   constexpr float LOG2E = 1.4426950408889634f;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
@@ -61,7 +100,8 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c16 = lane & 15;
   const int kg = KG > 1 ? wave >> 2 : 0, wq = wave & 3;  // key group; which 16 queries of the block
-  const int h = blockIdx.y, q0 = blockIdx.x * 64;
+  // head group: HG query heads that share one KV head, 4 waves each, staging every K/V tile once
+  const int h = blockIdx.y * HG + (HG > 1 ? wave >> 2 : 0), q0 = blockIdx.x * 64;
   const int kvh = h / (heads / kv);
 
   // Q fragments first: nothing below depends on them until the first MFMA
@@ -86,19 +126,16 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
   // keys every live query of the wave sees: [max low, min high) (a query past T does not constrain it)
   int wl2[2] = {qi < T ? rq.x : INT_MIN, qi < T ? rq.z : INT_MIN};
   int wh2[2] = {qi < T ? rq.y : INT_MAX, qi < T ? rq.w : INT_MAX};
+  // (every row of 16 lanes holds the same 16 queries of the wave, so a row reduction is the wave's value)
 #pragma unroll
-  for (int x = 1; x < 64; x <<= 1)
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      blo[s] = min(blo[s], __shfl_xor(blo[s], x, 64));
-      bhi[s] = max(bhi[s], __shfl_xor(bhi[s], x, 64));
-      if (x < 16) {
-        wlo[s] = min(wlo[s], __shfl_xor(wlo[s], x, 64));
-        whi[s] = max(whi[s], __shfl_xor(whi[s], x, 64));
-        wl2[s] = max(wl2[s], __shfl_xor(wl2[s], x, 64));
-        wh2[s] = min(wh2[s], __shfl_xor(wh2[s], x, 64));
-      }
-    }
+  for (int s = 0; s < 2; ++s) {
+    blo[s] = wave_reduce<false>(blo[s]);
+    bhi[s] = wave_reduce<true>(bhi[s]);
+    wlo[s] = row_reduce<false>(wlo[s]);
+    whi[s] = row_reduce<true>(whi[s]);
+    wl2[s] = row_reduce<true>(wl2[s]);
+    wh2[s] = row_reduce<false>(wh2[s]);
+  }
   const int loA = max(__builtin_amdgcn_readfirstlane(blo[0]), 0), hiA = min(__builtin_amdgcn_readfirstlane(bhi[0]), A.rows);
   const int loB = max(__builtin_amdgcn_readfirstlane(blo[1]), 0), hiB = min(__builtin_amdgcn_readfirstlane(bhi[1]), B.rows);
 #pragma unroll
@@ -153,6 +190,19 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
     for (int p = 0; p < NS - 1; ++p) issue(j0 + min(p, nloc - 1), p);  // a short range re-loads its last tile
   }
 
+  // V^T fragment of 32-key step t, dims 16 db..+15 (A operand of O^T += V^T P^T), by two transposing reads:
+  // within 16 lanes, lane i points at key 32t + 4g + i/4, dims 16db + 4(i%4)..+3, and receives dim 16db + i of
+  // keys 32t + 4g + 0..3 (then the same 16 keys on), the key order of the S^T accumulator that became P^T
+  auto read_vt = [&](const uint8_t *vt, int t, int db) -> h8 {
+    const int key = 32 * t + 4 * g + (c16 >> 2);
+    const int c = 2 * db + ((c16 & 3) >> 1), half8 = (c16 & 1) * 8;
+    const uint8_t *p0 = vt + key * (2 * D) + ((c ^ S::vswz(key)) * 16) + half8;
+    const uint8_t *p1 = vt + (key + 16) * (2 * D) + ((c ^ S::vswz(key + 16)) * 16) + half8;
+    const h4 lo = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p0));
+    const h4 hi4 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p1));
+    return (h8){lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+  };
+
   f4 o[NDB];
 #pragma unroll
   for (int i = 0; i < NDB; ++i) o[i] = (f4){0.f, 0.f, 0.f, 0.f};
@@ -173,18 +223,34 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
     const int qlo = sb ? rq.z : rq.x, qhi = sb ? rq.w : rq.y;
     const int kb0 = k0 + KW * kg;  // this wave's keys of the tile: [kb0, kb0 + KW)
     if (kb0 < whi[sb] && kb0 + KW > wlo[sb]) {
+      // Every K fragment of the tile (and at D <= 128 every V^T fragment) is read from LDS before the first
+      // MFMA, so a tile waits for one LDS latency instead of one per MFMA pair; V needs no score, so its reads
+      // run under the QK^T MFMAs and the softmax. The scheduling barrier keeps the compiler from sinking the
+      // reads back to their uses.
+      h8 kf[NB][NS_];
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) {
+        const int r = 16 * (NB * kg + bb) + c16;
+#pragma unroll
+        for (int s = 0; s < NS_; ++s) kf[bb][s] = __builtin_bit_cast(h8, Ks[r * CH + ((4 * s + g) ^ (r & KSW))]);
+      }
+      const uint8_t *vt = st + TILE;
+      h8 vf[PRE_V ? NT : 1][NDB];
+      if constexpr (PRE_V) {
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) vf[tt][db] = read_vt(vt, NT * kg + tt, db);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       // S^T[key, q] = K . Q^T: A = 16 keys x 32 dims of K, B = the query fragment
       f4 sc[NB];
 #pragma unroll
-      for (int bb = 0; bb < NB; ++bb) {
-        sc[bb] = (f4){0.f, 0.f, 0.f, 0.f};
-        const int r = 16 * (NB * kg + bb) + c16;
+      for (int bb = 0; bb < NB; ++bb) sc[bb] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < NS_; ++s) {
-          const h8 kf = __builtin_bit_cast(h8, Ks[r * CH + ((4 * s + g) ^ (r & KSW))]);
-          sc[bb] = MFMA16(kf, qf[s], sc[bb]);
-        }
-      }
+      for (int s = 0; s < NS_; ++s)
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) sc[bb] = MFMA16(kf[bb][s], qf[s], sc[bb]);
       // Tiles that every query of the wave sees whole (all but the diagonal ones of a causal block) skip the
       // per-key mask.
       const bool whole = kb0 >= wl2[sb] && kb0 + KW <= wh2[sb] && kb0 + KW <= hi;
@@ -209,8 +275,7 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
             tmax = fmaxf(tmax, v);
           }
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+      tmax = xmax4(tmax);
       // Lazy rescaling: the reference point m moves (and O, l are rescaled) only when some query's maximum
       // has grown by more than 8 (log2 units); otherwise p = exp2(s - m) <= 2^8 stays exact enough in f16
       // and O / l is unchanged. The first live tile always moves m off -1e30.
@@ -233,25 +298,12 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
           pf[bb >> 1][(bb & 1) * 4 + r] = (_Float16)p;
         }
       lsum += ps;
-      // O^T[d, q] += V^T . P^T. A = V^T (16 dims x keys {32t + 4g + 0..3, 32t + 16 + 4g + 0..3}, the key order
-      // of the S^T accumulator that became P^T) read by two transposing loads: within 16 lanes, lane i points
-      // at key 32t + 4g + i/4, dims 16db + 4(i%4)..+3, and receives dim 16db + i of keys 32t + 4g + 0..3.
-      const uint8_t *vt = st + TILE;
+      // O^T[d, q] += V^T . P^T: A = V^T (16 dims x keys {32t + 4g + 0..3, 32t + 16 + 4g + 0..3}, read_vt), B = P^T
 #pragma unroll
-      for (int tt = 0; tt < NT; ++tt) {
-        const int t = NT * kg + tt;
-        const int key = 32 * t + 4 * g + (c16 >> 2);
+      for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const int c = 2 * db + ((c16 & 3) >> 1), half8 = (c16 & 1) * 8;
-          const uint8_t *p0 = vt + key * (2 * D) + ((c ^ S::vswz(key)) * 16) + half8;
-          const uint8_t *p1 = vt + (key + 16) * (2 * D) + ((c ^ S::vswz(key + 16)) * 16) + half8;
-          const h4 lo = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p0));
-          const h4 hi4 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4 *)p1));
-          const h8 vf = {lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-          o[db] = MFMA16(vf, pf[tt], o[db]);
-        }
-      }
+        for (int db = 0; db < NDB; ++db)
+          o[db] = MFMA16(PRE_V ? vf[PRE_V ? tt : 0][db] : read_vt(vt, NT * kg + tt, db), pf[tt], o[db]);
     }
   }
   wait_vm<0>();  // the clamped tail DMAs land before the wave ends
@@ -279,8 +331,7 @@ __global__ __launch_bounds__(256 * KG) void k_attn(int T, int heads, int kv, con
     m = mm;
   }
 
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
+  lsum = xsum4(lsum);
   if (splits > 1) {
     // partial of this split: unnormalized f32 O^T and (m, l) per query and head, merged by k_attn_combine
     if (qi < T) {
@@ -363,6 +414,16 @@ __global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int spli
   for (int i = 0; i < DPL; ++i) o[i] = __builtin_bit_cast(uint16_t, (_Float16)(L > 0.f ? acc[i] / L : 0.f));
 }
 
+// Launch with one workgroup shape; a shape whose K/V tile does not split into whole 1 KB DMAs per wave is never
+// picked, nor one that would spill registers (the launcher falls back to HG 1 for them).
+template <int D, int RING, int KG, int HG>
+static void attn_launch(dim3 g3, hipStream_t s, int T, int heads, int kv, const uint16_t *Q, int q_stride,
+                        dj_kv_src A, dj_kv_src B, const int4 *r4, float scale, uint16_t *O, int splits, float *part) {
+  if constexpr ((64 * 2 * D) % (1024 * 4 * KG * HG) == 0 && D * HG <= 256 &&  // (D 128 x HG 4 would spill)
+                RING * 2 * (64 * 2 * D) <= 160 * 1024)
+    k_attn<D, RING, KG, HG><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);
+}
+
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O) {
   hipStream_t s = c->stream;
@@ -387,19 +448,35 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
     if (splits > 1 && c->gemm_ws) part = c->gemm_ws;
     else splits = 1;
   }
-  const dim3 g3(qblocks, heads, splits);
-  // two-stage ring: two workgroups fit per CU and hide each other's latency. Measured on MI355X (D 128,
-  // causal): 13.6 vs 18.0 us with a 4-stage ring (one workgroup per CU) at T = 1152, 504 vs 719 us at 86016
+  // Ring depth: two stages for 4-wave workgroups (two workgroups fit per CU and hide each other's latency:
+  // 13.6 vs 18.0 us with a 4-stage ring, one workgroup per CU, at T = 1152, D 128 causal; 504 vs 719 us at
+  // 86016), and the deepest that fits 128 KB for head groups.
   // key groups per workgroup: one. Two (8 waves, each scoring half of every key tile, merged in LDS) measured
   // slower at D 128 (32.7 vs 30.3 us at 1 x 1152, 46.8 vs 42.5 at 16 x 384) and mixed at D 256 (35.1 vs 37.6
   // us at 2 x 1024 causal, 8 heads, but 23.5 vs 20.5 us in the encoder's 384-token layer). DJ_ATTN_KG=2
   // selects them (tuning sweeps; covered by the attention tests).
   const char *kgs = getenv("DJ_ATTN_KG");
   const int kg = kgs ? atoi(kgs) : 1;
+  // head groups: HG query heads sharing a KV head in one workgroup (4 HG waves) stage each K/V tile once, which
+  // halves (HG 2) the workgroups and the K/V reads and leaves LDS for a 4-stage ring (one workgroup per CU).
+  // DJ_ATTN_HG=<1|2|4> forces it (tuning sweeps).
+  const char *hgs = getenv("DJ_ATTN_HG");
+  // By default only large grids take them (the 192-sequence batch: 592 vs 616 us); at a ticket's few hundred
+  // workgroups the 4-wave form is faster (14.3 vs 15.1 us at 3 x 384, 11.0 vs 14.7 at 1 x 384; MI355X).
+  int hg = hgs ? atoi(hgs) : (splits == 1 && (heads / kv) % 2 == 0 && grid >= 16L * c->cus ? 2 : 1);
+  if (kg > 1 || (hg != 1 && hg != 2 && hg != 4) || (heads / kv) % hg || (128 * D) % (4096 * hg) || D * hg > 256) hg = 1;
+  // DJ_ATTN_RING=<3|4> deepens the 4-wave form's ring (tuning sweeps; at D 256 a stage is 64 KB, so 2)
+  const char *rs = getenv("DJ_ATTN_RING");
+  const int ring = rs && D <= 128 ? atoi(rs) : 2;
+  const dim3 g3(qblocks, heads / hg, splits);
 #define DJ_ATTN_CASE(DD)                                                                                              \
   case DD:                                                                                                            \
-    if (kg == 1) k_attn<DD, 2, 1><<<g3, 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);    \
-    else k_attn<DD, 2, 2><<<g3, 512, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);            \
+    if (kg > 1) attn_launch<DD, 2, 2, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);         \
+    else if (hg == 2) attn_launch<DD, 0, 1, 2>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);   \
+    else if (hg == 4) attn_launch<DD, 0, 1, 4>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);   \
+    else if (ring == 3) attn_launch<DD, 3, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); \
+    else if (ring == 4) attn_launch<DD, 4, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); \
+    else attn_launch<DD, 2, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);                \
     break;
   switch (D) {
     DJ_ATTN_CASE(64)

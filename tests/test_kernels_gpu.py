@@ -295,12 +295,18 @@ def _forest_case(rng, trunks_branches):
     return meta, ref.forest_ranges(meta)
 
 
-@pytest.mark.parametrize("kg", [1, 2])
-@pytest.mark.parametrize("heads,kv,D", [(16, 8, 128), (16, 2, 128), (12, 2, 128), (3, 1, 256), (4, 2, 64)])
-def test_attention_forest(pkg, ctx, monkeypatch, heads, kv, D, kg):
-    """The forest mask through both workgroup forms: one key group (the default) and two (8 waves, each
-    scoring half of every key tile, merged through LDS)."""
-    monkeypatch.setenv("DJ_ATTN_KG", str(kg))
+ATTN_FORMS = {"default": {}, "kg2": {"DJ_ATTN_KG": "2"}, "hg1": {"DJ_ATTN_HG": "1"}, "hg2": {"DJ_ATTN_HG": "2"},
+              "hg4": {"DJ_ATTN_HG": "4"}}
+
+
+@pytest.mark.parametrize("form", list(ATTN_FORMS))
+@pytest.mark.parametrize("heads,kv,D", [(16, 8, 128), (16, 2, 128), (12, 2, 128), (3, 1, 256), (4, 2, 64), (8, 2, 256)])
+def test_attention_forest(pkg, ctx, monkeypatch, heads, kv, D, form):
+    """The forest mask through every workgroup form: one head and one key group (4 waves), two key groups (8
+    waves, each scoring half of every key tile, merged through LDS), and head groups of 2 or 4 query heads
+    sharing a KV head (8 or 16 waves staging each K/V tile once); a form that does not apply falls back."""
+    for k, v in ATTN_FORMS[form].items():
+        monkeypatch.setenv(k, v)
     dj = _dj()
     rng = np.random.default_rng(heads + kv + D)
     meta, rng4 = _forest_case(rng, [(100, [20, 37, 5]), (70, [64, 1]), (0, [90]), (130, [])])
@@ -320,11 +326,12 @@ def test_attention_forest(pkg, ctx, monkeypatch, heads, kv, D, kg):
     assert err < 4e-3
 
 
-@pytest.mark.parametrize("kg", [1, 2])
-def test_attention_large_grid(pkg, ctx, monkeypatch, kg):
+@pytest.mark.parametrize("form", list(ATTN_FORMS))
+def test_attention_large_grid(pkg, ctx, monkeypatch, form):
     """A varlen batch of causal sequences large enough (>= 512 workgroups) for the two-stage K/V ring, and
     long enough that the lazy max-rescaling and the unmasked-tile path both run many times."""
-    monkeypatch.setenv("DJ_ATTN_KG", str(kg))
+    for k, v in ATTN_FORMS[form].items():
+        monkeypatch.setenv(k, v)
     dj = _dj()
     rng = np.random.default_rng(41)
     heads, kv, D = 16, 8, 128
@@ -365,13 +372,16 @@ def test_attention_bidirectional_and_windows(pkg, ctx, D):
         assert np.abs(got - want).max() < 4e-3
 
 
-@pytest.mark.parametrize("P,splits", [(300, None), (1100, None), (300, 4), (1100, 16), (1100, 1)])
-def test_attention_kept_prefix(pkg, ctx, monkeypatch, P, splits):
+@pytest.mark.parametrize("P,splits,hg", [(300, None, None), (1100, None, None), (300, 4, None), (1100, 16, None),
+                                         (1100, 1, None), (1100, 4, 2), (1100, 1, 2), (300, None, 1)])
+def test_attention_kept_prefix(pkg, ctx, monkeypatch, P, splits, hg):
     """Source A = a kept K/V cache (the shared state), source B = the current rows: same result as one pass.
     A 1100-row cache is split over workgroups by default (partials merged by k_attn_combine); the split count
-    is also forced (4, 16) and turned off (1)."""
+    is also forced (4, 16) and turned off (1), alone and with head groups of 2 forced (or off)."""
     if splits is not None:
         monkeypatch.setenv("DJ_ATTN_SPLITS", str(splits))
+    if hg is not None:
+        monkeypatch.setenv("DJ_ATTN_HG", str(hg))
     dj = _dj()
     rng = np.random.default_rng(5 + P)
     heads, kv, D = 12, 2, 128
