@@ -167,12 +167,37 @@ __device__ __forceinline__ float2 rope_cs(float ps, int j, int rot, float theta,
 }
 // One lane's share of a head row: LPH consecutive lanes hold the row. A pair lane (pl) holds dims d0..d0+7 in
 // x and their partners d0 + rot/2.. in y; a tail lane (tl) holds 8 unrotated dims in x (y zero); others hold
-// zeros. Every lane of the group must call this (the row's sum of squares is a shuffle over LPH lanes).
+// zeros. Every lane of the group must call this (the row's sum of squares is a reduction over LPH lanes).
 // x / rms(row) (when norm), times the norm weight w (when given), then the rotation by cs(i) = (cos, sin) of
 // pair d0 + i (when rope); results rounded to f16.
 struct h8x2 {
   h8 x, y;
 };
+
+// Sums over aligned groups of L lanes (L = 4 ... 64) without LDS permutes: the row-swapping permlanes add lanes
+// l ^ 32 (L = 64) and l ^ 16 (L >= 32); then DPP within each 16-lane row adds l ^ 8 (row_ror 8, L >= 16), the
+// mirror lane of each half-row (row_half_mirror, L >= 8), l ^ 2 and l ^ 1 (quad_perm). Each step adds a lane to its partner, so
+// every lane of a group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(L == 4 || L == 8 || L == 16 || L == 32 || L == 64, "lane groups of 4 to 64");
+  if constexpr (L == 64) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  if constexpr (L >= 32) {
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  }
+  if constexpr (L >= 16) v += dpp_f<0x128>(v);
+  if constexpr (L >= 8) v += dpp_f<0x141>(v);
+  v += dpp_f<0x4E>(v);
+  return v + dpp_f<0xB1>(v);
+}
 template <int LPH, typename CS>
 __device__ __forceinline__ h8x2 norm_rope_lane(h8 x, h8 y, h8 wx, h8 wy, bool has_w, bool norm, bool rope, bool pl, int D,
                                                float eps, CS cs) {
@@ -180,8 +205,7 @@ __device__ __forceinline__ h8x2 norm_rope_lane(h8 x, h8 y, h8 wx, h8 wy, bool ha
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i] + (float)y[i] * (float)y[i];
-#pragma unroll
-  for (int o = LPH / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = group_sum<LPH>(ss);
   const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
   if (pl) {
 #pragma unroll

@@ -7,11 +7,7 @@
 
 #define WAVE 64
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 __device__ __forceinline__ _Float16 u2h(uint16_t u) { return __builtin_bit_cast(_Float16, u); }
 __device__ __forceinline__ uint16_t h2u(_Float16 h) { return __builtin_bit_cast(uint16_t, h); }
