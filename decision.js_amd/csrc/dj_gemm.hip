@@ -133,7 +133,9 @@ struct GemmShape {
   // LDS for more workgroups per CU, which on MI355X hides more latency than a deeper ring does.
   // (a RING deeper than LDS holds, e.g. for the twice-as-large f16 weight blocks, is cut to what fits)
   static constexpr int NS_FIT = 160 * 1024 / STAGE;
-  static constexpr int NS = RING ? (RING < NS_FIT ? RING : NS_FIT) : 4 * STAGE <= 160 * 1024 ? 4 : 3;
+  // RING < 0: a paired ring of -RING stages (steps land, and the workgroup synchronizes, two at a time)
+  static constexpr bool PAIRED = RING < 0;
+  static constexpr int NS = PAIRED ? -RING : RING ? (RING < NS_FIT ? RING : NS_FIT) : 4 * STAGE <= 160 * 1024 ? 4 : 3;
   static constexpr int TA = A_BYTES / 1024, IA = (TA + NW - 1) / NW; // 16-byte-per-lane DMAs per wave and step
   static constexpr int TB = B_BYTES / 1024, IB = (TB + NW - 1) / NW;
   static constexpr int IS = BITS == 16 ? 0 : 1;                       // 4-byte-per-lane DMA (scales)
@@ -141,6 +143,7 @@ struct GemmShape {
   static_assert(A_BYTES % 1024 == 0, "A stage must split into whole 1 KB rows");
   static_assert(NB <= 4 * NW, "scale rows cover 4 blocks per wave");
   static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
+  static_assert(!PAIRED || (NS % 2 == 0 && NS >= 4 && (NS / 2 - 2) * 2 * I < 64), "paired ring");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
   // waves per SIMD that LDS allows (workgroups per CU x waves per workgroup / 4 SIMDs): the register budget
   // the compiler may use without costing occupancy. Left to itself it squeezes a 128x128 tile to 120 VGPRs
@@ -270,12 +273,31 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
   // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
   // have been issued (min(NS - 2, KS - 1) for t = 0), so min(NS - 3, KS - 1 - t) later steps may still be in
   // flight — the full ring depth until the tail, then exact counts (no re-loads of the last step to wait for).
-  // prologue: steps 0 .. NS-2 in flight
+  // prologue: steps 0 .. NS-2 in flight (paired ring: pairs 0 .. NS/2-2, steps 0 .. NS-3)
 #pragma unroll
-  for (int p = 0; p < NS - 1; ++p)
+  for (int p = 0; p < (S::PAIRED ? NS - 2 : NS - 1); ++p)
     if (p < KS) issue(p, p);
 
-  if constexpr (NS == 2) {
+  if constexpr (S::PAIRED) {
+    // Paired ring (NP = NS / 2 pairs of stages; KS even): steps land two at a time, so the counter wait and the
+    // workgroup barrier come once per 128 K. At pair p: pairs p+1 .. p+NP-2 may still be in flight; after the
+    // barrier every wave is done with pair p-1, whose stages take pair p+NP-1. Both steps' fragments are read
+    // before the first MFMA.
+    constexpr int NP = NS / 2;
+    const int KP = KS / 2;
+    h8 a0[FM][2], a1[FM][2];
+    RawB<BITS> r0[FN], r1[FN];
+    uint32_t p0[FN], p1[FN];
+    for (int kp = 0; kp < KP; ++kp) {
+      wait_steps_barrier<2 * S::I, NP - 2>(min(NP - 2, KP - 1 - kp));
+      const int nx = kp + NP - 1;
+      if (nx < KP) { issue(2 * nx, (2 * nx) % NS); issue(2 * nx + 1, (2 * nx + 1) % NS); }
+      DJ_READ(2 * kp, a0, r0, p0);
+      DJ_READ(2 * kp + 1, a1, r1, p1);
+      DJ_MMA(a0, r0, p0);
+      DJ_MMA(a1, r1, p1);
+    }
+  } else if constexpr (NS == 2) {
     // two stages: read a step's fragments right after its barrier, then compute it
     for (int kt = 0; kt < KS; ++kt) {
       // this wave's DMAs of step kt are done (nothing later is in flight); after the barrier every wave's
@@ -636,7 +658,9 @@ struct GemmCfg {
   X(33, "128x128n6", 1, 4, 8, 2, 6) X(34, "64x128n4", 1, 4, 4, 2, 4) X(35, "64x128n6", 1, 4, 4, 2, 6)        \
   X(36, "144x128w8", 1, 8, 9, 1, 2) X(37, "144x128w8r3", 1, 8, 9, 1, 3) X(38, "128x128w8", 2, 4, 4, 2, 2)     \
   X(39, "64x128w8", 1, 8, 4, 1, 2) X(40, "32x64w8", 2, 4, 1, 1, 0) X(41, "128x256w8", 1, 8, 8, 2, 2)          \
-  X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)
+  X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)                                    \
+  X(44, "32x64p4", 1, 4, 2, 1, -4) X(45, "32x64p6", 1, 4, 2, 1, -6) X(46, "128x128np4", 1, 4, 8, 2, -4)      \
+  X(47, "144x128np4", 1, 4, 9, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)
 #define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -662,8 +686,8 @@ static void launch_index(int i, hipStream_t s, GemmArgs a) {
 
 // epi: 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (the tile is one 128-wide head, <= 144 rows)
 static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
-  (void)K;
-  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144));
+  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144)) &&
+         (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time
 }
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
@@ -675,7 +699,8 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
 //   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
 //               against 17-18 for 64x128n),
 //   64x128n     when it gives >= 2 tiles per CU,
-//   32x64       when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows),
+//   32x64p4     when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows; the paired 4-stage ring,
+//               K / 64 even: 13.4 vs 13.9 us and 19.2 vs 19.9 us at 1152 x 1024 x 2048 / 3072), else 32x64,
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
 static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int &splits) {
@@ -689,8 +714,8 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; } rules[] = {
-        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {24, 1.0, 0}, {21, 2.0, 0}, {8, 2.0, 0},
-        {16, 2.0, 0}};
+        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {24, 1.0, 0}, {21, 2.0, 0}, {44, 2.0, 0},
+        {8, 2.0, 0}, {16, 2.0, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
@@ -715,7 +740,7 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
     const long t = tiles(cfg);
     while (t * splits * 4 < cus && KT % (splits * 2) == 0 && KT / (splits * 2) >= 4) splits *= 2;
   }
-  if (splits < 1 || KT % splits || !ws_ok || glu == 2) splits = 1;
+  if (splits < 1 || KT % splits || !ws_ok || glu == 2 || kCfgs[cfg].ring < 0) splits = 1;
 }
 
 // Profile labels "matmul[_glu|_rope]_<q4|q8|f16>_<tile>", built when the library loads.
