@@ -133,9 +133,12 @@ struct GemmShape {
   // LDS for more workgroups per CU, which on MI355X hides more latency than a deeper ring does.
   // (a RING deeper than LDS holds, e.g. for the twice-as-large f16 weight blocks, is cut to what fits)
   static constexpr int NS_FIT = 160 * 1024 / STAGE;
-  // RING < 0: a paired ring of -RING stages (steps land, and the workgroup synchronizes, two at a time)
-  static constexpr bool PAIRED = RING < 0;
-  static constexpr int NS = PAIRED ? -RING : RING ? (RING < NS_FIT ? RING : NS_FIT) : 4 * STAGE <= 160 * 1024 ? 4 : 3;
+  // RING < 0: a paired ring of -RING stages (steps land, and the workgroup synchronizes, two at a time), cut to
+  // the even depth LDS holds; where that is under 4 (f16 weight blocks on wide tiles) a plain 2-stage ring
+  static constexpr int NS_PAIR = -RING < (NS_FIT & ~1) ? -RING : (NS_FIT & ~1);
+  static constexpr bool PAIRED = RING < 0 && NS_PAIR >= 4;
+  static constexpr int NS = PAIRED ? NS_PAIR : RING < 0 ? 2 : RING ? (RING < NS_FIT ? RING : NS_FIT)
+                                                                     : 4 * STAGE <= 160 * 1024 ? 4 : 3;
   static constexpr int TA = A_BYTES / 1024, IA = (TA + NW - 1) / NW; // 16-byte-per-lane DMAs per wave and step
   static constexpr int TB = B_BYTES / 1024, IB = (TB + NW - 1) / NW;
   static constexpr int IS = BITS == 16 ? 0 : 1;                       // 4-byte-per-lane DMA (scales)
@@ -660,7 +663,9 @@ struct GemmCfg {
   X(39, "64x128w8", 1, 8, 4, 1, 2) X(40, "32x64w8", 2, 4, 1, 1, 0) X(41, "128x256w8", 1, 8, 8, 2, 2)          \
   X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)                                    \
   X(44, "32x64p4", 1, 4, 2, 1, -4) X(45, "32x64p6", 1, 4, 2, 1, -6) X(46, "128x128np4", 1, 4, 8, 2, -4)      \
-  X(47, "144x128np4", 1, 4, 9, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)
+  X(47, "144x128np4", 1, 4, 9, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)     \
+  X(50, "96x128np4", 1, 4, 6, 2, -4) X(51, "64x64p4", 2, 2, 2, 2, -4) X(52, "32x128p4", 1, 4, 2, 2, -4)         \
+  X(53, "48x128np4", 1, 4, 3, 2, -4) X(54, "128x256w8p4", 1, 8, 8, 2, -4)
 #define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -687,11 +692,16 @@ static void launch_index(int i, hipStream_t s, GemmArgs a) {
 // epi: 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (the tile is one 128-wide head, <= 144 rows)
 static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
   return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144)) &&
-         (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time
+         (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time (the 2-stage
+                                               // fallback of a paired tile takes any count; the check keeps
+                                               // the rule simple)
 }
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from
 // sweeps on MI355X with warm clocks (q8; M 1152-86016; the decoders' N and K), first rule that fits:
+//   128x256w8p4 when its tiles fill one round (0.75-1 per CU): one 8-wave workgroup per CU, so the paired
+//               4-stage ring costs no occupancy (the 1152-row GLU: 216 tiles, 18.3-18.9 us against 19.5-21.8
+//               for 128x128n),
 //   128x256w8   when it gives >= 8 tiles per CU (large M: 950-980 TFLOP/s at 86016 rows, 3-8% over 128x128n;
 //               at 1536 rows the 3B GLU's 1032 tiles ran 3% slower than 128x128n),
 //   128x128n    when it gives >= 1.5 tiles per CU (the 1152-row GLU), or >= 0.5 per CU when K >= 4096 (few
@@ -713,11 +723,15 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
       if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) cfg = i;
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
-    static const struct { int cfg; double per_cu; int min_k; } rules[] = {
-        {41, 8.0, 0}, {19, 1.5, 0}, {19, 0.5, 4096}, {25, 2.0, 0}, {24, 1.0, 0}, {21, 2.0, 0}, {44, 2.0, 0},
-        {8, 2.0, 0}, {16, 2.0, 0}};
+    static const struct { int cfg; double per_cu; int min_k; double max_per_cu; } rules[] = {
+        {54, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
+        {24, 1.0, 0, 1e9}, {21, 2.0, 0, 1e9}, {44, 2.0, 0, 1e9}, {8, 2.0, 0, 1e9}, {16, 2.0, 0, 1e9}};
     for (const auto &r : rules)
-      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus) { cfg = r.cfg; break; }
+      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
+          tiles(r.cfg) <= r.max_per_cu * cus) {
+        cfg = r.cfg;
+        break;
+      }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
                     // the rows need (a 128-row tile on 32 rows does 4x the matrix work: 25 us against 9 for
                     // 32x64 on M = 32, 1536 x 4608)

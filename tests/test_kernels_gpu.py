@@ -173,7 +173,8 @@ def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
                                               ("32x64", 2, False), ("64x128n", 8, False), ("144x128n", 1, False),
                                               ("144x64n", 2, False), ("96x128n", 1, True), ("48x128n", 4, True),
                                               ("32x64p4", 1, False), ("32x64p6", 1, False), ("128x128np4", 1, True),
-                                              ("64x128np4", 1, False), ("144x64np4", 2, False)])
+                                              ("64x128np4", 1, False), ("144x64np4", 2, False), ("128x256w8p4", 1, True),
+                                              ("128x256w8p4", 1, False)])
 def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, glu):
     """Every tile shape and the split-K path (f32 partial slices in a workspace, summed in split order by a
     second kernel that runs the epilogue) agree with the oracle; run twice on fresh inputs so a stale slice
