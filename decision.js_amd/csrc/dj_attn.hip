@@ -254,15 +254,14 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
       // Tiles that every query of the wave sees whole (all but the diagonal ones of a causal block) skip the
       // per-key mask.
       const bool whole = kb0 >= wl2[sb] && kb0 + KW <= wh2[sb] && kb0 + KW <= hi;
+      // The max is taken on the raw scores (the scale is positive, so it commutes) and scaled once; the exp2
+      // argument below is one fma per score.
       float tmax = -INFINITY;
       if (whole) {
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            sc[bb][r] *= sl;
-            tmax = fmaxf(tmax, sc[bb][r]);
-          }
+          for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sc[bb][r]);
       } else {
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb)
@@ -270,12 +269,11 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
           for (int r = 0; r < 4; ++r) {
             const int kk = kb0 + 16 * bb + 4 * g + r;
             const bool ok = kk >= qlo && kk < qhi && kk < hi;
-            const float v = ok ? sc[bb][r] * sl : -INFINITY;
-            sc[bb][r] = v;
-            tmax = fmaxf(tmax, v);
+            sc[bb][r] = ok ? sc[bb][r] : -INFINITY;
+            tmax = fmaxf(tmax, sc[bb][r]);
           }
       }
-      tmax = xmax4(tmax);
+      tmax = xmax4(tmax) * sl;
       // Lazy rescaling: the reference point m moves (and O, l are rescaled) only when some query's maximum
       // has grown by more than 8 (log2 units); otherwise p = exp2(s - m) <= 2^8 stays exact enough in f16
       // and O / l is unchanged. The first live tile always moves m off -1e30.
@@ -293,7 +291,7 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
       for (int bb = 0; bb < NB; ++bb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(sc[bb][r] - m);  // exp2(-inf) = 0 for masked keys
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[bb][r], sl, -m));  // exp2(-inf) = 0: masked
           ps += p;
           pf[bb >> 1][(bb & 1) * 4 + r] = (_Float16)p;
         }
@@ -505,6 +503,7 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
                  q_stride >= heads * D,
              "decision.js: attention: bad arguments (heads %d, kv %d, q_stride %d)", heads, kv, q_stride);
   DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_OP_BEGIN(rec, "attention");
   if (T > 0) {

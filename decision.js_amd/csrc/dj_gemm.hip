@@ -663,9 +663,7 @@ struct GemmCfg {
   X(39, "64x128w8", 1, 8, 4, 1, 2) X(40, "32x64w8", 2, 4, 1, 1, 0) X(41, "128x256w8", 1, 8, 8, 2, 2)          \
   X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)                                    \
   X(44, "32x64p4", 1, 4, 2, 1, -4) X(45, "32x64p6", 1, 4, 2, 1, -6) X(46, "128x128np4", 1, 4, 8, 2, -4)      \
-  X(47, "144x128np4", 1, 4, 9, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)     \
-  X(50, "96x128np4", 1, 4, 6, 2, -4) X(51, "64x64p4", 2, 2, 2, 2, -4) X(52, "32x128p4", 1, 4, 2, 2, -4)         \
-  X(53, "48x128np4", 1, 4, 3, 2, -4) X(54, "128x256w8p4", 1, 8, 8, 2, -4)
+  X(47, "128x256w8p4", 1, 8, 8, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)
 #define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -724,7 +722,7 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; double max_per_cu; } rules[] = {
-        {54, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
+        {47, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
         {24, 1.0, 0, 1e9}, {21, 2.0, 0, 1e9}, {44, 2.0, 0, 1e9}, {8, 2.0, 0, 1e9}, {16, 2.0, 0, 1e9}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&

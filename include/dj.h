@@ -204,7 +204,8 @@ typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_co
  * online softmax (m0 = -1e30), output f16(acc / l). This covers the causal forest of ATTENTION
  * (kernels.ts:114-147; mask of line 135 as ranges), the bidirectional/windowed ranges of eg2 attention
  * (eg2-kernels.ts:98-163) and the trunk+branch ranges of attention256 (d3-kernels.ts:180-240, without its
- * gate), and a kept prefix KV (kvA = the cache) for the shared-state mode. D in {64, 128, 256}. */
+ * gate), and a kept prefix KV (kvA = the cache) for the shared-state mode. D in {64, 128, 256}; scale > 0
+ * (the reference's 1/sqrt(D), or 1 for eg2), else DJ_EINVAL. */
 int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
                  dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, uint16_t *O_dev);
 

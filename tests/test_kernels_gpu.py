@@ -415,6 +415,24 @@ def test_attention_kept_prefix(pkg, ctx, monkeypatch, P, splits, hg):
     assert np.abs(got - want).max() < 4e-3
 
 
+def test_attention_rejects_nonpositive_scale(pkg, ctx):
+    """The kernel takes the row max on raw scores (it commutes with a positive scale): a scale <= 0 is refused
+    before anything is launched."""
+    dj = _dj()
+    heads, kv, D, T = 4, 2, 128, 8
+    stride = (heads + 2 * kv) * D
+    dZ, dO = ctx.alloc(T * stride * 2), ctx.alloc(T * heads * D * 2)
+    drng = ctx.array(np.array([(0, t + 1, 0, 0) for t in range(T)], dtype=np.int32))
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    for bad in (0.0, -0.5):
+        rec = ctx.recorder()
+        try:
+            with pytest.raises(dj.DJError, match="score scale must be positive"):
+                rec.attention(T, heads, kv, D, dZ, stride, src, src, drng, bad, dO)
+        finally:
+            rec.finish()  # the refused op launched nothing; the (empty) forward completes
+
+
 def test_kv_store(pkg, ctx):
     rng = np.random.default_rng(3)
     heads, kv, D, T = 4, 2, 128, 70
