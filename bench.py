@@ -86,26 +86,46 @@ def roofline_from_profile(table):
 def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
     """That GEMM alone: the model's own weight of this shape, `reps` launches captured in one HIP graph and
     replayed `rounds` times between two HIP events on the engine's stream. Back-to-back launches in a graph
-    leave no per-launch event overhead, so this is the kernel's own duration (what rocprofv3 reports)."""
+    leave no per-launch event overhead, so this is the kernel's own duration (what rocprofv3 reports). The
+    fused qkv + q/k norm + RoPE product is timed as that op (layer 0's weight and norms, the RoPE table made
+    once beforehand), not as a plain product of its shape, which would pick another tile."""
     from decision_js_amd import _dj
     M, N, K = shape
     glu = name.startswith("matmul_glu")
+    rope = name.startswith("matmul_rope")
     want = _dj.W_MFMA_GLU if glu else _dj.W_MFMA
     w = next((w for w in eng.w.values() if isinstance(w, _dj.Weight) and w.N == N and w.K == K
               and (w.layout & ~_dj.W_DIRECT) == want), None)
-    if w is None:
+    if rope:  # the fused qkv + q/k norm + RoPE op itself, on layer 0's weights and norms
+        w = eng.w.get("layers.0.qkv")
+    if w is None or (rope and (w.N, w.K) != (N, K)):
         return None
     ctx = eng.ctx
     rng = np.random.default_rng(5)
     X = ctx.array((rng.standard_normal((M, K)) * 0.5).astype(np.float16))
     Y = ctx.alloc(M * (N // 2 if glu else N) * 2)
-    key = 0x6A5EB0000 + (M * 131 + N * 7 + K) % 65521
+    key = 0x6A5EB0000 + (M * 131 + N * 7 + K) % 65521 + (1 << 20 if rope else 0)
+    if rope:
+        pos = ctx.array((np.arange(M) % 384).astype(np.int32))
+        tab = ctx.alloc(M * (eng.D // 2) * 8)
+        rec = ctx.recorder()
+        rec.rope_table(M, pos, 1, eng.theta, eng.D, tab)  # the forward's angle table, made once outside the timing
+        rec.finish()
+        qn, kn = eng.w.get("layers.0.q_norm"), eng.w.get("layers.0.k_norm")
+
+    def one(rec):
+        if rope:
+            rec.matmul_qkv_rope(X, w, Y, M, eng.h, eng.kv, eng.D, qn, kn, False, pos, 1, eng.eps, eng.theta, tab)
+        elif glu:
+            rec.matmul_glu(X, w, Y, M)
+        else:
+            rec.matmul(X, w, Y, M)
 
     def run():
         rec = ctx.recorder(key)
         if not rec.replay:
             for _ in range(reps):
-                rec.matmul_glu(X, w, Y, M) if glu else rec.matmul(X, w, Y, M)
+                one(rec)
         rec.finish()
 
     run()
@@ -115,6 +135,9 @@ def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
     ms = ctx.timer_end() / (rounds * reps)
     X.free()
     Y.free()
+    if rope:
+        pos.free()
+        tab.free()
     return ms
 
 

@@ -703,8 +703,10 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
 //               for 128x128n),
 //   128x256w8   when it gives >= 8 tiles per CU (large M: 950-980 TFLOP/s at 86016 rows, 3-8% over 128x128n;
 //               at 1536 rows the 3B GLU's 1032 tiles ran 3% slower than 128x128n),
-//   128x128n    when it gives >= 1.5 tiles per CU (the 1152-row GLU), or >= 0.5 per CU when K >= 4096 (few
-//               long tiles beat many short ones: 3B's w2),
+//   128x128n    when it gives >= 1.5 tiles per CU, or >= 0.5 per CU when K >= 4096 (few long tiles beat many
+//               short ones: 3B's w2) — on the paired 4-stage ring (128x128np4) where those fill one round: the
+//               3B w2 (192 tiles at 1536 rows) takes its weights cold from HBM in the forward, and the deeper ring
+//               took the 3B ticket from 12.35 to 11.76 ms (same box),
 //   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
 //               against 17-18 for 64x128n),
 //   64x128n     when it gives >= 2 tiles per CU,
@@ -727,7 +729,7 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
   if (cfg < 0 && glu == 2 && cfg_fits(kCfgs[50], N, K, glu) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; double max_per_cu; } rules[] = {
-        {47, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
+        {47, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {46, 0.5, 4096, 1.0}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
         {24, 1.0, 0, 1e9}, {21, 2.0, 0, 1e9}, {44, 2.0, 0, 1e9}, {8, 2.0, 0, 1e9}, {16, 2.0, 0, 1e9}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
