@@ -168,6 +168,33 @@ def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
     assert worst <= 1.0
 
 
+@pytest.mark.parametrize("tile,K,glu", [("32x64p4", 128, False), ("32x64p4", 64, False), ("32x64p4", 1088, False),
+                                         ("128x256w8p4", 128, True), ("128x256w8p4", 1088, True),
+                                         ("128x128np4", 256, False)])
+def test_matmul_paired_ring_edges(pkg, ctx, monkeypatch, tile, K, glu):
+    """Paired-ring tiles take 64-K steps two at a time: one pair only (K = 128), and step counts that are odd
+    (K = 64, 1088), where the forced tile does not apply and the policy picks another; all match the oracle."""
+    dj = _dj()
+    monkeypatch.setenv("DJ_GEMM_TILE", tile)
+    rng = np.random.default_rng(K)
+    M, N = 300, 1024
+    codes, scales = quant(rng, N, K, 8)
+    W16 = ref.dequant_f16(codes, scales, 8)
+    W = ctx.weight_q(codes, scales, N, K, 8, dj.W_MFMA_GLU if glu else dj.W_MFMA)
+    X = rand_f16(rng, (M, K))
+    dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+    if glu:
+        run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
+        ab = ref.matmul(X, W16, np.float64)
+        want = ref.silu_mul(ab[:, :N // 2], ab[:, N // 2:], np.float64)
+        got = dY.read(np.float16, (M, N // 2))
+        assert np.abs(got.astype(np.float64) - want.astype(np.float64)).max() < 2e-2
+    else:
+        run(ctx, lambda r: r.matmul(dX, W, dY, M))
+        want = ref.matmul(X, W16, np.float64)
+        assert f16_close(dY.read(np.float16, (M, N)), want, ulps=1.0, atol=2e-5) <= 1.0
+
+
 @pytest.mark.parametrize("tile,splits,glu", [("128x128", 4, False), ("64x64", 2, False), ("128x128", 2, True),
                                               ("256x128", 1, False), ("32x128", 8, False), ("128x128n", 4, True),
                                               ("32x64", 2, False), ("64x128n", 8, False), ("144x128n", 1, False),
