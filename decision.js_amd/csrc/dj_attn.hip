@@ -101,7 +101,12 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
   const int g = lane >> 4, c16 = lane & 15;
   const int kg = KG > 1 ? wave >> 2 : 0, wq = wave & 3;  // key group; which 16 queries of the block
   // head group: HG query heads that share one KV head, 4 waves each, staging every K/V tile once
-  const int h = blockIdx.y * HG + (HG > 1 ? wave >> 2 : 0), q0 = blockIdx.x * 64;
+  // Workgroups dispatch in linear order (x fastest); take (query block, head group) from that order with the
+  // query block descending outermost, so later blocks — the longer key ranges of a causal sequence — start
+  // first, and the workgroups past one per CU are the short first blocks of a sequence (longest first).
+  const int lin = blockIdx.x + blockIdx.y * gridDim.x;
+  const int qb = gridDim.x - 1 - lin / gridDim.y, hgi = lin % gridDim.y;
+  const int h = hgi * HG + (HG > 1 ? wave >> 2 : 0), q0 = qb * 64;
   const int kvh = h / (heads / kv);
 
   // Q fragments first: nothing below depends on them until the first MFMA
