@@ -281,6 +281,18 @@ def run_workload(args):
             eng.run_shared(stt, branches[:1], groups[:1])
         q_wall = (time.perf_counter() - t1) / steps
         q_gpu = eng.ctx.timer_end() / steps
+        # the question alone once more with every op timed on its own (HIP events on the engine's stream)
+        eng.graphs = False
+        eng.ctx.profile_reset()
+        eng.ctx.profile(True)
+        eng.run_shared(stt, branches[:1], groups[:1])
+        eng.ctx.profile(False)
+        table = eng.ctx.profile_table()
+        eng.graphs = not args.no_graphs
+        total = sum(v[0] for v in table.values())
+        log(f"question alone, per op (launched one at a time, {1e3 * total:.0f} us in all):")
+        for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
+            log(f"  {k:48s} {1e3 * kms:8.1f} us/question  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:6.1f} us each)")
         stt.free()
         roof = _forward_fraction(cfg, 1024 + 256, [1024] + [32] * 8, gpu_ms)
         q_roof = _forward_fraction(cfg, 32, [32], q_gpu)

@@ -516,14 +516,21 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws
 // fragments (L2-resident) — straight into registers, then runs their MFMAs; with up to 16 waves per
 // workgroup that keeps enough weight bytes in flight. The waves' partial tiles are added through LDS in wave
 // order (deterministic), and wave 0 runs the same epilogue as the tiled kernel.
-template <int BITS, int MT, int CB, bool GLU>
-__global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
+//
+// MAXW is the most waves a launch may use. MAXW = 16: 128 VGPRs per lane, so a batch stages about 80 VGPRs
+// (3 steps at M = 32) and past-the-end steps re-load the last one. MAXW = 8 (the default launch): two waves
+// per SIMD, 256 VGPRs per lane, so a batch stages about 176 VGPRs (9 steps at M = 32: all of a 4608-long K
+// over 8 waves in one round trip) and loads past the end are skipped, not repeated.
+template <int BITS, int MT, int CB, bool GLU, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
   constexpr int CBYTES = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;
-  // steps per load batch: about 80 VGPRs of staging (X fragments 8 MT, weight blocks 4 or 8 and a scale word
-  // per block and step), so 16 waves per workgroup (128 VGPRs each) fit without spilling
+  // steps per load batch: the staging budget above over the VGPRs of one step (X fragments 8 MT, weight
+  // blocks 4 or 8 and a scale word per block)
+  constexpr bool WIDE = MAXW <= 8;
   constexpr int PER_STEP = 8 * MT + (BITS == 16 ? 8 : 5) * CB;
-  constexpr int BATCH = 80 / PER_STEP < 1 ? 1 : 80 / PER_STEP > 8 ? 8 : 80 / PER_STEP;
-  __shared__ f4 red[15 * MT * CB * 64];
+  constexpr int BUDGET = WIDE ? 176 : 80, BMAX = WIDE ? 12 : 8;
+  constexpr int BATCH = BUDGET / PER_STEP < 1 ? 1 : BUDGET / PER_STEP > BMAX ? BMAX : BUDGET / PER_STEP;
+  __shared__ f4 red[(MAXW - 1) * MT * CB * 64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, KW = blockDim.x >> 6;
   const int nb0 = blockIdx.x * CB;
   const int M = g.M, K = g.K, KT = K >> 6;
@@ -543,7 +550,9 @@ __global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
     uint32_t sp[BATCH][CB];
 #pragma unroll
     for (int q = 0; q < BATCH; ++q) {
-      const int kt = min(kb + q * KW, KT - 1);  // past the end: re-load the last step (not accumulated)
+      // past the end: skipped (WIDE, wave-uniform) or the last step re-loaded; neither is accumulated
+      if (WIDE && kb + q * KW >= KT) break;
+      const int kt = min(kb + q * KW, KT - 1);
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -621,17 +630,32 @@ __global__ __launch_bounds__(1024) void k_gemv(GemmArgs g) {
   }
 }
 
-// Waves per workgroup for the skinny kernel: about two steps each, 4..15 waves (the LDS reduction holds 15
-// partial tiles).
-static int gemv_waves(int KT) { return KT / 2 < 4 ? 4 : KT / 2 > 15 ? 15 : KT / 2; }
+// Waves per workgroup for the skinny kernel: about two steps each, 4..8 waves on the wide-batch form.
+// DJ_GEMV_WAVES=<n> (1..16) forces the count (tuning sweeps; above 8 the 16-wave form runs).
+static int gemv_waves(int KT) {
+  static const int forced = [] {
+    const char *s = getenv("DJ_GEMV_WAVES");
+    const int n = s ? atoi(s) : 0;
+    return n >= 1 && n <= 16 ? n : 0;
+  }();
+  if (forced) return forced;
+  return KT / 2 < 4 ? 4 : KT / 2 > 8 ? 8 : KT / 2;
+}
+
+template <int BITS, bool GLU, int MAXW>
+static void launch_gemv_w(hipStream_t s, GemmArgs a, int waves) {
+  constexpr int CB = GLU ? 2 : 1;
+  const dim3 grid(a.N / 16 / CB), block(64 * waves);
+  if (a.M <= 16) k_gemv<BITS, 1, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
+  else if (a.M <= 32) k_gemv<BITS, 2, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
+  else k_gemv<BITS, 4, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
+}
 
 template <int BITS, bool GLU>
 static void launch_gemv(hipStream_t s, GemmArgs a) {
-  constexpr int CB = GLU ? 2 : 1;
-  const dim3 grid(a.N / 16 / CB), block(64 * gemv_waves(a.K / 64));
-  if (a.M <= 16) k_gemv<BITS, 1, CB, GLU><<<grid, block, 0, s>>>(a);
-  else if (a.M <= 32) k_gemv<BITS, 2, CB, GLU><<<grid, block, 0, s>>>(a);
-  else k_gemv<BITS, 4, CB, GLU><<<grid, block, 0, s>>>(a);
+  const int waves = gemv_waves(a.K / 64);
+  if (waves <= 8) launch_gemv_w<BITS, GLU, 8>(s, a, waves);
+  else launch_gemv_w<BITS, GLU, 16>(s, a, waves);
 }
 
 // ---------------------------------------------------------------- dispatch
