@@ -165,6 +165,18 @@ def cpu_baseline(model_dir, ticket, budget_s):
                       f"oracle/ref.decoder_forward (numpy f32, CPU restatement of the reference path); {el:.1f} s"}
 
 
+def calibration_copy(ctx, mib):
+    """A plain device copy of `mib` MiB (the library's copy kernel), the known-size reference that scales the
+    FETCH_SIZE / WRITE_SIZE counters of the same run."""
+    src, dst = ctx.alloc(mib << 20), ctx.alloc(mib << 20)
+    dst.copy_from(src)
+    ctx.timer_begin()
+    dst.copy_from(src)
+    log(f"calibration copy {mib} MiB: {ctx.timer_end():.3f} ms")
+    src.free()
+    dst.free()
+
+
 def _line(metric, value, unit, steps, warmup, ms, dtype, workload, roofline, extra=None):
     out = {"metric": metric, "value": round(value, 3), "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
@@ -294,6 +306,8 @@ def run_workload(args):
         for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
             log(f"  {k:48s} {1e3 * kms:8.1f} us/question  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:6.1f} us each)")
         stt.free()
+        if args.calib_mb:
+            calibration_copy(eng.ctx, args.calib_mb)
         roof = _forward_fraction(cfg, 1024 + 256, [1024] + [32] * 8, gpu_ms)
         q_roof = _forward_fraction(cfg, 32, [32], q_gpu)
         log(f"shared: prefill 1024 + 8 x 32 questions {gpu_ms:.3f} ms (GPU); one question alone {q_gpu:.3f} ms "
@@ -431,11 +445,7 @@ def main():
     flops, wbytes = model_flops_bytes(cfg, T, [args.seq_len] * 3)
     t_roof_ms = max(flops / (MFMA_F16_PEAK_TFLOPS * 1e12), wbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     if args.calib_mb:
-        src, dst = eng.ctx.alloc(args.calib_mb << 20), eng.ctx.alloc(args.calib_mb << 20)
-        dst.copy_from(src)
-        eng.ctx.timer_begin()
-        dst.copy_from(src)
-        log(f"calibration copy {args.calib_mb} MiB: {eng.ctx.timer_end():.3f} ms")
+        calibration_copy(eng.ctx, args.calib_mb)
     # HBM bytes per launch of this kernel from the committed counter summary that names it (FETCH_SIZE and
     # WRITE_SIZE, each scaled by its reading for a copy of known size)
     if roof:

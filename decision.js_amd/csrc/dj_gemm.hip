@@ -633,12 +633,9 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
 // Waves per workgroup for the skinny kernel: about two steps each, 4..8 waves on the wide-batch form.
 // DJ_GEMV_WAVES=<n> (1..16) forces the count (tuning sweeps; above 8 the 16-wave form runs).
 static int gemv_waves(int KT) {
-  static const int forced = [] {
-    const char *s = getenv("DJ_GEMV_WAVES");
-    const int n = s ? atoi(s) : 0;
-    return n >= 1 && n <= 16 ? n : 0;
-  }();
-  if (forced) return forced;
+  const char *s = getenv("DJ_GEMV_WAVES");
+  const int forced = s ? atoi(s) : 0;
+  if (forced >= 1 && forced <= 16) return forced;
   return KT / 2 < 4 ? 4 : KT / 2 > 8 ? 8 : KT / 2;
 }
 

@@ -229,6 +229,31 @@ def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, gl
             assert f16_close(dY.read(np.float16, (M, N)), want, ulps=1.0, atol=2e-5) <= 1.0
 
 
+@pytest.mark.parametrize("waves", [1, 5, 8, 9, 16])
+@pytest.mark.parametrize("M,N,K,bits,glu", [(1, 2048, 832, 8, False), (32, 1536, 4608, 8, False),
+                                            (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True)])
+def test_gemv_wave_counts(pkg, ctx, monkeypatch, waves, M, N, K, bits, glu):
+    """The skinny kernel at forced wave counts: 1-8 run the 8-wave form (batches of up to 12 K-steps, loads
+    past the end skipped), 9-16 the 16-wave form (small batches, the last step re-loaded); K = 832 is 13 steps,
+    which no count above 1 divides. Each matches the oracle to the product's one-ulp bound."""
+    dj = _dj()
+    monkeypatch.setenv("DJ_GEMV_WAVES", str(waves))
+    rng = np.random.default_rng(waves * 31 + M + K)
+    codes, scales = quant(rng, N, K, bits)
+    W16 = ref.dequant_f16(codes, scales, bits)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA_GLU if glu else dj.W_MFMA)
+    X = rand_f16(rng, (M, K))
+    dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+    ab = ref.matmul(X, W16, np.float64)
+    if glu:
+        run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
+        want = ref.silu_mul(ab[:, :N // 2], ab[:, N // 2:], np.float64)
+        assert np.abs(dY.read(np.float16, (M, N // 2)).astype(np.float64) - want.astype(np.float64)).max() < 2e-2
+    else:
+        run(ctx, lambda r: r.matmul(dX, W, dY, M))
+        assert f16_close(dY.read(np.float16, (M, N)), ab, ulps=1.0, atol=2e-5) <= 1.0
+
+
 # ---------------------------------------------------------------- q/k norm + rope
 
 @pytest.mark.parametrize("heads,kv,D,qk,vnorm,mode,rot", [
