@@ -531,9 +531,14 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
   constexpr int BUDGET = WIDE ? 176 : 80, BMAX = WIDE ? 12 : 8;
   constexpr int BATCH = BUDGET / PER_STEP < 1 ? 1 : BUDGET / PER_STEP > BMAX ? BMAX : BUDGET / PER_STEP;
   __shared__ f4 red[(MAXW - 1) * MT * CB * 64];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, KW = blockDim.x >> 6;
+  // `wave` through readfirstlane: the batch guards below must be scalar branches. As vector compares they
+  // become EXEC-masked regions, and an MFMA runs whatever EXEC says, so a skipped slot would still add its
+  // (unloaded) registers into the accumulator.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, KW = blockDim.x >> 6;
   const int nb0 = blockIdx.x * CB;
   const int M = g.M, K = g.K, KT = K >> 6;
+  // split along K (gridDim.y > 1): this workgroup takes the KS steps from k0 and leaves f32 partials
+  const int KS = g.ksteps, k0 = blockIdx.y * KS;
 
   f4 acc[MT][CB];
 #pragma unroll
@@ -544,15 +549,15 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) xr[i] = g.X + (size_t)min(16 * i + (lane & 15), M - 1) * K + (lane >> 4) * 8;
 
-  for (int kb = wave; kb < KT; kb += KW * BATCH) {
+  for (int kb = wave; kb < KS; kb += KW * BATCH) {
     h8 a[BATCH][MT][2];
     RawB<BITS> b[BATCH][CB];
     uint32_t sp[BATCH][CB];
 #pragma unroll
     for (int q = 0; q < BATCH; ++q) {
       // past the end: skipped (WIDE, wave-uniform) or the last step re-loaded; neither is accumulated
-      if (WIDE && kb + q * KW >= KT) break;
-      const int kt = min(kb + q * KW, KT - 1);
+      if (WIDE && kb + q * KW >= KS) break;
+      const int kt = k0 + min(kb + q * KW, KS - 1);
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -571,7 +576,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
     }
 #pragma unroll
     for (int q = 0; q < BATCH; ++q) {
-      if (kb + q * KW < KT) {
+      if (kb + q * KW < KS) {
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -602,6 +607,18 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
   // accumulators hold blocks of Y^T (weight fragment first): lane l has row 16 i + l%16 and the 4 consecutive
   // columns 4(l/16)..+3 of a 16-column block, one 8-byte store
   const int N = g.N, c4 = 4 * (lane >> 4);
+  if (gridDim.y > 1) {  // a K split: f32 partial rows [split][M][N], summed in split order by the consumer
+    if constexpr (!GLU) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
+          const int m = 16 * i + (lane & 15), n = (nb0 + j) * 16 + c4;
+          if (m < M) *(f4 *)(g.ws + ((size_t)blockIdx.y * M + m) * N + n) = acc[i][j];
+        }
+    }
+    return;
+  }
   if constexpr (!GLU) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
@@ -642,7 +659,7 @@ static int gemv_waves(int KT) {
 template <int BITS, bool GLU, int MAXW>
 static void launch_gemv_w(hipStream_t s, GemmArgs a, int waves) {
   constexpr int CB = GLU ? 2 : 1;
-  const dim3 grid(a.N / 16 / CB), block(64 * waves);
+  const dim3 grid(a.N / 16 / CB, a.splits), block(64 * waves);
   if (a.M <= 16) k_gemv<BITS, 1, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
   else if (a.M <= 32) k_gemv<BITS, 2, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
   else k_gemv<BITS, 4, CB, GLU, MAXW><<<grid, block, 0, s>>>(a);
@@ -650,7 +667,7 @@ static void launch_gemv_w(hipStream_t s, GemmArgs a, int waves) {
 
 template <int BITS, bool GLU>
 static void launch_gemv(hipStream_t s, GemmArgs a) {
-  const int waves = gemv_waves(a.K / 64);
+  const int waves = gemv_waves(a.ksteps);
   if (waves <= 8) launch_gemv_w<BITS, GLU, 8>(s, a, waves);
   else launch_gemv_w<BITS, GLU, 16>(s, a, waves);
 }
@@ -818,6 +835,7 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
     GemmArgs a{};
     a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y;
     a.M = M; a.N = N; a.K = K; a.act = act;
+    a.splits = 1; a.ksteps = K / 64;
     launch_gemv<BITS, GLU>(c->stream, a);
     *name = kGemvNames[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU];
     *splits_out = 1;
@@ -914,9 +932,84 @@ int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y
   return glu ? launch_bits<16, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<16, false>(c, X, w, Y, M, 0, name, splits);
 }
 
+// K splits for a held skinny product (1: not worth holding): two, where the 64-K steps divide evenly into
+// splits of >= 8 and the grid stays within two workgroups per CU. Measured on the 0.8B decoder's question
+// alone (M = 32; one box, two runs each): 2 splits 1.182 ms, 3-4 splits (w2 4, o_proj 3) 1.273 ms, no holding
+// 1.274 ms — more splits make the GEMV no faster and the norm reads more partials. DJ_GEMV_SPLIT=0 turns
+// holding off; DJ_GEMV_SPLIT=<n> forces n where it divides.
+static int gemv_split_count(int M, int N, int K, int cus, size_t ws_floats) {
+  const int KT = K / 64;
+  const char *f = getenv("DJ_GEMV_SPLIT");
+  if (f) {
+    const int n = atoi(f);
+    return n >= 2 && KT % n == 0 && (size_t)n * M * N <= ws_floats ? n : 1;
+  }
+  const int S = 2;
+  return KT % S == 0 && KT / S >= 8 && (long)(N / 16) * S <= 2L * cus && (size_t)S * M * N <= ws_floats ? S : 1;
+}
+
+// A product the recorder may hold back by one op: plain (not gated), on the skinny kernel's rows, with a K
+// split worth taking, and no forced tile (sweeps time what they issue).
+static bool holdable(dj_rec *rec, const dj_weight *w, int M) {
+  if (!rec || !rec->ctx || rec->ctx->active != rec || rec->replay || rec->error || getenv("DJ_GEMM_TILE")) return false;
+  const int N = w->N, K = w->K;
+  const bool skinny = M >= 1 && M <= 64 && N % 16 == 0 && (M <= 16 || N <= 4096);
+  return skinny && gemv_split_count(M, N, K, rec->ctx->cus, rec->ctx->gemm_ws_floats) > 1;
+}
+
+static int matmul_now(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M);
+
 extern "C" int dj_matmul(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M) {
   DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA, "decision.js: matmul needs an MFMA-tiled weight (DJ_W_MFMA)");
   DJ_REQUIRE(X && Y && M >= 0, "decision.js: matmul: bad arguments");
+  if (holdable(rec, w, M)) {
+    if (int st = dj_release_held(rec)) return st;  // one product held at a time
+    rec->held.X = X;
+    rec->held.w = w;
+    rec->held.Y = Y;
+    rec->held.M = M;
+    rec->holding = true;
+    return DJ_OK;
+  }
+  return matmul_now(rec, X, w, Y, M);
+}
+
+int dj_release_held(dj_rec *rec) {
+  if (!rec || !rec->holding) return DJ_OK;
+  rec->holding = false;
+  return matmul_now(rec, rec->held.X, rec->held.w, rec->held.Y, rec->held.M);
+}
+
+int dj_take_held_split(dj_rec *rec, const uint16_t *Y, int T, int H, const float **parts, int *S) {
+  *parts = nullptr;
+  *S = 1;
+  if (!rec || !rec->ctx || rec->ctx->active != rec || !rec->holding || rec->held.Y != Y || rec->held.M != T ||
+      rec->held.w->N != H)
+    return DJ_OK;
+  rec->holding = false;
+  dj_ctx *c = rec->ctx;
+  const dj_weight *w = rec->held.w;
+  const int M = T, N = w->N, K = w->K;
+  const int splits = gemv_split_count(M, N, K, c->cus, c->gemm_ws_floats);
+  if (splits < 2) return matmul_now(rec, rec->held.X, w, rec->held.Y, M);
+  DJ_OP_BEGIN(rec, "matmul");
+  GemmArgs a{};
+  a.X = rec->held.X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = rec->held.Y; a.ws = c->gemm_ws;
+  a.M = M; a.N = N; a.K = K; a.act = 0;
+  a.splits = splits; a.ksteps = (K / 64) / splits;
+  const int bits = (w->layout & DJ_W_DIRECT) ? 16 : w->bits;  // direct weights: f16 blocks
+  if (bits == 8) launch_gemv<8, false>(c->stream, a);
+  else if (bits == 4) launch_gemv<4, false>(c->stream, a);
+  else launch_gemv<16, false>(c->stream, a);
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]/k%d+norm", M, N, K, splits);
+  if (int st = dj_op_end(rec, kGemvNames[bits == 4 ? 0 : bits == 8 ? 1 : 2][0], shape)) return st;
+  *parts = c->gemm_ws;
+  *S = splits;
+  return DJ_OK;
+}
+
+static int matmul_now(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M) {
   DJ_OP_BEGIN(rec, "matmul");
   const char *name = "matmul";
   int splits = 1;

@@ -88,7 +88,23 @@ struct dj_rec {
   size_t snap_index = 0;
   std::vector<dj_snapshot> snaps;
   int error = 0;
+  // A skinny-M product held back by one op (dj_matmul): when the next op is the residual + RMSNorm of its
+  // output, the product runs split along K and the norm sums its f32 partials (no summing kernel between);
+  // anything else that touches the stream first launches it as an ordinary product (dj_release_held).
+  bool holding = false;
+  struct {
+    const uint16_t *X = nullptr;
+    const dj_weight *w = nullptr;
+    uint16_t *Y = nullptr;
+    int M = 0;
+  } held;
 };
+
+// Launches a held product as an ordinary dj_matmul (DJ_OK if nothing is held).
+int dj_release_held(dj_rec *rec);
+// The same for the context's active recorder, if any: called by every entry point that touches the stream
+// outside an op, so work runs in the order the caller issued it.
+int dj_settle(dj_ctx *c);
 
 // ---------------------------------------------------------------- launch plumbing
 // Opens an op: validates the recorder, honours replay (ops ignored) and fault injection, and starts a
@@ -109,6 +125,10 @@ int dj_op_end(dj_rec *rec, const char *name, const char *detail = nullptr);
 int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
                    const char **name, int *splits);
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws);
+// If `rec` holds the product whose output is Y ([T, H]), launches it split along K into the context workspace
+// and returns its partials (*S slices of [T, H] f32, in split order) for the residual + RMSNorm to sum; the
+// norm kernel also writes the product's f16 rounding to Y. *parts = nullptr (nothing launched) otherwise.
+int dj_take_held_split(dj_rec *rec, const uint16_t *Y, int T, int H, const float **parts, int *S);
 // QK_NORM_ROPE kernel launch (checked arguments)
 int dj_launch_qk_norm_rope(hipStream_t s, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
                            const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta, int rot,

@@ -59,10 +59,12 @@ extern "C" int dj_gather_q(dj_rec *rec, const uint32_t *ids, int T, const dj_wei
 // ---------------------------------------------------------------- residual + RMSNorm (kernels.ts:23-46)
 // One wave per row, 8 halves per lane per chunk; NC = ceil(H / 512) chunks per lane stay in registers
 // between the sum of squares and the scaling (NC = 0: rows too long for that, re-read from memory).
-template <int NC>
+// PARTS: Y arrives as S f32 partial slices of a product split along K (P, `slice` floats apart).
+template <int NC, bool PARTS>
 __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, float eps, uint16_t *__restrict__ X,
                                                      const uint16_t *__restrict__ Y, const uint16_t *__restrict__ W,
-                                                     uint16_t *__restrict__ O) {
+                                                     uint16_t *__restrict__ O, const float *__restrict__ P, int S,
+                                                     size_t slice, uint16_t *__restrict__ YW) {
   const int row = blockIdx.x * 4 + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (row >= T) return;
   const size_t base = (size_t)row * H;
@@ -72,7 +74,23 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(int T, int H, int add, floa
   auto step = [&](int k, h8 &x) {
     x = *(const h8 *)(X + base + k);
     if (add) {
-      const h8 y = *(const h8 *)(Y + base + k);
+      h8 y;
+      if constexpr (PARTS) {  // Y is a K-split product: its f32 partials added in split order, rounded to f16
+        const float *p = P + base + k;
+        f4 lo = *(const f4 *)p, hi = *(const f4 *)(p + 4);
+        for (int s = 1; s < S; ++s) {
+          lo += *(const f4 *)(p + s * slice);
+          hi += *(const f4 *)(p + s * slice + 4);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          y[j] = (_Float16)lo[j];
+          y[j + 4] = (_Float16)hi[j];
+        }
+        *(h8 *)(YW + base + k) = y;  // the product's own output
+      } else {
+        y = *(const h8 *)(Y + base + k);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float v = (float)x[j] + (float)y[j];
@@ -132,12 +150,38 @@ static int row_chunks(int H) {
     default: KERNEL<0><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;          \
   }
 
+// row kernels templated on (chunks, bool)
+#define DJ_ROW_DISPATCH_B(KERNEL, B, H, grid, stream, ...)                        \
+  switch (row_chunks(H)) {                                                        \
+    case 1: KERNEL<1, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 2: KERNEL<2, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 3: KERNEL<3, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 4: KERNEL<4, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 5: KERNEL<5, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 6: KERNEL<6, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 7: KERNEL<7, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    case 8: KERNEL<8, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;           \
+    default: KERNEL<0, B><<<grid, 256, 0, stream>>>(__VA_ARGS__); break;          \
+  }
+
 extern "C" int dj_add_rmsnorm(dj_rec *rec, int T, int H, int add, float eps, uint16_t *X, const uint16_t *Y,
                               const uint16_t *W, uint16_t *O) {
   DJ_REQUIRE(X && W && O && (Y || !add) && T >= 0 && H > 0 && H % 8 == 0,
              "decision.js: add_rmsnorm: bad arguments (H = %d must be a multiple of 8)", H);
+  // a skinny product of Y held by the recorder runs split along K now, and this kernel sums its partials
+  const float *parts = nullptr;
+  int S = 1;
+  if (add && T > 0)
+    if (int st = dj_take_held_split(rec, Y, T, H, &parts, &S)) return st;
   DJ_OP_BEGIN(rec, "add_rmsnorm");
-  if (T > 0) DJ_ROW_DISPATCH(k_add_rmsnorm, H, dj_cdiv(T, 4), rec->ctx->stream, T, H, add, eps, X, Y, W, O);
+  if (T > 0) {
+    if (parts)
+      DJ_ROW_DISPATCH_B(k_add_rmsnorm, true, H, dj_cdiv(T, 4), rec->ctx->stream, T, H, add, eps, X, Y, W, O, parts, S,
+                        (size_t)T * H, const_cast<uint16_t *>(Y))
+    else
+      DJ_ROW_DISPATCH_B(k_add_rmsnorm, false, H, dj_cdiv(T, 4), rec->ctx->stream, T, H, add, eps, X, Y, W, O, nullptr, 1,
+                        (size_t)0, nullptr)
+  }
   return dj_op_end(rec, "add_rmsnorm");
 }
 

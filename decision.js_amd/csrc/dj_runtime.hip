@@ -120,6 +120,7 @@ extern "C" int dj_buf_free(dj_ctx *c, void *dev) {
   if (!dev) return DJ_OK;
   auto it = c->buffers.find(dev);
   DJ_REQUIRE(it != c->buffers.end(), "decision.js: dj_buf_free: %p is not a buffer of this context", dev);
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipStreamSynchronize(c->stream));
   DJ_HIP(hipFree(dev));
   c->buffers.erase(it);
@@ -130,6 +131,7 @@ extern "C" int dj_buf_write(dj_ctx *c, void *dev, const void *host, size_t bytes
   DJ_REQUIRE(c && (dev || !bytes) && (host || !bytes), "decision.js: dj_buf_write: null argument");
   DJ_REQUIRE(!c->active || !c->active->capturing, "decision.js: dj_buf_write while a graph is captured");
   if (!bytes) return DJ_OK;
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipStreamSynchronize(c->stream));
   DJ_HIP(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice));
   return DJ_OK;
@@ -139,6 +141,7 @@ extern "C" int dj_buf_read(dj_ctx *c, void *host, const void *dev, size_t bytes)
   DJ_REQUIRE(c && (dev || !bytes) && (host || !bytes), "decision.js: dj_buf_read: null argument");
   DJ_REQUIRE(!c->active || !c->active->capturing, "decision.js: dj_buf_read while a graph is captured");
   if (!bytes) return DJ_OK;
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipStreamSynchronize(c->stream));
   DJ_HIP(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost));
   return DJ_OK;
@@ -146,6 +149,7 @@ extern "C" int dj_buf_read(dj_ctx *c, void *host, const void *dev, size_t bytes)
 
 extern "C" int dj_buf_copy(dj_ctx *c, void *dst, const void *src, size_t bytes) {
   DJ_REQUIRE(c && (dst || !bytes) && (src || !bytes), "decision.js: dj_buf_copy: null argument");
+  if (int st = dj_settle(c)) return st;
   return dj_launch_copy(c->stream, dst, src, bytes);
 }
 
@@ -154,6 +158,7 @@ extern "C" int dj_upload(dj_ctx *c, void *dev, const void *host, size_t bytes) {
   DJ_REQUIRE(!c->active || !c->active->capturing,
              "decision.js: dj_upload while a graph is captured (upload before dj_rec_begin)");
   if (!bytes) return DJ_OK;
+  if (int st = dj_settle(c)) return st;
   size_t need = (bytes + 255) & ~(size_t)255;
   if (c->pinned_used + need > c->pinned_cap) {
     DJ_HIP(hipStreamSynchronize(c->stream));  // every earlier upload has landed: the arena is free again
@@ -325,6 +330,7 @@ extern "C" int dj_weight_free(dj_ctx *c, dj_weight *w) {
   if (!w) return DJ_OK;
   auto it = std::find(c->weights.begin(), c->weights.end(), w);
   DJ_REQUIRE(it != c->weights.end(), "decision.js: dj_weight_free: not a weight of this context");
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipStreamSynchronize(c->stream));
   (void)hipFree(w->codes);
   (void)hipFree(w->scales);
@@ -377,6 +383,10 @@ int dj_op_begin(dj_rec *rec, const char *name) {
   if (!rec || !rec->ctx) return -dj_fail(DJ_ESTATE, "decision.js: %s: no recorder", name);
   dj_ctx *c = rec->ctx;
   if (c->active != rec) return -dj_fail(DJ_ESTATE, "decision.js: %s: recorder is not active", name);
+  if (rec->holding) {  // the held product runs first, in the order the ops were issued
+    const int st = dj_release_held(rec);
+    if (st) return -st;
+  }
   if (rec->replay) return 1;
   if (!c->fault_op.empty() && (c->fault_op == name || c->fault_op == "*"))
     return -dj_fail(DJ_EINJECT, "decision.js: fault injected in %s (DJ_FAULT_INJECT)", name);
@@ -403,10 +413,13 @@ int dj_op_end(dj_rec *rec, const char *name, const char *detail) {
   return DJ_OK;
 }
 
+int dj_settle(dj_ctx *c) { return c->active ? dj_release_held(c->active) : DJ_OK; }
+
 extern "C" int dj_rec_snapshot(dj_rec *rec, const void *dev, size_t bytes, void *host) {
   DJ_REQUIRE(rec && rec->ctx && host, "decision.js: dj_rec_snapshot: null argument");
   dj_ctx *c = rec->ctx;
   DJ_REQUIRE(c->active == rec, "decision.js: dj_rec_snapshot: recorder is not active");
+  if (int st = dj_release_held(rec)) return st;
   if (rec->replay) {
     auto &g = c->graphs[rec->key];
     DJ_REQUIRE(rec->snap_index < g.staging.size() && g.staging_bytes[rec->snap_index] == bytes,
@@ -450,6 +463,9 @@ extern "C" int dj_rec_finish(dj_rec *r) {
   DJ_REQUIRE(r && r->ctx, "decision.js: dj_rec_finish: null recorder");
   dj_ctx *c = r->ctx;
   DJ_REQUIRE(c->active == r, "decision.js: dj_rec_finish: recorder is not active");
+  if (int st = dj_release_held(r)) {
+    if (!r->error) r->error = st;
+  }
   c->active = nullptr;
   int status = DJ_OK;
   std::string msg;
@@ -519,12 +535,14 @@ extern "C" int dj_graph_clear(dj_ctx *c) {
 
 extern "C" int dj_timer_begin(dj_ctx *c) {
   DJ_REQUIRE(c, "decision.js: null context");
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipEventRecord(c->t0, c->stream));
   return DJ_OK;
 }
 
 extern "C" int dj_timer_end(dj_ctx *c, float *ms) {
   DJ_REQUIRE(c && ms, "decision.js: null argument");
+  if (int st = dj_settle(c)) return st;
   DJ_HIP(hipEventRecord(c->t1, c->stream));
   DJ_HIP(hipEventSynchronize(c->t1));
   DJ_HIP(hipEventElapsedTime(ms, c->t0, c->t1));

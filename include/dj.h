@@ -151,7 +151,12 @@ int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, uint16_t *X_d
 /* Y[M, N] = X[M, K] . W^T, f16 in and out, f32 accumulation on f16 MFMA, W dequantized in registers
  * exactly as the gather (bit-exact f16 weights). `w` must be DJ_W_MFMA. X rows are M (no padding needed).
  * Replaces recorder().matmul (gpu.ts:202-226) and MATMUL_Q8/Q4_SG32, MATMUL_DIRECT, matmulSplitK,
- * matmulPortable* (kernels.ts:298-385, 441-520, 545-768). */
+ * matmulPortable* (kernels.ts:298-385, 441-520, 545-768).
+ * On a few rows (M <= 64, q8/q4, K long enough to split) the recorder may hold the product back by one
+ * call: if the next op is dj_add_rmsnorm(add) of Y with T = M and H = N, the product runs split along K and
+ * that norm sums its f32 partials (it also writes Y); any other op, snapshot, dj_rec_finish or stream-using
+ * buffer call launches it first as an ordinary product. Y holds the product either way; a launch error
+ * of a held product is reported by the call that launched it. DJ_GEMV_SPLIT=0 turns this off. */
 int dj_matmul(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *Y_dev, int M);
 
 enum { DJ_ACT_SILU = 0, DJ_ACT_GELU_TANH = 1 };

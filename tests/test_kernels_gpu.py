@@ -231,17 +231,21 @@ def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, gl
 
 @pytest.mark.parametrize("waves", [1, 5, 8, 9, 16])
 @pytest.mark.parametrize("M,N,K,bits,glu", [(1, 2048, 832, 8, False), (32, 1536, 4608, 8, False),
-                                            (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True)])
+                                            (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True),
+                                            (5, 2048, 1536, 16, False), (16, 1024, 2048, 16, True)])
 def test_gemv_wave_counts(pkg, ctx, monkeypatch, waves, M, N, K, bits, glu):
     """The skinny kernel at forced wave counts: 1-8 run the 8-wave form (batches of up to 12 K-steps, loads
     past the end skipped), 9-16 the 16-wave form (small batches, the last step re-loaded); K = 832 is 13 steps,
-    which no count above 1 divides. Each matches the oracle to the product's one-ulp bound."""
+    which no count above 1 divides. Each matches the oracle to the product's one-ulp bound. bits 16: q8 weights
+    loaded as direct f16 blocks (the 16-bit kernel)."""
     dj = _dj()
     monkeypatch.setenv("DJ_GEMV_WAVES", str(waves))
     rng = np.random.default_rng(waves * 31 + M + K)
+    direct = bits == 16
+    bits = 8 if direct else bits
     codes, scales = quant(rng, N, K, bits)
     W16 = ref.dequant_f16(codes, scales, bits)
-    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA_GLU if glu else dj.W_MFMA)
+    W = ctx.weight_q(codes, scales, N, K, bits, (dj.W_MFMA_GLU if glu else dj.W_MFMA) | (dj.W_DIRECT if direct else 0))
     X = rand_f16(rng, (M, K))
     dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
     ab = ref.matmul(X, W16, np.float64)
@@ -252,6 +256,104 @@ def test_gemv_wave_counts(pkg, ctx, monkeypatch, waves, M, N, K, bits, glu):
     else:
         run(ctx, lambda r: r.matmul(dX, W, dY, M))
         assert f16_close(dY.read(np.float16, (M, N)), ab, ulps=1.0, atol=2e-5) <= 1.0
+
+
+def _held_case(ctx, rng, M, N, K, bits, direct):
+    dj = _dj()
+    codes, scales = quant(rng, N, K, bits)
+    W16 = ref.dequant_f16(codes, scales, bits)
+    W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA | (dj.W_DIRECT if direct else 0))
+    X, Xr = rand_f16(rng, (M, K)), rand_f16(rng, (M, N))
+    w = (1 + rng.standard_normal(N) * 0.1).astype(np.float16)
+    return W, W16, X, Xr, w
+
+
+@pytest.mark.parametrize("M,N,K,bits,direct", [(32, 1536, 4608, 8, False), (32, 1536, 1536, 8, False),
+                                               (16, 1024, 2048, 4, False), (5, 2048, 1536, 8, False),
+                                               (16, 2048, 1536, 8, False), (64, 512, 1024, 8, False),
+                                               (5, 2048, 1536, 8, True), (32, 1536, 4608, 8, True)])
+@pytest.mark.parametrize("split", [None, "0", "3", "4"])
+def test_held_product_into_norm(pkg, ctx, monkeypatch, M, N, K, bits, direct, split):
+    """matmul followed by the residual + RMSNorm of its output: on skinny rows the recorder holds the product
+    and runs it split along K with the norm summing the f32 partials (split None: automatic, two; "0": holding
+    off; "3", "4": forced where they divide the K steps). Either way the product buffer holds the product (one f16 ulp of float64), and x and the normed rows
+    are the oracle's add_rmsnorm of that product: x bit-exact, the normed rows within one ulp. Direct (f16)
+    weights at M = 5 have the largest load batch of the skinny kernel, whose slots are mostly empty here."""
+    if split is not None:
+        monkeypatch.setenv("DJ_GEMV_SPLIT", split)
+    rng = np.random.default_rng(M * 13 + N + K + bits)
+    W, W16, X, Xr, w = _held_case(ctx, rng, M, N, K, bits, direct)
+    dX, dY, dx, dw, dO = ctx.array(X), ctx.alloc(M * N * 2), ctx.array(Xr), ctx.array(w), ctx.alloc(M * N * 2)
+
+    def body(r):
+        r.matmul(dX, W, dY, M)
+        r.add_rmsnorm(M, N, True, 1e-6, dx, dY, dw, dO)
+
+    for rep in range(2):  # twice: the second call reuses the workspace slices
+        dx.upload(Xr)
+        run(ctx, body)
+        Y = dY.read(np.float16, (M, N))
+        assert f16_close(Y, ref.matmul(X, W16, np.float64), ulps=1.0, atol=2e-5) <= 1.0
+        xn, O = ref.add_rmsnorm(Xr, Y, w, 1e-6, add=True, acc=np.float64)
+        assert np.array_equal(dx.read(np.float16, (M, N)).view(np.uint16), xn.view(np.uint16))
+        assert f16_close(dO.read(np.float16, (M, N)), O, ulps=1.0) <= 1.0
+
+
+@pytest.mark.parametrize("after", ["finish", "snapshot", "matmul", "other_norm", "copy"])
+def test_held_product_released_in_order(pkg, ctx, after):
+    """A held product that the next op does not consume runs first, in issue order: before another op,
+    a snapshot of its output, the end of the forward, a norm of another buffer, or a buffer copy."""
+    rng = np.random.default_rng(7)
+    M, N, K = 32, 1536, 4608
+    W, W16, X, Xr, w = _held_case(ctx, rng, M, N, K, 8, False)
+    want = ref.matmul(X, W16, np.float64)
+    dX, dY, dY2, dx, dw, dO = (ctx.array(X), ctx.alloc(M * N * 2), ctx.alloc(M * N * 2), ctx.array(Xr), ctx.array(w),
+                               ctx.alloc(M * N * 2))
+    dZ = ctx.alloc(M * N * 2)
+    rec = ctx.recorder()
+    rec.matmul(dX, W, dY, M)
+    snap = None
+    if after == "snapshot":
+        snap = rec.snapshot(dY, M * N * 2, np.float16, (M, N))
+    elif after == "matmul":  # a product reading the held one's output
+        rec.matmul(dY, ctx.weight_q(*quant(rng, N, N, 8), N, N, 8, _dj().W_MFMA), dY2, M)
+    elif after == "other_norm":
+        rec.add_rmsnorm(M, N, True, 1e-6, dx, dZ, dw, dO)
+    elif after == "copy":
+        dY2.copy_from(dY)
+    got = rec.finish()
+    Y = got[snap] if snap is not None else dY.read(np.float16, (M, N))
+    assert f16_close(Y, want, ulps=1.0, atol=2e-5) <= 1.0
+    if after == "copy":
+        assert np.array_equal(dY2.read(np.float16, (M, N)).view(np.uint16), Y.view(np.uint16))
+
+
+def test_held_product_graph_replays(pkg, ctx):
+    """The held product and its norm captured in a HIP graph: every replay (with eager work and reads in
+    between) gives the bits of the eager run."""
+    rng = np.random.default_rng(11)
+    M, N, K = 32, 1536, 4608
+    W, W16, X, Xr, w = _held_case(ctx, rng, M, N, K, 8, False)
+    dX, dY, dx, dw, dO = ctx.array(X), ctx.alloc(M * N * 2), ctx.array(Xr), ctx.array(w), ctx.alloc(M * N * 2)
+
+    def body(r):
+        r.matmul(dX, W, dY, M)
+        r.add_rmsnorm(M, N, True, 1e-6, dx, dY, dw, dO)
+
+    dx.upload(Xr)
+    run(ctx, body)
+    eager = [b.read(np.float16, (M, N)).view(np.uint16).copy() for b in (dY, dx, dO)]
+    for rep in range(4):
+        dx.upload(Xr)
+        dY.upload(np.zeros((M, N), np.float16))
+        dO.upload(np.zeros((M, N), np.float16))
+        rec = ctx.recorder(0x4E1D0)
+        if not rec.replay:
+            body(rec)
+        rec.finish()
+        for b, e in zip((dY, dx, dO), eager):
+            assert np.array_equal(b.read(np.float16, (M, N)).view(np.uint16), e), f"replay {rep}"
+        run(ctx, lambda r: r.add_rmsnorm(M, N, False, 1e-6, dx, None, dw, dO))  # eager work between replays
 
 
 # ---------------------------------------------------------------- q/k norm + rope
