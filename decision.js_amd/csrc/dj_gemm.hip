@@ -752,7 +752,8 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
 //               K / 64 even: 13.4 vs 13.9 us and 19.2 vs 19.9 us at 1152 x 1024 x 2048 / 3072), else 32x64,
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
-static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int &splits) {
+static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &cfg, int &splits) {
+  const bool ws_ok = ws_floats > 0;
   const char *force = getenv("DJ_GEMM_TILE");
   const char *fs = getenv("DJ_GEMM_SPLITK");
   cfg = -1;
@@ -765,14 +766,27 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
   // workgroup per CU, so the deeper ring costs no occupancy; the 1152-row qkv, 256 tiles: 2.628 -> 2.616 ms
   // per ticket, same box)
   if (cfg < 0 && glu == 2 && cfg_fits(kCfgs[50], N, K, glu) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
+  // long K on one round of tiles: 128x128n split 4 ways along K (the 3B w2, 1536 x 2048 x 11008 q4, alone on
+  // cold weights: 92.9 us against 107.0 on the paired ring, the summing kernel included);
+  // DJ_GEMM_LONGK_SPLIT=1 keeps the paired ring unsplit
+  const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
+  const int longk = lks ? atoi(lks) : 4;
+  int rule_splits = 0;
   if (cfg < 0) {
-    static const struct { int cfg; double per_cu; int min_k; double max_per_cu; } rules[] = {
-        {47, 0.75, 0, 1.0}, {41, 8.0, 0, 1e9}, {19, 1.5, 0, 1e9}, {46, 0.5, 4096, 1.0}, {19, 0.5, 4096, 1e9}, {25, 2.0, 0, 1e9},
-        {24, 1.0, 0, 1e9}, {21, 2.0, 0, 1e9}, {44, 2.0, 0, 1e9}, {8, 2.0, 0, 1e9}, {16, 2.0, 0, 1e9}};
+    static const struct { int cfg; double per_cu; int min_k; double max_per_cu; int ks; } rules[] = {
+        {47, 0.75, 0, 1.0, 0}, {41, 8.0, 0, 1e9, 0}, {19, 1.5, 0, 1e9, 0}, {19, 0.5, 4096, 1.0, -1}, {19, 0.5, 4096, 1e9, 0},
+        {25, 2.0, 0, 1e9, 0}, {24, 1.0, 0, 1e9, 0}, {21, 2.0, 0, 1e9, 0}, {44, 2.0, 0, 1e9, 0}, {8, 2.0, 0, 1e9, 0},
+        {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
           tiles(r.cfg) <= r.max_per_cu * cus) {
         cfg = r.cfg;
+        if (r.ks < 0) {  // the long-K rule: the split where it divides K and fits the workspace, else the ring
+          if (longk > 1 && ws_ok && glu != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats)
+            rule_splits = longk;
+          else if (cfg_fits(kCfgs[46], N, K, glu))
+            cfg = 46;
+        }
         break;
       }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
@@ -793,6 +807,8 @@ static void pick(int M, int N, int K, int glu, int cus, int ws_ok, int &cfg, int
   const int KT = K / 64;
   if (fs) {
     splits = atoi(fs);
+  } else if (rule_splits) {
+    splits = rule_splits;
   } else {
     const long t = tiles(cfg);
     while (t * splits * 4 < cus && KT % (splits * 2) == 0 && KT / (splits * 2) >= 4) splits *= 2;
@@ -843,7 +859,7 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   }
   float *ws = nullptr;
   int cfg, splits;
-  pick(M, N, K, GLU, c->cus, 1, cfg, splits);
+  pick(M, N, K, GLU, c->cus, c->gemm_ws ? c->gemm_ws_floats : 0, cfg, splits);
   if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, &ws) != DJ_OK) splits = 1;
   if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
   const char *label = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];

@@ -103,6 +103,8 @@ def test_sandwich(pkg, ctx, with_y, with_w2, H):
     # skinny M (the GEMV-style kernel): one row, a single K step, 16/17/32/64 rows, long K in several batches
     (1, 2048, 1536, 8), (8, 1536, 64, 8), (16, 1536, 4608, 8), (17, 2048, 1536, 4), (32, 1536, 1536, 8),
     (64, 2560, 2048, 4), (32, 2048, 11008, 4),
+    # long K on one round of 128x128 tiles: split 4 ways along K (K / 64 divisible by 4), else unsplit
+    (1024, 2048, 4096, 4), (1152, 2560, 4352, 8), (1024, 2048, 4160, 8),
 ])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul(pkg, ctx, M, N, K, bits, direct):
@@ -354,6 +356,7 @@ def test_held_product_graph_replays(pkg, ctx):
         for b, e in zip((dY, dx, dO), eager):
             assert np.array_equal(b.read(np.float16, (M, N)).view(np.uint16), e), f"replay {rep}"
         run(ctx, lambda r: r.add_rmsnorm(M, N, False, 1e-6, dx, None, dw, dO))  # eager work between replays
+    ctx.graph_clear()  # the cached graph points at this test's buffers
 
 
 # ---------------------------------------------------------------- q/k norm + rope
