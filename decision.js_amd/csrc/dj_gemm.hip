@@ -766,15 +766,16 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
   // workgroup per CU, so the deeper ring costs no occupancy; the 1152-row qkv, 256 tiles: 2.628 -> 2.616 ms
   // per ticket, same box)
   if (cfg < 0 && glu == 2 && cfg_fits(kCfgs[50], N, K, glu) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
-  // long K on one round of tiles: 128x128n split 4 ways along K (the 3B w2, 1536 x 2048 x 11008 q4, alone on
-  // cold weights: 92.9 us against 107.0 on the paired ring, the summing kernel included);
+  // long K on at most one round of tiles (0.25-1 per CU): 128x128n split 4 ways along K (alone on cold weights,
+  // the summing kernel included: the 3B w2, 1536 x 2048 x 11008 q4, 92.9 us against 107.0 on the paired ring;
+  // the 0.8B prefill's w2, 1024 x 1536 x 4608 q8, 32.8 against 36.6);
   // DJ_GEMM_LONGK_SPLIT=1 keeps the paired ring unsplit
   const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
   const int longk = lks ? atoi(lks) : 4;
   int rule_splits = 0;
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; double max_per_cu; int ks; } rules[] = {
-        {47, 0.75, 0, 1.0, 0}, {41, 8.0, 0, 1e9, 0}, {19, 1.5, 0, 1e9, 0}, {19, 0.5, 4096, 1.0, -1}, {19, 0.5, 4096, 1e9, 0},
+        {47, 0.75, 0, 1.0, 0}, {41, 8.0, 0, 1e9, 0}, {19, 1.5, 0, 1e9, 0}, {19, 0.25, 4096, 1.0, -1}, {19, 0.5, 4096, 1e9, 0},
         {25, 2.0, 0, 1e9, 0}, {24, 1.0, 0, 1e9, 0}, {21, 2.0, 0, 1e9, 0}, {44, 2.0, 0, 1e9, 0}, {8, 2.0, 0, 1e9, 0},
         {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules)

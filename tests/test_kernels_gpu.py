@@ -104,7 +104,7 @@ def test_sandwich(pkg, ctx, with_y, with_w2, H):
     (1, 2048, 1536, 8), (8, 1536, 64, 8), (16, 1536, 4608, 8), (17, 2048, 1536, 4), (32, 1536, 1536, 8),
     (64, 2560, 2048, 4), (32, 2048, 11008, 4),
     # long K on one round of 128x128 tiles: split 4 ways along K (K / 64 divisible by 4), else unsplit
-    (1024, 2048, 4096, 4), (1152, 2560, 4352, 8), (1024, 2048, 4160, 8),
+    (1024, 2048, 4096, 4), (1152, 2560, 4352, 8), (1024, 2048, 4160, 8), (1024, 1536, 4608, 8),
 ])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul(pkg, ctx, M, N, K, bits, direct):
