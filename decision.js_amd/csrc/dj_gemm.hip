@@ -768,7 +768,8 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
   if (cfg < 0 && glu == 2 && cfg_fits(kCfgs[50], N, K, glu) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
   // long K on at most one round of tiles (0.25-1 per CU): 128x128n split 4 ways along K (alone on cold weights,
   // the summing kernel included: the 3B w2, 1536 x 2048 x 11008 q4, 92.9 us against 107.0 on the paired ring;
-  // the 0.8B prefill's w2, 1024 x 1536 x 4608 q8, 32.8 against 36.6);
+  // the 0.8B prefill's w2, 1024 x 1536 x 4608 q8, 32.8 against 36.6); below that, 64x128n split 4 ways at
+  // 0.1-0.25 tiles per CU (the 0.8B 8-question pass's w2, 256 x 1536 x 4608: 19.7 against 23.8 on 32x64);
   // DJ_GEMM_LONGK_SPLIT=1 keeps the paired ring unsplit
   const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
   const int longk = lks ? atoi(lks) : 4;
@@ -776,18 +777,24 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
   if (cfg < 0) {
     static const struct { int cfg; double per_cu; int min_k; double max_per_cu; int ks; } rules[] = {
         {47, 0.75, 0, 1.0, 0}, {41, 8.0, 0, 1e9, 0}, {19, 1.5, 0, 1e9, 0}, {19, 0.25, 4096, 1.0, -1}, {19, 0.5, 4096, 1e9, 0},
+        {21, 0.1, 4096, 0.25, -1},
         {25, 2.0, 0, 1e9, 0}, {24, 1.0, 0, 1e9, 0}, {21, 2.0, 0, 1e9, 0}, {44, 2.0, 0, 1e9, 0}, {8, 2.0, 0, 1e9, 0},
         {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules)
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
           tiles(r.cfg) <= r.max_per_cu * cus) {
-        cfg = r.cfg;
-        if (r.ks < 0) {  // the long-K rule: the split where it divides K and fits the workspace, else the ring
-          if (longk > 1 && ws_ok && glu != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats)
+        if (r.ks < 0) {  // a long-K rule: the split where it divides K and fits the workspace; else what the rules
+                         // chose before it (the paired ring at 0.5-1 per CU, otherwise the rules below)
+          if (longk > 1 && ws_ok && glu != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats) {
             rule_splits = longk;
-          else if (cfg_fits(kCfgs[46], N, K, glu))
+          } else if (r.cfg == 19 && tiles(19) >= 0.5 * cus && cfg_fits(kCfgs[46], N, K, glu)) {
             cfg = 46;
+            break;
+          } else {
+            continue;
+          }
         }
+        cfg = r.cfg;
         break;
       }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than

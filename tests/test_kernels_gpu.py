@@ -105,6 +105,7 @@ def test_sandwich(pkg, ctx, with_y, with_w2, H):
     (64, 2560, 2048, 4), (32, 2048, 11008, 4),
     # long K on one round of 128x128 tiles: split 4 ways along K (K / 64 divisible by 4), else unsplit
     (1024, 2048, 4096, 4), (1152, 2560, 4352, 8), (1024, 2048, 4160, 8), (1024, 1536, 4608, 8),
+    (256, 1536, 4608, 8), (256, 2048, 4160, 4),
 ])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul(pkg, ctx, M, N, K, bits, direct):
