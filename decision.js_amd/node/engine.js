@@ -97,6 +97,7 @@ class GpuEngine {
     this.stats = { forwards: 0, tokens: 0 };
     this.bufs = {};
     this.gen = 0;
+    this.seen = new Set(); // graph keys used once (captured on their second use)
     this.serial = ++engineSerial;
     this.ownsCtx = !this.opts.device;
   }
@@ -115,8 +116,15 @@ class GpuEngine {
     this.gen += 1;
     this.ctx.graphClear();
   }
+  // The graph key of a forward, from its second use on: the first forward with a key runs eagerly (0n), the
+  // second captures the graph, later ones replay it (capturing costs more than launching once).
   key(...parts) {
-    return this.graphs ? hashKey(JSON.stringify([this.serial, this.gen].concat(parts))) : 0n;
+    if (!this.graphs) return 0n;
+    const k = hashKey(JSON.stringify([this.serial, this.gen].concat(parts)));
+    if (this.seen.has(k)) return k;
+    if (this.seen.size >= 4096) this.seen.clear();
+    this.seen.add(k);
+    return 0n;
   }
 }
 

@@ -156,14 +156,15 @@ def test_shared_state_equals_forest(pkg, models):
         forest = eng.run([tree])["scores"][0]
         st = eng.prefill(tree["trunk"])
         shared = eng.run_shared(st, tree["branches"], tree["groups"])
-        shared2 = eng.run_shared(st, tree["branches"], tree["groups"])  # replay of the captured graph
+        shared2 = eng.run_shared(st, tree["branches"], tree["groups"])  # second use: captures the graph
+        shared3 = eng.run_shared(st, tree["branches"], tree["groups"])  # replays it
         want, _ = _oracle_forest(model, [tree])
         gaps = []
-        for f, s, s2, w in zip(forest, shared, shared2, want[0]):
+        for f, s, s2, s3, w in zip(forest, shared, shared2, shared3, want[0]):
             pf, ps, pw = ref.softmax(f), ref.softmax(s), ref.softmax(w)
             gaps.append((max(abs(a - b) for a, b in zip(pf, pw)), max(abs(a - b) for a, b in zip(ps, pw)),
                          max(abs(a - b) for a, b in zip(pf, ps))))
-            assert s == s2
+            assert s == s2 == s3
         print("per question (forest-oracle, shared-oracle, forest-shared): " +
               " ".join(f"({a:.1e},{b:.1e},{c:.1e})" for a, b, c in gaps))
         assert max(g[0] for g in gaps) < PROB_TOL and max(g[1] for g in gaps) < PROB_TOL
@@ -179,9 +180,9 @@ def test_graph_replay_is_bit_identical(pkg, models):
     try:
         rng = np.random.default_rng(4)
         V = 4096
-        a = [_tree(rng, V, 100, [20, 20, 20])]
-        b = [_tree(rng, V, 100, [20, 20, 20])]  # same shapes, other ids: replays a's graph
-        ra1, rb, ra2 = eng.run(a)["logits"], eng.run(b)["logits"], eng.run(a)["logits"]
+        a = [_tree(rng, V, 100, [20, 20, 20])]  # first use of the shapes: eager
+        b = [_tree(rng, V, 100, [20, 20, 20])]  # same shapes, other ids: captures the graph
+        ra1, rb, ra2 = eng.run(a)["logits"], eng.run(b)["logits"], eng.run(a)["logits"]  # ra2: a replay
         eng.graphs = False
         ra_eager = eng.run(a)["logits"]
         assert np.array_equal(ra1, ra2) and np.array_equal(ra1, ra_eager) and not np.array_equal(ra1, rb)
