@@ -26,6 +26,12 @@ async function main(req) {
           return { error: e.message };
         }
       });
+    case "graphkeys": {
+      // graph keys handed out over a sequence of forwards (no device: key() reads only the engine's own state)
+      const { GpuEngine } = require(path.join(root, "engine"));
+      const e = new GpuEngine(null, {}, {}, { graphs: req.graphs });
+      return req.seq.map((parts) => String(e.key(...parts)));
+    }
     case "passes": {
       const d = Object.create(host.D1.prototype);
       d.tokensPerPass = req.budget;

@@ -174,3 +174,28 @@ def test_node_decision_matches_python_host(tmp_path):
         key = "noul" if n == "churn" else "confidence"
         assert abs(js["shared"]["answers"][n][key] - js["one"]["answers"][n][key]) < 5e-4
     assert js["shared2"] == js["shared"]
+
+
+def test_graph_keys_from_second_use_match_python_host():
+    """Both hosts run a forward's first use of a key eagerly (key 0), capture on the second and replay after;
+    with graphs off every key is 0."""
+    load_pkg()
+    from decision_js_amd.engine import GpuEngine
+    seq = [["run", 100, 3, 5], ["run", 100, 3, 5], ["run", 100, 3, 5], ["run", 60, 3, 5], ["shared", 1, 32, 8, 5],
+           ["run", 60, 3, 5], ["shared", 2, 32, 8, 5]]
+
+    def py_keys(graphs):
+        e = GpuEngine.__new__(GpuEngine)
+        e.graphs, e._gen, e._seen = graphs, 0, set()
+        return [e._key(*p) for p in seq]
+
+    for graphs in (True, False):
+        js = [int(k) for k in node({"cmd": "graphkeys", "graphs": graphs, "seq": seq})]
+        py = py_keys(graphs)
+        for keys in (js, py):
+            if not graphs:
+                assert keys == [0] * len(seq)
+                continue
+            assert keys[0] == 0 and keys[1] == keys[2] != 0  # eager, capture, replay
+            assert keys[3] == 0 and keys[5] not in (0, keys[1])  # another shape: eager, then its own graph
+            assert keys[4] == 0 and keys[6] == 0  # a new state's questions: eager each time
