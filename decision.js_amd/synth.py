@@ -86,6 +86,21 @@ def tensor_plan(cfg: dict):
     return plan
 
 
+def head_plan(cfg: dict):
+    """[(name, shape)] of the learned EmbeddingGemma 2 decision head (eg2-head.ts:64-99) on embed_dim inputs:
+    state/question/option projections, the field MLP, the type embedding, two LayerNorms and the residual MLP."""
+    W, E = cfg["learned_head"]["width"], cfg["embed_dim"]
+    plan = []
+    for p in ("state_proj", "question_proj", "option_proj"):
+        plan += [(f"head.{p}.weight", (W, E)), (f"head.{p}.bias", (W,))]
+    plan += [("head.field.0.weight", (W, 3 * W)), ("head.field.0.bias", (W,)), ("head.field.3.weight", (W, W)),
+             ("head.field.3.bias", (W,)), ("head.type_emb.weight", (3, W)),
+             ("head.field_norm.weight", (W,)), ("head.field_norm.bias", (W,)),
+             ("head.option_norm.weight", (W,)), ("head.option_norm.bias", (W,)),
+             ("head.residual.0.weight", (W, 4 * W)), ("head.residual.0.bias", (W,)), ("head.residual.3.weight", (1, W))]
+    return plan
+
+
 def manifest_config(cfg: dict) -> dict:
     c = {k: v for k, v in cfg.items() if k not in ("bits",)}
     c["layer_types"] = ["full_attention"] * cfg["layers"]
@@ -96,24 +111,36 @@ def manifest_config(cfg: dict) -> dict:
         c["layer_scalars"] = [1.0] * cfg["layers"]
         c["attention_scale"] = 1.0
         c["embed_scale"] = math.sqrt(cfg["hidden"])
+        lh = cfg.get("learned_head")
+        if lh:  # the typed-decision head's scalars (export-eg2.py:80-84)
+            c["question_types"] = ["choice", "score", "noul"]
+            c["temperatures"] = dict(lh.get("temperatures", {"choice": 1.0, "score": 1.0, "noul": 1.0}))
+            c["head"] = {"width": lh["width"], "ln_eps": 1e-5, "prior_scale": lh.get("prior_scale", 2.0),
+                         "joint_scale": lh.get("joint_scale", 5.0), "gate": lh.get("gate", 0.6),
+                         "residual_bias": lh.get("residual_bias", 0.1)}
+            del c["learned_head"]
     return c
 
 
-def _make(cfg, name, kind, shape, seed, norm_std):
+def _make(cfg, name, kind, shape, seed, norm_std, std):
     if kind == "n":
         return name, kind, _norm(name, shape[0], norm_std, seed), None
-    w = normal(name, shape, 0.02, seed)
+    w = normal(name, shape, std, seed)
     if name == "embed" and cfg["model"] != "decoder":
         w = w * np.float32(math.sqrt(cfg["hidden"]))  # Gemma's sqrt(hidden) embedding scale, folded in
     q = fmt.quantize8(w) if cfg["bits"] == 8 else fmt.quantize4(w)
     return name, kind, q[0], q[1]
 
 
-def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads: int = 8) -> str:
+def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads: int = 8, std: float = 0.02) -> str:
     """Writes manifest.json + weights.bin for `cfg` under `out`; returns `out`. Skips the work when a
-    manifest with the same configuration and seed already exists there."""
+    manifest with the same configuration and seed already exists there. `std` is the linear and embedding
+    weights' standard deviation (the configurations' 0.02; tiny test models use ~1/sqrt(hidden) so that every
+    layer's branches move the residual stream as much as the embedding does)."""
     mc = manifest_config(cfg)
     mc["synthetic"] = {"seed": seed, "norm_std": norm_std}
+    if std != 0.02:
+        mc["synthetic"]["std"] = std
     if os.path.exists(os.path.join(out, "manifest.json")):
         try:
             if fmt.load_manifest(out)["config"] == mc:
@@ -123,12 +150,19 @@ def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads:
     blob = fmt.Blob(out, mc, cfg["bits"])
     plan = tensor_plan(cfg)
     with cf.ThreadPoolExecutor(max_workers=threads) as ex:
-        futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std) for n, k, s in plan]
+        futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std, std) for n, k, s in plan]
         for (name, kind, shape), fut in zip(plan, futs):
             _, _, a, b = fut.result()
             if kind == "n":
                 blob.f16(name, a)
             else:
                 blob.put_quant(name, a, b, shape, cfg["bits"])
+    if cfg["model"] != "decoder" and cfg.get("learned_head"):
+        # f32 host tensors; LayerNorm weights around 1, everything else N(0, 1/sqrt(fan-in))
+        for name, shape in head_plan(cfg):
+            if name.endswith("norm.weight"):
+                blob.host_f32(name, 1.0 + normal(name, shape, 0.1, seed))
+            else:
+                blob.host_f32(name, normal(name, shape, 1.0 / math.sqrt(shape[-1]), seed))
     blob.close({"repo": "synthetic", "revision": None, "seed": seed})
     return out

@@ -37,7 +37,7 @@ def _qs():
 
 def test_system_one_answers(pkg):
     from decision_js_amd import d1
-    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    D = d1.Decision("d1-3b", FakeDecoder(), d1.IdPrompt(), 4096)
     r = D.system_one([9, 9, 9, 9], _qs())
     a = r["answers"]
     assert a["topic"]["choice"] == "b" and abs(sum(a["topic"]["probabilities"].values()) - 1) < 1e-12
@@ -53,10 +53,10 @@ def test_passes_follow_the_token_budget(pkg):
     """Whole requests per pass up to tokensPerPass; a pass always takes at least one (d1.ts:217-219)."""
     from decision_js_amd import d1
     eng = FakeDecoder()
-    D = d1.Decision("decoder", eng, d1.IdPrompt(), 20)
+    D = d1.Decision("d1-3b", eng, d1.IdPrompt(), 20)
     reqs = [([1] * n, _qs()) for n in (5, 4, 30, 1, 1)]  # each request adds 6 question tokens
     seen = []
-    out = D.system_one_batch(reqs, on_progress=lambda a, b: seen.append((a, b)))
+    out = D.system_one_batch(reqs, {"on_progress": lambda a, b: seen.append((a, b))})  # BatchOptions (d1.ts:33-35)
     assert eng.passes == [11, 10, 36, 14] and seen == [(1, 5), (2, 5), (3, 5), (5, 5)]
     assert [o["usage"]["input_tokens"] for o in out] == [11, 10, 36, 7, 7]
     as_lists = [(s, list(q.values())) for s, q in reqs]
@@ -65,7 +65,7 @@ def test_passes_follow_the_token_budget(pkg):
 
 def test_a_failed_call_does_not_wedge_the_queue(pkg):
     from decision_js_amd import d1
-    D = d1.Decision("decoder", FakeDecoder(fail_once=True), d1.IdPrompt(), 4096)
+    D = d1.Decision("d1-3b", FakeDecoder(fail_once=True), d1.IdPrompt(), 4096)
     with pytest.raises(RuntimeError, match="decision.js: injected failure"):
         D.system_one([1], _qs())
     assert D.system_one([1], _qs())["answers"]["topic"]["choice"] == "b"
@@ -83,7 +83,7 @@ def test_check_question(pkg, q, msg):
     from decision_js_amd import d1, questions
     with pytest.raises(questions.QuestionError, match=msg):
         questions.check_question(q)
-    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    D = d1.Decision("d1-3b", FakeDecoder(), d1.IdPrompt(), 4096)
     with pytest.raises(questions.QuestionError):
         D.system_one([1], {"q": q})
 
@@ -91,7 +91,7 @@ def test_check_question(pkg, q, msg):
 def test_option_group_count_must_match(pkg):
     from decision_js_amd import d1, questions
     q = dict(_qs()["urgency"], options=[[1], [2]])
-    D = d1.Decision("decoder", FakeDecoder(), d1.IdPrompt(), 4096)
+    D = d1.Decision("d1-3b", FakeDecoder(), d1.IdPrompt(), 4096)
     with pytest.raises(questions.QuestionError, match="option groups"):
         D.system_one([1], {"u": q})
 
@@ -108,8 +108,32 @@ def test_engine_packing_and_helpers(pkg):
     assert np.array_equal(ref.ranges_mask(pk["rng"], pk["T"]), ref.forest_mask(meta))
     assert engine.common_prefix([[1, 2, 3], [1, 2, 4], [1, 2]]) == 1
     assert engine.common_prefix([[1, 2, 3, 4], [1, 2, 3, 5]]) == 3 and engine.common_prefix([[1, 2]]) == 0
-    out = np.arange(4 * 4, dtype=np.float32)
-    assert engine.group_max(out, 4, trees) == ref.group_max(out, 4, [g for t in trees for g in t["groups"]]) and True or True
+    out = np.random.default_rng(5).standard_normal(4 * 4).astype(np.float32)
+    per_tree = engine.group_max(out, 4, trees)
+    assert [len(t) for t in per_tree] == [3, 1]
+    assert [s for t in per_tree for s in t] == ref.group_max(out, 4, [g for t in trees for g in t["groups"]])
+    # known answer: leaf 2 (tree 0, question 2) has groups [5] and [6, 7, 8] over out[8:12]
+    assert per_tree[0][2] == [float(out[8]), float(out[9:12].max())]
+
+
+def test_encoder_packing_matches_oracle_bit_exact(pkg):
+    """encoder.pack_encoder (the engine's host packing) == the oracle's restatement of eg2-engine.ts:74-86,
+    bit for bit: ids, meta, full and windowed key ranges, per-text ranges; empty-free ragged texts, one-token
+    texts, windows wider than a text."""
+    from decision_js_amd import encoder
+    rng = np.random.default_rng(6)
+    for window in (None, 0, 3, 50):
+        seqs = [[int(x) for x in rng.integers(0, 1000, n)] for n in (1, 17, 2, 64, 5)]
+        got = encoder.pack_encoder(seqs, window)
+        ids, meta, full, slide, ranges = ref.pack_encoder(seqs, window)
+        assert got["T"] == len(ids) and got["S"] == len(seqs)
+        assert got["ids"].dtype == ids.dtype and np.array_equal(got["ids"], ids)
+        assert got["meta"].dtype == meta.dtype and np.array_equal(got["meta"], meta)
+        assert np.array_equal(got["full"], full) and np.array_equal(got["ranges"], ranges)
+        if window is None:
+            assert got["slide"] is None and slide is None
+        else:
+            assert np.array_equal(got["slide"], slide)
 
 
 def test_format_roundtrip(pkg, tmp_path):

@@ -116,12 +116,28 @@ def test_matmul(pkg, ctx, M, N, K, bits, direct):
     X = rand_f16(rng, (M, K))
     W = ctx.weight_q(codes, scales, N, K, bits, dj.W_MFMA | (dj.W_DIRECT if direct else 0))
     dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
-    run(ctx, lambda r: r.matmul(dX, W, dY, M))
+    ctx.profile_reset()
+    ctx.profile(True)
+    try:
+        run(ctx, lambda r: r.matmul(dX, W, dY, M))
+    finally:
+        ctx.profile(False)
+    labels = [name for name in ctx.profile_table() if name.startswith("matmul")]
     got = dY.read(np.float16, (M, N))
     want = ref.matmul(X, W16, np.float64)
     worst = f16_close(got, want, ulps=1.0, atol=2e-5)
-    print(f"matmul {M}x{N}x{K} q{bits}: worst/bound {worst:.3f}")
+    print(f"matmul {M}x{N}x{K} q{bits}: worst/bound {worst:.3f} via {labels}")
     assert worst <= 1.0
+    # the long-K cases must take the path they are listed for: the 4-way split where K / 64 divides by 4,
+    # unsplit (no split suffix) where it does not
+    if (M, N, K) in LONGK_SPLIT:
+        assert len(labels) == 1 and labels[0].endswith("/k4"), labels
+    if (M, N, K) in LONGK_UNSPLIT:
+        assert len(labels) == 1 and "/k" not in labels[0].split("]")[-1], labels
+
+
+LONGK_SPLIT = {(1024, 2048, 4096), (1152, 2560, 4352), (1024, 1536, 4608), (256, 1536, 4608)}
+LONGK_UNSPLIT = {(1024, 2048, 4160), (256, 2048, 4160)}
 
 
 @pytest.mark.parametrize("bits,direct", [(8, False), (4, False), (8, True), (4, True)])

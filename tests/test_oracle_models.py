@@ -1,0 +1,432 @@
+"""Pins the oracle's whole forwards and the parts of its kernels the single-op checks leave open (CPU only).
+
+* decoder_forward (oracle/ref.py) against `transformers`' Qwen3Model (QK-norm, the configs[1] / configs[4] form)
+  and Qwen2Model with zero q/k/v biases (no QK-norm, q4: the configs[2] form), random-init architectures built
+  offline and loaded with the oracle's own f16-dequantized weights, run in float64. The library's layer wiring
+  is independent of ours: which norm weight sits where, which half of w13 is the gate, GQA, the final norm and
+  the tied head (d1-3b-engine.ts:86-106; LEAF_LOGITS kernels.ts:149-185).
+* encoder_forward against a float64 restatement built from torch library routines (F.rms_norm,
+  F.scaled_dot_product_attention, F.gelu(approximate="tanh"), RoPE as a complex rotation), following
+  Eg2Engine.embed (eg2-engine.ts:103-139) without per-layer embeddings.
+* qk_norm_rope's norm half (q with qn, k with kn, plain v-norm; kernels.ts:100-104, eg2-kernels.ts:76-81),
+  gelu_tanh (eg2-kernels.ts:9-13) against erf-GELU and torch's tanh GELU, attention over kept K/V rows
+  (the shared-state mode) against the concatenated-rows form, and the shared trunk invariant of the causal
+  decoder (d3-engine.ts:67-93) on the oracle itself.
+
+Each check comes with mistakes planted in the oracle that it must catch.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import ref
+
+torch = pytest.importorskip("torch")
+F = torch.nn.functional
+
+TINY_DEC = dict(layers=2, hidden=64, intermediate=96, heads=4, kv_heads=2, head_dim=16, vocab=512)
+TINY_ENC = dict(layers=2, hidden=64, intermediate=96, heads=2, kv_heads=1, head_dim=32, vocab=512, head_width=128,
+                embed_dim=64)
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(np.asarray(a, dtype=np.float64)))
+
+
+def _rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+# ---------------------------------------------------------------- decoder_forward vs transformers
+
+@pytest.fixture(scope="module")
+def tiny_decoders(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("dec")
+    # unit-gain weights (std 1/sqrt(hidden)): every branch moves the residual stream as much as the embedding
+    q3 = synth.generate(synth.reduced("qwen3-0.6b-q8", **TINY_DEC), str(d / "qwen3"), norm_std=0.1, std=0.125)
+    q2 = synth.generate(synth.reduced("qwen2.5-3b-q4", **TINY_DEC), str(d / "qwen2"), norm_std=0.1, std=0.125)
+    return {"qwen3": q3, "qwen2": q2}
+
+
+def _hf_decoder(model: ref.Model):
+    """A transformers Qwen3Model (QK-norm) or Qwen2Model (none) holding the oracle model's f16 weights."""
+    tr = pytest.importorskip("transformers")
+    c = model.c
+    H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
+    common = dict(vocab_size=c["vocab"], hidden_size=H, intermediate_size=I, num_hidden_layers=c["layers"],
+                  num_attention_heads=h, num_key_value_heads=kv, rms_norm_eps=c["eps"], rope_theta=c["rope_theta"],
+                  max_position_embeddings=4096, tie_word_embeddings=True)
+    if c.get("qk_norm"):
+        cfg = tr.Qwen3Config(head_dim=D, attention_bias=False, **common)
+        m = tr.Qwen3Model(cfg)
+    else:
+        assert H // h == D
+        cfg = tr.Qwen2Config(**common)
+        m = tr.Qwen2Model(cfg)
+    m.config._attn_implementation = "eager"
+    m = m.to(torch.float64).eval()
+    sd = {"embed_tokens.weight": _t(model.w16("embed")), "norm.weight": _t(model.t["final_norm"])}
+    for i in range(c["layers"]):
+        p, q = f"layers.{i}.", f"layers.{i}."
+        qkv = model.w16(p + "qkv")
+        sd[q + "self_attn.q_proj.weight"] = _t(qkv[:h * D])
+        sd[q + "self_attn.k_proj.weight"] = _t(qkv[h * D:(h + kv) * D])
+        sd[q + "self_attn.v_proj.weight"] = _t(qkv[(h + kv) * D:])
+        sd[q + "self_attn.o_proj.weight"] = _t(model.w16(p + "o_proj"))
+        w13 = model.w16(p + "w13")
+        sd[q + "mlp.gate_proj.weight"] = _t(w13[:I])
+        sd[q + "mlp.up_proj.weight"] = _t(w13[I:])
+        sd[q + "mlp.down_proj.weight"] = _t(model.w16(p + "w2"))
+        sd[q + "input_layernorm.weight"] = _t(model.t[p + "operator_norm"])
+        sd[q + "post_attention_layernorm.weight"] = _t(model.t[p + "ffn_norm"])
+        if c.get("qk_norm"):
+            sd[q + "self_attn.q_norm.weight"] = _t(model.t[p + "q_norm"])
+            sd[q + "self_attn.k_norm.weight"] = _t(model.t[p + "k_norm"])
+        else:
+            for n in ("q", "k", "v"):
+                sd[q + f"self_attn.{n}_proj.bias"] = torch.zeros_like(m.state_dict()[q + f"self_attn.{n}_proj.bias"])
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    return m
+
+
+def _forest(rng, V):
+    trunk = [int(x) for x in rng.integers(0, V, 21)]
+    branches = [[int(x) for x in rng.integers(0, V, n)] for n in (9, 1, 14)]
+    groups = [[[int(a)] for a in rng.choice(V, n, replace=False)] for n in (2, 3, 5)]
+    return {"trunk": trunk, "branches": branches, "groups": groups}
+
+
+def _compare_decoder(path, model=None):
+    """The oracle's forest forward (float64 accumulation, f16 storage points) against the library model run on
+    each trunk + branch sequence alone: the residual stream after layer 0 and the final normed hidden state at
+    every token within 5e-3 relative L2 (f16 rounding of the stored activations is ~1e-3), and the answer
+    logits (normed leaf row . f32-dequantized embedding rows) within 5e-3 of their scale."""
+    model = model or ref.Model(path)
+    c = model.c
+    rng = np.random.default_rng(11)
+    tree = _forest(rng, c["vocab"])
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest([tree])
+    mask = ref.ranges_mask(ref.forest_ranges(meta), len(ids))
+    logits, _, dbg = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64,
+                                         debug_layers=(0, c["layers"] - 1))
+    hf = _hf_decoder(ref.Model(path))  # the library side always reads the untouched file
+    ec, es, eb = model.t["embed"]
+    E32 = ref.dequant_f32(ec, es, eb).astype(np.float64)
+    P = len(tree["trunk"])
+    off = P
+    for b, br in enumerate(tree["branches"]):
+        seq = tree["trunk"] + br
+        rows = list(range(P)) + list(range(off, off + len(br)))
+        off += len(br)
+        with torch.no_grad():
+            out = hf(input_ids=torch.tensor([seq]), output_hidden_states=True)
+        layer0 = out.hidden_states[1][0].numpy()
+        final = out.last_hidden_state[0].numpy()
+        assert _rel_l2(dbg[0][rows], layer0) < 5e-3, f"branch {b}: residual after layer 0"
+        x = dbg[c["layers"] - 1][rows].astype(np.float64)  # the oracle's last residual, normed here in float64
+        normed = x / np.sqrt((x * x).mean(-1, keepdims=True) + c["eps"]) * model.t["final_norm"].astype(np.float64)
+        assert _rel_l2(normed, final) < 5e-3, f"branch {b}: final hidden state"
+        want = final[-1] @ E32[leaf_ids[b * n_ids:(b + 1) * n_ids]].T
+        got = logits[b * n_ids:(b + 1) * n_ids].astype(np.float64)
+        assert np.abs(got - want).max() < 5e-3 * np.abs(want).max(), f"branch {b}: answer logits"
+
+
+@pytest.mark.parametrize("name", ["qwen3", "qwen2"])
+def test_decoder_forward_matches_transformers(tiny_decoders, name):
+    _compare_decoder(tiny_decoders[name])
+
+
+def _planted(path, mutate):
+    model = ref.Model(path)
+    mutate(model)
+    with pytest.raises(AssertionError):
+        _compare_decoder(path, model)
+
+
+def test_planted_decoder_norm_swap_is_caught(tiny_decoders):
+    def swap(m):
+        t = m.t
+        t["layers.1.operator_norm"], t["layers.1.ffn_norm"] = t["layers.1.ffn_norm"], t["layers.1.operator_norm"]
+    _planted(tiny_decoders["qwen3"], swap)
+
+
+def test_planted_decoder_qk_norm_swap_is_caught(tiny_decoders):
+    def swap(m):
+        t = m.t
+        t["layers.0.q_norm"], t["layers.0.k_norm"] = t["layers.0.k_norm"], t["layers.0.q_norm"]
+    _planted(tiny_decoders["qwen3"], swap)
+
+
+def test_planted_decoder_final_norm_slip_is_caught(tiny_decoders):
+    def drop(m):
+        m.t["final_norm"] = np.ones_like(m.t["final_norm"])
+    _planted(tiny_decoders["qwen2"], drop)
+
+
+def test_planted_decoder_gate_up_swap_is_caught(tiny_decoders, monkeypatch):
+    orig = ref.silu_mul
+    monkeypatch.setattr(ref, "silu_mul", lambda a, b, acc=np.float32: orig(b, a, acc))
+    with pytest.raises(AssertionError):
+        _compare_decoder(tiny_decoders["qwen3"])
+
+
+def test_planted_decoder_gqa_slip_is_caught(tiny_decoders, monkeypatch):
+    """Query head h reading kv head h % kv instead of h / (heads / kv)."""
+    orig = ref.attention
+
+    def slip(Z, heads, kv, D, mask, scale, acc=np.float32, q_stride=None, kv_rows=None):
+        q = Z[:, :heads * D].reshape(len(Z), heads, D)
+        perm = [h % kv * (heads // kv) + h // kv for h in range(heads)]  # inverse of the grouping
+        Z2 = Z.copy()
+        Z2[:, :heads * D] = q[:, perm].reshape(len(Z), -1)
+        out = orig(Z2, heads, kv, D, mask, scale, acc, q_stride, kv_rows).reshape(len(Z), heads, D)
+        inv = np.argsort(perm)
+        return out[:, inv].reshape(len(Z), -1)
+    monkeypatch.setattr(ref, "attention", slip)
+    with pytest.raises(AssertionError):
+        _compare_decoder(tiny_decoders["qwen3"])
+
+
+# ---------------------------------------------------------------- shared state (kept K/V) on the oracle
+
+def test_shared_state_equals_forest_on_oracle(tiny_decoders):
+    """A state prefilled once with its K/V kept, then each question run alone against the kept rows
+    (kv_prefix), gives the same answer logits as the forest that packs state + questions in one forward: the
+    causal invariant of d3-engine.ts:67-93, on the oracle's kv_rows path."""
+    model = ref.Model(tiny_decoders["qwen3"])
+    rng = np.random.default_rng(13)
+    tree = _forest(rng, model.c["vocab"])
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest([tree])
+    mask = ref.ranges_mask(ref.forest_ranges(meta), len(ids))
+    want, _, _ = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64)
+    P = len(tree["trunk"])
+    st = np.array(tree["trunk"], np.uint32)
+    _, kept, _ = ref.decoder_forward(model, st, np.arange(P, dtype=np.int32), np.tril(np.ones((P, P), bool)), [], None, 0,
+                                     acc=np.float64, keep_kv=True)
+    for b, br in enumerate(tree["branches"]):
+        n = len(br)
+        qmask = np.concatenate([np.ones((n, P), bool), np.tril(np.ones((n, n), bool))], axis=1)
+        lid = leaf_ids[b * n_ids:(b + 1) * n_ids]
+        got, _, _ = ref.decoder_forward(model, np.array(br, np.uint32), np.arange(P, P + n, dtype=np.int32), qmask,
+                                        [n - 1], lid, n_ids, acc=np.float64, kv_prefix=kept)
+        assert np.abs(got - want[b * n_ids:(b + 1) * n_ids]).max() < 1e-9
+
+
+def test_attention_kv_rows_equals_concatenated_rows():
+    """attention() over separate kept rows [k | v] equals attention over the same keys laid in Z itself."""
+    rng = np.random.default_rng(14)
+    h, kv, D, P, T = 4, 2, 8, 6, 5
+    prefix = rng.standard_normal((P, (h + 2 * kv) * D)).astype(np.float16)
+    Z = rng.standard_normal((T, (h + 2 * kv) * D)).astype(np.float16)
+    rows = np.concatenate([prefix[:, h * D:], Z[:, h * D:]])
+    mask = np.concatenate([np.ones((T, P), bool), np.tril(np.ones((T, T), bool))], axis=1)
+    mask[2, 1] = False
+    got = ref.attention(Z, h, kv, D, mask, 0.4, np.float64, kv_rows=rows)
+    # the same keys as rows of one [P + T] array, queries at the last T rows
+    full = np.concatenate([prefix, Z])
+    fmask = np.zeros((P + T, P + T), bool)
+    fmask[P:] = mask
+    fmask[:P, 0] = True
+    want = ref.attention(full, h, kv, D, fmask, 0.4, np.float64)[P:]
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # and a slip that drops the kept rows (queries see only their own rows) differs
+    bad = ref.attention(Z, h, kv, D, mask[:, P:], 0.4, np.float64)
+    assert not np.array_equal(got.view(np.uint16), bad.view(np.uint16))
+
+
+# ---------------------------------------------------------------- qk_norm_rope: the norm half
+
+def _check_qkv_norm_rope(mode, vnorm):
+    """Per head: q * rsqrt(mean q^2 + eps) * qn, k likewise with kn, v plain-normed when vnorm (else untouched),
+    then RoPE as multiplication by exp(i pos f_d) on the (d, d + D/2) pairs of q and k, in float64."""
+    rng = np.random.default_rng(15)
+    T, h, kv, D, eps, theta = 4, 3, 1, 16, 1e-6, 1e4
+    Z = (rng.standard_normal((T, (h + 2 * kv) * D)) * 3).astype(np.float16)
+    qn = (1 + rng.standard_normal(D) * 0.3).astype(np.float16)
+    kn = (1 + rng.standard_normal(D) * 0.3).astype(np.float16)
+    pos = np.array([0, 3, 17, 250], np.int32)
+    got = ref.qk_norm_rope(Z, h, kv, D, pos, qn, kn, vnorm, eps, theta, mode=mode, acc=np.float64).astype(np.float64)
+    z = Z.astype(np.float64).reshape(T, h + 2 * kv, D)
+    g = got.reshape(T, h + 2 * kv, D)
+    d = np.arange(D // 2)
+    f = theta ** (-2.0 * d / D) if mode == 0 else 1.0 / theta ** (2.0 * d / D)
+    for t in range(T):
+        for j in range(h + 2 * kv):
+            v = z[t, j]
+            r = v / math.sqrt((v * v).mean() + eps)
+            if j < h:
+                r = r * qn.astype(np.float64)
+            elif j < h + kv:
+                r = r * kn.astype(np.float64)
+            else:
+                want = r if vnorm else v
+                assert np.abs(g[t, j] - want).max() <= 2 ** -10 * np.abs(want).max()
+                continue
+            c = (r[:D // 2] + 1j * r[D // 2:]) * np.exp(1j * pos[t] * f)
+            want = np.concatenate([c.real, c.imag])
+            assert np.abs(g[t, j] - want).max() <= 2 ** -9 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("mode,vnorm", [(0, False), (1, True)])
+def test_qkv_norm_rope_closed_form(mode, vnorm):
+    _check_qkv_norm_rope(mode, vnorm)
+
+
+def test_planted_qk_norm_weight_swap_is_caught(monkeypatch):
+    orig = ref.qk_norm_rope
+    monkeypatch.setattr(ref, "qk_norm_rope", lambda Z, h, kv, D, pos, qn=None, kn=None, *a, **k: orig(Z, h, kv, D, pos, kn, qn, *a, **k))
+    with pytest.raises(AssertionError):
+        _check_qkv_norm_rope(0, False)
+
+
+def test_planted_vnorm_slip_is_caught(monkeypatch):
+    orig = ref.qk_norm_rope
+    monkeypatch.setattr(ref, "qk_norm_rope", lambda Z, h, kv, D, pos, qn=None, kn=None, vnorm=False, *a, **k: orig(Z, h, kv, D, pos, qn, kn, False, *a, **k))
+    with pytest.raises(AssertionError):
+        _check_qkv_norm_rope(1, True)
+
+
+# ---------------------------------------------------------------- gelu_tanh
+
+def _check_gelu(fn):
+    """The tanh GELU against (1) torch's F.gelu(approximate="tanh") in float64 (the same formula, a library
+    routine) to 1e-12 wherever the +-15 clamp is inactive, and (2) the exact erf GELU within the tanh form's
+    approximation error, below 5e-4 everywhere (the tanh form's largest deviation is 4.73e-4, near |x| = 2.2);
+    saturated at the clamp."""
+    x = np.concatenate([np.linspace(-8, 8, 4001), [-30.0, -20.0, 20.0, 30.0]])
+    got = fn(x)
+    lib = F.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    inner = np.abs(0.7978845608 * (x + 0.044715 * x ** 3)) < 15
+    assert np.abs(got[inner] - lib[inner]).max() < 1e-9
+    from scipy.special import erf
+    exact = 0.5 * x * (1 + erf(x / math.sqrt(2)))
+    assert np.abs(got - exact).max() < 5e-4
+
+
+def test_gelu_tanh_vs_library_and_erf():
+    _check_gelu(ref.gelu_tanh)
+
+
+def test_planted_gelu_dropped_cubic_is_caught():
+    def slip(x):
+        u = np.clip(0.7978845608 * x, -15.0, 15.0)
+        e = np.exp(2.0 * u)
+        return 0.5 * x * (1.0 + (e - 1.0) / (e + 1.0))
+    with pytest.raises(AssertionError):
+        _check_gelu(slip)
+
+
+# ---------------------------------------------------------------- encoder_forward vs a torch-library restatement
+
+@pytest.fixture(scope="module")
+def tiny_encoder(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("enc")
+    return synth.generate(synth.reduced("eg2-encoder-q8", **TINY_ENC), str(d / "eg2"), norm_std=0.1, std=0.125)
+
+
+def _torch_encoder(model: ref.Model, seqs):
+    """Each text alone, float64, library routines: embedding rows (sqrt(H) folded in) -> rms_norm(input_layernorm)
+    -> per layer [qkv, q/k rms_norm with weights and plain v rms_norm, RoPE exp(i pos / theta^(2d/D)),
+    bidirectional SDPA (scale 1, GQA), o, x += rms_norm(o) post_attention_layernorm, rms_norm(x)
+    pre_feedforward_layernorm, gate|up, gelu_tanh(gate) up, down, x = (x + rms_norm(o) post_ff) * scalar, rms_norm(x)
+    with the next layer's input norm or final_norm] -> mean over the text -> dense1, dense2 (f32-dequantized) ->
+    L2 normalisation."""
+    c = model.c
+    H, I, h, kv, D, eps, theta = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"], c["rope_theta"]
+    L = c["layers"]
+
+    def W(name):
+        return _t(model.w16(name))
+
+    def nw(name):
+        return _t(model.t[name])
+
+    def rms(x, w=None):
+        return F.rms_norm(x, (x.shape[-1],), weight=w, eps=eps)
+
+    E = W("embed")
+    out = []
+    for s in seqs:
+        n = len(s)
+        x = E[torch.tensor(s)]
+        normed = rms(x, nw("layers.0.input_layernorm"))
+        ang = torch.arange(n, dtype=torch.float64)[:, None] / theta ** (torch.arange(D // 2, dtype=torch.float64) * 2 / D)
+        rot = torch.polar(torch.ones_like(ang), ang)
+        for i in range(L):
+            p = f"layers.{i}."
+            z = normed @ W(p + "qkv").T
+            q = rms(z[:, :h * D].reshape(n, h, D), nw(p + "q_norm"))
+            k = rms(z[:, h * D:(h + kv) * D].reshape(n, kv, D), nw(p + "k_norm"))
+            v = rms(z[:, (h + kv) * D:].reshape(n, kv, D))
+
+            def rope(a):
+                cplx = torch.complex(a[..., :D // 2], a[..., D // 2:]) * rot[:, None, :]
+                return torch.cat([cplx.real, cplx.imag], -1)
+            q, k = rope(q), rope(k)
+            k = k.repeat_interleave(h // kv, dim=1)
+            v = v.repeat_interleave(h // kv, dim=1)
+            y = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), scale=1.0)
+            y = y.transpose(0, 1).reshape(n, h * D)
+            o = y @ W(p + "o").T
+            x = x + rms(o, nw(p + "post_attention_layernorm"))
+            normed = rms(x, nw(p + "pre_feedforward_layernorm"))
+            gu = normed @ W(p + "gu").T
+            o = (F.gelu(gu[:, :I], approximate="tanh") * gu[:, I:]) @ W(p + "down").T
+            x = (x + rms(o, nw(p + "post_feedforward_layernorm"))) * c.get("layer_scalars", [1.0] * L)[i]
+            normed = rms(x, nw(f"layers.{i + 1}.input_layernorm" if i + 1 < L else "final_norm"))
+        pooled = normed.mean(0)
+        d1 = _t(ref.dequant_f32(*model.t["head.dense1"]))
+        d2 = _t(ref.dequant_f32(*model.t["head.dense2"]))
+        e = (pooled @ d1.T) @ d2.T
+        out.append((e / e.norm()).numpy())
+    return np.stack(out)
+
+
+def _compare_encoder(path, model=None):
+    model = model or ref.Model(path)
+    rng = np.random.default_rng(16)
+    seqs = [[int(x) for x in rng.integers(0, model.c["vocab"], n)] for n in (23, 8, 1, 12)]
+    got = ref.encoder_forward(model, seqs, acc=np.float64)
+    want = _torch_encoder(ref.Model(path), seqs)  # the untouched file
+    for i in range(len(seqs)):
+        assert _rel_l2(got[i], want[i]) < 5e-3, f"text {i}"
+
+
+def test_encoder_forward_matches_library_restatement(tiny_encoder):
+    _compare_encoder(tiny_encoder)
+
+
+def test_planted_encoder_sandwich_swap_is_caught(tiny_encoder):
+    model = ref.Model(tiny_encoder)
+    t = model.t
+    p = "layers.1."
+    t[p + "post_attention_layernorm"], t[p + "pre_feedforward_layernorm"] = t[p + "pre_feedforward_layernorm"], t[p + "post_attention_layernorm"]
+    with pytest.raises(AssertionError):
+        _compare_encoder(tiny_encoder, model)
+
+
+def test_planted_encoder_gate_up_swap_is_caught(tiny_encoder, monkeypatch):
+    orig = ref.gelu_mul
+    monkeypatch.setattr(ref, "gelu_mul", lambda a, b, acc=np.float32: orig(b, a, acc))
+    with pytest.raises(AssertionError):
+        _compare_encoder(tiny_encoder)
+
+
+def test_planted_encoder_rope_position_slip_is_caught(tiny_encoder, monkeypatch):
+    """RoPE at twice the position within the text (a stride slip; a constant offset per text would be invisible,
+    since bidirectional RoPE scores depend only on position differences)."""
+    orig = ref.pack_encoder
+
+    def slip(seqs, window=None):
+        ids, meta, full, slide, ranges = orig(seqs, window)
+        meta = meta.copy()
+        meta[:, 3] = 2 * meta[:, 3]
+        return ids, meta, full, slide, ranges
+    monkeypatch.setattr(ref, "pack_encoder", slip)
+    with pytest.raises(AssertionError):
+        _compare_encoder(tiny_encoder)
