@@ -55,7 +55,10 @@ SIGNATURES = {
     "dj_buf_copy": [_P, _P, _P, _SZ],
     "dj_rec_snapshot": [_P, _P, _SZ, _P],
     "dj_rec_finish": [_P],
+    "dj_rec_abort": [_P],
     "dj_graph_clear": [_P],
+    "dj_graph_drop": [_P, _U64],
+    "dj_graph_count": [_P, C.POINTER(_I)],
     "dj_timer_begin": [_P],
     "dj_timer_end": [_P, C.POINTER(_F)],
     "dj_profile_enable": [_P, _I],
@@ -212,6 +215,14 @@ class Context:
     def graph_clear(self):
         check(lib().dj_graph_clear(self.h))
 
+    def graph_drop(self, key: int):
+        check(lib().dj_graph_drop(self.h, key))
+
+    def graph_count(self) -> int:
+        n = C.c_int()
+        check(lib().dj_graph_count(self.h, C.byref(n)))
+        return n.value
+
     # timing / profiling (gpu.ts:29-34, 185-197)
     def timer_begin(self):
         check(lib().dj_timer_begin(self.h))
@@ -314,6 +325,21 @@ class Recorder:
         h, self.h = self.h, None
         check(lib().dj_rec_finish(h))
         return self._snaps
+
+    def abort(self):
+        """Ends a recording that failed (dj_rec_abort): nothing more runs and the context is free for the next
+        forward. Its own status is not raised: the error being handled is the one to report."""
+        if self.h is not None:
+            h, self.h = self.h, None
+            lib().dj_rec_abort(h)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        if exc_type is not None:
+            self.abort()
+        return False
 
 
 def kv_src(buf, rows, stride, k_col, v_col) -> KVSrc:

@@ -44,6 +44,7 @@ struct dj_snapshot {
 
 struct dj_graph_entry {
   hipGraphExec_t exec = nullptr;
+  uint64_t last_use = 0;        // the context's graph clock at the last capture or replay (LRU eviction)
   std::vector<void *> staging;  // snapshot buffers written by the graph, reused on replay
   std::vector<size_t> staging_bytes;
 };
@@ -62,8 +63,9 @@ struct dj_ctx {
   // pinned staging for dj_upload (bump allocated, reset when the stream is drained)
   uint8_t *pinned = nullptr;
   size_t pinned_cap = 0, pinned_used = 0;
-  // graph cache
+  // graph cache: at most graph_cap() entries, the least recently used evicted first
   std::unordered_map<uint64_t, dj_graph_entry> graphs;
+  uint64_t graph_clock = 0;
   dj_rec *active = nullptr;
   // timers
   hipEvent_t t0 = nullptr, t1 = nullptr;
@@ -73,7 +75,8 @@ struct dj_ctx {
   std::vector<hipEvent_t> event_pool;
   std::unordered_map<std::string, std::pair<double, int64_t>> prof;
   std::vector<std::string> prof_order;
-  std::string fault_op;  // DJ_FAULT_INJECT
+  std::string fault_op;  // DJ_FAULT_INJECT: the op name (or "*") that fails ...
+  long fault_left = -1;  // ... this many more times (-1: every time)
   // split-K GEMM / split-KV attention workspace: f32 partials, written and read by consecutive kernels of
   // the stream (free between ops)
   float *gemm_ws = nullptr;

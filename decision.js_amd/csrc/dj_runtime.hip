@@ -48,8 +48,15 @@ extern "C" int dj_init(int ordinal, dj_ctx **out) {
   }
   DJ_HIP(hipEventCreate(&c->t0));
   DJ_HIP(hipEventCreate(&c->t1));
-  const char *f = getenv("DJ_FAULT_INJECT");
-  if (f) c->fault_op = f;
+  // DJ_FAULT_INJECT=<op>[:<n>]: the op fails (before launching anything) every time, or its next n times
+  if (const char *f = getenv("DJ_FAULT_INJECT")) {
+    c->fault_op = f;
+    const size_t colon = c->fault_op.find(':');
+    if (colon != std::string::npos) {
+      c->fault_left = atol(c->fault_op.c_str() + colon + 1);
+      c->fault_op.resize(colon);
+    }
+  }
   // split-K / split-KV workspace: 64 MiB of f32 partials (every slice is written before it is read)
   const size_t ws_floats = (size_t)16 << 20;
   if (hipMalloc((void **)&c->gemm_ws, ws_floats * 4) == hipSuccess) c->gemm_ws_floats = ws_floats;
@@ -73,12 +80,38 @@ extern "C" int dj_device_info(dj_ctx *ctx, char *name, size_t cap, int *cus, siz
   return DJ_OK;
 }
 
+static void free_graph(dj_graph_entry &g) {
+  if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  for (void *p : g.staging) (void)hipFree(p);
+  g.exec = nullptr;
+  g.staging.clear();
+}
+
 static void free_graphs(dj_ctx *c) {
-  for (auto &kv : c->graphs) {
-    if (kv.second.exec) (void)hipGraphExecDestroy(kv.second.exec);
-    for (void *p : kv.second.staging) (void)hipFree(p);
-  }
+  for (auto &kv : c->graphs) free_graph(kv.second);
   c->graphs.clear();
+}
+
+// Most graphs a context keeps (DJ_GRAPH_CAP, default 64): a long-running host that sees many shapes or many
+// shared states holds a bounded number of graph execs and snapshot staging buffers.
+static size_t graph_cap() {
+  const char *e = getenv("DJ_GRAPH_CAP");
+  const long n = e ? atol(e) : 64;
+  return n >= 1 ? (size_t)n : 1;
+}
+
+// Makes room for one more graph: evicts least recently used entries until fewer than the cap remain. Called
+// with the stream drained (every forward waits for its work in dj_rec_finish), so no evicted exec is running.
+static void evict_graphs(dj_ctx *c, uint64_t keep) {
+  const size_t cap = graph_cap();
+  while (c->graphs.size() >= cap) {
+    auto victim = c->graphs.end();
+    for (auto it = c->graphs.begin(); it != c->graphs.end(); ++it)
+      if (it->first != keep && (victim == c->graphs.end() || it->second.last_use < victim->second.last_use)) victim = it;
+    if (victim == c->graphs.end()) break;
+    free_graph(victim->second);
+    c->graphs.erase(victim);
+  }
 }
 
 extern "C" int dj_destroy(dj_ctx *c) {
@@ -353,6 +386,7 @@ extern "C" int dj_rec_begin(dj_ctx *c, uint64_t key, dj_rec **out, int *replay) 
     auto it = c->graphs.find(key);
     if (it != c->graphs.end()) {
       r->replay = true;
+      it->second.last_use = ++c->graph_clock;
     } else {
       hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeRelaxed);
       if (e != hipSuccess) {
@@ -388,8 +422,10 @@ int dj_op_begin(dj_rec *rec, const char *name) {
     if (st) return -st;
   }
   if (rec->replay) return 1;
-  if (!c->fault_op.empty() && (c->fault_op == name || c->fault_op == "*"))
+  if (!c->fault_op.empty() && c->fault_left != 0 && (c->fault_op == name || c->fault_op == "*")) {
+    if (c->fault_left > 0) c->fault_left--;
     return -dj_fail(DJ_EINJECT, "decision.js: fault injected in %s (DJ_FAULT_INJECT)", name);
+  }
   if (c->profiling && !rec->capturing) {
     dj_prof_slot s{name, pool_event(c), pool_event(c)};
     (void)hipEventRecord(s.a, c->stream);
@@ -487,6 +523,8 @@ extern "C" int dj_rec_finish(dj_rec *r) {
           ge.staging.push_back(s.staging);
           ge.staging_bytes.push_back(s.bytes);
         }
+        ge.last_use = ++c->graph_clock;
+        evict_graphs(c, r->key);
         c->graphs[r->key] = ge;
         e = hipGraphLaunch(ge.exec, c->stream);
         if (e != hipSuccess) fail(DJ_EHIP, std::string("decision.js: hipGraphLaunch: ") + hipGetErrorString(e));
@@ -523,11 +561,49 @@ extern "C" int dj_rec_finish(dj_rec *r) {
   return DJ_OK;
 }
 
+extern "C" int dj_rec_abort(dj_rec *r) {
+  DJ_REQUIRE(r && r->ctx, "decision.js: dj_rec_abort: null recorder");
+  dj_ctx *c = r->ctx;
+  DJ_REQUIRE(c->active == r, "decision.js: dj_rec_abort: recorder is not active");
+  c->active = nullptr;
+  r->holding = false;  // a held product is dropped, never launched
+  if (r->capturing) {  // the partial capture becomes no graph
+    hipGraph_t graph = nullptr;
+    (void)hipStreamEndCapture(c->stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
+  (void)hipStreamSynchronize(c->stream);  // ops already launched run to their end; their results are dropped
+  c->pinned_used = 0;
+  if (c->profiling) drain_profile(c);
+  if (!r->replay)  // a replay's snapshots are the cached graph's own staging buffers
+    for (auto &s : r->snaps) (void)hipFree(s.staging);
+  delete r;
+  (void)hipGetLastError();
+  return DJ_OK;
+}
+
 extern "C" int dj_graph_clear(dj_ctx *c) {
   DJ_REQUIRE(c, "decision.js: null context");
   DJ_REQUIRE(!c->active, "decision.js: dj_graph_clear during a forward");
   DJ_HIP(hipStreamSynchronize(c->stream));
   free_graphs(c);
+  return DJ_OK;
+}
+
+extern "C" int dj_graph_drop(dj_ctx *c, uint64_t key) {
+  DJ_REQUIRE(c, "decision.js: null context");
+  DJ_REQUIRE(!c->active, "decision.js: dj_graph_drop during a forward");
+  auto it = c->graphs.find(key);
+  if (it == c->graphs.end()) return DJ_OK;
+  DJ_HIP(hipStreamSynchronize(c->stream));
+  free_graph(it->second);
+  c->graphs.erase(it);
+  return DJ_OK;
+}
+
+extern "C" int dj_graph_count(dj_ctx *c, int *n) {
+  DJ_REQUIRE(c && n, "decision.js: dj_graph_count: null argument");
+  *n = (int)c->graphs.size();
   return DJ_OK;
 }
 

@@ -13,8 +13,17 @@ import threading
 import numpy as np
 
 from . import questions as Q
+from .eg2_head import Eg2Head
 from .encoder import EncoderEngine, cosine_logits
 from .engine import DecoderEngine
+
+
+def _on_progress(opts):
+    """BatchOptions.onProgress (d1.ts:33-35): opts is {"on_progress": f} (or "onProgress"); a bare callable is
+    taken as that callback."""
+    if opts is None or callable(opts):
+        return opts
+    return opts.get("on_progress") or opts.get("onProgress")
 
 
 def softmax(s):
@@ -44,41 +53,46 @@ class IdPrompt:
 
 
 class Decision:
-    """D1 (d1.ts:38-227): a model and the serial queue of its calls."""
+    """D1 (d1.ts:38-227): a model and the serial queue of its calls. `kind` is the reference's ModelKind
+    (d1.ts:17): "d1-3b" for the causal decoders (run as d1-3B's forest), "eg2" for the encoder."""
 
-    def __init__(self, kind, engine, prompt, tokens_per_pass, share_state=False):
+    def __init__(self, kind, engine, prompt, tokens_per_pass, share_state=False, workflow=""):
         self.kind, self.engine, self.prompt = kind, engine, prompt
         self.tokens_per_pass = tokens_per_pass
-        self.share_state = share_state
+        self.share_state = share_state  # d3-lite's shareState; can be switched between calls (d1.ts:51-52)
+        self.workflow = workflow  # EmbeddingGemma 2's LoadOptions.workflow, for a prompt that renders states
         self._lock = threading.Lock()  # one call at a time on the GPU (d1.ts:112-119)
         self._states = {}  # share_state: prefilled states by their ids (oldest dropped first)
         self._embeddings = {}  # encoder: normalized embeddings of the texts seen so far (d1.ts:44, 206-209)
+        self._head = None  # encoder: the learned decision head, when the model has one (d1.ts:174)
 
     @classmethod
     def load(cls, base: str, opts: dict = None):
         """A model in the decision.js format at `base` (manifest.json + weights.bin). opts: device,
-        on_progress, share_state, tokens_per_pass, graphs, prompt, direct_weights (LoadOptions.directWeights,
-        gpu.ts:20). The kind comes from manifest.config.model (d1.ts:63-64)."""
+        on_progress, share_state, tokens_per_pass, workflow, graphs, prompt, direct_weights
+        (LoadOptions.directWeights, gpu.ts:20). The kind comes from manifest.config.model (d1.ts:63-64)."""
         opts = dict(opts or {})
         from .fmt import load_manifest
         model = load_manifest(base if base.endswith("/") else base + "/")["config"].get("model")
         if model in ("decoder", "d1-3b"):
-            kind, engine = "decoder", DecoderEngine.load(base, opts)
-        elif model == "eg2-encoder":
-            kind, engine = "encoder", EncoderEngine.load(base, opts)
+            kind, engine = "d1-3b", DecoderEngine.load(base, opts)
+        elif model in ("eg2-encoder", "eg2"):
+            kind, engine = "eg2", EncoderEngine.load(base, opts)
         else:
             raise ValueError(f"decision.js: unknown model kind {model!r}")
-        # MI355X default: one pass holds every request that fits 128k tokens (d1.ts:78 uses 4096 / 8192 to
-        # bound the memory of browser GPUs; activations here are ~25 KB per token of 288 GB)
-        tpp = opts.get("tokens_per_pass") or 131072
-        return cls(kind, engine, opts.get("prompt") or IdPrompt(), tpp, bool(opts.get("share_state")))
+        # the reference's defaults (d1.ts:78): 4096 tokens per pass for d1-3B, 8192 otherwise; pass a larger
+        # tokens_per_pass to pack more requests into one forward (MI355X activations take ~25 KB per token)
+        tpp = opts.get("tokens_per_pass") or opts.get("tokensPerPass") or (4096 if kind == "d1-3b" else 8192)
+        return cls(kind, engine, opts.get("prompt") or IdPrompt(), tpp,
+                   bool(opts.get("share_state", opts.get("shareState"))), opts.get("workflow", ""))
 
     # ---- the public calls (d1.ts:81-110)
     def system_one(self, state, questions: dict):
         return self.system_one_batch([(state, questions)])[0]
 
-    def system_one_batch(self, requests, on_progress=None):
-        done = self._run([(s, list(qs.values())) for s, qs in requests], on_progress)
+    def system_one_batch(self, requests, opts=None):
+        """Many (state, {name: question}) requests packed into as few forwards as fit; opts: BatchOptions."""
+        done = self._run([(s, list(qs.values())) for s, qs in requests], _on_progress(opts))
         out = []
         for (s, qs), d in zip(requests, done):
             names = list(qs.keys())
@@ -89,12 +103,12 @@ class Decision:
     def probabilities(self, state, qs):
         return self._run([(state, list(qs))], None)[0]["probs"]
 
-    def probabilities_batch(self, requests, on_progress=None):
-        return [r["probs"] for r in self._run([(s, list(qs)) for s, qs in requests], on_progress)]
+    def probabilities_batch(self, requests, opts=None):
+        return [r["probs"] for r in self._run([(s, list(qs)) for s, qs in requests], _on_progress(opts))]
 
     def destroy(self):
         for st in self._states.values():
-            st.free()
+            self.engine.free_state(st)
         self._states = {}
         self.engine.destroy()
 
@@ -104,7 +118,7 @@ class Decision:
             for q in qs:
                 Q.check_question(q)
         with self._lock:  # a failed call releases the lock: the queue does not wedge (d1.ts:117)
-            if self.kind == "decoder":
+            if self.kind == "d1-3b":
                 return self._run_shared(requests, on_progress) if self.share_state else self._run_decoder(requests, on_progress)
             return self._run_encoder(requests, on_progress)
 
@@ -148,7 +162,7 @@ class Decision:
             if st is None:
                 if len(self._states) >= 64:
                     old = next(iter(self._states))
-                    self._states.pop(old).free()
+                    self.engine.free_state(self._states.pop(old))
                 st = self._states[key] = self.engine.prefill(trunk)
             branches = [p.branch(q) for q in qs]
             scores = self.engine.run_shared(st, branches, [p.readout_ids(q) for q in qs])
@@ -178,12 +192,21 @@ class Decision:
                 self._remember(tuple(texts[i + k]), e)
             if on_progress:
                 on_progress(j, len(texts))
+        c = self.engine.m["config"]
+        if self._head is None and c.get("head") and self.engine.host:
+            self._head = Eg2Head(c, self.engine.host)
+        temps = c.get("temperatures", {})
+        emb = lambda t: (tuple(t), self._embeddings[tuple(t)])  # noqa: E731
         out = []
         for r, (s, qs) in enumerate(requests):
             probs = []
             for q, (st, qi, opts) in zip(qs, asked[r]):
-                z = cosine_logits(self._embeddings[tuple(st)], self._embeddings[tuple(qi)], [self._embeddings[tuple(o)] for o in opts])
-                probs.append(softmax(z))
+                if self._head is not None:  # the learned head (eg2-head.ts:64-99)
+                    z = self._head.logits(q["type"], emb(st), emb(qi), [emb(o) for o in opts])
+                else:  # the cosine prior alone (the configured dense head has no learned scorer)
+                    z = cosine_logits(emb(st)[1], emb(qi)[1], [emb(o)[1] for o in opts])
+                t = float(temps.get(q["type"], 1.0))
+                probs.append(softmax(np.asarray(z, dtype=np.float64) / t))
             out.append({"probs": probs, "tokens": tokens[r]})
         return out
 

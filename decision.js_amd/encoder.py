@@ -4,7 +4,7 @@ configured head (Linear hidden->width, Linear width->embed_dim, in f32) and L2 n
 """
 import numpy as np
 
-from . import _dj
+from . import _dj, fmt
 from .engine import GpuEngine, load_weights
 
 
@@ -44,7 +44,11 @@ class EncoderEngine(GpuEngine):
         ctx, m, w = load_weights(base, opts)
         if m["config"].get("model") != "eg2-encoder":
             raise ValueError(f"decision.js: {base} is not an encoder model ({m['config'].get('model')})")
-        return cls(ctx, m, w, opts)
+        eng = cls(ctx, m, w, opts)
+        # the decision head's f32 tensors stay on the host (Eg2Engine.load, eg2-engine.ts:46-50)
+        tf = fmt.TensorFile(base if base.endswith("/") else base + "/")
+        eng.host = {name: np.array(tf.tensor(info), dtype=np.float32) for name, info in m.get("host", {}).items()}
+        return eng
 
     def __init__(self, ctx, m, w, opts=None):
         super().__init__(ctx, m, w, opts)
@@ -56,6 +60,7 @@ class EncoderEngine(GpuEngine):
         self.scale = c.get("attention_scale", 1.0)
         self.width, self.E = c["head_width"], c["embed_dim"]
         self.capacity = self.seq_capacity = 0
+        self.host = {}
 
     def ensure(self, T, S):
         if T <= self.capacity and S <= self.seq_capacity:
@@ -74,13 +79,26 @@ class EncoderEngine(GpuEngine):
         pk = pack_encoder(seqs)
         T, S = pk["T"], pk["S"]
         self.ensure(T, S)
-        B, w = self._bufs, self.w
+        B = self._bufs
         B["ids"].upload(pk["ids"])
         B["meta"].upload(pk["meta"])
         B["rng"].upload(pk["full"])
         B["seqs"].upload(pk["ranges"])
         debug_layers = tuple(sorted(set(debug_layers)))
-        rec = self.ctx.recorder(self._key("embed", T, S, debug_layers))
+        with self.ctx.recorder(self._key("embed", T, S, debug_layers)) as rec:  # aborted on an error
+            snaps = self._record(rec, T, S, debug_layers)
+            ei = rec.snapshot(B["emb"], S * self.E * 4, np.float32, (S, self.E))
+        got = rec.finish()
+        self.stats["forwards"] += 1
+        self.stats["tokens"] += T
+        e = got[ei].astype(np.float64)
+        n = np.maximum(np.sqrt((e * e).sum(-1, keepdims=True)), 1e-12)
+        return {"embeddings": (e / n).astype(np.float32), "debug": {i: got[k] for i, k in snaps.items()}}
+
+    def _record(self, rec, T, S, debug_layers):
+        """The encoder's ops on the recorder (eg2-engine.ts:103-129 without per-layer embeddings), then pooling
+        and the head; returns the debug snapshots' indices."""
+        B, w = self._bufs, self.w
         H, h, kv, D, eps = self.H, self.h, self.kv, self.D, self.eps
         snaps = {}
         if not rec.replay:
@@ -108,13 +126,7 @@ class EncoderEngine(GpuEngine):
         else:
             for i in debug_layers:
                 snaps[i] = rec.snapshot(B["x"], T * H * 2, np.float16, (T, H))
-        ei = rec.snapshot(B["emb"], S * self.E * 4, np.float32, (S, self.E))
-        got = rec.finish()
-        self.stats["forwards"] += 1
-        self.stats["tokens"] += T
-        e = got[ei].astype(np.float64)
-        n = np.maximum(np.sqrt((e * e).sum(-1, keepdims=True)), 1e-12)
-        return {"embeddings": (e / n).astype(np.float32), "debug": {i: got[k] for i, k in snaps.items()}}
+        return snaps
 
 
 def cosine_logits(state_e, question_e, option_es):

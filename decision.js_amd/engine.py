@@ -4,12 +4,17 @@ engine (d1-3b-engine.ts's forest; d3-engine.ts's shared prefix) driving libdj.so
 A forward is recorded into one dj recorder, as the reference records one command buffer (gpu.ts:176-281);
 with `graphs` on (the default), a forward whose shapes were seen before replays a captured HIP graph.
 """
+import itertools
 import math
-import zlib
 
 import numpy as np
 
 from . import _dj, fmt
+
+# Graph keys are handed out from one process-wide counter: every distinct forward (its exact key tuple, on any
+# engine) gets its own 64-bit number, so two forwards can never share a cached graph (no hash collisions), and
+# a number is never reused after its graph is dropped.
+_GRAPH_KEYS = itertools.count(1)
 
 # ---------------------------------------------------------------- weights (gpu.ts:57-88, 114-133)
 
@@ -78,7 +83,8 @@ class GpuEngine:
         self.stats = {"forwards": 0, "tokens": 0, "gpu_ms": 0.0}
         self._bufs = {}
         self._gen = 0  # bumped whenever buffers are reallocated: cached graphs point at the old ones
-        self._seen = set()  # graph keys used once (captured on their second use)
+        self._keys = {}  # key tuple -> 0 after its first use, its graph key from the second use on
+        self._state_keys = {}  # shared state serial -> the graph keys of forwards reading its K/V
         self.owns_ctx = "device" not in self.opts
 
     def destroy(self):
@@ -100,20 +106,34 @@ class GpuEngine:
         self._gen += 1
         self.ctx.graph_clear()
 
-    def _key(self, *parts) -> int:
-        """Graph key of a forward: every shape and pointer generation that the recorded ops depend on. A key is
-        handed out from its second use on: the first forward with it runs eagerly (0), the second captures the
-        graph, later ones replay it. Capturing costs more than launching once (a shared-state unit, whose
-        questions' key is new with every state: 6.1 ms captured against 5.0 eager on MI355X)."""
+    def _key(self, *parts, state=None) -> int:
+        """Graph key of a forward: every shape and pointer generation that the recorded ops depend on (`state`:
+        the serial of the shared state whose K/V it reads). A key is handed out from its second use on: the
+        first forward with it runs eagerly (0), the second captures the graph, later ones replay it. Capturing
+        costs more than launching once (a shared-state unit, whose questions' key is new with every state: 6.1
+        ms captured against 5.0 eager on MI355X). The library keeps at most DJ_GRAPH_CAP graphs (least
+        recently used evicted); forgetting a tuple here only costs a new capture."""
         if not self.graphs:
             return 0
-        key = zlib.crc32(repr((id(self), self._gen) + parts).encode()) | (1 << 40)
-        if key in self._seen:
-            return key
-        if len(self._seen) >= 4096:
-            self._seen.clear()
-        self._seen.add(key)
-        return 0
+        t = (self._gen, state) + parts
+        key = self._keys.get(t)
+        if key is None:
+            if len(self._keys) >= 4096:
+                self._keys.clear()
+            self._keys[t] = 0
+            return 0
+        if key == 0:
+            key = self._keys[t] = next(_GRAPH_KEYS)
+            if state is not None:
+                self._state_keys.setdefault(state, []).append(key)
+        return key
+
+    def free_state(self, state):
+        """Frees a shared state's kept K/V and drops the graphs captured against it (they point at its memory)."""
+        for key in self._state_keys.pop(state.serial, []):
+            self.ctx.graph_drop(key)
+        self._keys = {t: k for t, k in self._keys.items() if t[1] != state.serial}
+        state.free()
 
 
 # ---------------------------------------------------------------- packing (host side, d1-3b-engine.ts:46-72)
@@ -316,17 +336,17 @@ class DecoderEngine(GpuEngine):
                 B[k].copy_from(staged[k])
             else:
                 B[k].upload(pk[k])
-        rec = self.ctx.recorder(self._key("run", T, L, n_ids, tuple(debug_layers)))
         snaps = {}
-        if not rec.replay:
-            self._layers(rec, T, B, debug=debug_layers, snaps=snaps)
-            if L and n_ids:
-                rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
-                                self.w["embed"], B["out"])
-        else:
-            for i in debug_layers:
-                snaps[i] = rec.snapshot(B["x"], T * self.H * 2, np.float16, (T, self.H))
-        oi = rec.snapshot(B["out"], max(L * n_ids, 1) * 4, np.float32, (max(L * n_ids, 1),)) if L and n_ids else None
+        with self.ctx.recorder(self._key("run", T, L, n_ids, tuple(debug_layers))) as rec:  # aborted on an error
+            if not rec.replay:
+                self._layers(rec, T, B, debug=debug_layers, snaps=snaps)
+                if L and n_ids:
+                    rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
+                                    self.w["embed"], B["out"])
+            else:
+                for i in debug_layers:
+                    snaps[i] = rec.snapshot(B["x"], T * self.H * 2, np.float16, (T, self.H))
+            oi = rec.snapshot(B["out"], max(L * n_ids, 1) * 4, np.float32, (max(L * n_ids, 1),)) if L and n_ids else None
         got = self._finish(rec, T)
         out = got[oi] if oi is not None else np.zeros(0, np.float32)
         return {"scores": group_max(out, n_ids, trees), "debug": {i: got[k] for i, k in snaps.items()}, "logits": out}
@@ -344,9 +364,13 @@ class DecoderEngine(GpuEngine):
         B["pos"].upload(i)
         B["rng"].upload(np.stack([np.zeros(P, np.int32), i + 1, np.zeros(P, np.int32), np.zeros(P, np.int32)], 1))
         cache = self.ctx.alloc(self.layers * P * 2 * self.kv * self.D * 2)
-        rec = self.ctx.recorder(0)  # the cache pointer is new each time: no graph
-        self._layers(rec, P, B, kv_store=cache)
-        self._finish(rec, P)
+        try:
+            with self.ctx.recorder(0) as rec:  # the cache pointer is new each time: no graph
+                self._layers(rec, P, B, kv_store=cache)
+            self._finish(rec, P)
+        except BaseException:
+            cache.free()
+            raise
         return SharedState(P, cache, trunk)
 
     def run_shared(self, state: SharedState, branches, groups):
@@ -381,11 +405,11 @@ class DecoderEngine(GpuEngine):
         B["leaves"].upload(np.array(leaves, dtype=np.uint32))
         B["leaf_ids"].upload(flat)
         width = 2 * self.kv * self.D
-        rec = self.ctx.recorder(self._key("shared", state.serial, T, L, n_ids))
-        if not rec.replay:
-            self._layers(rec, T, B, kv_a=lambda i: _dj.kv_src(state.cache.at(i * P * width * 2), P, width, 0, self.kv * self.D))
-            rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
-                            self.w["embed"], B["out"])
-        oi = rec.snapshot(B["out"], L * n_ids * 4, np.float32, (L * n_ids,))
+        with self.ctx.recorder(self._key("shared", T, L, n_ids, state=state.serial)) as rec:
+            if not rec.replay:
+                self._layers(rec, T, B, kv_a=lambda i: _dj.kv_src(state.cache.at(i * P * width * 2), P, width, 0, self.kv * self.D))
+                rec.leaf_logits(T, L, self.H, n_ids, self.eps, B["x"], B["leaves"], self.w["final_norm"], B["leaf_ids"],
+                                self.w["embed"], B["out"])
+            oi = rec.snapshot(B["out"], L * n_ids * 4, np.float32, (L * n_ids,))
         out = self._finish(rec, T)[oi]
         return group_max(out, n_ids, [{"groups": groups}])[0]

@@ -109,6 +109,12 @@ class Blob:
         a = np.asarray(t, dtype=np.float32)
         self.manifest["tensors"][name] = {"dtype": "f32", "shape": list(a.shape), "offset": self.put(a.tobytes()), "bytes": a.nbytes}
 
+    def host_f32(self, name: str, t: np.ndarray):
+        """An f32 tensor read on the host, listed under the manifest's "host" (export-eg2.py:122-125: the
+        EmbeddingGemma 2 decision head)."""
+        self.f32(name, t)
+        self.manifest.setdefault("host", {})[name] = self.manifest["tensors"].pop(name)
+
     def close(self, source: dict = None):
         self.f.close()
         self.manifest["bytes"] = self.offset

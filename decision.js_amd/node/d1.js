@@ -9,7 +9,9 @@
  * plus `ids` (its tokens) and `options` (one token-id group per option, [yes, no] for a noul; each option
  * scores its best token, d1-3b-engine.ts:112-121). */
 const { DecoderEngine } = require("./engine");
-const { loadManifestSync } = require("./format");
+const { EncoderEngine, cosineLogits } = require("./encoder");
+const { Eg2Head } = require("./eg2_head");
+const { fileFetch } = require("./format");
 const Q = require("./questions");
 
 /** gpu.ts:294-297: max-subtracted exp (f64). */
@@ -27,27 +29,48 @@ const idPrompt = {
     if (q.options.length !== Q.nOptions(q)) throw new Q.QuestionError(`decision.js: ${q.options.length} option groups for a ${q.type} with ${Q.nOptions(q)} options`);
     return q.options.map((g) => Array.from(g, Number));
   },
+  // the encoder: state, question and each option are texts of their own (eg2-prompt.ts renders them)
+  texts: (state, q) => [Array.from(state.ids || state, Number), Array.from(q.ids, Number), q.option_ids.map((o) => Array.from(o, Number))],
 };
 
+/** BatchOptions (d1.ts:33-35): {onProgress(done, total)}; a bare function is taken as that callback. */
+const onProgressOf = (opts) => (typeof opts === "function" ? opts : opts && opts.onProgress);
+
+/** The reference's ModelKind (d1.ts:17, 63-64) for a manifest: "eg2" for the encoder, else "d1-3b" (a causal
+ * decoder without marker heads, run as d1-3B's forest). */
+function kindOf(config) {
+  const model = config && config.model;
+  if (model === "eg2" || model === "eg2-encoder") return "eg2";
+  if (model === "decoder" || model === "d1-3b" || !("head_layers" in (config || {}))) return "d1-3b";
+  throw new Error(`decision.js: unsupported model kind ${model}`);
+}
+
 class D1 {
-  /** A model in the decision.js format at `base` (manifest.json + weights.bin). opts: fetch, device,
-   * onProgress, directWeights, graphs, tokensPerPass (default 131072), shareState, prompt. */
+  /** A model in the decision.js format at `base` (manifest.json + weights.bin). opts (LoadOptions, d1.ts:19-28;
+   * gpu.ts:13-27): fetch (a Range-capable fetch; local files by default), device, onProgress, directWeights,
+   * graphs, tokensPerPass (the reference's defaults: 4096 for d1-3b, 8192 otherwise), shareState, workflow,
+   * prompt. */
   static async load(base, opts) {
-    opts = opts || {};
-    const model = opts.fetch ? null : loadManifestSync(base).config.model;
-    if (model !== null && model !== "decoder" && model !== "d1-3b") {
-      throw new Error(`decision.js: the Node host runs the causal decoders; ${base} is a ${model} model (use the Python host for encoders)`);
-    }
-    const engine = await DecoderEngine.load(base, opts);
-    return new D1(engine, opts);
+    opts = Object.assign({}, opts || {});
+    if (!base.endsWith("/")) base += "/";
+    opts.fetch = opts.fetch || fileFetch();
+    const manifest = await (await opts.fetch(`${base}manifest.json`)).json();
+    const kind = kindOf(manifest.config);
+    const engine = kind === "eg2" ? await EncoderEngine.load(base, opts) : await DecoderEngine.load(base, opts);
+    return new D1(kind, engine, opts);
   }
 
-  constructor(engine, opts) {
+  constructor(kind, engine, opts) {
+    this.kind = kind;
     this.engine = engine;
+    this.tokenizer = null; // text-to-ids is upstream of this build: `prompt` takes token ids
     this.prompt = opts.prompt || idPrompt;
-    this.tokensPerPass = opts.tokensPerPass || 131072;
-    this.shareState = !!opts.shareState;
+    this.tokensPerPass = opts.tokensPerPass || (kind === "d1-3b" ? 4096 : 8192);
+    this.shareState = !!opts.shareState; // can be switched between calls (d1.ts:51-52)
+    this.workflow = opts.workflow || ""; // EmbeddingGemma 2: for a prompt that renders states (d1.ts:53-54)
     this.states = new Map(); // shareState: prefilled states by their ids, oldest dropped first
+    this.embeddings = new Map(); // eg2: normalized embeddings of the texts seen so far (d1.ts:44)
+    this.eg2Head = null;
     this.queue = Promise.resolve();
   }
 
@@ -55,9 +78,9 @@ class D1 {
     return this.systemOneBatch([[state, questions]]).then((r) => r[0]);
   }
 
-  systemOneBatch(requests, onProgress) {
+  systemOneBatch(requests, opts = {}) {
     return this.enqueue(async () => {
-      const done = await this.runAll(requests.map(([s, qs]) => [s, Object.values(qs)]), onProgress);
+      const done = await this.runAll(requests.map(([s, qs]) => [s, Object.values(qs)]), onProgressOf(opts));
       return requests.map(([, qs], r) => {
         const names = Object.keys(qs), answers = {};
         names.forEach((n, j) => (answers[n] = Q.answer(qs[n], done[r].probs[j])));
@@ -70,12 +93,12 @@ class D1 {
     return this.enqueue(async () => (await this.runAll([[state, Array.from(questions)]]))[0].probs);
   }
 
-  probabilitiesBatch(requests, onProgress) {
-    return this.enqueue(async () => (await this.runAll(requests.map(([s, qs]) => [s, Array.from(qs)]), onProgress)).map((r) => r.probs));
+  probabilitiesBatch(requests, opts = {}) {
+    return this.enqueue(async () => (await this.runAll(requests.map(([s, qs]) => [s, Array.from(qs)]), onProgressOf(opts))).map((r) => r.probs));
   }
 
   destroy() {
-    for (const st of this.states.values()) st.free();
+    for (const st of this.states.values()) this.engine.freeState(st);
     this.states.clear();
     this.engine.destroy();
   }
@@ -88,6 +111,7 @@ class D1 {
 
   async runAll(requests, onProgress) {
     for (const [, qs] of requests) qs.forEach(Q.checkQuestion);
+    if (this.kind === "eg2") return this.runEg2(requests, onProgress);
     return this.shareState ? this.runShared(requests, onProgress) : this.runDecoder(requests, onProgress);
   }
 
@@ -129,7 +153,7 @@ class D1 {
       if (!st) {
         if (this.states.size >= 64) {
           const oldest = this.states.keys().next().value;
-          this.states.get(oldest).free();
+          this.engine.freeState(this.states.get(oldest));
           this.states.delete(oldest);
         }
         st = await this.engine.prefill(trunk);
@@ -142,6 +166,49 @@ class D1 {
     }
     return out;
   }
+
+  /** runEg2 (d1.ts:172-204): every distinct text (state, question, option) embedded once and cached, in passes
+   * of at most tokensPerPass tokens; then the head on the host — the learned decision head when the model has
+   * one (eg2-head.ts), else the cosine prior — and a softmax at the type's temperature. */
+  async runEg2(requests, onProgress) {
+    const p = this.prompt, c = this.engine.m.config;
+    if (!this.eg2Head && c.head && Object.keys(this.engine.host).length) this.eg2Head = new Eg2Head(c, this.engine.host);
+    const asked = requests.map(([s, qs]) => qs.map((q) => p.texts(s, q)));
+    const todo = new Map(), tokens = requests.map(() => 0);
+    asked.forEach((perQ, r) => {
+      for (const [st, qi, opts] of perQ) {
+        for (const t of [st, qi, ...opts]) {
+          const key = t.join(",");
+          if (this.embeddings.has(key) || todo.has(key)) continue;
+          todo.set(key, t);
+          tokens[r] += t.length;
+        }
+      }
+    });
+    const keys = Array.from(todo.keys());
+    for (const [i, j] of keys.length ? this.passes(keys.map((k) => todo.get(k).length)) : []) {
+      const { embeddings } = await this.engine.embed(keys.slice(i, j).map((k) => todo.get(k)));
+      embeddings.forEach((e, k) => this.remember(keys[i + k], e));
+      if (onProgress) onProgress(j, keys.length);
+    }
+    const temps = c.temperatures || {};
+    const emb = (t) => [t.join(","), this.embeddings.get(t.join(","))];
+    return requests.map(([, qs], r) => ({
+      probs: qs.map((q, k) => {
+        const [st, qi, opts] = asked[r][k];
+        const z = this.eg2Head ? this.eg2Head.logits(q.type, emb(st), emb(qi), opts.map(emb))
+          : cosineLogits(emb(st)[1], emb(qi)[1], opts.map((o) => emb(o)[1]));
+        const tau = temps[q.type] === undefined ? 1 : temps[q.type];
+        return softmax(z.map((v) => v / tau));
+      }),
+      tokens: tokens[r],
+    }));
+  }
+
+  remember(key, e) {
+    if (this.embeddings.size >= 8192) this.embeddings.delete(this.embeddings.keys().next().value); // the oldest text first (d1.ts:207)
+    this.embeddings.set(key, e);
+  }
 }
 
-module.exports = { D1, softmax, idPrompt };
+module.exports = { D1, Decision: D1, softmax, idPrompt, kindOf };

@@ -90,6 +90,12 @@ class Context {
   graphClear() {
     lib().graphClear(this.h);
   }
+  graphDrop(key) {
+    lib().graphDrop(this.h, BigInt(key));
+  }
+  graphCount() {
+    return lib().graphCount(this.h);
+  }
   timerBegin() {
     lib().timerBegin(this.h);
   }
@@ -126,6 +132,8 @@ class Recorder {
     lib().attention(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, O);
   }
   kvStore(T, kv, D, Z, stride, kCol, cache, row0) { lib().kvStore(this.h, T, kv, D, Z, stride, kCol, cache, row0); }
+  meanPool(T, S, H, X, seqs, out) { lib().meanPool(this.h, T, S, H, X, seqs, out); }
+  denseF32(M, inp, w, out) { lib().denseF32(this.h, M, inp, w.h, out); }
   leafLogits(T, L, H, nIds, eps, X, leaves, w, ids, embed, out) {
     lib().leafLogits(this.h, T, L, H, nIds, eps, X, leaves, w, ids, embed.h, out);
   }
@@ -135,6 +143,27 @@ class Recorder {
     lib().recSnapshot(this.h, ptr, host);
     this.snaps.push(host);
     return this.snaps.length - 1;
+  }
+  /** Ends a recording that failed (dj_rec_abort): nothing more runs and the context is free for the next
+   * forward. Its own status is not thrown: the error being handled is the one to report. */
+  abort() {
+    if (!this.h) return;
+    const h = this.h;
+    this.h = 0n;
+    try {
+      lib().recAbort(h);
+    } catch (e) {
+      // the original error is reported by the caller
+    }
+  }
+  /** Runs `body(this)` (the op calls); on any error aborts the recording and rethrows. */
+  record(body) {
+    try {
+      return body(this);
+    } catch (e) {
+      this.abort();
+      throw e;
+    }
   }
   /** Submits the forward (or replays its captured graph); resolves to the snapshots. */
   async finish() {

@@ -348,9 +348,27 @@ napi_value RecFinishAsync(napi_env env, napi_callback_info info) {
   return promise;
 }
 
+napi_value RecAbort(napi_env env, napi_callback_info info) {  // (rec)
+  BEGIN(1);
+  END(dj_rec_abort((dj_rec *)ptr(c, 0)));
+}
+
 napi_value GraphClear(napi_env env, napi_callback_info info) {
   BEGIN(1);
   END(dj_graph_clear((dj_ctx *)ptr(c, 0)));
+}
+
+napi_value GraphDrop(napi_env env, napi_callback_info info) {  // (ctx, key BigInt)
+  BEGIN(2);
+  END(dj_graph_drop((dj_ctx *)ptr(c, 0), (uint64_t)num(c, 1)));
+}
+
+napi_value GraphCount(napi_env env, napi_callback_info info) {  // (ctx) -> number of cached graphs
+  BEGIN(1);
+  int n = 0;
+  const int st = dj_graph_count((dj_ctx *)ptr(c, 0), &n);
+  if (!c.ok) return nullptr;
+  return done(env, st, number(env, n));
 }
 
 napi_value TimerBegin(napi_env env, napi_callback_info info) {
@@ -477,7 +495,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"bufRead", BufRead}, {"upload", Upload}, {"bufCopy", BufCopy}, {"weightQ", WeightQ},
       {"weightFree", WeightFree}, {"weightBytes", WeightBytes}, {"recBegin", RecBegin},
       {"recSnapshot", RecSnapshot}, {"recFinish", RecFinish}, {"recFinishAsync", RecFinishAsync},
-      {"graphClear", GraphClear}, {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
+      {"recAbort", RecAbort}, {"graphClear", GraphClear}, {"graphDrop", GraphDrop}, {"graphCount", GraphCount},
+      {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
       {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"kvStore", KvStore},

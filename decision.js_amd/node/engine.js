@@ -78,14 +78,10 @@ function groupMax(out, nIds, trees) {
   return scores;
 }
 
-// FNV-1a over a string, 64-bit: the key of a captured forward graph
-function hashKey(s) {
-  let h = 0xcbf29ce484222325n;
-  for (let i = 0; i < s.length; ++i) h = BigInt.asUintN(64, (h ^ BigInt(s.charCodeAt(i))) * 0x100000001b3n);
-  return h | 1n;
-}
-
-let engineSerial = 0, stateSerial = 0;
+// Graph keys come from one process-wide counter: every distinct forward (its exact key string, on any engine)
+// gets its own 64-bit number, so two forwards never share a cached graph and a dropped key is never reused.
+let nextGraphKey = 0n;
+let stateSerial = 0;
 
 class GpuEngine {
   constructor(ctx, m, w, opts) {
@@ -97,8 +93,8 @@ class GpuEngine {
     this.stats = { forwards: 0, tokens: 0 };
     this.bufs = {};
     this.gen = 0;
-    this.seen = new Set(); // graph keys used once (captured on their second use)
-    this.serial = ++engineSerial;
+    this.keys = new Map(); // key string -> 0n after its first use, its graph key from the second use on
+    this.stateKeys = new Map(); // shared state serial -> graph keys of the forwards reading its K/V
     this.ownsCtx = !this.opts.device;
   }
   /** Frees every weight and buffer (gpu.ts:108-110). */
@@ -117,14 +113,34 @@ class GpuEngine {
     this.ctx.graphClear();
   }
   // The graph key of a forward, from its second use on: the first forward with a key runs eagerly (0n), the
-  // second captures the graph, later ones replay it (capturing costs more than launching once).
-  key(...parts) {
+  // second captures the graph, later ones replay it (capturing costs more than launching once). `state`: the
+  // serial of the shared state whose K/V the forward reads (its graphs are dropped with the state). The library
+  // keeps at most DJ_GRAPH_CAP graphs; forgetting a key string here only costs a new capture.
+  key(parts, state) {
     if (!this.graphs) return 0n;
-    const k = hashKey(JSON.stringify([this.serial, this.gen].concat(parts)));
-    if (this.seen.has(k)) return k;
-    if (this.seen.size >= 4096) this.seen.clear();
-    this.seen.add(k);
-    return 0n;
+    const t = JSON.stringify([this.gen, state === undefined ? null : state].concat(parts));
+    let k = this.keys.get(t);
+    if (k === undefined) {
+      if (this.keys.size >= 4096) this.keys.clear();
+      this.keys.set(t, 0n);
+      return 0n;
+    }
+    if (k === 0n) {
+      k = ++nextGraphKey;
+      this.keys.set(t, k);
+      if (state !== undefined) {
+        if (!this.stateKeys.has(state)) this.stateKeys.set(state, []);
+        this.stateKeys.get(state).push(k);
+      }
+    }
+    return k;
+  }
+  /** Frees a shared state's kept K/V and drops the graphs captured against it (they point at its memory). */
+  freeState(st) {
+    for (const k of this.stateKeys.get(st.serial) || []) this.ctx.graphDrop(k);
+    this.stateKeys.delete(st.serial);
+    for (const t of Array.from(this.keys.keys())) if (JSON.parse(t)[1] === st.serial) this.keys.delete(t);
+    st.free();
   }
 }
 
@@ -226,12 +242,14 @@ class DecoderEngine extends GpuEngine {
       B.leaves.upload(pk.leaves);
       B.leafIds.upload(pk.leafIds);
     }
-    const rec = this.ctx.recorder(this.key("run", T, L, nIds));
-    if (!rec.replay) {
-      this.recordLayers(rec, T, B, null, null);
-      if (L && nIds) rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
-    }
-    const oi = L && nIds ? rec.snapshot(B.out.ptr, Float32Array, L * nIds) : -1;
+    const rec = this.ctx.recorder(this.key(["run", T, L, nIds]));
+    const oi = rec.record(() => { // aborted on an error
+      if (!rec.replay) {
+        this.recordLayers(rec, T, B, null, null);
+        if (L && nIds) rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
+      }
+      return L && nIds ? rec.snapshot(B.out.ptr, Float32Array, L * nIds) : -1;
+    });
     const got = await this.finish(rec, T);
     const out = oi >= 0 ? got[oi] : new Float32Array(0);
     return { scores: groupMax(out, nIds, trees), logits: out };
@@ -252,9 +270,14 @@ class DecoderEngine extends GpuEngine {
     B.pos.upload(pos);
     B.rng.upload(rng);
     const cache = this.ctx.alloc(this.layers * P * 2 * this.kv * this.D * 2);
-    const rec = this.ctx.recorder(0n); // the cache pointer is new each time: no graph
-    this.recordLayers(rec, P, B, null, cache);
-    await this.finish(rec, P);
+    try {
+      const rec = this.ctx.recorder(0n); // the cache pointer is new each time: no graph
+      rec.record(() => this.recordLayers(rec, P, B, null, cache));
+      await this.finish(rec, P);
+    } catch (e) {
+      cache.free();
+      throw e;
+    }
     return new SharedState(P, cache, trunk.slice());
   }
 
@@ -287,15 +310,17 @@ class DecoderEngine extends GpuEngine {
     B.leaves.upload(Uint32Array.from(leaves));
     B.leafIds.upload(leafIds);
     const width = 2 * this.kv * this.D;
-    const rec = this.ctx.recorder(this.key("shared", state.serial, T, L, nIds));
-    if (!rec.replay) {
-      this.recordLayers(rec, T, B, (i) => kvSrc(state.cache.at(i * P * width * 2), P, width, 0, this.kv * this.D), null);
-      rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
-    }
-    const oi = rec.snapshot(B.out.ptr, Float32Array, L * nIds);
+    const rec = this.ctx.recorder(this.key(["shared", T, L, nIds], state.serial));
+    const oi = rec.record(() => {
+      if (!rec.replay) {
+        this.recordLayers(rec, T, B, (i) => kvSrc(state.cache.at(i * P * width * 2), P, width, 0, this.kv * this.D), null);
+        rec.leafLogits(T, L, this.H, nIds, this.eps, B.x.ptr, B.leaves.ptr, this.w.final_norm.ptr, B.leafIds.ptr, this.w.embed, B.out.ptr);
+      }
+      return rec.snapshot(B.out.ptr, Float32Array, L * nIds);
+    });
     const out = (await this.finish(rec, T))[oi];
     return groupMax(out, nIds, [{ groups }])[0];
   }
 }
 
-module.exports = { packForest, groupMax, hashKey, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };
+module.exports = { packForest, groupMax, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };

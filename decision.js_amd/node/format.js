@@ -89,7 +89,13 @@ async function loadWeights(base, opts, layout) {
       }
     }));
   }
-  return { ctx, m, w };
+  // f32 tensors read on the host (the manifest's "host" list: EmbeddingGemma 2's decision head, eg2-engine.ts:46-50)
+  const host = {};
+  for (const [name, t] of Object.entries(m.host || {})) {
+    const raw = await range(t.offset, t.bytes);
+    host[name] = new Float32Array(raw.buffer, raw.byteOffset, raw.byteLength / 4);
+  }
+  return { ctx, m, w, host };
 }
 
 function loadManifestSync(base) {

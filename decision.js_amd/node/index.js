@@ -1,9 +1,15 @@
 "use strict";
-/* decision.js on MI355X, Node host: `const { D1 } = require(".../decision.js_amd/node")`. */
-const { D1, softmax } = require("./d1");
+/* decision.js on MI355X, Node host: `const { D1 } = require(".../decision.js_amd/node")` — the reference's
+ * exports of index.ts: D1 (and its alias Decision), answer and checkQuestion, the engines. */
+const { D1, Decision, softmax } = require("./d1");
 const { DecoderEngine, packForest, groupMax } = require("./engine");
+const { EncoderEngine, packEncoder } = require("./encoder");
+const { Eg2Head } = require("./eg2_head");
 const { loadWeights, fileFetch } = require("./format");
 const questions = require("./questions");
 const dj = require("./dj");
 
-module.exports = { D1, DecoderEngine, packForest, groupMax, loadWeights, fileFetch, softmax, questions, dj };
+module.exports = {
+  D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, Eg2Head,
+  packForest, packEncoder, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+};

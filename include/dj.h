@@ -32,7 +32,8 @@ enum {
   DJ_EHIP = 2,      /* the HIP runtime reported an error */
   DJ_ENOMEM = 3,    /* device or host allocation failed */
   DJ_ESTATE = 4,    /* call out of order (e.g. an op outside a recorder) */
-  DJ_EINJECT = 5,   /* an error forced by DJ_FAULT_INJECT (tests of the host's error path) */
+  DJ_EINJECT = 5,   /* an error forced by DJ_FAULT_INJECT=<op>[:<n>] (tests of the host's error path: the op
+                       fails before launching, every time or its next n times; read by dj_init) */
 };
 
 typedef struct dj_ctx dj_ctx;
@@ -111,8 +112,19 @@ int dj_rec_snapshot(dj_rec *rec, const void *dev, size_t bytes, void *host);
 /* Runs (or replays) the forward, waits for it, fills the snapshots, and frees the recorder.
  * Replaces: finish(tokens) (gpu.ts:245-279). */
 int dj_rec_finish(dj_rec *rec);
+/* Ends a forward whose recording failed (an op returned an error) without running what remains: nothing
+ * more is launched, a partial capture becomes no graph, ops already launched are waited for, and the recorder's
+ * temporaries are freed, so the next forward on the context starts clean. Replaces: finish()'s error path,
+ * which destroys the forward's temporaries and throws (gpu.ts:255-260). */
+int dj_rec_abort(dj_rec *rec);
 /* Drops every cached graph (call after reallocating buffers a cached graph points to). */
 int dj_graph_clear(dj_ctx *ctx);
+/* Drops the graph cached under `key`, if any (call when memory one graph points to is freed, e.g. a shared
+ * state's kept K/V). The cache also holds at most DJ_GRAPH_CAP graphs (default 64), evicting the least
+ * recently used. No counterpart in the reference (WebGPU has no graphs); the hosts' shared-state free calls it. */
+int dj_graph_drop(dj_ctx *ctx, uint64_t key);
+/* Number of graphs in the cache (monitoring and tests). */
+int dj_graph_count(dj_ctx *ctx, int *n);
 
 /* ---------------------------------------------------------------- timing and profiling (gpu.ts:29-34, 185-197) */
 

@@ -27,10 +27,66 @@ async function main(req) {
         }
       });
     case "graphkeys": {
-      // graph keys handed out over a sequence of forwards (no device: key() reads only the engine's own state)
+      // graph keys handed out over a sequence of forwards, then a shared state freed (no device: key() reads
+      // only the engine's own state; a stand-in context records the dropped graphs)
       const { GpuEngine } = require(path.join(root, "engine"));
-      const e = new GpuEngine(null, {}, {}, { graphs: req.graphs });
-      return req.seq.map((parts) => String(e.key(...parts)));
+      const dropped = [];
+      const e = new GpuEngine({ graphDrop: (k) => dropped.push(String(k)) }, {}, {}, { graphs: req.graphs });
+      const keys = req.seq.map(([parts, st]) => String(e.key(parts, st === null ? undefined : st)));
+      e.freeState({ serial: req.free, free: () => undefined });
+      const again = req.seq.find(([, st]) => st === req.free);
+      return { keys, dropped, after: String(e.key(again[0], req.free)) };
+    }
+    case "packenc": {
+      const pk = host.packEncoder(req.seqs);
+      return { ids: typed(pk.ids), meta: typed(pk.meta), full: typed(pk.full), ranges: typed(pk.ranges), T: pk.T, S: pk.S };
+    }
+    case "eg2head": {
+      // the learned head on given tensors and embeddings (no device)
+      const t = {};
+      for (const [k, v] of Object.entries(req.tensors)) t[k] = Float32Array.from(v);
+      const head = new host.Eg2Head(req.config, t);
+      return req.calls.map(([type, s, q, opts]) => head.logits(type, [s[0], Float32Array.from(s[1])], [q[0], Float32Array.from(q[1])],
+        opts.map(([k, e]) => [k, Float32Array.from(e)])));
+    }
+    case "kinds":
+      return req.configs.map((c) => {
+        try {
+          return require(path.join(root, "d1")).kindOf(c);
+        } catch (e) {
+          return { error: e.message };
+        }
+      });
+    case "encode": {
+      const d = await host.Decision.load(req.model, req.opts || {});
+      try {
+        const out = { kind: d.kind, tokensPerPass: d.tokensPerPass };
+        const seen = [];
+        out.batch = await d.systemOneBatch(req.batch, { onProgress: (a, b) => seen.push([a, b]) });
+        out.progress = seen;
+        out.again = await d.systemOneBatch(req.batch); // every text cached: no forward
+        out.embeddings = (await d.engine.embed(req.texts)).embeddings.map(typed);
+        return out;
+      } finally {
+        d.destroy();
+      }
+    }
+    case "fault": {
+      // the test sets DJ_FAULT_INJECT=<op>:1 in this process's environment: the first forward fails
+      const d = await host.D1.load(req.model, req.opts || {});
+      try {
+        const out = {};
+        try {
+          await d.probabilities(req.state, Object.values(req.questions));
+        } catch (e) {
+          out.error = e.message;
+        }
+        out.after = await d.probabilities(req.state, Object.values(req.questions));
+        out.again = await d.probabilities(req.state, Object.values(req.questions));
+        return out;
+      } finally {
+        d.destroy();
+      }
     }
     case "passes": {
       const d = Object.create(host.D1.prototype);
@@ -61,7 +117,10 @@ async function main(req) {
         if (req.batch) {
           d.tokensPerPass = req.budget;
           const seen = [];
-          out.batch = await d.systemOneBatch(req.batch, (a, b) => seen.push([a, b]));
+          out.batch = await d.systemOneBatch(req.batch, { onProgress: (a, b) => seen.push([a, b]) }); // BatchOptions
+          const seenP = [];
+          out.probsBatch = await d.probabilitiesBatch(req.batch.map(([s, qs]) => [s, Object.values(qs)]), { onProgress: (a, b) => seenP.push([a, b]) });
+          out.progressP = seenP;
           out.progress = seen;
         }
         if (req.shared) {

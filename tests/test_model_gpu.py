@@ -249,7 +249,7 @@ def test_decision_api(pkg, models):
         reqs = [([int(x) for x in rng.integers(0, V, n)], qs) for n in (50, 300, 10)]
         d.tokens_per_pass = 400
         seen = []
-        batch = d.system_one_batch(reqs, on_progress=lambda a, b: seen.append((a, b)))
+        batch = d.system_one_batch(reqs, {"onProgress": lambda a, b: seen.append((a, b))})
         assert seen[-1] == (3, 3) and len(seen) >= 2
         for (s, q), b in zip(reqs, batch):
             one = d.system_one(s, q)
@@ -286,3 +286,78 @@ def test_decision_api_encoder(pkg, models):
         assert r2["usage"]["input_tokens"] == 0 and r2["answers"] == r["answers"]
     finally:
         d.destroy()
+
+
+@pytest.mark.parametrize("op,graphs", [("matmul", True), ("attention", False), ("matmul_glu", True)])
+def test_injected_fault_surfaces_and_next_call_succeeds(pkg, models, monkeypatch, op, graphs):
+    """An error inside a forward (DJ_FAULT_INJECT=<op>:1: the op fails once, before launching anything)
+    surfaces as the library's "decision.js: ..." error, the failed recording is aborted (dj_rec_abort), and the
+    next call on the same Decision succeeds with the answers a clean run gives (the reference's finish() error
+    path, gpu.ts:255-260; SURVEY's injected-error check). Also through the shared-state path."""
+    from decision_js_amd import _dj
+    from decision_js_amd.d1 import Decision
+    rng = np.random.default_rng(9)
+    V = 4096
+    state = [int(x) for x in rng.integers(0, V, 100)]
+    qs = _questions(rng, V)
+    clean = Decision.load(models["q8"], {"graphs": graphs})
+    try:
+        want = clean.probabilities(state, list(qs.values()))
+    finally:
+        clean.destroy()
+    monkeypatch.setenv("DJ_FAULT_INJECT", f"{op}:2")
+    d = Decision.load(models["q8"], {"graphs": graphs})  # the context reads DJ_FAULT_INJECT when it opens
+    monkeypatch.delenv("DJ_FAULT_INJECT")
+    try:
+        with pytest.raises(_dj.DJError, match=f"decision.js: fault injected in {op} "):
+            d.probabilities(state, list(qs.values()))
+        d.share_state = True
+        with pytest.raises(_dj.DJError, match="decision.js: fault injected"):  # the state's prefill fails
+            d.probabilities(state, list(qs.values()))
+        assert not d._states  # nothing kept from the failed prefill
+        shared = d.probabilities(state, list(qs.values()))
+        d.share_state = False
+        for _ in range(3):  # eager, then captured, then replayed where graphs are on
+            got = d.probabilities(state, list(qs.values()))
+            assert got == want
+        for a, b in zip(shared, want):
+            assert max(abs(x - y) for x, y in zip(a, b)) < INVARIANCE_TOL
+    finally:
+        d.destroy()
+
+
+def test_graph_cache_stays_bounded(pkg, models, monkeypatch):
+    """A long-running shareState loop holds a bounded number of cached graphs: 200 states, each asked three
+    times (eager, captured, replayed), keep at most the 64 live states' graphs, because a freed state's graphs
+    are dropped with it; and with DJ_GRAPH_CAP=8 the library evicts the least recently used graph, an evicted
+    forward being recorded again with the same results."""
+    from decision_js_amd.d1 import Decision
+    rng = np.random.default_rng(10)
+    V = 4096
+    q = {"type": "noul", "instructions": "?", "ids": [int(x) for x in rng.integers(0, V, 4)], "options": [[3], [4]]}
+    d = Decision.load(models["shared"], {"share_state": True})
+    try:
+        first = None
+        for i in range(200):
+            state = [int(x) for x in rng.integers(0, V, 16)]
+            got = [d.probabilities(state, [q]) for _ in range(3)]
+            assert got[0] == got[1] == got[2]
+            first = first or (state, got[0])
+        assert len(d._states) == 64
+        assert d.engine.ctx.graph_count() <= 64
+        # the oldest state was freed (its graph with it): asked again, it is prefilled and answered anew
+        assert d.probabilities(first[0], [q]) == first[1]
+    finally:
+        d.destroy()
+    monkeypatch.setenv("DJ_GRAPH_CAP", "8")
+    from decision_js_amd.engine import DecoderEngine
+    eng = DecoderEngine.load(models["q8"])
+    try:
+        trees = [_tree(rng, V, 20 + 3 * k, [5, 7]) for k in range(12)]
+        want = [eng.run([t])["logits"] for t in trees]  # eager
+        for _ in range(2):  # captured, then replayed while older graphs are evicted
+            for t, w in zip(trees, want):
+                assert np.array_equal(eng.run([t])["logits"], w)
+                assert eng.ctx.graph_count() <= 8
+    finally:
+        eng.destroy()

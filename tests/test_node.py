@@ -20,9 +20,9 @@ ADDON = os.path.join(ROOT, "decision.js_amd", "lib", "dj_napi.node")
 pytestmark = pytest.mark.skipif(NODE is None, reason="node is not installed")
 
 
-def node(req, timeout=120):
+def node(req, timeout=120, env=None):
     r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "check.js")], input=json.dumps(req),
-                       capture_output=True, text=True, timeout=timeout)
+                       capture_output=True, text=True, timeout=timeout, env=dict(os.environ, **(env or {})))
     if r.returncode != 0:
         raise RuntimeError(f"node failed: {r.stderr}")
     return json.loads(r.stdout)
@@ -93,6 +93,37 @@ def test_questions_match_python_host():
             assert j == {"error": str(e)}
             continue
         assert j == want
+
+
+def test_encoder_packing_kinds_and_head_match_python_host():
+    """Encoder packing equals the Python host's bit for bit; manifests route to the reference's kinds
+    (d1.ts:63-64); the learned decision head (eg2-head.ts) gives the Python host's logits."""
+    load_pkg()
+    from decision_js_amd import encoder
+    from decision_js_amd.eg2_head import Eg2Head
+    seqs = [[5, 6, 7], [1], list(range(40)), [9, 9]]
+    js = node({"cmd": "packenc", "seqs": seqs})
+    py = encoder.pack_encoder(seqs)
+    assert js["T"] == py["T"] and js["S"] == py["S"]
+    for k in ("ids", "meta", "full", "ranges"):
+        assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), k
+    kinds = node({"cmd": "kinds", "configs": [{"model": "decoder"}, {"model": "d1-3b"}, {"model": "eg2-encoder"},
+                                                {"model": "eg2"}, {"model": "omni", "head_layers": 2}]})
+    assert kinds[:4] == ["d1-3b", "d1-3b", "eg2", "eg2"] and "error" in kinds[4]
+    import test_eg2_head as H
+    tensors = H._tensors(3)
+    rng = np.random.default_rng(4)
+    calls = []
+    for qtype in ("choice", "noul", "score", "choice"):
+        s, q = H._unit(rng), H._unit(rng)
+        opts = [(f"o{len(calls)}{i}", H._unit(rng)) for i in range(3)]
+        calls.append((qtype, ("s", s) if len(calls) != 2 else ("s2", s), (f"q{len(calls)}", q), opts))
+    js = node({"cmd": "eg2head", "config": H.CFG, "tensors": {k: [float(x) for x in v.reshape(-1)] for k, v in tensors.items()},
+               "calls": [[t, [s[0], s[1].tolist()], [q[0], q[1].tolist()], [[k, e.tolist()] for k, e in o]] for t, s, q, o in calls]})
+    head = Eg2Head(H.CFG, tensors)
+    for got, (t, s, q, o) in zip(js, calls):
+        want = head.logits(t, s, q, o)
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6), (got, want)
 
 
 def test_pass_splitting_matches_python_host():
@@ -168,6 +199,9 @@ def test_node_decision_matches_python_host(tmp_path):
     assert js["again"] == js["one"] and js["afterError"] == js["one"]
     assert js["badError"] == "decision.js: a choice needs criteria {name: description} with at least two options"
     assert js["progress"][-1] == [3, 3] and len(js["progress"]) >= 2
+    assert js["progressP"] == js["progress"]  # probabilitiesBatch(requests, {onProgress}) as well
+    for a, b in zip(js["probsBatch"], py_batch):
+        assert abs(a[1][0] - b["answers"]["churn"]["noul"]) < 1e-12
     for a, b in zip(js["batch"], py_batch):
         assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-12
     for n in qs:
@@ -178,24 +212,105 @@ def test_node_decision_matches_python_host(tmp_path):
 
 def test_graph_keys_from_second_use_match_python_host():
     """Both hosts run a forward's first use of a key eagerly (key 0), capture on the second and replay after;
-    with graphs off every key is 0."""
+    distinct forwards never share a key; a shared state's graphs are dropped when the state is freed (and
+    only they); with graphs off every key is 0."""
     load_pkg()
     from decision_js_amd.engine import GpuEngine
-    seq = [["run", 100, 3, 5], ["run", 100, 3, 5], ["run", 100, 3, 5], ["run", 60, 3, 5], ["shared", 1, 32, 8, 5],
-           ["run", 60, 3, 5], ["shared", 2, 32, 8, 5]]
+    seq = [[["run", 100, 3, 5], None], [["run", 100, 3, 5], None], [["run", 100, 3, 5], None], [["run", 60, 3, 5], None],
+           [["shared", 32, 8, 5], 1], [["run", 60, 3, 5], None], [["shared", 32, 8, 5], 2], [["shared", 32, 8, 5], 1],
+           [["shared", 32, 8, 5], 1]]
+
+    class FakeCtx:
+        def __init__(self):
+            self.dropped = []
+
+        def graph_drop(self, key):
+            self.dropped.append(key)
+
+    class FakeState:
+        serial = 1
+
+        def free(self):
+            pass
 
     def py_keys(graphs):
         e = GpuEngine.__new__(GpuEngine)
-        e.graphs, e._gen, e._seen = graphs, 0, set()
-        return [e._key(*p) for p in seq]
+        e.graphs, e._gen, e._keys, e._state_keys, e.ctx = graphs, 0, {}, {}, FakeCtx()
+        keys = [e._key(*parts, state=st) for parts, st in seq]
+        e.free_state(FakeState())
+        after = e._key(*seq[7][0], state=1)  # the freed state's forward starts over: eager
+        return keys, [int(k) for k in e.ctx.dropped], after
 
     for graphs in (True, False):
-        js = [int(k) for k in node({"cmd": "graphkeys", "graphs": graphs, "seq": seq})]
+        js = node({"cmd": "graphkeys", "graphs": graphs, "seq": seq, "free": 1})
         py = py_keys(graphs)
-        for keys in (js, py):
+        for keys, dropped, after in ([int(k) for k in js["keys"]], [int(k) for k in js["dropped"]], int(js["after"])), py:
             if not graphs:
-                assert keys == [0] * len(seq)
+                assert keys == [0] * len(seq) and dropped == [] and after == 0
                 continue
             assert keys[0] == 0 and keys[1] == keys[2] != 0  # eager, capture, replay
             assert keys[3] == 0 and keys[5] not in (0, keys[1])  # another shape: eager, then its own graph
             assert keys[4] == 0 and keys[6] == 0  # a new state's questions: eager each time
+            assert keys[7] == keys[8] != 0 and keys[7] not in (keys[1], keys[5])  # state 1's second use
+            assert dropped == [keys[7]] and after == 0
+
+
+@pytest.mark.gpu
+def test_node_encoder_matches_python_host(tmp_path):
+    """The EmbeddingGemma-shaped encoder through the Node host (D1 kind "eg2", runEg2 with the learned decision
+    head) against the Python host: the same embeddings and probabilities, progress through BatchOptions, and
+    cached texts skipped on the second call."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.reduced("eg2-encoder-q8", layers=2, vocab=2048, learned_head={"width": 64})
+    mdir = synth.generate(cfg, str(tmp_path / "enc"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(8)
+    ids = lambda n: [int(x) for x in rng.integers(0, 2048, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(24),
+                    "option_ids": [ids(8), ids(8), ids(6)]},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(20), "option_ids": [ids(3), ids(2)]}}
+    batch = [[ids(n), qs] for n in (60, 33)]
+    texts = [ids(n) for n in (12, 1, 40)]
+    js = node({"cmd": "encode", "model": mdir, "batch": batch, "texts": texts}, timeout=300)
+    assert js["kind"] == "eg2" and js["tokensPerPass"] == 8192
+    d = Decision.load(mdir)
+    try:
+        py = d.system_one_batch([tuple(b) for b in batch])
+        emb = d.engine.embed(texts)["embeddings"]
+    finally:
+        d.destroy()
+    assert np.allclose(np.asarray(js["embeddings"], dtype=np.float32), emb, rtol=0, atol=1e-6)
+    for a, b in zip(js["batch"], py):
+        assert a["answers"]["topic"]["choice"] == b["answers"]["topic"]["choice"]
+        assert abs(a["answers"]["topic"]["confidence"] - b["answers"]["topic"]["confidence"]) < 1e-6
+        assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-6
+        assert a["usage"] == b["usage"]
+    assert js["progress"] and js["progress"][-1][0] == js["progress"][-1][1]
+    assert js["again"][0]["usage"]["input_tokens"] == 0 and js["again"][0]["answers"] == js["batch"][0]["answers"]
+
+
+@pytest.mark.gpu
+def test_node_injected_fault_surfaces_and_next_call_succeeds(tmp_path):
+    """DJ_FAULT_INJECT=matmul:1 in the Node process: the first forward rejects with the library's "decision.js:
+    fault injected in matmul" error (the recording aborted), and the next calls give the Python host's clean
+    probabilities."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    mdir = synth.generate(synth.reduced("qwen3-0.6b-q8", layers=2, vocab=4096), str(tmp_path / "m"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(12)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"churn": {"type": "noul", "instructions": "?", "ids": ids(20), "options": [[5], [6, 7]]},
+          "topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": ""}, "ids": ids(9), "options": [[1], [2]]}}
+    state = ids(150)
+    js = node({"cmd": "fault", "model": mdir, "state": state, "questions": qs}, timeout=300, env={"DJ_FAULT_INJECT": "matmul:1"})
+    assert js["error"].startswith("decision.js: fault injected in matmul")
+    d = Decision.load(mdir)
+    try:
+        want = d.probabilities(state, list(qs.values()))
+    finally:
+        d.destroy()
+    for got in (js["after"], js["again"]):
+        for a, b in zip(got, want):
+            assert np.allclose(a, b, rtol=0, atol=1e-12)
