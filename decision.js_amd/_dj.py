@@ -73,6 +73,7 @@ SIGNATURES = {
     "dj_rope_table": [_P, _I, _P, _I, _F, _I, _I, _P],
     "dj_matmul_qkv_rope": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P],
     "dj_attention": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
+    "dj_attention_noalloc": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_kv_store": [_P, _I, _I, _I, _P, _I, _I, _P, _I],
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
     "dj_readout": [_P, _I, _I, _I, _P, _P, _I, _P, _P],
@@ -296,6 +297,9 @@ class Recorder:
 
     def attention(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))
+
+    def attention_noalloc(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
+        check(lib().dj_attention_noalloc(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))
 
     def kv_store(self, T, kv, D, Z, stride, k_col, cache, row0):
         check(lib().dj_kv_store(self.h, T, kv, D, ptr(Z), stride, k_col, ptr(cache), row0))

@@ -427,30 +427,32 @@ static void attn_launch(dim3 g3, hipStream_t s, int T, int heads, int kv, const 
     k_attn<D, RING, KG, HG><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);
 }
 
+// The split-KV plan of a launch: small grids (a short question against a long state: one query block per head)
+// split each block's key tiles over up to 16 workgroups, their f32 partials (splits * T * heads * (D + 2) floats)
+// in a workspace of ws_floats floats, merged by k_attn_combine; large grids run whole (1). Splits that do not fit
+// the workspace are reduced until they do. DJ_ATTN_SPLITS=<n> forces the split count (tuning sweeps).
+// Only long key sources are split: a 32-token question on a 1056-row kept state runs 14.1 us split against 25.0
+// whole, while the encoder's 384-token layer (at most 4 tiles per block) runs 21.4 split against 15.9 whole, the
+// merge costing as much as it saves (measured on MI355X).
+static int attn_splits(int cus, int T, int heads, int D, const dj_kv_src &A, const dj_kv_src &B, size_t ws_floats) {
+  const long grid = (long)dj_cdiv(T, 64) * heads;
+  const char *force = getenv("DJ_ATTN_SPLITS");
+  const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
+  if (!force && !(grid < cus && max_tiles >= 16)) return 1;
+  int splits = force ? atoi(force) : (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * cus, grid));
+  splits = std::max(1, std::min(splits, 64));
+  while (splits > 1 && (size_t)splits * T * heads * (D + 2) > ws_floats) --splits;
+  return splits;
+}
+
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
-                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O) {
+                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats) {
   hipStream_t s = c->stream;
   const int qblocks = dj_cdiv(T, 64);
   const long grid = (long)qblocks * heads;
   const int4 *r4 = (const int4 *)rng;
-  // Small grids (a short question against a long state: one query block per head) split each block's key
-  // tiles over up to 16 workgroups, partials in the context's workspace (free between kernels of the
-  // stream), merged by k_attn_combine. Large grids run whole.
-  // DJ_ATTN_SPLITS=<n> forces the split count (tuning sweeps)
-  int splits = 1;
-  float *part = nullptr;
-  const char *force = getenv("DJ_ATTN_SPLITS");
-  // Only long key sources are split: a 32-token question on a 1056-row kept state runs 14.1 us split against
-  // 25.0 whole, while the encoder's 384-token layer (at most 4 tiles per block) runs 21.4 split against 15.9
-  // whole, the merge costing as much as it saves (measured on MI355X).
-  const int max_tiles = dj_cdiv(A.rows, 64) + dj_cdiv(B.rows, 64);
-  if (force || (grid < c->cus && max_tiles >= 16)) {
-    splits = force ? atoi(force) : (int)std::min<long>(std::min(16, max_tiles), dj_cdiv(2L * c->cus, grid));
-    splits = std::max(1, std::min(splits, 64));
-    while (splits > 1 && (size_t)splits * T * heads * (D + 2) > c->gemm_ws_floats) --splits;
-    if (splits > 1 && c->gemm_ws) part = c->gemm_ws;
-    else splits = 1;
-  }
+  int splits = ws ? attn_splits(c->cus, T, heads, D, A, B, ws_floats) : 1;
+  float *part = splits > 1 ? ws : nullptr;
   // Ring depth: two stages for 4-wave workgroups (two workgroups fit per CU and hide each other's latency:
   // 13.6 vs 18.0 us with a 4-stage ring, one workgroup per CU, at T = 1152, D 128 causal; 504 vs 719 us at
   // 86016), and the deepest that fits 128 KB for head groups.
@@ -512,10 +514,57 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_OP_BEGIN(rec, "attention");
   if (T > 0) {
-    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O);
+    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O, rec->ctx->gemm_ws,
+                                 rec->ctx->gemm_ws_floats);
     if (st) return st;
   }
   char shape[48];
   snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
   return dj_op_end(rec, "attention", shape);
+}
+
+// ---------------------------------------------------------------- the entry point that allocates nothing
+
+// Split-KV partials of dj_attention_noalloc: 8 MiB of f32 per GPU, held until the process ends. Every call on
+// a GPU shares that GPU's array (calls that overlap on one GPU race); every partial is written before it is
+// read, so nothing needs clearing. Host code never uses this name as an address: dj_attn_scratch_init takes the
+// device's own address of the array with hipGetSymbolAddress.
+constexpr size_t kScratchFloats = (size_t)2 << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+int dj_attn_scratch_init(dj_ctx *c) {  // with c's device current (dj_init)
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return dj_fail(DJ_EHIP, "decision.js: the attention scratch has no device address (%s)", hipGetErrorString(e));
+  c->attn_scratch = (float *)p;
+  return DJ_OK;
+}
+
+extern "C" int dj_attention_noalloc(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
+                                    dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, uint16_t *O) {
+  DJ_REQUIRE(Q && rng && O && T >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && q_stride % 8 == 0 &&
+                 q_stride >= heads * D,
+             "decision.js: attention: bad arguments (heads %d, kv %d, q_stride %d)", heads, kv, q_stride);
+  DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
+  DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
+  DJ_REQUIRE(rec && rec->ctx && rec->ctx->attn_scratch, "decision.js: dj_attention_noalloc: no recorder or scratch");
+  // the plan dj_attention takes; refused (not shrunk) where its partials exceed the scratch, so both entry
+  // points always compute the same thing
+  const int splits = attn_splits(rec->ctx->cus, T, heads, D, A, B, rec->ctx->gemm_ws ? rec->ctx->gemm_ws_floats : 0);
+  const size_t need = splits > 1 ? (size_t)splits * T * heads * (D + 2) : 0;
+  DJ_REQUIRE(need <= kScratchFloats,
+             "decision.js: dj_attention_noalloc: T %d x %d heads of %d dims split %d ways needs %.1f MB of scratch, "
+             "more than its %.1f MB (use dj_attention)",
+             T, heads, D, splits, need * 4 / 1e6, kScratchFloats * 4 / 1e6);
+  DJ_OP_BEGIN(rec, "attention_noalloc");
+  if (T > 0) {
+    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O, rec->ctx->attn_scratch,
+                                 kScratchFloats);
+    if (st) return st;
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]/k%d", T, heads, kv, D, splits);
+  return dj_op_end(rec, "attention_noalloc", shape);
 }

@@ -48,6 +48,12 @@ extern "C" int dj_init(int ordinal, dj_ctx **out) {
   }
   DJ_HIP(hipEventCreate(&c->t0));
   DJ_HIP(hipEventCreate(&c->t1));
+  // this device's address of the static attention scratch (dj_attention_noalloc), taken with the device current
+  if (int st = dj_attn_scratch_init(c)) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return st;
+  }
   // DJ_FAULT_INJECT=<op>[:<n>]: the op fails (before launching anything) every time, or its next n times
   if (const char *f = getenv("DJ_FAULT_INJECT")) {
     c->fault_op = f;

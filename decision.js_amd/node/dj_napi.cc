@@ -464,6 +464,12 @@ napi_value Attention(napi_env env, napi_callback_info info) {
   const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
   END(dj_attention(R(0), I(1), I(2), I(3), I(4), P16(5), I(6), a, b, PI32(9), F(10), P16(11)));
 }
+
+napi_value AttentionNoalloc(napi_env env, napi_callback_info info) {
+  BEGIN(12);
+  const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
+  END(dj_attention_noalloc(R(0), I(1), I(2), I(3), I(4), P16(5), I(6), a, b, PI32(9), F(10), P16(11)));
+}
 napi_value KvStore(napi_env env, napi_callback_info info) {
   BEGIN(9);
   END(dj_kv_store(R(0), I(1), I(2), I(3), P16(4), I(5), I(6), P16(7), I(8)));
@@ -499,7 +505,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
-      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"kvStore", KvStore},
+      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
       {"leafLogits", LeafLogits}, {"readout", Readout}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
   };
   for (const auto &f : fns) {

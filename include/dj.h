@@ -226,6 +226,15 @@ typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_co
 int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
                  dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, uint16_t *O_dev);
 
+/* dj_attention that allocates nothing, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid it). No counterpart in the reference. Same arguments and
+ * results as dj_attention; its split-KV partials (a short question against a long kept state) live in the
+ * library's static device scratch of 8 MiB per GPU instead of the context's workspace. A call whose split plan
+ * needs more than that (splits * T * heads * (D + 2) f32) is refused with DJ_EINVAL. Every call on a GPU shares
+ * that GPU's scratch: calls that overlap on one GPU race. */
+int dj_attention_noalloc(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
+                         dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, uint16_t *O_dev);
+
 /* Copies K and V of rows [0, T) of the fused rows Z into cache rows [row0, row0 + T) of layout
  * [rows, 2 * kv * D] (K heads then V heads): the kept KV of a prefilled shared state. */
 int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z_dev, int stride, int k_col,
