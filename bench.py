@@ -15,6 +15,9 @@ The JSON line also carries:
                 HIP events on the engine's stream; traffic = HBM bytes per launch from the FETCH_SIZE and
                 WRITE_SIZE counters (profiles/traffic.json, when it names the same kernel)
   cpu_baseline  the oracle (oracle/ref.py, numpy on the host cores) on one ticket of the same workload
+  north_star    the two targets on their own workloads: configs[3]'s batched prefill GEMMs against dense f16
+                peak, configs[4]'s single 32-token question against HBM bandwidth
+  cpu_reference_probe  whether the reference's own CPU path (WGSL via Node WebGPU on lavapipe) can run here
 """
 import argparse
 import json
@@ -199,6 +202,102 @@ def _forward_fraction(cfg, T, seqs, ms, causal=True):
             "traffic": None, "scope": "whole forward (quantized weight bytes)"}
 
 
+def probe_reference_cpu_path(timeout=20):
+    """The reference's own CPU path (its WGSL kernels through Node WebGPU/Dawn on a CPU Vulkan adapter) needs
+    Node >= 18, a WebGPU binding and a Vulkan ICD such as lavapipe. Records what this host has, run before the
+    GPU is touched (child processes only); nothing is installed."""
+    import shutil
+    import subprocess
+    out = {}
+    node = shutil.which("node")
+    out["node"] = None
+    if node:
+        try:
+            out["node"] = subprocess.run([node, "--version"], capture_output=True, text=True, timeout=timeout).stdout.strip()
+        except Exception as e:  # noqa: BLE001
+            out["node"] = f"error: {e}"
+    icd = "/usr/share/vulkan/icd.d"
+    out["vulkan_icds"] = sorted(os.listdir(icd)) if os.path.isdir(icd) else []
+    out["webgpu_binding"] = False
+    if node:
+        try:
+            r = subprocess.run([node, "-e", "require('webgpu')"], capture_output=True, text=True, timeout=timeout)
+            out["webgpu_binding"] = r.returncode == 0
+        except Exception:  # noqa: BLE001
+            pass
+    major = int(out["node"][1:].split(".")[0]) if out["node"] and out["node"].startswith("v") else 0
+    out["runnable"] = bool(major >= 18 and out["vulkan_icds"] and out["webgpu_binding"])
+    out["status"] = ("available" if out["runnable"] else
+                     "unavailable: the reference's WGSL path needs Node >= 18, a WebGPU binding and a Vulkan ICD "
+                     "(none installed here); cpu_baseline is this build's CPU restatement instead")
+    return out
+
+
+def batch_trees(cfg):
+    """192 sequences of U[128, 768] random ids (lengths seed 2, ids seed 1, answer sets seed 3)."""
+    lens_rng = np.random.Generator(np.random.PCG64(2))
+    ids_rng = np.random.Generator(np.random.PCG64(1))
+    ans_rng = np.random.Generator(np.random.PCG64(3))
+    V = cfg["vocab"]
+    lens = [int(x) for x in lens_rng.integers(128, 769, 192)]
+    trees = [{"trunk": [], "branches": [[int(x) for x in ids_rng.integers(0, V, n)]],
+              "groups": [[[int(a)] for a in ans_rng.choice(V, size=(2, 3, 5)[k % 3], replace=False)]]} for k, n in enumerate(lens)]
+    return trees, lens
+
+
+def batched_gemm_fraction(eng, cfg, st, T):
+    """One configs[3] forward with every op timed on its own (HIP events on the engine's stream): the prefill
+    GEMMs' FLOPs (2 T sum(N K) per layer) over their summed GPU time, against dense f16 peak."""
+    graphs = eng.graphs
+    eng.graphs = False
+    eng.ctx.profile_reset()
+    eng.ctx.profile(True)
+    eng.run_staged(st)
+    eng.ctx.profile(False)
+    table = eng.ctx.profile_table()
+    eng.graphs = graphs
+    total = sum(v[0] for v in table.values())
+    for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:8]:
+        log(f"  {k:48s} {kms:8.3f} ms/forward  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:8.1f} us each)")
+    gemm_ms = sum(v[0] for k, v in table.items() if k.startswith("matmul"))
+    gemm_flops = 2.0 * T * sum(n * k for n, k in _linear_shapes(cfg)) * cfg["layers"]
+    tf = gemm_flops / (gemm_ms * 1e-3) / 1e12
+    return {"tokens": T, "gemm_ms": round(gemm_ms, 3), "forward_ms_events": round(total, 3), "gemm_tflops": round(tf, 1),
+            "peak": MFMA_F16_PEAK_TFLOPS, "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "target": 0.60}
+
+
+def question_alone(eng, cfg, state, branch, group, steps, warmup, per_op=True):
+    """One 32-token question against a prefilled, kept state (configs[4]'s weight-streaming regime): GPU time
+    per question (HIP events over `steps` replayed forwards) and its quantized weight bytes over that time."""
+    stt = eng.prefill(state)
+    try:
+        for _ in range(warmup):
+            eng.run_shared(stt, [branch], [group])
+        eng.ctx.timer_begin()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            eng.run_shared(stt, [branch], [group])
+        wall = (time.perf_counter() - t1) / steps
+        gpu = eng.ctx.timer_end() / steps
+        if per_op:
+            graphs = eng.graphs
+            eng.graphs = False
+            eng.ctx.profile_reset()
+            eng.ctx.profile(True)
+            eng.run_shared(stt, [branch], [group])
+            eng.ctx.profile(False)
+            table = eng.ctx.profile_table()
+            eng.graphs = graphs
+            total = sum(v[0] for v in table.values())
+            log(f"question alone, per op (launched one at a time, {1e3 * total:.0f} us in all):")
+            for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
+                log(f"  {k:48s} {1e3 * kms:8.1f} us/question  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:6.1f} us each)")
+    finally:
+        eng.free_state(stt)
+    roof = _forward_fraction(cfg, 32, [32], gpu)
+    return wall, gpu, roof
+
+
 def run_workload(args):
     """The BASELINE configs other than the metric's, one JSON line each (not the driver's bench line):
     batch   configs[3]: 192 sequences of U[128, 768] random ids (lengths seed 2) on the 0.6B q8 decoder, packed
@@ -215,13 +314,7 @@ def run_workload(args):
         mdir = os.path.join(args.model_dir, "qwen3-0.6b-q8")
         synth.generate(cfg, mdir, seed=0, threads=16)
         eng = DecoderEngine.load(mdir, {"graphs": not args.no_graphs})
-        lens_rng = np.random.Generator(np.random.PCG64(2))
-        ids_rng = np.random.Generator(np.random.PCG64(1))
-        ans_rng = np.random.Generator(np.random.PCG64(3))
-        V = cfg["vocab"]
-        lens = [int(x) for x in lens_rng.integers(128, 769, 192)]
-        trees = [{"trunk": [], "branches": [[int(x) for x in ids_rng.integers(0, V, n)]],
-                  "groups": [[[int(a)] for a in ans_rng.choice(V, size=(2, 3, 5)[k % 3], replace=False)]]} for k, n in enumerate(lens)]
+        trees, lens = batch_trees(cfg)
         st = eng.stage(trees)
         T = sum(lens)
         log(f"batch: 192 sequences, T = {T}")
@@ -235,20 +328,8 @@ def run_workload(args):
         gpu_ms = eng.ctx.timer_end() / steps
         ms = 1e3 * wall / steps
         roof = _forward_fraction(cfg, T, lens, gpu_ms)
-        eng.graphs = False
-        eng.ctx.profile_reset()
-        eng.ctx.profile(True)
-        eng.run_staged(st)
-        eng.ctx.profile(False)
-        table = eng.ctx.profile_table()
-        eng.graphs = not args.no_graphs
-        total = sum(v[0] for v in table.values())
-        for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:8]:
-            log(f"  {k:48s} {kms:8.3f} ms/forward  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:8.1f} us each)")
-        gemm_ms = sum(v[0] for k, v in table.items() if k.startswith("matmul"))
-        gemm_flops = 2.0 * T * sum(n * k for n, k in _linear_shapes(cfg)) * cfg["layers"]
-        roof["gemm_tflops"] = round(gemm_flops / (gemm_ms * 1e-3) / 1e12, 1)
-        roof["gemm_frac"] = round(roof["gemm_tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+        g = batched_gemm_fraction(eng, cfg, st, T)
+        roof["gemm_tflops"], roof["gemm_frac"] = g["gemm_tflops"], g["frac"]
         log(f"forward {gpu_ms:.2f} ms (GPU), {192 * steps / wall:.1f} decisions/s; GEMMs {roof['gemm_tflops']} TFLOP/s "
             f"({100 * roof['gemm_frac']:.1f}% of dense f16 peak)")
         out = _line("decisions/sec (config-4 batch: 192 sequences, one varlen forward) on 1 MI355X", 192 * steps / wall,
@@ -272,7 +353,7 @@ def run_workload(args):
         def unit():
             stt = eng.prefill(state)
             eng.run_shared(stt, branches, groups)
-            stt.free()
+            eng.free_state(stt)
 
         for _ in range(warmup):
             unit()
@@ -284,32 +365,10 @@ def run_workload(args):
         gpu_ms = eng.ctx.timer_end() / steps
         ms = 1e3 * wall / steps
         # one question alone against a kept state: the weight-streaming (GEMV) regime
-        stt = eng.prefill(state)
-        for _ in range(warmup):
-            eng.run_shared(stt, branches[:1], groups[:1])
-        eng.ctx.timer_begin()
-        t1 = time.perf_counter()
-        for _ in range(steps):
-            eng.run_shared(stt, branches[:1], groups[:1])
-        q_wall = (time.perf_counter() - t1) / steps
-        q_gpu = eng.ctx.timer_end() / steps
-        # the question alone once more with every op timed on its own (HIP events on the engine's stream)
-        eng.graphs = False
-        eng.ctx.profile_reset()
-        eng.ctx.profile(True)
-        eng.run_shared(stt, branches[:1], groups[:1])
-        eng.ctx.profile(False)
-        table = eng.ctx.profile_table()
-        eng.graphs = not args.no_graphs
-        total = sum(v[0] for v in table.values())
-        log(f"question alone, per op (launched one at a time, {1e3 * total:.0f} us in all):")
-        for k, (kms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
-            log(f"  {k:48s} {1e3 * kms:8.1f} us/question  {100 * kms / total:5.1f}%  ({cnt} launches, {1e3 * kms / cnt:6.1f} us each)")
-        stt.free()
+        q_wall, q_gpu, q_roof = question_alone(eng, cfg, state, branches[0], groups[0], steps, warmup)
         if args.calib_mb:
             calibration_copy(eng.ctx, args.calib_mb)
         roof = _forward_fraction(cfg, 1024 + 256, [1024] + [32] * 8, gpu_ms)
-        q_roof = _forward_fraction(cfg, 32, [32], q_gpu)
         log(f"shared: prefill 1024 + 8 x 32 questions {gpu_ms:.3f} ms (GPU); one question alone {q_gpu:.3f} ms "
             f"({q_roof['achieved']} {q_roof['unit']}, {100 * q_roof['frac']:.1f}% of peak)")
         out = _line("decisions/sec (config-5: prefill 1024-token state + 8 questions x 32 tokens) on 1 MI355X", 8 * steps / wall,
@@ -376,12 +435,15 @@ def main():
                     help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
                          "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
     ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")
+    ap.add_argument("--no-north-star", action="store_true", help="skip the configs[3] / configs[4] target measurements")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the path shards by "
               f"independent tickets: see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    # the reference's CPU path is probed before anything touches the GPU (child processes only)
+    probe = probe_reference_cpu_path() if args.workload == "ticket" and not args.no_cpu else None
     pkg = load_pkg()
     from decision_js_amd import synth
     from decision_js_amd.engine import DecoderEngine
@@ -447,14 +509,19 @@ def main():
     if args.calib_mb:
         calibration_copy(eng.ctx, args.calib_mb)
     # HBM bytes per launch of this kernel from the committed counter summary that names it (FETCH_SIZE and
-    # WRITE_SIZE, each scaled by its reading for a copy of known size)
+    # WRITE_SIZE, each scaled by its reading for a copy of known size); not measured in this run
     if roof:
         import glob
         for f in sorted(glob.glob(os.path.join(ROOT, "profiles", "traffic_*.json"))):
             tr = json.load(open(f))
             if tr.get("kernel_key") == name:
                 roof["traffic"] = tr.get("bytes_per_launch")
-                roof["traffic_source"] = os.path.relpath(f, ROOT)
+                roof["traffic_source"] = os.path.relpath(f, ROOT) + " (committed rocprofv3 counter summary, not this run)"
+
+    # the north star's two targets, measured in this run on their own workloads
+    north = None
+    if not args.no_north_star and args.config == "qwen3-0.6b-q8":
+        north = north_star(args, eng, cfg)
 
     cpu = None
     if not args.no_cpu:
@@ -474,9 +541,51 @@ def main():
         "forward_roofline": {"t_roof_ms": round(t_roof_ms, 4), "frac_of_roofline": round(t_roof_ms / (gpu_ms / args.steps), 4),
                              "flops_per_ticket": flops, "weight_bytes": wbytes},
         "cpu_baseline": cpu,
+        "north_star": north,
+        "cpu_reference_probe": probe,
     }
     eng.destroy()
     print(json.dumps(out), flush=True)
+
+
+def north_star(args, eng, cfg):
+    """BASELINE.json's targets, each on its own configuration: (1) batched prefill GEMMs at >= 60% of dense f16
+    MFMA peak on configs[3] (192 sequences, one varlen forward on this same model: every op timed on its own);
+    (2) >= 70% of HBM bandwidth on a weight-bound single question of configs[4] (the ~0.8B q8 decoder, one
+    32-token question against a kept 1024-token state; GPU time of replayed forwards)."""
+    from decision_js_amd import synth
+    from decision_js_amd.engine import DecoderEngine
+    out = {}
+    t0 = time.time()
+    trees, lens = batch_trees(cfg)
+    st = eng.stage(trees)
+    T = sum(lens)
+    eng.run_staged(st)  # warm (buffers grown, kernels loaded)
+    out["batched_prefill_gemms"] = dict(batched_gemm_fraction(eng, cfg, st, T), workload="configs[3]: 192 x U[128,768] ids")
+    eng.free_staged(st)
+    log(f"north star 1: batched prefill GEMMs {out['batched_prefill_gemms']['gemm_tflops']} TFLOP/s "
+        f"({100 * out['batched_prefill_gemms']['frac']:.1f}% of dense f16) in {time.time() - t0:.1f} s")
+    t0 = time.time()
+    qcfg = synth.CONFIGS["d3lite-0.8b-q8"]
+    qdir = os.path.join(args.model_dir, "d3lite-0.8b-q8")
+    synth.generate(qcfg, qdir, seed=0, threads=16)
+    qeng = DecoderEngine.load(qdir, {"graphs": not args.no_graphs})
+    try:
+        ids_rng = np.random.Generator(np.random.PCG64(1))
+        ans_rng = np.random.Generator(np.random.PCG64(3))
+        V = qcfg["vocab"]
+        state = [int(x) for x in ids_rng.integers(0, V, 1024)]
+        branch = [int(x) for x in ids_rng.integers(0, V, 32)]
+        group = [[int(a)] for a in ans_rng.choice(V, size=2, replace=False)]
+        wall, gpu, roof = question_alone(qeng, qcfg, state, branch, group, steps=30, warmup=5)
+    finally:
+        qeng.destroy()
+    out["question_alone"] = {"gpu_ms": round(gpu, 4), "wall_ms": round(1e3 * wall, 4), "weight_gbs": roof["achieved"],
+                             "peak": HBM_PEAK_GBS, "frac": roof["frac"], "target": 0.70,
+                             "workload": "configs[4]: d3lite-0.8b-q8, one 32-id question on a kept 1024-id state"}
+    log(f"north star 2: question alone {gpu:.3f} ms, {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of HBM) "
+        f"in {time.time() - t0:.1f} s")
+    return out
 
 
 if __name__ == "__main__":
