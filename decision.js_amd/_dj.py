@@ -77,6 +77,7 @@ SIGNATURES = {
     "dj_kv_store": [_P, _I, _I, _I, _P, _I, _I, _P, _I],
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
     "dj_readout": [_P, _I, _I, _I, _P, _P, _I, _P, _P],
+    "dj_short_conv": [_P, _I, _I, _P, _P, _P, _P],
     "dj_mean_pool": [_P, _I, _I, _I, _P, _P, _P],
     "dj_dense_f32": [_P, _I, _P, _P, _P],
 }
@@ -306,6 +307,9 @@ class Recorder:
 
     def leaf_logits(self, T, L, H, nIds, eps, X, leaves, w, ids, embed: Weight, out):
         check(lib().dj_leaf_logits(self.h, T, L, H, nIds, eps, ptr(X), ptr(leaves), ptr(w), ptr(ids), embed.h, ptr(out)))
+
+    def short_conv(self, T, H, Z, w, taps, Y):
+        check(lib().dj_short_conv(self.h, T, H, ptr(Z), ptr(w), ptr(taps), ptr(Y)))
 
     def readout(self, T, P, H, X, R, codes, pairs, out):
         check(lib().dj_readout(self.h, T, P, H, ptr(X), ptr(R), codes, ptr(pairs), ptr(out)))

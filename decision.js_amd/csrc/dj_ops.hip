@@ -480,6 +480,58 @@ extern "C" int dj_readout(dj_rec *rec, int T, int P, int H, const uint16_t *X, c
   return dj_op_end(rec, "readout");
 }
 
+// ---------------------------------------------------------------- LFM2 short conv (kernels.ts:62-84)
+// One lane per (token, 8 channels): the token's C chunk and, for each of its three taps, the tapped token's B
+// and U chunks (16-byte loads of Z's [B | C | U] rows; consecutive lanes take consecutive chunks of one row),
+// conv = w0 (B U)[tap0] + w1 (B U)[tap1] + w2 (B U)[tap2] in f32 (a tap < 0 reads zero), Y = f16(C conv).
+// HBM-bound: at most 3 Z rows read and one H-wide row written per token.
+__global__ __launch_bounds__(256) void k_short_conv(int T, int H, const uint16_t *__restrict__ Z,
+                                                    const uint16_t *__restrict__ Wc, const int4 *__restrict__ taps,
+                                                    uint16_t *__restrict__ Y) {
+  const int chunks = H >> 3;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)T * chunks) return;
+  const int t = (int)(i / chunks), c0 = (int)(i % chunks) * 8;
+  const int4 tp = taps[t];
+  const int tt[3] = {tp.x, tp.y, tp.z};
+  // the chunk's 24 tap weights: Wc [H, 3] row-major, channels c0 .. c0 + 7
+  h8 w8[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) w8[q] = *(const h8 *)(Wc + (size_t)c0 * 3 + 8 * q);
+  float conv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) conv[k] = 0.f;
+  const size_t row = (size_t)3 * H;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    const int s = tt[j];
+    if (s < 0 || s >= T) continue;  // no token there: that tap reads zero
+    const h8 b = *(const h8 *)(Z + (size_t)s * row + c0);
+    const h8 u = *(const h8 *)(Z + (size_t)s * row + 2 * H + c0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int wi = k * 3 + j;  // channel c0 + k, tap j
+      const float w = (float)w8[wi >> 3][wi & 7];
+      conv[k] += w * ((float)b[k] * (float)u[k]);
+    }
+  }
+  const h8 c = *(const h8 *)(Z + (size_t)t * row + H + c0);
+  h8 y;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) y[k] = (_Float16)((float)c[k] * conv[k]);
+  *(h8 *)(Y + (size_t)t * H + c0) = y;
+}
+
+extern "C" int dj_short_conv(dj_rec *rec, int T, int H, const uint16_t *Z, const uint16_t *w, const int32_t *taps,
+                             uint16_t *Y) {
+  DJ_REQUIRE(Z && w && taps && Y && T >= 0 && H > 0 && H % 8 == 0,
+             "decision.js: short_conv: bad arguments (H %d must be a multiple of 8)", H);
+  DJ_OP_BEGIN(rec, "short_conv");
+  const long n = (long)T * (H / 8);
+  if (n > 0) k_short_conv<<<(unsigned)dj_cdiv(n, 256), 256, 0, rec->ctx->stream>>>(T, H, Z, w, (const int4 *)taps, Y);
+  return dj_op_end(rec, "short_conv");
+}
+
 // ---------------------------------------------------------------- mean pooling (eg2-kernels.ts:202-219)
 // One workgroup per (sequence, 64 columns): lane = column, the 4 waves take every 4th token (8 loads in
 // flight each), then wave 0 adds the 4 partial sums in wave order (deterministic) and divides.

@@ -76,6 +76,8 @@ class Decision:
         model = load_manifest(base if base.endswith("/") else base + "/")["config"].get("model")
         if model in ("decoder", "d1-3b"):
             kind, engine = "d1-3b", DecoderEngine.load(base, opts)
+        elif model == "d3":
+            kind, engine = "d3", DecoderEngine.load(base, opts)
         elif model in ("eg2-encoder", "eg2"):
             kind, engine = "eg2", EncoderEngine.load(base, opts)
         else:
@@ -120,6 +122,8 @@ class Decision:
         with self._lock:  # a failed call releases the lock: the queue does not wedge (d1.ts:117)
             if self.kind == "d1-3b":
                 return self._run_shared(requests, on_progress) if self.share_state else self._run_decoder(requests, on_progress)
+            if self.kind == "d3":
+                return self._run_d3(requests, on_progress)
             return self._run_encoder(requests, on_progress)
 
     def _passes(self, sizes):
@@ -148,6 +152,31 @@ class Decision:
                 out[i + r]["probs"] = [softmax(s) for s in per_q]
             if on_progress:
                 on_progress(j, len(trees))
+        return out
+
+    def _run_d3(self, requests, on_progress):
+        """runD3 (d1.ts:150-169): one sequence per question (the state's ids then the question's), its first
+        n-options codes read at its last token; with share_state each request's common prefix (the state) is
+        read once for all its questions (D3Engine's groups). Softmax at the model's temperature; a noul is read
+        as [false, true] and reversed to [yes, no]."""
+        p = self.prompt
+        seqs = [[{"ids": p.trunk(s) + p.branch(q), "options": Q.n_options(q)} for q in qs] for s, qs in requests]
+        sizes = [sum(len(x["ids"]) for x in g) for g in seqs]
+        temp = float(self.engine.m["config"].get("temperature", 1.0))
+        out = [{"probs": [], "tokens": n} for n in sizes]
+        for i, j in self._passes(sizes):
+            flat = [x for g in seqs[i:j] for x in g]
+            logits = self.engine.logits_d3(flat, [len(g) for g in seqs[i:j]] if self.share_state else None)
+            k = 0
+            for r in range(i, j):
+                probs = []
+                for q in requests[r][1]:
+                    pr = softmax(np.asarray(logits[k], dtype=np.float64) / temp)
+                    probs.append(pr[::-1] if q.get("type") == "noul" else pr)
+                    k += 1
+                out[r]["probs"] = probs
+            if on_progress:
+                on_progress(j, len(requests))
         return out
 
     def _run_shared(self, requests, on_progress):

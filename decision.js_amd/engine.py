@@ -151,6 +151,7 @@ def pack_forest(trees):
     pos = np.empty(T, dtype=np.int32)
     meta = np.empty((T, 4), dtype=np.int32)
     rng = np.zeros((T, 4), dtype=np.int32)
+    taps = np.zeros((T, 4), dtype=np.int32)  # the short conv's taps (d1-3b-engine.ts:56-64)
     leaves, leaf_ids = [], []
     off = 0
     for tr in trees:
@@ -163,6 +164,9 @@ def pack_forest(trees):
         meta[off:off + p] = np.stack([np.full(p, start), np.full(p, start + total), np.full(p, -1), i], 1)
         rng[off:off + p, 0] = start
         rng[off:off + p, 1] = start + i + 1
+        taps[off:off + p, 0] = np.where(i >= 2, start + i - 2, -1)
+        taps[off:off + p, 1] = np.where(i >= 1, start + i - 1, -1)
+        taps[off:off + p, 2] = start + i
         off += p
         for b, br in enumerate(tr["branches"]):
             n = len(br)
@@ -171,6 +175,9 @@ def pack_forest(trees):
             pos[off:off + n] = p + o
             meta[off:off + n] = np.stack([np.full(n, start), np.full(n, start + total), np.full(n, b), p + o], 1)
             rng[off:off + n] = np.stack([np.full(n, start), np.full(n, start + p), np.full(n, off), off + o + 1], 1)
+            for j in (1, 2):  # back j tokens: within the branch, else into the end of the trunk, else none
+                taps[off:off + n, 2 - j] = np.where(o - j >= 0, off + o - j, np.where(p + o - j >= 0, start + p + o - j, -1))
+            taps[off:off + n, 2] = off + o
             off += n
             leaves.append(off - 1)
             leaf_ids.append([x for g in tr["groups"][b] for x in g])
@@ -179,7 +186,7 @@ def pack_forest(trees):
     flat = np.zeros(max(L * n_ids, 1), dtype=np.uint32)
     for k, g in enumerate(leaf_ids):
         flat[k * n_ids:k * n_ids + len(g)] = g
-    return {"ids": ids, "pos": pos, "meta": meta, "rng": rng, "leaves": np.array(leaves, dtype=np.uint32),
+    return {"ids": ids, "pos": pos, "meta": meta, "rng": rng, "taps": taps, "leaves": np.array(leaves, dtype=np.uint32),
             "leaf_ids": flat, "n_ids": n_ids, "T": T, "L": L}
 
 
@@ -193,6 +200,38 @@ def common_prefix(seqs) -> int:
     while P < lim and all(s[P] == seqs[0][P] for s in seqs):
         P += 1
     return P
+
+
+def pack_shared(seqs, groups=None):
+    """D3Engine.logits's packing (d3-engine.ts:67-93). seqs: [{"ids", "options"}], one per question; groups:
+    sequences per request, consecutive (None: each sequence alone). A request's common token prefix (at least
+    one token left per question) is laid once as a trunk whose tokens see the trunk; each question's remaining
+    tokens see the trunk and themselves (noncausal within those ranges); without a prefix a sequence sees
+    itself. Positions are token indices within the original sequence. Per token: ids (u32), pos (i32), key
+    ranges rng (a0, a1, b0, b1); per option: pairs (the question's last row, code k)."""
+    sizes = groups if groups is not None else [1] * len(seqs)
+    if sum(sizes) != len(seqs):
+        raise ValueError(f"decision.js: groups cover {sum(sizes)} sequences, {len(seqs)} given")
+    ids, pos, rng, pairs = [], [], [], []
+    si = 0
+    for n in sizes:
+        group = seqs[si:si + n]
+        si += n
+        P = common_prefix([s["ids"] for s in group]) if n > 1 else 0
+        ts = len(ids)
+        for i in range(P):
+            ids.append(group[0]["ids"][i]); pos.append(i); rng.append((ts, ts + P, 0, 0))
+        for s in group:
+            bs = len(ids)
+            be = bs + len(s["ids"]) - P
+            for i in range(P, len(s["ids"])):
+                ids.append(s["ids"][i]); pos.append(i)
+                rng.append((ts, ts + P, bs, be) if P else (bs, be, 0, 0))
+            pairs += [(be - 1, k) for k in range(s["options"])]
+    T = len(ids)
+    return {"ids": np.array(ids, dtype=np.uint32), "pos": np.array(pos, dtype=np.int32),
+            "rng": np.array(rng, dtype=np.int32).reshape(T, 4), "pairs": np.array(pairs, dtype=np.uint32).reshape(-1, 2),
+            "T": T, "P": len(pairs)}
 
 
 def group_max(out: np.ndarray, n_ids: int, trees):
@@ -237,10 +276,11 @@ class DecoderEngine(GpuEngine):
     @classmethod
     def load(cls, base: str, opts: dict = None):
         ctx, m, w = load_weights(base, opts)
-        if m["config"].get("model") not in ("decoder", "d1-3b"):
-            raise ValueError(f"decision.js: {base} is not a causal decoder ({m['config'].get('model')})")
-        if any(t != "full_attention" for t in m["config"].get("layer_types", [])):
-            raise ValueError("decision.js: only attention layers are supported (LFM2 conv layers are not on this path)")
+        if m["config"].get("model") not in ("decoder", "d1-3b", "d3"):
+            raise ValueError(f"decision.js: {base} is not a decoder ({m['config'].get('model')})")
+        bad = sorted({t for t in m["config"].get("layer_types", []) if t not in ("full_attention", "conv")})
+        if bad:
+            raise ValueError(f"decision.js: unsupported layer types {bad} (attention and LFM2 conv layers run here)")
         return cls(ctx, m, w, opts)
 
     def __init__(self, ctx, m, w, opts=None):
@@ -248,6 +288,8 @@ class DecoderEngine(GpuEngine):
         c = m["config"]
         self.H, self.I, self.h, self.kv, self.D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
         self.layers = c.get("layers", len(c.get("layer_types", [])))
+        self.types = c.get("layer_types", ["full_attention"] * self.layers)
+        self.conv = "conv" in self.types
         self.eps, self.theta = c["eps"], c["rope_theta"]
         self.stride = (self.h + 2 * self.kv) * self.D
         self.capacity = 0
@@ -261,9 +303,11 @@ class DecoderEngine(GpuEngine):
         cap = (cap + 63) // 64 * 64
         lcap = max(L * max(n_ids, 1), self.leaf_capacity, 1024)
         H, I = self.H, self.I
-        self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * self.stride * 2,
-                     "y": cap * self.h * self.D * 2, "h": cap * I * 2, "ids": cap * 4, "pos": cap * 4, "rng": cap * 16,
-                     "rope": cap * (self.D // 2) * 8,
+        zw = max(self.stride, 3 * H if self.conv else 0)  # qkv rows, or a conv layer's [B | C | U]
+        yw = max(self.h * self.D, H if self.conv else 0)
+        self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * zw * 2,
+                     "y": cap * yw * 2, "h": cap * I * 2, "ids": cap * 4, "pos": cap * 4, "rng": cap * 16,
+                     "taps": cap * 16, "rope": cap * (self.D // 2) * 8,
                      "leaves": lcap * 4, "leaf_ids": lcap * 4, "out": lcap * 4})
         self.capacity, self.leaf_capacity = cap, lcap
 
@@ -279,13 +323,18 @@ class DecoderEngine(GpuEngine):
         rec.rope_table(T, B["pos"], 1, self.theta, D, B["rope"])
         for i in range(self.layers):
             p = f"layers.{i}."
-            rec.matmul_qkv_rope(B["normed"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"), w.get(p + "k_norm"), False,
-                                B["pos"], 1, eps, self.theta, B["rope"])
-            if kv_store is not None:
-                rec.kv_store(T, kv, D, z, self.stride, h * D, kv_store.at(i * T * 2 * kv * D * 2), 0)
-            a = src if kv_a is None else kv_a(i)
-            rec.attention(T, h, kv, D, z, self.stride, a, src, B["rng"], 1.0 / math.sqrt(D), B["y"])
-            rec.matmul(B["y"], w[p + "o_proj"], B["o"], T)
+            if self.types[i] == "conv":  # LFM2 short conv (d1-3b-engine.ts:90-93)
+                rec.matmul(B["normed"], w[p + "in_proj"], z, T)
+                rec.short_conv(T, H, z, w[p + "conv"], B["taps"], B["y"])
+                rec.matmul(B["y"], w[p + "out_proj"], B["o"], T)
+            else:
+                rec.matmul_qkv_rope(B["normed"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"), w.get(p + "k_norm"),
+                                    False, B["pos"], 1, eps, self.theta, B["rope"])
+                if kv_store is not None:
+                    rec.kv_store(T, kv, D, z, self.stride, h * D, kv_store.at(i * T * 2 * kv * D * 2), 0)
+                a = src if kv_a is None else kv_a(i)
+                rec.attention(T, h, kv, D, z, self.stride, a, src, B["rng"], 1.0 / math.sqrt(D), B["y"])
+                rec.matmul(B["y"], w[p + "o_proj"], B["o"], T)
             rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[p + "ffn_norm"], B["normed"])
             rec.matmul_glu(B["normed"], w[p + "w13"], B["h"], T, _dj.ACT_SILU)
             rec.matmul(B["h"], w[p + "w2"], B["o"], T)
@@ -300,7 +349,7 @@ class DecoderEngine(GpuEngine):
         self.stats["tokens"] += T
         return got
 
-    INPUTS = ("ids", "pos", "rng", "leaves", "leaf_ids")
+    INPUTS = ("ids", "pos", "rng", "taps", "leaves", "leaf_ids")
 
     def run(self, trees, debug_layers=()):
         """Option scores for every question of every tree: [tree][question][option] (max over the option's
@@ -351,12 +400,53 @@ class DecoderEngine(GpuEngine):
         out = got[oi] if oi is not None else np.zeros(0, np.float32)
         return {"scores": group_max(out, n_ids, trees), "debug": {i: got[k] for i, k in snaps.items()}, "logits": out}
 
+    def _no_conv(self, what):
+        if self.conv:
+            raise ValueError(f"decision.js: {what} is not available for models with LFM2 conv layers (their taps "
+                             "would need each state's last conv inputs): use run()")
+
+    # -- d3's code readout (D3Engine.logits, d3-engine.ts:67-139)
+    def logits_d3(self, seqs, groups=None):
+        """Code logits per question ([seq][its `options` codes], before the temperature): the sequences packed
+        by pack_shared (a request's common prefix read once when `groups` is given), every layer on those key
+        ranges, the final norm, then READOUT of each question's last row against the model's f32 `readout`
+        matrix [codes, hidden] (d3-kernels.ts:242-260)."""
+        if "readout" not in self.w:
+            raise ValueError("decision.js: this model has no code readout (a d3 export's `readout` matrix)")
+        self._no_conv("d3's code readout")
+        pk = pack_shared(seqs, groups)
+        T, P = pk["T"], pk["P"]
+        if T == 0:
+            return [[] for _ in seqs]
+        self.ensure(T, P, 2)  # leaf_ids holds the pairs (2 u32 each), out the P logits
+        B = self._bufs
+        B["ids"].upload(pk["ids"])
+        B["pos"].upload(pk["pos"])
+        B["rng"].upload(pk["rng"])
+        if P:
+            B["leaf_ids"].upload(pk["pairs"].reshape(-1))  # (row, code) pairs, 2 u32 each
+        R = self.w["readout"]
+        codes = R.host.shape[0]
+        with self.ctx.recorder(self._key("d3", T, P)) as rec:  # aborted on an error
+            if not rec.replay:
+                self._layers(rec, T, B)
+                if P:
+                    rec.readout(T, P, self.H, B["normed"], R, codes, B["leaf_ids"], B["out"])
+            oi = rec.snapshot(B["out"], max(P, 1) * 4, np.float32, (max(P, 1),)) if P else None
+        out = self._finish(rec, T)[oi] if P else np.zeros(0, np.float32)
+        res, k = [], 0
+        for s in seqs:
+            res.append([float(v) for v in out[k:k + s["options"]]])
+            k += s["options"]
+        return res
+
     # -- shared state: prefill once, keep the KV, answer questions against it
     def prefill(self, trunk) -> SharedState:
         """Runs the state alone (causal) and keeps every layer's K/V rows on the device."""
         P = len(trunk)
         if P == 0:
             raise ValueError("decision.js: an empty state has nothing to prefill")
+        self._no_conv("a kept shared state")
         self.ensure(P)
         B = self._bufs
         i = np.arange(P, dtype=np.int32)

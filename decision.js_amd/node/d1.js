@@ -41,6 +41,7 @@ const onProgressOf = (opts) => (typeof opts === "function" ? opts : opts && opts
 function kindOf(config) {
   const model = config && config.model;
   if (model === "eg2" || model === "eg2-encoder") return "eg2";
+  if (model === "d3") return "d3";
   if (model === "decoder" || model === "d1-3b" || !("head_layers" in (config || {}))) return "d1-3b";
   throw new Error(`decision.js: unsupported model kind ${model}`);
 }
@@ -112,6 +113,7 @@ class D1 {
   async runAll(requests, onProgress) {
     for (const [, qs] of requests) qs.forEach(Q.checkQuestion);
     if (this.kind === "eg2") return this.runEg2(requests, onProgress);
+    if (this.kind === "d3") return this.runD3(requests, onProgress);
     return this.shareState ? this.runShared(requests, onProgress) : this.runDecoder(requests, onProgress);
   }
 
@@ -163,6 +165,28 @@ class D1 {
       const scores = await this.engine.runShared(st, branches, qs.map(p.readoutIds));
       out.push({ probs: scores.map(softmax), tokens: trunk.length + branches.reduce((a, b) => a + b.length, 0) });
       if (onProgress) onProgress(k + 1, requests.length);
+    }
+    return out;
+  }
+
+  /** runD3 (d1.ts:150-169): one sequence per question (the state's ids, then the question's), its first
+   * n-options codes read at its last token; with shareState a request's common prefix (the state) is read once
+   * for all its questions. Softmax at the model's temperature; a noul is read as [false, true], reversed. */
+  async runD3(requests, onProgress) {
+    const p = this.prompt, temp = this.engine.m.config.temperature === undefined ? 1 : this.engine.m.config.temperature;
+    const seqs = requests.map(([s, qs]) => qs.map((q) => ({ ids: p.trunk(s).concat(p.branch(q)), options: Q.nOptions(q) })));
+    const sizes = seqs.map((g) => g.reduce((a, x) => a + x.ids.length, 0));
+    const out = sizes.map((n) => ({ probs: [], tokens: n }));
+    for (const [i, j] of this.passes(sizes)) {
+      const logits = await this.engine.logitsD3([].concat(...seqs.slice(i, j)), this.shareState ? seqs.slice(i, j).map((g) => g.length) : undefined);
+      let k = 0;
+      for (let r = i; r < j; ++r) {
+        out[r].probs = requests[r][1].map((q) => {
+          const pr = softmax(logits[k++].map((v) => v / temp));
+          return q.type === "noul" ? pr.reverse() : pr;
+        });
+      }
+      if (onProgress) onProgress(j, requests.length);
     }
     return out;
   }

@@ -133,6 +133,8 @@ class Recorder {
   }
   kvStore(T, kv, D, Z, stride, kCol, cache, row0) { lib().kvStore(this.h, T, kv, D, Z, stride, kCol, cache, row0); }
   meanPool(T, S, H, X, seqs, out) { lib().meanPool(this.h, T, S, H, X, seqs, out); }
+  readout(T, P, H, X, R, codes, pairs, out) { lib().readout(this.h, T, P, H, X, R, codes, pairs, out); }
+  shortConv(T, H, Z, w, taps, Y) { lib().shortConv(this.h, T, H, Z, w, taps, Y); }
   denseF32(M, inp, w, out) { lib().denseF32(this.h, M, inp, w.h, out); }
   leafLogits(T, L, H, nIds, eps, X, leaves, w, ids, embed, out) {
     lib().leafLogits(this.h, T, L, H, nIds, eps, X, leaves, w, ids, embed.h, out);

@@ -478,6 +478,11 @@ napi_value LeafLogits(napi_env env, napi_callback_info info) {
   BEGIN(12);
   END(dj_leaf_logits(R(0), I(1), I(2), I(3), I(4), F(5), P16(6), PU32(7), P16(8), PU32(9), W(10), PF32(11)));
 }
+napi_value ShortConv(napi_env env, napi_callback_info info) {
+  BEGIN(7);
+  END(dj_short_conv(R(0), I(1), I(2), P16(3), P16(4), PI32(5), P16(6)));
+}
+
 napi_value Readout(napi_env env, napi_callback_info info) {
   BEGIN(9);
   END(dj_readout(R(0), I(1), I(2), I(3), P16(4), PF32(5), I(6), PU32(7), PF32(8)));
@@ -506,7 +511,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
       {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
-      {"leafLogits", LeafLogits}, {"readout", Readout}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
+      {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
   };
   for (const auto &f : fns) {
     napi_value v;

@@ -26,7 +26,7 @@ function layoutFor(direct) {
 function packForest(trees) {
   let T = 0;
   for (const t of trees) T += t.trunk.length + t.branches.reduce((a, b) => a + b.length, 0);
-  const ids = new Uint32Array(T), pos = new Int32Array(T), rng = new Int32Array(T * 4);
+  const ids = new Uint32Array(T), pos = new Int32Array(T), rng = new Int32Array(T * 4), taps = new Int32Array(T * 4);
   const leaves = [], leafGroups = [];
   let off = 0;
   for (const tr of trees) {
@@ -36,6 +36,8 @@ function packForest(trees) {
       pos[off] = i;
       rng[4 * off] = start;
       rng[4 * off + 1] = start + i + 1;
+      // the short conv's taps (d1-3b-engine.ts:56-64): trunk tokens i-2, i-1, i
+      taps.set([i >= 2 ? start + i - 2 : -1, i >= 1 ? start + i - 1 : -1, start + i, 0], 4 * off);
     }
     tr.branches.forEach((br, b) => {
       const b0 = off;
@@ -43,6 +45,9 @@ function packForest(trees) {
         ids[off] = br[o];
         pos[off] = P + o;
         rng.set([start, start + P, b0, off + 1], 4 * off);
+        // back j tokens: within the branch, else into the end of the trunk, else none
+        const back = (j) => (o - j >= 0 ? off - j : P + o - j >= 0 ? start + P + o - j : -1);
+        taps.set([back(2), back(1), off, 0], 4 * off);
       }
       leaves.push(off - 1);
       leafGroups.push([].concat(...tr.groups[b]));
@@ -52,7 +57,50 @@ function packForest(trees) {
   const nIds = leafGroups.reduce((a, g) => Math.max(a, g.length), 0);
   const leafIds = new Uint32Array(Math.max(L * nIds, 1));
   leafGroups.forEach((g, k) => leafIds.set(g, k * nIds));
-  return { ids, pos, rng, leaves: Uint32Array.from(leaves), leafIds, nIds, T, L };
+  return { ids, pos, rng, taps, leaves: Uint32Array.from(leaves), leafIds, nIds, T, L };
+}
+
+/** The common token prefix of a request's sequences, leaving at least one token per sequence (d3-engine.ts:76-80). */
+function commonPrefix(seqs) {
+  if (seqs.length < 2) return 0;
+  const lim = Math.min(...seqs.map((s) => s.length)) - 1;
+  let P = 0;
+  while (P < lim && seqs.every((s) => s[P] === seqs[0][P])) ++P;
+  return P;
+}
+
+/** D3Engine.logits's packing (d3-engine.ts:67-93): seqs [{ids, options}], groups (sequences per request,
+ * consecutive; undefined: each alone). A request's common prefix is laid once as a trunk whose tokens see the
+ * trunk; each question's remaining tokens see the trunk and themselves; without a prefix a sequence sees
+ * itself. Positions are indices within the original sequence; pairs = (the question's last row, code k). */
+function packShared(seqs, groups) {
+  const sizes = groups || seqs.map(() => 1);
+  if (sizes.reduce((a, b) => a + b, 0) !== seqs.length) throw new Error(`decision.js: groups cover ${sizes.reduce((a, b) => a + b, 0)} sequences, ${seqs.length} given`);
+  const ids = [], pos = [], rng = [], pairs = [];
+  let si = 0;
+  for (const n of sizes) {
+    const group = seqs.slice(si, si + n);
+    si += n;
+    const P = n > 1 ? commonPrefix(group.map((s) => s.ids)) : 0;
+    const ts = ids.length;
+    for (let i = 0; i < P; ++i) {
+      ids.push(group[0].ids[i]);
+      pos.push(i);
+      rng.push(ts, ts + P, 0, 0);
+    }
+    for (const s of group) {
+      const bs = ids.length, be = bs + s.ids.length - P;
+      for (let i = P; i < s.ids.length; ++i) {
+        ids.push(s.ids[i]);
+        pos.push(i);
+        if (P) rng.push(ts, ts + P, bs, be);
+        else rng.push(bs, be, 0, 0);
+      }
+      for (let k = 0; k < s.options; ++k) pairs.push(be - 1, k);
+    }
+  }
+  return { ids: Uint32Array.from(ids), pos: Int32Array.from(pos), rng: Int32Array.from(rng), pairs: Uint32Array.from(pairs),
+    T: ids.length, P: pairs.length / 2 };
 }
 
 /** Readout of d1-3b-engine.ts:112-121: each option scores the max over its token group. */
@@ -164,10 +212,9 @@ class DecoderEngine extends GpuEngine {
     const direct = !!(opts.directWeights || opts.direct_weights);
     const { ctx, m, w } = await loadWeights(base, opts, layoutFor(direct));
     const model = m.config.model;
-    if (model !== "decoder" && model !== "d1-3b") throw new Error(`decision.js: ${base} is not a causal decoder (${model})`);
-    if ((m.config.layer_types || []).some((t) => t !== "full_attention")) {
-      throw new Error("decision.js: only attention layers are supported (LFM2 conv layers are not on this path)");
-    }
+    if (model !== "decoder" && model !== "d1-3b" && model !== "d3") throw new Error(`decision.js: ${base} is not a decoder (${model})`);
+    const bad = (m.config.layer_types || []).filter((t) => t !== "full_attention" && t !== "conv");
+    if (bad.length) throw new Error(`decision.js: unsupported layer types ${JSON.stringify(Array.from(new Set(bad)).sort())} (attention and LFM2 conv layers run here)`);
     return new DecoderEngine(ctx, m, w, opts);
   }
 
@@ -176,6 +223,8 @@ class DecoderEngine extends GpuEngine {
     const c = m.config;
     Object.assign(this, { H: c.hidden, I: c.intermediate, h: c.heads, kv: c.kv_heads, D: c.head_dim, eps: c.eps, theta: c.rope_theta });
     this.layers = c.layers !== undefined ? c.layers : (c.layer_types || []).length;
+    this.types = c.layer_types || new Array(this.layers).fill("full_attention");
+    this.conv = this.types.includes("conv");
     this.stride = (this.h + 2 * this.kv) * this.D;
     this.capacity = 0;
     this.leafCapacity = 0;
@@ -188,9 +237,10 @@ class DecoderEngine extends GpuEngine {
     cap = Math.ceil(cap / 64) * 64;
     const lcap = Math.max(L * Math.max(nIds, 1), this.leafCapacity, 1024);
     const { H, I } = this;
-    this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * this.stride * 2, y: cap * this.h * this.D * 2,
-      h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, rope: cap * (this.D / 2) * 8, leaves: lcap * 4,
-      leafIds: lcap * 4, out: lcap * 4 });
+    const zw = Math.max(this.stride, this.conv ? 3 * H : 0), yw = Math.max(this.h * this.D, this.conv ? H : 0);
+    this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * zw * 2, y: cap * yw * 2,
+      h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, taps: cap * 16, rope: cap * (this.D / 2) * 8,
+      leaves: lcap * 4, leafIds: lcap * 4, out: lcap * 4 });
     this.capacity = cap;
     this.leafCapacity = lcap;
   }
@@ -208,11 +258,17 @@ class DecoderEngine extends GpuEngine {
     rec.ropeTable(T, B.pos.ptr, 1, this.theta, D, B.rope.ptr, L.ROPE_POW_NEG);
     for (let i = 0; i < this.layers; ++i) {
       const p = `layers.${i}.`;
-      rec.matmulQkvRope(B.normed.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1, eps,
-        this.theta, B.rope.ptr, D, L.ROPE_POW_NEG);
-      if (kvStore) rec.kvStore(T, kv, D, z, this.stride, h * D, kvStore.at(i * T * 2 * kv * D * 2), 0);
-      rec.attention(T, h, kv, D, z, this.stride, kvA ? kvA(i) : src, src, B.rng.ptr, 1 / Math.sqrt(D), B.y.ptr);
-      rec.matmul(B.y.ptr, w[p + "o_proj"], B.o.ptr, T);
+      if (this.types[i] === "conv") { // LFM2 short conv (d1-3b-engine.ts:90-93)
+        rec.matmul(B.normed.ptr, w[p + "in_proj"], z, T);
+        rec.shortConv(T, H, z, ptr(p + "conv"), B.taps.ptr, B.y.ptr);
+        rec.matmul(B.y.ptr, w[p + "out_proj"], B.o.ptr, T);
+      } else {
+        rec.matmulQkvRope(B.normed.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1,
+          eps, this.theta, B.rope.ptr, D, L.ROPE_POW_NEG);
+        if (kvStore) rec.kvStore(T, kv, D, z, this.stride, h * D, kvStore.at(i * T * 2 * kv * D * 2), 0);
+        rec.attention(T, h, kv, D, z, this.stride, kvA ? kvA(i) : src, src, B.rng.ptr, 1 / Math.sqrt(D), B.y.ptr);
+        rec.matmul(B.y.ptr, w[p + "o_proj"], B.o.ptr, T);
+      }
       rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(p + "ffn_norm"), B.normed.ptr);
       rec.matmulGlu(B.normed.ptr, w[p + "w13"], B.h.ptr, T, L.ACT_SILU);
       rec.matmul(B.h.ptr, w[p + "w2"], B.o.ptr, T);
@@ -238,6 +294,7 @@ class DecoderEngine extends GpuEngine {
     B.ids.upload(pk.ids);
     B.pos.upload(pk.pos);
     B.rng.upload(pk.rng);
+    B.taps.upload(pk.taps);
     if (L) {
       B.leaves.upload(pk.leaves);
       B.leafIds.upload(pk.leafIds);
@@ -255,10 +312,45 @@ class DecoderEngine extends GpuEngine {
     return { scores: groupMax(out, nIds, trees), logits: out };
   }
 
+  /** d3's code logits per question ([seq][its options codes], before the temperature; D3Engine.logits,
+   * d3-engine.ts:67-139): packShared's ranges on every layer, the final norm, then READOUT of each question's
+   * last row against the model's f32 `readout` matrix [codes, hidden] (d3-kernels.ts:242-260). */
+  noConv(what) {
+    if (this.conv) throw new Error(`decision.js: ${what} is not available for models with LFM2 conv layers (their taps would need each state's last conv inputs): use run()`);
+  }
+
+  async logitsD3(seqs, groups) {
+    if (!this.w.readout) throw new Error("decision.js: this model has no code readout (a d3 export's `readout` matrix)");
+    this.noConv("d3's code readout");
+    const pk = packShared(seqs, groups);
+    const { T, P } = pk;
+    if (T === 0) return seqs.map(() => []);
+    this.ensure(T, P, 2); // leafIds holds the pairs (2 u32 each), out the P logits
+    const B = this.bufs;
+    B.ids.upload(pk.ids);
+    B.pos.upload(pk.pos);
+    B.rng.upload(pk.rng);
+    if (P) B.leafIds.upload(pk.pairs);
+    const R = this.w.readout, codes = this.m.tensors.readout.shape[0];
+    const rec = this.ctx.recorder(this.key(["d3", T, P]));
+    const oi = rec.record(() => { // aborted on an error
+      if (!rec.replay) {
+        this.recordLayers(rec, T, B, null, null);
+        if (P) rec.readout(T, P, this.H, B.normed.ptr, R.ptr, codes, B.leafIds.ptr, B.out.ptr);
+      }
+      return P ? rec.snapshot(B.out.ptr, Float32Array, P) : -1;
+    });
+    const got = await this.finish(rec, T);
+    const out = oi >= 0 ? got[oi] : new Float32Array(0);
+    let k = 0;
+    return seqs.map((s) => Array.from(out.subarray(k, (k += s.options))));
+  }
+
   /** Runs the state alone (causal) and keeps every layer's K/V rows on the device. */
   async prefill(trunk) {
     const P = trunk.length;
     if (P === 0) throw new Error("decision.js: an empty state has nothing to prefill");
+    this.noConv("a kept shared state");
     this.ensure(P);
     const B = this.bufs;
     const pos = new Int32Array(P), rng = new Int32Array(P * 4);
@@ -323,4 +415,4 @@ class DecoderEngine extends GpuEngine {
   }
 }
 
-module.exports = { packForest, groupMax, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };
+module.exports = { packForest, packShared, commonPrefix, groupMax, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };

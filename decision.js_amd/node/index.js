@@ -2,7 +2,7 @@
 /* decision.js on MI355X, Node host: `const { D1 } = require(".../decision.js_amd/node")` — the reference's
  * exports of index.ts: D1 (and its alias Decision), answer and checkQuestion, the engines. */
 const { D1, Decision, softmax } = require("./d1");
-const { DecoderEngine, packForest, groupMax } = require("./engine");
+const { DecoderEngine, packForest, packShared, groupMax } = require("./engine");
 const { EncoderEngine, packEncoder } = require("./encoder");
 const { Eg2Head } = require("./eg2_head");
 const { loadWeights, fileFetch } = require("./format");
@@ -11,5 +11,5 @@ const dj = require("./dj");
 
 module.exports = {
   D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, Eg2Head,
-  packForest, packEncoder, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+  packForest, packShared, packEncoder, groupMax, loadWeights, fileFetch, softmax, questions, dj,
 };

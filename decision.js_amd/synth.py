@@ -31,6 +31,21 @@ CONFIGS = {
     "d3lite-0.8b-q8": dict(model="decoder", bits=8, layers=20, hidden=1536, intermediate=4608, heads=12, kv_heads=2,
                            head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=True,
                            choices={"norm_weights": 1.0, "qk_norm": "yes (not stated)", "rope_theta": "1e6 (not stated)"}),
+    # d3-lite's readout form (D3Engine.logits, d3-engine.ts:67-139) on attention-only layers of the configs[4]
+    # shape: noncausal attention within each sequence (or trunk + question with a shared prefix), the final norm,
+    # then code logits READOUT from an f32 [codes, hidden] matrix at each sequence's last token
+    "d3-attn-0.8b-q8": dict(model="d3", bits=8, layers=20, hidden=1536, intermediate=4608, heads=12, kv_heads=2,
+                            head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=True,
+                            codes=["A", "B", "C", "D", "E", "F", "G", "H"], temperature=1.0,
+                            choices={"norm_weights": 1.0, "layers": "attention only (no Gated DeltaNet)"}),
+    # d1-3B's LFM2 backbone form (D13BEngine, d1-3b-engine.ts; export-3b.py): short-conv layers with attention
+    # layers between them, 64-dim heads with q/k norm, q4 linears, f16 conv taps [H, 3]. Not a BASELINE config:
+    # the layer pattern, widths and vocabulary are choices.
+    "lfm2-d1-3b-q4": dict(model="d1-3b", bits=4, layers=30, hidden=2048, intermediate=8192, heads=32, kv_heads=8,
+                          head_dim=64, vocab=65536, eps=1e-5, rope_theta=1e6, qk_norm=True,
+                          layer_types=["full_attention" if i % 3 == 2 else "conv" for i in range(30)],
+                          choices={"norm_weights": 1.0, "layer_types": "attention every third layer (not stated)",
+                                   "intermediate": "8192 (not stated)", "vocab": "65536 (not stated)"}),
     # EmbeddingGemma-shaped bidirectional encoder, q8, mean-pool + 768->3072->768 head
     "eg2-encoder-q8": dict(model="encoder", bits=8, layers=24, hidden=768, intermediate=1152, heads=3, kv_heads=1,
                            head_dim=256, vocab=262144, eps=1e-6, rope_theta=1e4, head_width=3072, embed_dim=768,
@@ -66,14 +81,21 @@ def tensor_plan(cfg: dict):
     """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
     H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
     plan = [("embed", "q", (V, H))]
-    if cfg["model"] == "decoder":
+    if cfg["model"] in ("decoder", "d3", "d1-3b"):
         plan.append(("final_norm", "n", (H,)))
+        types = cfg.get("layer_types") or ["full_attention"] * L
         for i in range(L):
             p = f"layers.{i}."
-            plan += [(p + "operator_norm", "n", (H,)), (p + "ffn_norm", "n", (H,)), (p + "qkv", "q", ((h + 2 * kv) * D, H)),
-                     (p + "o_proj", "q", (H, h * D)), (p + "w13", "q", (2 * I, H)), (p + "w2", "q", (H, I))]
+            plan += [(p + "operator_norm", "n", (H,)), (p + "ffn_norm", "n", (H,)), (p + "w13", "q", (2 * I, H)),
+                     (p + "w2", "q", (H, I))]
+            if types[i] == "conv":  # LFM2 short conv (export-3b.py: in_proj, out_proj, conv taps [H, 3])
+                plan += [(p + "in_proj", "q", (3 * H, H)), (p + "out_proj", "q", (H, H)), (p + "conv", "c", (H, 3))]
+                continue
+            plan += [(p + "qkv", "q", ((h + 2 * kv) * D, H)), (p + "o_proj", "q", (H, h * D))]
             if cfg.get("qk_norm"):
                 plan += [(p + "q_norm", "n", (D,)), (p + "k_norm", "n", (D,))]
+        if cfg["model"] == "d3":
+            plan.append(("readout", "r", (len(cfg["codes"]), H)))  # f32 code matrix (d3-kernels.ts:242-260)
     else:
         for i in range(L):
             p = f"layers.{i}."
@@ -103,9 +125,9 @@ def head_plan(cfg: dict):
 
 def manifest_config(cfg: dict) -> dict:
     c = {k: v for k, v in cfg.items() if k not in ("bits",)}
-    c["layer_types"] = ["full_attention"] * cfg["layers"]
-    if cfg["model"] == "decoder":
-        c["model"] = "decoder"
+    c["layer_types"] = list(cfg.get("layer_types") or ["full_attention"] * cfg["layers"])
+    if cfg["model"] in ("decoder", "d3", "d1-3b"):
+        c["model"] = cfg["model"]
     else:
         c["model"] = "eg2-encoder"
         c["layer_scalars"] = [1.0] * cfg["layers"]
@@ -125,8 +147,12 @@ def manifest_config(cfg: dict) -> dict:
 def _make(cfg, name, kind, shape, seed, norm_std, std):
     if kind == "n":
         return name, kind, _norm(name, shape[0], norm_std, seed), None
+    if kind == "r":  # an f32 readout matrix, N(0, std)
+        return name, kind, normal(name, shape, std, seed), None
+    if kind == "c":  # f16 conv taps, N(0, 0.5): each tap moves its channel by about as much as the others
+        return name, kind, normal(name, shape, 0.5, seed), None
     w = normal(name, shape, std, seed)
-    if name == "embed" and cfg["model"] != "decoder":
+    if name == "embed" and cfg["model"] == "encoder":
         w = w * np.float32(math.sqrt(cfg["hidden"]))  # Gemma's sqrt(hidden) embedding scale, folded in
     q = fmt.quantize8(w) if cfg["bits"] == 8 else fmt.quantize4(w)
     return name, kind, q[0], q[1]
@@ -153,11 +179,13 @@ def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads:
         futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std, std) for n, k, s in plan]
         for (name, kind, shape), fut in zip(plan, futs):
             _, _, a, b = fut.result()
-            if kind == "n":
+            if kind in ("n", "c"):
                 blob.f16(name, a)
+            elif kind == "r":
+                blob.f32(name, a)
             else:
                 blob.put_quant(name, a, b, shape, cfg["bits"])
-    if cfg["model"] != "decoder" and cfg.get("learned_head"):
+    if cfg["model"] == "encoder" and cfg.get("learned_head"):
         # f32 host tensors; LayerNorm weights around 1, everything else N(0, 1/sqrt(fan-in))
         for name, shape in head_plan(cfg):
             if name.endswith("norm.weight"):

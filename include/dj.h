@@ -240,6 +240,16 @@ int dj_attention_noalloc(dj_rec *rec, int T, int heads, int kv, int D, const uin
 int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z_dev, int stride, int k_col,
                 uint16_t *cache_dev, int row0);
 
+/* ---------------------------------------------------------------- ops: LFM2 short conv */
+
+/* Y[t, c] = f16(C[t, c] * sum_j w[c, j] * B[tap_j, c] * U[tap_j, c]) for the fused in_proj rows
+ * Z[T, 3H] = [B | C | U] and conv taps w f16 [H, 3] (the depthwise conv weight), products in f32; taps i32
+ * [T, 4] names the tokens taps 0..2 read (-1 or >= T: zero; the 4th is unused): (t-2, t-1, t) for d1-3B's
+ * causal forest, a branch continuing its trunk, or (t-1, t, t+1) within a sequence for d1-omni. H % 8 == 0.
+ * Replaces SHORT_CONV (kernels.ts:62-84). */
+int dj_short_conv(dj_rec *rec, int T, int H, const uint16_t *Z_dev, const uint16_t *w_dev, const int32_t *taps_dev,
+                  uint16_t *Y_dev);
+
 /* ---------------------------------------------------------------- ops: readouts and pooling */
 
 /* out[l * nIds + j] = rmsnorm_f32(X[leaves[l]]) * w  .  dequant_f32(embed row ids[l * nIds + j]) in f32:

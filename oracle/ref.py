@@ -179,6 +179,44 @@ def pack_forest(trees):
             np.array(leaves, dtype=np.uint32), flat, n_ids)
 
 
+def forest_taps(trees):
+    """The short conv's taps of D13BEngine.run (d1-3b-engine.ts:56-64): per token the rows its three taps read
+    (-1: none), causal over the forest: a trunk token i reads trunk tokens i-2, i-1, i; a branch token reads back
+    through its own branch and then into the end of its trunk. [T, 4] i32 (the 4th unused, 0)."""
+    taps, n = [], 0
+    for tr in trees:
+        start, p = n, len(tr["trunk"])
+        for i in range(p):
+            taps.append((start + i - 2 if i >= 2 else -1, start + i - 1 if i >= 1 else -1, start + i, 0))
+        n += p
+        for br in tr["branches"]:
+            for o in range(len(br)):
+                t = n + o
+
+                def back(j):
+                    if o - j >= 0:
+                        return t - j
+                    return start + p + (o - j) if p + (o - j) >= 0 else -1
+                taps.append((back(2), back(1), t, 0))
+            n += len(br)
+    return np.array(taps, dtype=np.int32).reshape(-1, 4)
+
+
+def short_conv(Z, H, w, taps, acc=F32):
+    """SHORT_CONV (kernels.ts:62-84): Z [T, 3H] = [B | C | U]; conv = sum_j w[c, j] * f32(B[tap_j]) * f32(U[tap_j])
+    (a tap < 0 reads zero); Y = f16(f32(C) * conv)."""
+    Z = Z.astype(acc)
+    B, C, U = Z[:, :H], Z[:, H:2 * H], Z[:, 2 * H:3 * H]
+    bu = B * U
+    conv = np.zeros((Z.shape[0], H), dtype=acc)
+    w = w.astype(acc).reshape(H, 3)
+    for j in range(3):
+        tj = taps[:, j]
+        ok = tj >= 0
+        conv[ok] += w[:, j][None, :] * bu[tj[ok]]
+    return (C * conv).astype(F16)
+
+
 def forest_mask(meta, bidir=False):
     """Boolean [T, T] key mask of ATTENTION (kernels.ts:133-136): key k in [start, end) of the query's tree,
     and (bidir or (k is a trunk token and (the query is a branch token or pos_k <= pos_q)) or (same branch,
@@ -382,15 +420,19 @@ class Model:
 
 
 def decoder_forward(model: Model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=F32, layers=None, kv_prefix=None,
-                    keep_kv=False, debug_layers=()):
+                    keep_kv=False, debug_layers=(), pairs=None, taps=None):
     """The causal decoder forward of D13BEngine.run (d1-3b-engine.ts:86-106) on attention-only layers:
     gather -> rmsnorm -> per layer [qkv, qk-norm+rope, attention, o_proj, add+rmsnorm, w13+SwiGLU, w2,
     add+rmsnorm] -> LEAF_LOGITS at the leaves. kv_prefix: per-layer [P, 2 kv D] kept K/V rows that the mask's
-    first P columns refer to (shared-state mode). Returns (logits [L * nIds], per-layer K/V rows if keep_kv,
-    debug {layer: x})."""
+    first P columns refer to (shared-state mode). pairs: (row, code) pairs of d3's READOUT (d3-engine.ts:128-131,
+    d3-kernels.ts:242-260): the code logits of the final norm's f16 output against the model's f32 `readout`
+    matrix replace the leaf logits. Returns (logits [L * nIds] or [pairs], per-layer K/V rows if keep_kv,
+    debug {layer: x}). LFM2 conv layers (layer_types "conv", d1-3b-engine.ts:90-93) run in_proj, SHORT_CONV on
+    `taps` (forest_taps) and out_proj in place of attention."""
     c = model.c
     H, I, h, kv, D, eps = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
     L = c["layers"] if layers is None else layers
+    types = c.get("layer_types", ["full_attention"] * L)
     ec, es, eb = model.t["embed"]
     x = gather(ids, ec, es, eb)
     T = x.shape[0]
@@ -399,17 +441,23 @@ def decoder_forward(model: Model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=F
     kept, dbg = [], {}
     for i in range(L):
         p = f"layers.{i}."
-        z = matmul(normed, model.w16(p + "qkv"), acc)
-        z = qk_norm_rope(z, h, kv, D, pos, model.t.get(p + "q_norm"), model.t.get(p + "k_norm"), False, eps,
-                         c["rope_theta"], acc=acc)
-        if keep_kv:
-            kept.append(z[:, h * D:(h + 2 * kv) * D].copy())
-        if kv_prefix is not None:
-            rows = np.concatenate([kv_prefix[i], z[:, h * D:(h + 2 * kv) * D]])
-            y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc, kv_rows=rows)
+        if types[i] == "conv":
+            z = matmul(normed, model.w16(p + "in_proj"), acc)
+            o = matmul(short_conv(z, H, model.t[p + "conv"], taps, acc), model.w16(p + "out_proj"), acc)
+            if keep_kv:
+                kept.append(None)
         else:
-            y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc)
-        o = matmul(y, model.w16(p + "o_proj"), acc)
+            z = matmul(normed, model.w16(p + "qkv"), acc)
+            z = qk_norm_rope(z, h, kv, D, pos, model.t.get(p + "q_norm"), model.t.get(p + "k_norm"), False, eps,
+                             c["rope_theta"], acc=acc)
+            if keep_kv:
+                kept.append(z[:, h * D:(h + 2 * kv) * D].copy())
+            if kv_prefix is not None:
+                rows = np.concatenate([kv_prefix[i], z[:, h * D:(h + 2 * kv) * D]])
+                y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc, kv_rows=rows)
+            else:
+                y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc)
+            o = matmul(y, model.w16(p + "o_proj"), acc)
         x, normed = add_rmsnorm(x, o, model.t[p + "ffn_norm"], eps, acc=acc)
         ab = matmul(normed, model.w16(p + "w13"), acc)
         hh = silu_mul(ab[:, :I], ab[:, I:], acc)
@@ -418,6 +466,8 @@ def decoder_forward(model: Model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=F
         x, normed = add_rmsnorm(x, o, model.t[nxt], eps, acc=acc)
         if i in debug_layers:
             dbg[i] = x.copy()
+    if pairs is not None:
+        return readout(normed, model.t["readout"], pairs), kept, dbg
     logits = leaf_logits(x, leaves, model.t["final_norm"], leaf_ids, n_ids, ec, es, eb, eps, acc) if len(leaves) else None
     return logits, kept, dbg
 

@@ -13,7 +13,7 @@ async function main(req) {
       return Object.keys(host.dj.lib());
     case "pack": {
       const pk = host.packForest(req.trees);
-      return { ids: typed(pk.ids), pos: typed(pk.pos), rng: typed(pk.rng), leaves: typed(pk.leaves), leafIds: typed(pk.leafIds), nIds: pk.nIds, T: pk.T, L: pk.L };
+      return { ids: typed(pk.ids), pos: typed(pk.pos), rng: typed(pk.rng), taps: typed(pk.taps), leaves: typed(pk.leaves), leafIds: typed(pk.leafIds), nIds: pk.nIds, T: pk.T, L: pk.L };
     }
     case "groupmax":
       return host.groupMax(req.out, req.nIds, req.trees);
@@ -36,6 +36,31 @@ async function main(req) {
       e.freeState({ serial: req.free, free: () => undefined });
       const again = req.seq.find(([, st]) => st === req.free);
       return { keys, dropped, after: String(e.key(again[0], req.free)) };
+    }
+    case "d3": {
+      const d = await host.Decision.load(req.model, req.opts || {});
+      try {
+        const reqs = req.batch.map(([s, qs]) => [s, Object.values(qs)]);
+        const out = { kind: d.kind };
+        out.plain = await d.probabilitiesBatch(reqs);
+        d.shareState = true;
+        out.shared = await d.probabilitiesBatch(reqs);
+        return out;
+      } finally {
+        d.destroy();
+      }
+    }
+    case "logits": {
+      const e = await host.DecoderEngine.load(req.model, req.opts || {});
+      try {
+        return { logits: typed((await e.run(req.trees)).logits) };
+      } finally {
+        e.destroy();
+      }
+    }
+    case "packshared": {
+      const pk = host.packShared(req.seqs, req.groups === null ? undefined : req.groups);
+      return { ids: typed(pk.ids), pos: typed(pk.pos), rng: typed(pk.rng), pairs: typed(pk.pairs), T: pk.T, P: pk.P };
     }
     case "packenc": {
       const pk = host.packEncoder(req.seqs);

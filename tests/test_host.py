@@ -106,6 +106,7 @@ def test_engine_packing_and_helpers(pkg):
     assert np.array_equal(pk["ids"], ids) and np.array_equal(pk["meta"], meta) and np.array_equal(pk["leaves"], leaves)
     assert np.array_equal(pk["leaf_ids"], leaf_ids) and pk["n_ids"] == n_ids == 4
     assert np.array_equal(ref.ranges_mask(pk["rng"], pk["T"]), ref.forest_mask(meta))
+    assert np.array_equal(pk["taps"], ref.forest_taps(trees))  # the short conv's taps, bit for bit
     assert engine.common_prefix([[1, 2, 3], [1, 2, 4], [1, 2]]) == 1
     assert engine.common_prefix([[1, 2, 3, 4], [1, 2, 3, 5]]) == 3 and engine.common_prefix([[1, 2]]) == 0
     out = np.random.default_rng(5).standard_normal(4 * 4).astype(np.float32)
@@ -175,3 +176,69 @@ def test_synthetic_generator(pkg, tmp_path):
     assert synth.generate(cfg, p, norm_std=0.1) == p and os.path.getmtime(os.path.join(p, "weights.bin")) == mt  # cached
     a = synth.normal("x", (4,), seed=0)
     assert np.array_equal(a, synth.normal("x", (4,), seed=0)) and not np.array_equal(a, synth.normal("y", (4,), seed=0))
+
+
+def _d3_seqs(rng, groups):
+    """Requests whose questions share a state prefix (sometimes all of a question, sometimes nothing)."""
+    seqs = []
+    for n in groups:
+        state = [int(x) for x in rng.integers(0, 50, rng.integers(0, 12))]
+        for _ in range(n):
+            q = [int(x) for x in rng.integers(0, 50, rng.integers(1, 6))]
+            seqs.append({"ids": state + q, "options": int(rng.integers(1, 5))})
+    return seqs
+
+
+def test_shared_prefix_packing_matches_oracle_bit_exact(pkg):
+    """engine.pack_shared (the product path of D3Engine.logits's packing, d3-engine.ts:67-93) equals the oracle's
+    restatement bit for bit: ids, key ranges, (row, code) pairs, and positions = the oracle's meta positions;
+    ragged groups, one-question groups, identical questions (the prefix stops one token short), no groups."""
+    from decision_js_amd import engine
+    rng = np.random.default_rng(31)
+    cases = [[1, 3, 2], [4], [1, 1, 1], [2, 2]]
+    for groups in cases:
+        seqs = _d3_seqs(rng, groups)
+        if groups == [2, 2]:
+            seqs[1]["ids"] = list(seqs[0]["ids"])  # two identical questions: each keeps its last token
+        for g in (groups, None):
+            got = engine.pack_shared(seqs, g)
+            ids, meta, r, pairs = ref.pack_shared(seqs, g)
+            assert np.array_equal(got["ids"], ids) and np.array_equal(got["rng"], r)
+            assert np.array_equal(got["pos"], meta[:, 3]) and np.array_equal(got["pairs"], pairs)
+            assert got["T"] == len(ids) and got["P"] == len(pairs)
+    with pytest.raises(ValueError, match="groups cover"):
+        engine.pack_shared(_d3_seqs(rng, [2]), [3])
+
+
+class FakeD3:
+    """logits_d3 stand-in: code k of a sequence scores k * (its length) / 10; records the groups it was given."""
+
+    def __init__(self, temperature=2.0):
+        self.calls, self.m = [], {"config": {"temperature": temperature}}
+
+    def logits_d3(self, seqs, groups=None):
+        self.calls.append((len(seqs), groups))
+        return [[k * len(s["ids"]) / 10 for k in range(s["options"])] for s in seqs]
+
+    def destroy(self):
+        pass
+
+
+def test_run_d3_temperature_noul_and_groups(pkg):
+    """runD3 (d1.ts:150-169): one sequence per question (state ids then question ids) with its option count,
+    softmax at the model's temperature, a noul reversed to [yes, no]; share_state passes each request's question
+    count as its group; passes follow the token budget."""
+    from decision_js_amd import d1
+    eng = FakeD3()
+    D = d1.Decision("d3", eng, d1.IdPrompt(), 4096)
+    qs = _qs()
+    r = D.system_one([9] * 5, qs)
+    n = {"topic": 5 + 2, "churn": 5 + 1, "urgency": 5 + 3}
+    want_topic = ref.softmax([k * n["topic"] / 10 / 2.0 for k in range(3)])
+    assert abs(r["answers"]["topic"]["confidence"] - max(want_topic)) < 1e-12
+    churn = ref.softmax([0.0, n["churn"] / 10 / 2.0])
+    assert abs(r["answers"]["churn"]["noul"] - churn[1]) < 1e-12  # [false, true] reversed
+    assert eng.calls == [(3, None)]
+    D.share_state = True
+    D.probabilities_batch([([1, 2], list(qs.values())), ([3], list(qs.values())[:2])])
+    assert eng.calls[-1] == (5, [3, 2])

@@ -760,3 +760,33 @@ def test_errors_surface(pkg, ctx):
     rec.finish()
     with pytest.raises(dj.DJError, match="K must be a multiple of 32"):
         ctx.weight_q(np.zeros((4, 40), np.uint8), np.zeros((4, 1), np.float16), 4, 40, 8, dj.W_PLAIN)
+
+
+# ---------------------------------------------------------------- LFM2 short conv
+
+@pytest.mark.parametrize("H", [2048, 64, 1536])
+def test_short_conv(pkg, ctx, H):
+    """dj_short_conv against a float64 closed form of SHORT_CONV (kernels.ts:62-84) on forest taps (causal,
+    branches continuing their trunk), with taps of -1 and out of range (read as zero): within one f16 ulp of
+    the float64 value plus the f32 accumulation's error."""
+    rng = np.random.default_rng(H)
+    trees = [{"trunk": [0] * 40, "branches": [[0] * 9, [0] * 1, [0] * 17], "groups": []},
+             {"trunk": [], "branches": [[0] * 5], "groups": []}, {"trunk": [0] * 2, "branches": [], "groups": []}]
+    taps = ref.forest_taps(trees)
+    T = len(taps)
+    taps[3, 0] = T + 5  # out of range: reads zero
+    Z = rand_f16(rng, (T, 3 * H))
+    w = rand_f16(rng, (H, 3), 0.5)
+    dZ, dw, dT, dY = ctx.array(Z), ctx.array(w), ctx.array(taps), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.short_conv(T, H, dZ, dw, dT, dY))
+    got = dY.read(np.float16, (T, H))
+    t64 = taps.copy()
+    t64[3, 0] = -1
+    want = ref.short_conv(Z, H, w, t64, np.float64)
+    z = Z.astype(np.float64)
+    bu = np.abs(z[:, :H] * z[:, 2 * H:])
+    # f32 rounding of the three products and sums, on the magnitude of the terms
+    mag = np.abs(z[:, H:2 * H]) * sum(np.abs(w[:, j].astype(np.float64))[None, :] * np.where((t64[:, j] >= 0)[:, None], bu[t64[:, j]], 0) for j in range(3))
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert (err <= 2.0 ** -10 * np.abs(want.astype(np.float64)) + 4 * 2.0 ** -24 * mag + 1e-7).all()
+    assert not np.isnan(got.astype(np.float32)).any()

@@ -36,6 +36,8 @@ def models(pkg, tmp_path_factory):
         "q4": synth.reduced("qwen2.5-3b-q4", layers=2, vocab=4096),
         "shared": synth.reduced("d3lite-0.8b-q8", layers=2, vocab=4096),
         "enc": synth.reduced("eg2-encoder-q8", layers=2, vocab=4096),
+        "d3": synth.reduced("d3-attn-0.8b-q8", layers=2, vocab=4096),
+        "lfm2": synth.reduced("lfm2-d1-3b-q4", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
     }
     for k, cfg in specs.items():
         out[k] = synth.generate(cfg, str(root / k), seed=0, norm_std=0.1)
@@ -52,10 +54,11 @@ def _tree(rng, V, trunk, branches, n_opts=(2, 3, 5)):
             "branches": [[int(x) for x in rng.integers(0, V, b)] for b in branches], "groups": groups}
 
 
-def _oracle_forest(model, trees, debug=()):
+def _oracle_forest(model, trees, debug=(), taps=None):
     ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest(trees)
     mask = ref.ranges_mask(ref.forest_ranges(meta), len(ids))
-    logits, _, dbg = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64, debug_layers=debug)
+    logits, _, dbg = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64, debug_layers=debug,
+                                         taps=taps)
     scores = []
     leaf = 0
     for tr in trees:
@@ -359,5 +362,100 @@ def test_graph_cache_stays_bounded(pkg, models, monkeypatch):
             for t, w in zip(trees, want):
                 assert np.array_equal(eng.run([t])["logits"], w)
                 assert eng.ctx.graph_count() <= 8
+    finally:
+        eng.destroy()
+
+
+def _d3_requests(rng, V):
+    state = [int(x) for x in rng.integers(0, V, 150)]
+    other = [int(x) for x in rng.integers(0, V, 40)]
+    qs = [[int(x) for x in rng.integers(0, V, n)] for n in (20, 9, 31, 1, 14)]
+    seqs = [{"ids": state + q, "options": n} for q, n in zip(qs[:3], (2, 8, 5))]
+    seqs += [{"ids": other + q, "options": n} for q, n in zip(qs[3:], (3, 2))]
+    return seqs, [3, 2]
+
+
+def test_d3_readout_matches_oracle(pkg, models):
+    """d3's code readout on the product path (D3Engine.logits, d3-engine.ts:67-139): sequences packed with and
+    without each request's common prefix shared (pack_shared: noncausal key ranges, (row, code) pairs), every
+    layer on those ranges, the final norm, READOUT against the f32 code matrix: per-question probabilities within
+    1e-3 of the oracle's forward on the same ranges and pairs; eager, captured and replayed forwards identical."""
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models["d3"])
+    rng = np.random.default_rng(12)
+    seqs, groups = _d3_requests(rng, 4096)
+    eng = DecoderEngine.load(models["d3"])
+    try:
+        for g in (groups, None):
+            runs = [eng.logits_d3(seqs, g) for _ in range(3)]  # eager, capture, replay
+            assert runs[0] == runs[1] == runs[2]
+            ids, meta, r, pairs = ref.pack_shared(seqs, g)
+            want, _, _ = ref.decoder_forward(model, ids, meta[:, 3], ref.ranges_mask(r, len(ids)), [], None, 0,
+                                             acc=np.float64, pairs=pairs)
+            k = 0
+            for s, got in zip(seqs, runs[0]):
+                w = want[k:k + s["options"]]
+                k += s["options"]
+                assert len(got) == s["options"]
+                assert max(abs(a - b) for a, b in zip(ref.softmax(got), ref.softmax(w))) < PROB_TOL
+                assert np.abs(np.asarray(got) - w).max() < 2e-2 * max(1.0, np.abs(w).max())
+    finally:
+        eng.destroy()
+
+
+def test_decision_api_d3(pkg, models):
+    """The d3 kind through the Decision API (runD3, d1.ts:150-169): answers equal the oracle's (temperature
+    softmax, a noul reversed from [false, true]); share_state reads each request's state once."""
+    from decision_js_amd.d1 import Decision
+    rng = np.random.default_rng(13)
+    V = 4096
+    d = Decision.load(models["d3"])
+    try:
+        assert d.kind == "d3" and d.tokens_per_pass == 8192
+        state = [int(x) for x in rng.integers(0, V, 120)]
+        qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""},
+                        "ids": [int(x) for x in rng.integers(0, V, 12)]},
+              "churn": {"type": "noul", "instructions": "?", "ids": [int(x) for x in rng.integers(0, V, 7)]}}
+        model = ref.Model(models["d3"])
+        temp = model.c["temperature"]
+        for share in (False, True):
+            d.share_state = share
+            r = d.system_one(state, qs)
+            seqs = [{"ids": state + q["ids"], "options": 3 if q["type"] == "choice" else 2} for q in qs.values()]
+            ids, meta, rr, pairs = ref.pack_shared(seqs, [2] if share else None)
+            z, _, _ = ref.decoder_forward(model, ids, meta[:, 3], ref.ranges_mask(rr, len(ids)), [], None, 0,
+                                          acc=np.float64, pairs=pairs)
+            topic = ref.softmax(z[:3] / temp)
+            churn = ref.softmax(z[3:5] / temp)[::-1]
+            assert abs(r["answers"]["topic"]["confidence"] - max(topic)) < PROB_TOL
+            assert abs(r["answers"]["churn"]["noul"] - churn[0]) < PROB_TOL
+            assert r["usage"]["input_tokens"] == 2 * 120 + 12 + 7
+    finally:
+        d.destroy()
+
+
+def test_lfm2_conv_forest_matches_oracle(pkg, models):
+    """d1-3B's LFM2 form on the product path (D13BEngine.run, d1-3b-engine.ts:46-106): conv layers (in_proj,
+    dj_short_conv on the forest's taps, out_proj) between attention layers, trees with shared trunks and
+    branches: answer probabilities within 1e-3 of the oracle (whose conv layers are pinned against
+    transformers' Lfm2Model); final hidden states within 2e-2 relative L2; graph replay identical; a kept shared
+    state and d3's readout are refused for conv models."""
+    from decision_js_amd.engine import DecoderEngine
+    rng = np.random.default_rng(15)
+    V = 4096
+    trees = [_tree(rng, V, 70, [12, 1, 30]), _tree(rng, V, 0, [25]), _tree(rng, V, 2, [3, 3])]
+    model = ref.Model(models["lfm2"])
+    want, dbg = _oracle_forest(model, trees, debug=(2,), taps=ref.forest_taps(trees))
+    eng = DecoderEngine.load(models["lfm2"])
+    try:
+        runs = [eng.run(trees, debug_layers=(2,)) for _ in range(3)]
+        for r in runs[1:]:
+            assert r["scores"] == runs[0]["scores"]
+        for got_t, want_t in zip(runs[0]["scores"], want):
+            for g, w in zip(got_t, want_t):
+                assert max(abs(a - b) for a, b in zip(ref.softmax(g), ref.softmax(w))) < PROB_TOL
+        assert rel_l2(runs[0]["debug"][2], dbg[2]) < HIDDEN_TOL
+        with pytest.raises(ValueError, match="LFM2 conv layers"):
+            eng.prefill([1, 2, 3])
     finally:
         eng.destroy()

@@ -65,7 +65,7 @@ def test_packing_and_readout_match_python_host():
     js = node({"cmd": "pack", "trees": trees})
     py = engine.pack_forest(trees)
     assert js["T"] == py["T"] and js["L"] == py["L"] and js["nIds"] == py["n_ids"]
-    for k_js, k_py in [("ids", "ids"), ("pos", "pos"), ("rng", "rng"), ("leaves", "leaves"), ("leafIds", "leaf_ids")]:
+    for k_js, k_py in [("ids", "ids"), ("pos", "pos"), ("rng", "rng"), ("taps", "taps"), ("leaves", "leaves"), ("leafIds", "leaf_ids")]:
         assert np.array_equal(np.asarray(js[k_js]), np.asarray(py[k_py]).reshape(-1)), k_js
     out = rng.standard_normal(py["L"] * py["n_ids"]).astype(np.float32)
     got = node({"cmd": "groupmax", "out": [float(x) for x in out], "nIds": py["n_ids"], "trees": trees})
@@ -124,6 +124,22 @@ def test_encoder_packing_kinds_and_head_match_python_host():
     for got, (t, s, q, o) in zip(js, calls):
         want = head.logits(t, s, q, o)
         assert np.allclose(got, want, rtol=1e-5, atol=1e-6), (got, want)
+
+
+def test_shared_prefix_packing_matches_python_host():
+    """packShared (Node) == engine.pack_shared (Python) bit for bit, with and without groups."""
+    load_pkg()
+    from decision_js_amd import engine
+    import test_host
+    rng = np.random.default_rng(33)
+    for groups in ([2, 1, 3], [1, 1], [4]):
+        seqs = test_host._d3_seqs(rng, groups)
+        for g in (groups, None):
+            js = node({"cmd": "packshared", "seqs": seqs, "groups": g})
+            py = engine.pack_shared(seqs, g)
+            assert js["T"] == py["T"] and js["P"] == py["P"]
+            for k in ("ids", "pos", "rng", "pairs"):
+                assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), k
 
 
 def test_pass_splitting_matches_python_host():
@@ -314,3 +330,50 @@ def test_node_injected_fault_surfaces_and_next_call_succeeds(tmp_path):
     for got in (js["after"], js["again"]):
         for a, b in zip(got, want):
             assert np.allclose(a, b, rtol=0, atol=1e-12)
+
+
+@pytest.mark.gpu
+def test_node_d3_matches_python_host(tmp_path):
+    """The d3 kind through Node (kindOf -> runD3 -> logitsD3 -> READOUT) against the Python host: identical code
+    logits (the same packing, op sequence and library) with and without shareState."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    mdir = synth.generate(synth.reduced("d3-attn-0.8b-q8", layers=2, vocab=4096), str(tmp_path / "d3"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(14)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": "", "d": ""}, "ids": ids(16)},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(5)}}
+    batch = [[ids(90), qs], [ids(33), qs]]
+    js = node({"cmd": "d3", "model": mdir, "batch": batch}, timeout=300)
+    assert js["kind"] == "d3"
+    d = Decision.load(mdir)
+    try:
+        for share, key in ((False, "plain"), (True, "shared")):
+            d.share_state = share
+            py = d.probabilities_batch([(s, list(q.values())) for s, q in batch])
+            for a, b in zip(js[key], py):
+                for x, y in zip(a, b):
+                    assert np.allclose(x, y, rtol=0, atol=1e-12)
+    finally:
+        d.destroy()
+
+
+@pytest.mark.gpu
+def test_node_lfm2_matches_python_host(tmp_path):
+    """A model with LFM2 conv layers through the Node host (taps packed in packForest, dj_short_conv in the
+    layer loop) gives the Python host's logits bit for bit."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.engine import DecoderEngine
+    cfg = synth.reduced("lfm2-d1-3b-q4", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"])
+    mdir = synth.generate(cfg, str(tmp_path / "lfm2"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(16)
+    trees = _trees(rng, V=4096)
+    js = node({"cmd": "logits", "model": mdir, "trees": trees}, timeout=300)
+    eng = DecoderEngine.load(mdir)
+    try:
+        py = eng.run(trees)["logits"]
+    finally:
+        eng.destroy()
+    assert np.array_equal(np.asarray(js["logits"], dtype=np.float32), py)

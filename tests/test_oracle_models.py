@@ -430,3 +430,194 @@ def test_planted_encoder_rope_position_slip_is_caught(tiny_encoder, monkeypatch)
     monkeypatch.setattr(ref, "pack_encoder", slip)
     with pytest.raises(AssertionError):
         _compare_encoder(tiny_encoder)
+
+
+# ---------------------------------------------------------------- LFM2 short conv (d1-3B's conv layers)
+
+def _check_short_conv(fn=None):
+    """SHORT_CONV against an element-by-element float64 loop: y[t, c] = C[t, c] * sum_j w[c, j] * B[s_j, c] *
+    U[s_j, c] over the three taps s_j of token t (a tap < 0 contributes nothing), with Z = [B | C | U]."""
+    fn = fn or ref.short_conv
+    rng = np.random.default_rng(40)
+    T, H = 7, 16
+    Z = rng.standard_normal((T, 3 * H)).astype(np.float16)
+    w = rng.standard_normal((H, 3)).astype(np.float16)
+    taps = np.array([[-1, -1, 0, 0], [-1, 0, 1, 0], [0, 1, 2, 0], [1, 2, 3, 0], [-1, -1, 4, 0], [1, 2, 5, 0], [-1, 5, 6, 0]],
+                    np.int32)
+    got = fn(Z, H, w, taps, np.float64).astype(np.float64)
+    z = Z.astype(np.float64)
+    for t in range(T):
+        for c in range(H):
+            conv = sum(float(w[c, j]) * z[taps[t, j], c] * z[taps[t, j], 2 * H + c] for j in range(3) if taps[t, j] >= 0)
+            want = z[t, H + c] * conv
+            assert abs(got[t, c] - want) <= 2 ** -10 * abs(want) + 1e-6
+
+
+def test_short_conv_closed_form():
+    _check_short_conv()
+
+
+def test_planted_short_conv_slips_are_caught():
+    """Taps applied in reverse order, and C and U swapped in the [B | C | U] split."""
+    with pytest.raises(AssertionError):
+        _check_short_conv(lambda Z, H, w, taps, acc: ref.short_conv(Z, H, w[:, ::-1].copy(), taps, acc))
+
+    def swapped(Z, H, w, taps, acc):
+        Z2 = Z.copy()
+        Z2[:, H:2 * H], Z2[:, 2 * H:] = Z[:, 2 * H:], Z[:, H:2 * H]
+        return ref.short_conv(Z2, H, w, taps, acc)
+    with pytest.raises(AssertionError):
+        _check_short_conv(swapped)
+
+
+def _check_forest_taps(fn=None):
+    """Brute force: a token's taps are the packed rows of the two tokens before it and itself in its own
+    sequence (its tree's trunk, then its branch), -1 past the sequence's start."""
+    fn = fn or ref.forest_taps
+    rng = np.random.default_rng(41)
+    for _ in range(10):
+        trees = [{"trunk": [0] * int(rng.integers(0, 4)), "branches": [[0] * int(rng.integers(1, 4)) for _ in range(rng.integers(0, 3))],
+                  "groups": []} for _ in range(3)]
+        taps = fn(trees)
+        rows, off = [], 0
+        for tr in trees:
+            trunk = list(range(off, off + len(tr["trunk"])))
+            rows += [trunk[:i + 1] for i in range(len(trunk))]
+            off += len(trunk)
+            for br in tr["branches"]:
+                own = list(range(off, off + len(br)))
+                rows += [trunk + own[:o + 1] for o in range(len(br))]
+                off += len(br)
+        assert len(taps) == len(rows)
+        for t, seq in enumerate(rows):
+            want = ([-1, -1] + seq)[-3:]
+            assert list(taps[t, :3]) == want, (t, seq, taps[t])
+
+
+def test_forest_taps_brute_force():
+    _check_forest_taps()
+
+
+def test_planted_forest_taps_slip_is_caught():
+    """Branch taps that reach back into the previous branch (packed order) instead of the trunk."""
+    def slip(trees):
+        taps, n = [], 0
+        for tr in trees:
+            L = len(tr["trunk"]) + sum(len(b) for b in tr["branches"])
+            for i in range(L):
+                taps.append((n + i - 2 if i >= 2 else -1, n + i - 1 if i >= 1 else -1, n + i, 0))
+            n += L
+        return np.array(taps, dtype=np.int32).reshape(-1, 4)
+    with pytest.raises(AssertionError):
+        _check_forest_taps(slip)
+
+
+TINY_LFM2 = dict(layers=3, hidden=64, intermediate=96, heads=4, kv_heads=2, head_dim=16, vocab=512,
+                 layer_types=["conv", "full_attention", "conv"])
+
+
+@pytest.fixture(scope="module")
+def tiny_lfm2(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("lfm2")
+    return synth.generate(synth.reduced("lfm2-d1-3b-q4", **TINY_LFM2), str(d / "lfm2"), norm_std=0.1, std=0.125)
+
+
+def _hf_lfm2(model: ref.Model):
+    """A transformers Lfm2Model holding the oracle model's f16 weights (float64)."""
+    tr = pytest.importorskip("transformers")
+    c = model.c
+    H, I, h, kv = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"]
+    cfg = tr.Lfm2Config(vocab_size=c["vocab"], hidden_size=H, intermediate_size=I, num_hidden_layers=c["layers"],
+                        num_attention_heads=h, num_key_value_heads=kv, norm_eps=c["eps"], rope_theta=c["rope_theta"],
+                        layer_types=c["layer_types"], conv_L_cache=3, conv_bias=False, block_auto_adjust_ff_dim=False,
+                        max_position_embeddings=4096, tie_word_embeddings=True)
+    m = tr.Lfm2Model(cfg)
+    m.config._attn_implementation = "eager"
+    m = m.to(torch.float64).eval()
+    sd = {"embed_tokens.weight": _t(model.w16("embed")), "embedding_norm.weight": _t(model.t["final_norm"])}
+    D = c["head_dim"]
+    for i, t in enumerate(c["layer_types"]):
+        p = f"layers.{i}."
+        w13 = model.w16(p + "w13")
+        sd[p + "feed_forward.w1.weight"] = _t(w13[:I])
+        sd[p + "feed_forward.w3.weight"] = _t(w13[I:])
+        sd[p + "feed_forward.w2.weight"] = _t(model.w16(p + "w2"))
+        sd[p + "operator_norm.weight"] = _t(model.t[p + "operator_norm"])
+        sd[p + "ffn_norm.weight"] = _t(model.t[p + "ffn_norm"])
+        if t == "conv":
+            sd[p + "conv.in_proj.weight"] = _t(model.w16(p + "in_proj"))
+            sd[p + "conv.out_proj.weight"] = _t(model.w16(p + "out_proj"))
+            sd[p + "conv.conv.weight"] = _t(model.t[p + "conv"]).reshape(H, 1, 3)
+        else:
+            qkv = model.w16(p + "qkv")
+            sd[p + "self_attn.q_proj.weight"] = _t(qkv[:h * D])
+            sd[p + "self_attn.k_proj.weight"] = _t(qkv[h * D:(h + kv) * D])
+            sd[p + "self_attn.v_proj.weight"] = _t(qkv[(h + kv) * D:])
+            sd[p + "self_attn.out_proj.weight"] = _t(model.w16(p + "o_proj"))
+            sd[p + "self_attn.q_layernorm.weight"] = _t(model.t[p + "q_norm"])
+            sd[p + "self_attn.k_layernorm.weight"] = _t(model.t[p + "k_norm"])
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    return m
+
+
+def _compare_lfm2(path, model=None):
+    """The oracle's forest forward with conv layers (forest taps) against Lfm2Model on each trunk + branch
+    alone: the final normed hidden state within 5e-3 relative L2 and the answer logits within 5e-3 of scale."""
+    model = model or ref.Model(path)
+    c = model.c
+    rng = np.random.default_rng(42)
+    tree = _forest(rng, c["vocab"])
+    ids, pos, meta, leaves, leaf_ids, n_ids = ref.pack_forest([tree])
+    mask = ref.ranges_mask(ref.forest_ranges(meta), len(ids))
+    logits, _, dbg = ref.decoder_forward(model, ids, pos, mask, leaves, leaf_ids, n_ids, acc=np.float64,
+                                         debug_layers=(c["layers"] - 1,), taps=ref.forest_taps([tree]))
+    hf = _hf_lfm2(ref.Model(path))
+    ec, es, eb = model.t["embed"]
+    E32 = ref.dequant_f32(ec, es, eb).astype(np.float64)
+    P, off = len(tree["trunk"]), len(tree["trunk"])
+    for b, br in enumerate(tree["branches"]):
+        rows = list(range(P)) + list(range(off, off + len(br)))
+        off += len(br)
+        with torch.no_grad():
+            final = hf(input_ids=torch.tensor([tree["trunk"] + br])).last_hidden_state[0].numpy()
+        x = dbg[c["layers"] - 1][rows].astype(np.float64)
+        normed = x / np.sqrt((x * x).mean(-1, keepdims=True) + c["eps"]) * model.t["final_norm"].astype(np.float64)
+        assert _rel_l2(normed, final) < 5e-3, f"branch {b}: final hidden state"
+        want = final[-1] @ E32[leaf_ids[b * n_ids:(b + 1) * n_ids]].T
+        got = logits[b * n_ids:(b + 1) * n_ids].astype(np.float64)
+        assert np.abs(got - want).max() < 5e-3 * np.abs(want).max(), f"branch {b}: answer logits"
+
+
+def test_lfm2_forward_matches_transformers(tiny_lfm2):
+    _compare_lfm2(tiny_lfm2)
+
+
+def test_planted_lfm2_tap_order_slip_is_caught(tiny_lfm2):
+    def flip(m):
+        m.t["layers.0.conv"] = np.ascontiguousarray(m.t["layers.0.conv"].reshape(-1, 3)[:, ::-1])
+    model = ref.Model(tiny_lfm2)
+    flip(model)
+    with pytest.raises(AssertionError):
+        _compare_lfm2(tiny_lfm2, model)
+
+
+def test_planted_lfm2_branch_taps_slip_is_caught(tiny_lfm2, monkeypatch):
+    """Branch tokens whose conv taps restart at the branch (the trunk not continued)."""
+    orig = ref.forest_taps
+
+    def slip(trees):
+        taps = orig(trees).copy()
+        P = len(trees[0]["trunk"])
+        off = P
+        for br in trees[0]["branches"]:
+            for o in range(len(br)):
+                for j in (1, 2):
+                    if o - j < 0:
+                        taps[off + o, 2 - j] = -1
+            off += len(br)
+        return taps
+    monkeypatch.setattr(ref, "forest_taps", slip)
+    with pytest.raises(AssertionError):
+        _compare_lfm2(tiny_lfm2)
