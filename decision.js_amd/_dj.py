@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libdj.so")
 
 DJ_OK, DJ_EINVAL, DJ_EHIP, DJ_ENOMEM, DJ_ESTATE, DJ_EINJECT = range(6)
 W_PLAIN, W_MFMA, W_MFMA_GLU = 0, 1, 2
+BIAS_NONE, BIAS_RELU, BIAS_GELU_ERF = 0, 1, 2
 W_DIRECT = 16  # flag: f16 weights dequantized once at load (the reference's directWeights)
 ACT_SILU, ACT_GELU_TANH = 0, 1
 ROPE_POW_NEG, ROPE_INV_POW = 0, 1
@@ -78,6 +79,11 @@ SIGNATURES = {
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
     "dj_readout": [_P, _I, _I, _I, _P, _P, _I, _P, _P],
     "dj_short_conv": [_P, _I, _I, _P, _P, _P, _P],
+    "dj_add_rows": [_P, _I, _I, _P, _P, _P, _I, _P],
+    "dj_bias_act": [_P, _I, _I, _P, _P, _I],
+    "dj_add_layernorm": [_P, _I, _I, _I, _F, _P, _P, _P, _P, _P],
+    "dj_gather_rows": [_P, _I, _I, _I, _P, _P, _P],
+    "dj_score": [_P, _I, _I, _P, _P, _P, _P],
     "dj_mean_pool": [_P, _I, _I, _I, _P, _P, _P],
     "dj_dense_f32": [_P, _I, _P, _P, _P],
 }
@@ -307,6 +313,21 @@ class Recorder:
 
     def leaf_logits(self, T, L, H, nIds, eps, X, leaves, w, ids, embed: Weight, out):
         check(lib().dj_leaf_logits(self.h, T, L, H, nIds, eps, ptr(X), ptr(leaves), ptr(w), ptr(ids), embed.h, ptr(out)))
+
+    def add_rows(self, T, H, Xi, idx, E, rows, Xo):
+        check(lib().dj_add_rows(self.h, T, H, ptr(Xi), ptr(idx), ptr(E), rows, ptr(Xo)))
+
+    def bias_act(self, T, N, Y, b, act=0):
+        check(lib().dj_bias_act(self.h, T, N, ptr(Y), ptr(b), act))
+
+    def add_layernorm(self, T, H, add, eps, X, Y, w, b, O):
+        check(lib().dj_add_layernorm(self.h, T, H, 1 if add else 0, eps, ptr(X), ptr(Y), ptr(w), ptr(b), ptr(O)))
+
+    def gather_rows(self, M, H, T, X, rows, G):
+        check(lib().dj_gather_rows(self.h, M, H, T, ptr(X), ptr(rows), ptr(G)))
+
+    def score(self, M, H, Y, w, b, out):
+        check(lib().dj_score(self.h, M, H, ptr(Y), ptr(w), ptr(b), ptr(out)))
 
     def short_conv(self, T, H, Z, w, taps, Y):
         check(lib().dj_short_conv(self.h, T, H, ptr(Z), ptr(w), ptr(taps), ptr(Y)))

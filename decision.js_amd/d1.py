@@ -6,8 +6,12 @@ object turns states and questions into token ids. The default, IdPrompt, takes t
   state:     a list of token ids
   question:  the reference's question dict plus "ids" (its token ids) and "options" (one token-id group per
              option, [yes, no] for a noul: each option scores its best token, d1-3b-engine.ts:112-121);
-             for the encoder, "option_ids" (one token-id list per option text)
+             for EmbeddingGemma 2, "option_ids" (one token-id list per option text, in the model's order: a
+             noul as [no, yes], eg2-prompt.ts:27-33); for d1-omni, "markers" (the position of each option's
+             marker within the question's ids, in the model's order: a noul as [false, true],
+             omni-prompt.ts:18-27)
 """
+import json
 import threading
 
 import numpy as np
@@ -16,6 +20,7 @@ from . import questions as Q
 from .eg2_head import Eg2Head
 from .encoder import EncoderEngine, cosine_logits
 from .engine import DecoderEngine
+from .omni import OmniEngine, temperature as omni_temperature
 
 
 def _on_progress(opts):
@@ -51,10 +56,42 @@ class IdPrompt:
     def texts(self, state, q):
         return self.trunk(state), self.branch(q), [[int(t) for t in o] for o in q["option_ids"]]
 
+    def sequence(self, state, q):
+        """d1-omni's sequence of one question over one state (omni-prompt.ts:33-51 on ids): the state's ids, then
+        the question's; its markers shifted past the state."""
+        trunk, ids = self.trunk(state), self.branch(q)
+        markers = [int(m) for m in q["markers"]]
+        if len(markers) != Q.n_options(q):
+            raise Q.QuestionError(f"decision.js: {len(markers)} markers for a {q['type']} with {Q.n_options(q)} options")
+        if any(not 0 <= m < len(ids) for m in markers):
+            raise Q.QuestionError("decision.js: a marker outside the question's ids")
+        return {"ids": trunk + ids, "markers": [len(trunk) + m for m in markers], "type": q["type"]}
+
+
+def criterion(v):
+    """The legend text of a score level for every kind but d1-3b (omni-prompt.ts:16: the text, else Python's
+    json.dumps of it)."""
+    return v if isinstance(v, str) else json.dumps(v, ensure_ascii=False)
+
+
+def _kind(config):
+    """The reference's ModelKind of a manifest (d1.ts:63-64)."""
+    model = config.get("model")
+    if model == "laya":
+        return "laya"
+    if model in ("eg2-encoder", "eg2"):
+        return "eg2"
+    if model == "d3":
+        return "d3"
+    if model in ("decoder", "d1-3b") or "head_layers" not in config:
+        return "d1-3b"
+    return "d1-omni"
+
 
 class Decision:
     """D1 (d1.ts:38-227): a model and the serial queue of its calls. `kind` is the reference's ModelKind
-    (d1.ts:17): "d1-3b" for the causal decoders (run as d1-3B's forest), "eg2" for the encoder."""
+    (d1.ts:17): "d1-3b" for the causal decoders (run as d1-3B's forest), "d3" for the code readout, "d1-omni"
+    for the marker-head encoder, "eg2" for EmbeddingGemma 2."""
 
     def __init__(self, kind, engine, prompt, tokens_per_pass, share_state=False, workflow=""):
         self.kind, self.engine, self.prompt = kind, engine, prompt
@@ -73,15 +110,11 @@ class Decision:
         (LoadOptions.directWeights, gpu.ts:20). The kind comes from manifest.config.model (d1.ts:63-64)."""
         opts = dict(opts or {})
         from .fmt import load_manifest
-        model = load_manifest(base if base.endswith("/") else base + "/")["config"].get("model")
-        if model in ("decoder", "d1-3b"):
-            kind, engine = "d1-3b", DecoderEngine.load(base, opts)
-        elif model == "d3":
-            kind, engine = "d3", DecoderEngine.load(base, opts)
-        elif model in ("eg2-encoder", "eg2"):
-            kind, engine = "eg2", EncoderEngine.load(base, opts)
-        else:
-            raise ValueError(f"decision.js: unknown model kind {model!r}")
+        config = load_manifest(base if base.endswith("/") else base + "/")["config"]
+        kind = _kind(config)
+        if kind == "laya":
+            raise ValueError("decision.js: Laya (ModernBERT) models do not run on this build")
+        engine = {"d1-3b": DecoderEngine, "d3": DecoderEngine, "eg2": EncoderEngine, "d1-omni": OmniEngine}[kind].load(base, opts)
         # the reference's defaults (d1.ts:78): 4096 tokens per pass for d1-3B, 8192 otherwise; pass a larger
         # tokens_per_pass to pack more requests into one forward (MI355X activations take ~25 KB per token)
         tpp = opts.get("tokens_per_pass") or opts.get("tokensPerPass") or (4096 if kind == "d1-3b" else 8192)
@@ -95,10 +128,11 @@ class Decision:
     def system_one_batch(self, requests, opts=None):
         """Many (state, {name: question}) requests packed into as few forwards as fit; opts: BatchOptions."""
         done = self._run([(s, list(qs.values())) for s, qs in requests], _on_progress(opts))
+        legend = str if self.kind == "d1-3b" else criterion  # d1.ts:91
         out = []
         for (s, qs), d in zip(requests, done):
             names = list(qs.keys())
-            out.append({"answers": {n: Q.answer(qs[n], d["probs"][j]) for j, n in enumerate(names)},
+            out.append({"answers": {n: Q.answer(qs[n], d["probs"][j], legend) for j, n in enumerate(names)},
                         "usage": {"input_tokens": d["tokens"], "output_tokens": 0}})
         return out
 
@@ -124,6 +158,8 @@ class Decision:
                 return self._run_shared(requests, on_progress) if self.share_state else self._run_decoder(requests, on_progress)
             if self.kind == "d3":
                 return self._run_d3(requests, on_progress)
+            if self.kind == "d1-omni":
+                return self._run_omni(requests, on_progress)
             return self._run_encoder(requests, on_progress)
 
     def _passes(self, sizes):
@@ -173,6 +209,30 @@ class Decision:
                 for q in requests[r][1]:
                     pr = softmax(np.asarray(logits[k], dtype=np.float64) / temp)
                     probs.append(pr[::-1] if q.get("type") == "noul" else pr)
+                    k += 1
+                out[r]["probs"] = probs
+            if on_progress:
+                on_progress(j, len(requests))
+        return out
+
+    def _run_omni(self, requests, on_progress):
+        """runEncoder (d1.ts:121-147) for d1-omni: one sequence per question (the state read anew for each),
+        whole requests per pass up to the token budget; each question's marker logits divided by its
+        temperature (omni-prompt.ts temperatureKey: type and option-count bucket), softmax, a noul read as
+        [false, true] and reversed to [yes, no]."""
+        seqs = [[self.prompt.sequence(s, q) for q in qs] for s, qs in requests]
+        sizes = [sum(len(x["ids"]) for x in g) for g in seqs]
+        c = self.engine.m["config"]
+        out = [{"probs": [], "tokens": n} for n in sizes]
+        for i, j in self._passes(sizes):
+            logits = self.engine.logits([x for g in seqs[i:j] for x in g])["logits"]
+            k = 0
+            for r in range(i, j):
+                probs = []
+                for q in requests[r][1]:
+                    t = omni_temperature(c, q["type"], Q.n_options(q))
+                    pr = softmax(np.asarray(logits[k], dtype=np.float64) / t)
+                    probs.append(pr[::-1] if q["type"] == "noul" else pr)
                     k += 1
                 out[r]["probs"] = probs
             if on_progress:
@@ -235,7 +295,8 @@ class Decision:
                 else:  # the cosine prior alone (the configured dense head has no learned scorer)
                     z = cosine_logits(emb(st)[1], emb(qi)[1], [emb(o)[1] for o in opts])
                 t = float(temps.get(q["type"], 1.0))
-                probs.append(softmax(np.asarray(z, dtype=np.float64) / t))
+                pr = softmax(np.asarray(z, dtype=np.float64) / t)
+                probs.append(pr[::-1] if q["type"] == "noul" else pr)  # the model reads a noul as [no, yes]
             out.append({"probs": probs, "tokens": tokens[r]})
         return out
 

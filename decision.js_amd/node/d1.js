@@ -7,9 +7,13 @@
  * Text-to-ids is upstream of the scoring path: `prompt` turns states and questions into token ids. The
  * default takes them already tokenized — a state is a list of ids; a question is the reference's question
  * plus `ids` (its tokens) and `options` (one token-id group per option, [yes, no] for a noul; each option
- * scores its best token, d1-3b-engine.ts:112-121). */
+ * scores its best token, d1-3b-engine.ts:112-121); for EmbeddingGemma 2, `option_ids` (one token-id list per
+ * option text, in the model's order: a noul as [no, yes], eg2-prompt.ts:27-33); for d1-omni, `markers` (each
+ * option's marker position within the question's ids, in the model's order: a noul as [false, true]). */
 const { DecoderEngine } = require("./engine");
 const { EncoderEngine, cosineLogits } = require("./encoder");
+const { OmniEngine, temperature: omniTemperature } = require("./omni");
+const { criterion } = require("./py");
 const { Eg2Head } = require("./eg2_head");
 const { fileFetch } = require("./format");
 const Q = require("./questions");
@@ -31,19 +35,27 @@ const idPrompt = {
   },
   // the encoder: state, question and each option are texts of their own (eg2-prompt.ts renders them)
   texts: (state, q) => [Array.from(state.ids || state, Number), Array.from(q.ids, Number), q.option_ids.map((o) => Array.from(o, Number))],
+  // d1-omni: one sequence per question over its state (omni-prompt.ts:33-51 on ids), markers shifted past the state
+  sequence: (state, q) => {
+    const trunk = Array.from(state.ids || state, Number), ids = Array.from(q.ids, Number), markers = Array.from(q.markers, Number);
+    if (markers.length !== Q.nOptions(q)) throw new Q.QuestionError(`decision.js: ${markers.length} markers for a ${q.type} with ${Q.nOptions(q)} options`);
+    if (markers.some((m) => !(m >= 0 && m < ids.length))) throw new Q.QuestionError("decision.js: a marker outside the question's ids");
+    return { ids: trunk.concat(ids), markers: markers.map((m) => trunk.length + m), type: q.type };
+  },
 };
 
 /** BatchOptions (d1.ts:33-35): {onProgress(done, total)}; a bare function is taken as that callback. */
 const onProgressOf = (opts) => (typeof opts === "function" ? opts : opts && opts.onProgress);
 
-/** The reference's ModelKind (d1.ts:17, 63-64) for a manifest: "eg2" for the encoder, else "d1-3b" (a causal
- * decoder without marker heads, run as d1-3B's forest). */
+/** The reference's ModelKind (d1.ts:17, 63-64) for a manifest: laya, d3, eg2 by name; d1-3b for a causal
+ * decoder without marker heads (run as d1-3B's forest); else d1-omni. */
 function kindOf(config) {
   const model = config && config.model;
+  if (model === "laya") return "laya";
   if (model === "eg2" || model === "eg2-encoder") return "eg2";
   if (model === "d3") return "d3";
   if (model === "decoder" || model === "d1-3b" || !("head_layers" in (config || {}))) return "d1-3b";
-  throw new Error(`decision.js: unsupported model kind ${model}`);
+  return "d1-omni";
 }
 
 class D1 {
@@ -57,7 +69,9 @@ class D1 {
     opts.fetch = opts.fetch || fileFetch();
     const manifest = await (await opts.fetch(`${base}manifest.json`)).json();
     const kind = kindOf(manifest.config);
-    const engine = kind === "eg2" ? await EncoderEngine.load(base, opts) : await DecoderEngine.load(base, opts);
+    if (kind === "laya") throw new Error("decision.js: Laya (ModernBERT) models do not run on this build");
+    const engine = kind === "eg2" ? await EncoderEngine.load(base, opts) : kind === "d1-omni" ? await OmniEngine.load(base, opts)
+      : await DecoderEngine.load(base, opts);
     return new D1(kind, engine, opts);
   }
 
@@ -82,9 +96,10 @@ class D1 {
   systemOneBatch(requests, opts = {}) {
     return this.enqueue(async () => {
       const done = await this.runAll(requests.map(([s, qs]) => [s, Object.values(qs)]), onProgressOf(opts));
+      const legend = this.kind === "d1-3b" ? String : criterion; // d1.ts:91
       return requests.map(([, qs], r) => {
         const names = Object.keys(qs), answers = {};
-        names.forEach((n, j) => (answers[n] = Q.answer(qs[n], done[r].probs[j])));
+        names.forEach((n, j) => (answers[n] = Q.answer(qs[n], done[r].probs[j], legend)));
         return { answers, usage: { input_tokens: done[r].tokens, output_tokens: 0 } };
       });
     });
@@ -114,6 +129,7 @@ class D1 {
     for (const [, qs] of requests) qs.forEach(Q.checkQuestion);
     if (this.kind === "eg2") return this.runEg2(requests, onProgress);
     if (this.kind === "d3") return this.runD3(requests, onProgress);
+    if (this.kind === "d1-omni") return this.runOmni(requests, onProgress);
     return this.shareState ? this.runShared(requests, onProgress) : this.runDecoder(requests, onProgress);
   }
 
@@ -191,6 +207,29 @@ class D1 {
     return out;
   }
 
+  /** runEncoder (d1.ts:121-147) for d1-omni: one sequence per question (the state read anew for each), whole
+   * requests per pass up to the token budget; marker logits over the question's temperature (type and
+   * option-count bucket), softmax, a noul read as [false, true] and reversed to [yes, no]. */
+  async runOmni(requests, onProgress) {
+    const p = this.prompt, c = this.engine.m.config;
+    const seqs = requests.map(([s, qs]) => qs.map((q) => p.sequence(s, q)));
+    const sizes = seqs.map((g) => g.reduce((a, x) => a + x.ids.length, 0));
+    const out = sizes.map((n) => ({ probs: [], tokens: n }));
+    for (const [i, j] of this.passes(sizes)) {
+      const { logits } = await this.engine.logits([].concat(...seqs.slice(i, j)));
+      let k = 0;
+      for (let r = i; r < j; ++r) {
+        out[r].probs = requests[r][1].map((q) => {
+          const t = omniTemperature(c, q.type, Q.nOptions(q));
+          const pr = softmax(logits[k++].map((v) => v / t));
+          return q.type === "noul" ? pr.reverse() : pr;
+        });
+      }
+      if (onProgress) onProgress(j, requests.length);
+    }
+    return out;
+  }
+
   /** runEg2 (d1.ts:172-204): every distinct text (state, question, option) embedded once and cached, in passes
    * of at most tokensPerPass tokens; then the head on the host — the learned decision head when the model has
    * one (eg2-head.ts), else the cosine prior — and a softmax at the type's temperature. */
@@ -223,7 +262,8 @@ class D1 {
         const z = this.eg2Head ? this.eg2Head.logits(q.type, emb(st), emb(qi), opts.map(emb))
           : cosineLogits(emb(st)[1], emb(qi)[1], opts.map((o) => emb(o)[1]));
         const tau = temps[q.type] === undefined ? 1 : temps[q.type];
-        return softmax(z.map((v) => v / tau));
+        const pr = softmax(z.map((v) => v / tau));
+        return q.type === "noul" ? pr.reverse() : pr; // the model reads a noul as [no, yes]
       }),
       tokens: tokens[r],
     }));

@@ -135,6 +135,11 @@ class Recorder {
   meanPool(T, S, H, X, seqs, out) { lib().meanPool(this.h, T, S, H, X, seqs, out); }
   readout(T, P, H, X, R, codes, pairs, out) { lib().readout(this.h, T, P, H, X, R, codes, pairs, out); }
   shortConv(T, H, Z, w, taps, Y) { lib().shortConv(this.h, T, H, Z, w, taps, Y); }
+  addRows(T, H, Xi, idx, E, rows, Xo) { lib().addRows(this.h, T, H, Xi, idx, E, rows, Xo); }
+  biasAct(T, N, Y, b, act = 0) { lib().biasAct(this.h, T, N, Y, b, act); }
+  addLayernorm(T, H, add, eps, X, Y, w, b, O) { lib().addLayernorm(this.h, T, H, add ? 1 : 0, eps, X, Y, w, b, O); }
+  gatherRows(M, H, T, X, rows, G) { lib().gatherRows(this.h, M, H, T, X, rows, G); }
+  score(M, H, Y, w, b, out) { lib().score(this.h, M, H, Y, w, b, out); }
   denseF32(M, inp, w, out) { lib().denseF32(this.h, M, inp, w.h, out); }
   leafLogits(T, L, H, nIds, eps, X, leaves, w, ids, embed, out) {
     lib().leafLogits(this.h, T, L, H, nIds, eps, X, leaves, w, ids, embed.h, out);

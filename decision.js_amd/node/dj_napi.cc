@@ -478,6 +478,31 @@ napi_value LeafLogits(napi_env env, napi_callback_info info) {
   BEGIN(12);
   END(dj_leaf_logits(R(0), I(1), I(2), I(3), I(4), F(5), P16(6), PU32(7), P16(8), PU32(9), W(10), PF32(11)));
 }
+napi_value AddRows(napi_env env, napi_callback_info info) {
+  BEGIN(8);
+  END(dj_add_rows(R(0), I(1), I(2), P16(3), PU32(4), P16(5), I(6), P16(7)));
+}
+
+napi_value BiasAct(napi_env env, napi_callback_info info) {
+  BEGIN(6);
+  END(dj_bias_act(R(0), I(1), I(2), P16(3), P16(4), I(5)));
+}
+
+napi_value AddLayernorm(napi_env env, napi_callback_info info) {
+  BEGIN(10);
+  END(dj_add_layernorm(R(0), I(1), I(2), I(3), F(4), P16(5), P16(6), P16(7), P16(8), P16(9)));
+}
+
+napi_value GatherRows(napi_env env, napi_callback_info info) {
+  BEGIN(7);
+  END(dj_gather_rows(R(0), I(1), I(2), I(3), P16(4), PU32(5), P16(6)));
+}
+
+napi_value Score(napi_env env, napi_callback_info info) {
+  BEGIN(7);
+  END(dj_score(R(0), I(1), I(2), P16(3), P16(4), P16(5), PF32(6)));
+}
+
 napi_value ShortConv(napi_env env, napi_callback_info info) {
   BEGIN(7);
   END(dj_short_conv(R(0), I(1), I(2), P16(3), P16(4), PI32(5), P16(6)));
@@ -511,7 +536,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
       {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
-      {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
+      {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"addRows", AddRows}, {"biasAct", BiasAct},
+      {"addLayernorm", AddLayernorm}, {"gatherRows", GatherRows}, {"score", Score}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
   };
   for (const auto &f : fns) {
     napi_value v;
@@ -523,7 +549,8 @@ napi_value Module(napi_env env, napi_value exports) {
     int value;
   } consts[] = {{"W_PLAIN", DJ_W_PLAIN}, {"W_MFMA", DJ_W_MFMA}, {"W_MFMA_GLU", DJ_W_MFMA_GLU},
                 {"W_DIRECT", DJ_W_DIRECT}, {"ACT_SILU", DJ_ACT_SILU}, {"ACT_GELU_TANH", DJ_ACT_GELU_TANH},
-                {"ROPE_POW_NEG", DJ_ROPE_POW_NEG}, {"ROPE_INV_POW", DJ_ROPE_INV_POW}, {"ABI_VERSION", DJ_ABI_VERSION}};
+                {"ROPE_POW_NEG", DJ_ROPE_POW_NEG}, {"ROPE_INV_POW", DJ_ROPE_INV_POW},
+                {"BIAS_NONE", DJ_BIAS_NONE}, {"BIAS_RELU", DJ_BIAS_RELU}, {"BIAS_GELU_ERF", DJ_BIAS_GELU_ERF}, {"ABI_VERSION", DJ_ABI_VERSION}};
   for (const auto &k : consts) napi_set_named_property(env, exports, k.name, number(env, k.value));
   return exports;
 }

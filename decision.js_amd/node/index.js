@@ -4,12 +4,13 @@
 const { D1, Decision, softmax } = require("./d1");
 const { DecoderEngine, packForest, packShared, groupMax } = require("./engine");
 const { EncoderEngine, packEncoder } = require("./encoder");
+const { OmniEngine, packOmni } = require("./omni");
 const { Eg2Head } = require("./eg2_head");
 const { loadWeights, fileFetch } = require("./format");
 const questions = require("./questions");
 const dj = require("./dj");
 
 module.exports = {
-  D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, Eg2Head,
-  packForest, packShared, packEncoder, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+  D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, OmniEngine,
+  Eg2Head, packForest, packShared, packEncoder, packOmni, groupMax, loadWeights, fileFetch, softmax, questions, dj,
 };

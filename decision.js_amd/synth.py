@@ -46,6 +46,20 @@ CONFIGS = {
                           layer_types=["full_attention" if i % 3 == 2 else "conv" for i in range(30)],
                           choices={"norm_weights": 1.0, "layer_types": "attention every third layer (not stated)",
                                    "intermediate": "8192 (not stated)", "vocab": "65536 (not stated)"}),
+    # d1-omni's form (D1OmniEngine, omni-engine.ts; export-omni.py): a bidirectional LFM2 trunk shaped like
+    # LFM2-350M (its published q8 size, 405 MB with the head, fits this shape) and the marker head. Not a BASELINE
+    # config: the layer pattern, widths, head sizes and temperatures are choices.
+    "d1-omni-q8": dict(model="d1-omni", bits=8, layers=16, hidden=1024, intermediate=4608, heads=16, kv_heads=8,
+                       head_dim=64, vocab=65536, eps=1e-5, rope_theta=1e6, qk_norm=True,
+                       layer_types=["conv", "conv", "full_attention", "conv", "conv", "full_attention", "conv", "conv",
+                                    "full_attention", "conv", "full_attention", "conv", "full_attention", "conv",
+                                    "full_attention", "conv"],
+                       head_layers=2, head_heads=16, head_ff=4096, ln_eps=1e-5, max_length=16384,
+                       temperatures={"choice": 1.1, "score": 0.9, "noul": 1.2, "choice:2": 1.05, "choice:3-5": 1.15,
+                                     "score:6-10": 0.8, "noul:2": 1.25},
+                       choices={"norm_weights": 1.0, "layer_types": "LFM2-350M's pattern (not stated)",
+                                "head": "2 layers, 16 heads, ff 4096 (not stated)", "biases": "N(0, 0.1)",
+                                "type_emb": "N(0, 0.5)", "temperatures": "synthetic"}),
     # EmbeddingGemma-shaped bidirectional encoder, q8, mean-pool + 768->3072->768 head
     "eg2-encoder-q8": dict(model="encoder", bits=8, layers=24, hidden=768, intermediate=1152, heads=3, kv_heads=1,
                            head_dim=256, vocab=262144, eps=1e-6, rope_theta=1e4, head_width=3072, embed_dim=768,
@@ -81,7 +95,7 @@ def tensor_plan(cfg: dict):
     """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
     H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
     plan = [("embed", "q", (V, H))]
-    if cfg["model"] in ("decoder", "d3", "d1-3b"):
+    if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
         plan.append(("final_norm", "n", (H,)))
         types = cfg.get("layer_types") or ["full_attention"] * L
         for i in range(L):
@@ -96,6 +110,19 @@ def tensor_plan(cfg: dict):
                 plan += [(p + "q_norm", "n", (D,)), (p + "k_norm", "n", (D,))]
         if cfg["model"] == "d3":
             plan.append(("readout", "r", (len(cfg["codes"]), H)))  # f32 code matrix (d3-kernels.ts:242-260)
+        if cfg["model"] == "d1-omni":  # the decision head and scorer (export-omni.py:70-90)
+            F = cfg["head_ff"]
+            plan.append(("head.type_emb", "e", (3, H)))
+            for i in range(cfg["head_layers"]):
+                p = f"head.{i}."
+                plan += [(p + "in_proj", "q", (3 * H, H)), (p + "in_proj_bias", "b", (3 * H,)),
+                         (p + "out_proj", "q", (H, H)), (p + "out_proj_bias", "b", (H,)),
+                         (p + "linear1", "q", (F, H)), (p + "linear1_bias", "b", (F,)),
+                         (p + "linear2", "q", (H, F)), (p + "linear2_bias", "b", (H,))]
+                for nm in ("norm1", "norm2"):
+                    plan += [(p + nm, "n", (H,)), (p + nm + "_bias", "b", (H,))]
+            plan += [("scorer.norm", "n", (H,)), ("scorer.norm_bias", "b", (H,)), ("scorer.fc", "q", (H, H)),
+                     ("scorer.fc_bias", "b", (H,)), ("scorer.out", "v", (H,)), ("scorer.out_bias", "s", (2,))]
     else:
         for i in range(L):
             p = f"layers.{i}."
@@ -126,7 +153,7 @@ def head_plan(cfg: dict):
 def manifest_config(cfg: dict) -> dict:
     c = {k: v for k, v in cfg.items() if k not in ("bits",)}
     c["layer_types"] = list(cfg.get("layer_types") or ["full_attention"] * cfg["layers"])
-    if cfg["model"] in ("decoder", "d3", "d1-3b"):
+    if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
         c["model"] = cfg["model"]
     else:
         c["model"] = "eg2-encoder"
@@ -151,6 +178,14 @@ def _make(cfg, name, kind, shape, seed, norm_std, std):
         return name, kind, normal(name, shape, std, seed), None
     if kind == "c":  # f16 conv taps, N(0, 0.5): each tap moves its channel by about as much as the others
         return name, kind, normal(name, shape, 0.5, seed), None
+    if kind == "b":  # f16 biases, N(0, 0.1)
+        return name, kind, normal(name, shape, 0.1, seed), None
+    if kind == "e":  # the f16 question-type rows, N(0, 0.5): each type moves the head's input visibly
+        return name, kind, normal(name, shape, 0.5, seed), None
+    if kind == "v":  # an f16 weight row (the scorer's last Linear(H, 1)), N(0, std)
+        return name, kind, normal(name, shape, std, seed), None
+    if kind == "s":  # the scorer's bias and a zero half (export-omni.py:90: one aligned word)
+        return name, kind, np.array([normal(name, (1,), 0.1, seed)[0], 0.0], dtype=np.float32), None
     w = normal(name, shape, std, seed)
     if name == "embed" and cfg["model"] == "encoder":
         w = w * np.float32(math.sqrt(cfg["hidden"]))  # Gemma's sqrt(hidden) embedding scale, folded in
@@ -179,7 +214,7 @@ def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads:
         futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std, std) for n, k, s in plan]
         for (name, kind, shape), fut in zip(plan, futs):
             _, _, a, b = fut.result()
-            if kind in ("n", "c"):
+            if kind in ("n", "c", "b", "e", "v", "s"):
                 blob.f16(name, a)
             elif kind == "r":
                 blob.f32(name, a)

@@ -250,6 +250,25 @@ int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z_dev, int st
 int dj_short_conv(dj_rec *rec, int T, int H, const uint16_t *Z_dev, const uint16_t *w_dev, const int32_t *taps_dev,
                   uint16_t *Y_dev);
 
+/* ---------------------------------------------------------------- ops: d1-omni's decision head (kernels.ts:186-283) */
+
+/* Xo[t, :] = f16(f32(Xi[t, :]) + f32(E[idx[t], :])) for E f16 [rows, H] (the question-type embedding); idx past
+ * the table reads its last row. H % 8 == 0. Replaces ADD_ROWS (kernels.ts:188-201). */
+int dj_add_rows(dj_rec *rec, int T, int H, const uint16_t *Xi_dev, const uint32_t *idx_dev, const uint16_t *E_dev,
+                int rows, uint16_t *Xo_dev);
+enum { DJ_BIAS_NONE = 0, DJ_BIAS_RELU = 1, DJ_BIAS_GELU_ERF = 2 };
+/* Y[t, n] = f16(act(f32(Y[t, n]) + f32(b[n]))) in place, act none / ReLU / GELU with the Abramowitz & Stegun
+ * 7.1.26 erf. N % 8 == 0. Replaces BIAS_ACT (kernels.ts:203-222). */
+int dj_bias_act(dj_rec *rec, int T, int N, uint16_t *Y_dev, const uint16_t *b_dev, int act);
+/* Per row: if add, X += Y (stored f16); O = f16((f32(X) - mean) / sqrt(max(E[x^2] - mean^2, 0) + eps) * w + b)
+ * with the mean and E[x^2] of the unrounded sum. H % 8 == 0. Replaces ADD_LAYERNORM (kernels.ts:224-255). */
+int dj_add_layernorm(dj_rec *rec, int T, int H, int add, float eps, uint16_t *X_dev, const uint16_t *Y_dev,
+                     const uint16_t *w_dev, const uint16_t *b_dev, uint16_t *O_dev);
+/* G[m, :] = X[rows[m], :] for m < M (rows clamped to [0, T)). Replaces GATHER_ROWS (kernels.ts:257-267). */
+int dj_gather_rows(dj_rec *rec, int M, int H, int T, const uint16_t *X_dev, const uint32_t *rows_dev, uint16_t *G_dev);
+/* out[m] = Y[m, :] . w + b[0] in f32 (the scorer's last Linear(H, 1)). Replaces SCORE (kernels.ts:269-283). */
+int dj_score(dj_rec *rec, int M, int H, const uint16_t *Y_dev, const uint16_t *w_dev, const uint16_t *b_dev, float *out_dev);
+
 /* ---------------------------------------------------------------- ops: readouts and pooling */
 
 /* out[l * nIds + j] = rmsnorm_f32(X[leaves[l]]) * w  .  dequant_f32(embed row ids[l * nIds + j]) in f32:

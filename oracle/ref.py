@@ -368,6 +368,130 @@ def dense_f32(inp, codes, scales, bits):
     return (inp.astype(F32) @ dequant_f32(codes, scales, bits).T).astype(F32)
 
 
+# ---------------------------------------------------------------- d1-omni's decision head (kernels.ts:186-283)
+
+def add_rows(X, idx, E, acc=F32):
+    """ADD_ROWS (kernels.ts:188-201): f16(f32(X[t]) + f32(E[idx[t]])) (idx past the table: its last row)."""
+    idx = np.minimum(np.asarray(idx, dtype=np.int64), E.shape[0] - 1)
+    return (X.astype(acc) + E[idx].astype(acc)).astype(F16)
+
+
+def erf_as(x):
+    """erf of BIAS_ACT (kernels.ts:208-212): Abramowitz & Stegun 7.1.26, |error| < 1.5e-7."""
+    x = np.asarray(x)
+    t = 1.0 / (1.0 + 0.3275911 * np.abs(x))
+    y = 1.0 - ((((1.061405429 * t - 1.453152027) * t + 1.421413741) * t - 0.284496736) * t + 0.254829592) * t * np.exp(-x * x)
+    return np.where(x >= 0, y, -y)
+
+
+def bias_act(Y, b, act=0, acc=F32):
+    """BIAS_ACT (kernels.ts:203-222): f16(act(f32(Y) + f32(b))), act 0 none, 1 ReLU, 2 GELU with erf_as."""
+    v = Y.astype(acc) + b.astype(acc)
+    if act == 1:
+        v = np.maximum(v, acc(0))
+    elif act == 2:
+        v = acc(0.5) * v * (acc(1) + erf_as(v * acc(0.70710678)).astype(acc))
+    return v.astype(F16)
+
+
+def add_layernorm(X, Y, w, b, eps, add=True, acc=F32):
+    """ADD_LAYERNORM (kernels.ts:224-255): v = X (+ Y), X <- f16(v); mean and E[v^2] of the unrounded v;
+    var = max(E[v^2] - mean^2, 0); O = f16((f32(X_f16) - mean) / sqrt(var + eps) * w + b). Returns (X_new, O)."""
+    v = X.astype(acc)
+    if add:
+        v = v + Y.astype(acc)
+    H = X.shape[-1]
+    mean = v.sum(-1, keepdims=True, dtype=acc) / acc(H)
+    var = np.maximum((v * v).sum(-1, keepdims=True, dtype=acc) / acc(H) - mean * mean, acc(0))
+    Xn = v.astype(F16)
+    inv = (1.0 / np.sqrt(var + eps)).astype(acc)
+    return Xn, ((Xn.astype(acc) - mean) * inv * w.astype(acc) + b.astype(acc)).astype(F16)
+
+
+def score(Y, w, b, acc=F32):
+    """SCORE (kernels.ts:269-283): out[m] = Y[m] . w + b[0], f32."""
+    return ((Y.astype(acc) @ w.astype(acc)) + acc(b[0])).astype(F32)
+
+
+def pack_omni(seqs):
+    """D1OmniEngine.logits's packing (omni-engine.ts:62-75): per token its id, its position in its sequence, its
+    question type (choice 0, score 1, noul 2), the centred taps (t-1, t, t+1; -1 past either end of the
+    sequence) and its key range [start, end) (bidirectional within the sequence); per option marker its row.
+    seqs: [{"ids", "markers", "type"}]."""
+    QT = {"choice": 0, "score": 1, "noul": 2}
+    ids, pos, qtype, taps, rng, markers = [], [], [], [], [], []
+    for s in seqs:
+        start, end = len(ids), len(ids) + len(s["ids"])
+        for i, tok in enumerate(s["ids"]):
+            t = start + i
+            ids.append(tok); pos.append(i); qtype.append(QT[s["type"]])
+            taps.append((t - 1 if t > start else -1, t, t + 1 if t + 1 < end else -1, 0))
+            rng.append((start, end, 0, 0))
+        markers.extend(start + m for m in s["markers"])
+    return {"ids": np.array(ids, dtype=np.uint32), "pos": np.array(pos, dtype=np.uint32),
+            "qtype": np.array(qtype, dtype=np.uint32), "taps": np.array(taps, dtype=np.int32).reshape(-1, 4),
+            "rng": np.array(rng, dtype=np.int32).reshape(-1, 4), "markers": np.array(markers, dtype=np.uint32), "T": len(ids)}
+
+
+def omni_temperature(temps, qtype, options):
+    """temperature() of omni-engine.ts:22-26 (prompt.py temperature_key): "<type>:<bucket>" with buckets 2,
+    3-5, 6-10, 11+, else "<type>", else 1."""
+    k = "2" if options <= 2 else "3-5" if options <= 5 else "6-10" if options <= 10 else "11+"
+    return float(temps.get(f"{qtype}:{k}", temps.get(qtype, 1.0)))
+
+
+def omni_forward(model: "Model", seqs, acc=F32, layers=None):
+    """D1OmniEngine.logits (omni-engine.ts:55-149): the bidirectional LFM2 trunk (conv layers on the centred
+    taps, attention layers with q/k norm + RoPE over the whole sequence, SwiGLU, final norm), then the head:
+    the question-type row added, `head_layers` pre-norm transformer layers (LayerNorm with bias, fused
+    in_proj + bias, attention over the sequence at scale 1/sqrt(D), out_proj + bias, LayerNorm, linear1 + bias
+    + ReLU, linear2 + bias), the last residual with the scorer's LayerNorm, then at each marker Linear + bias +
+    GELU (erf) and Linear(H, 1). Returns (marker logits f32 [M], {"trunk": f16 [T, H], "head": f16 [T, H]})."""
+    c = model.c
+    H, I, h, kv, D, eps = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
+    types = c["layer_types"]
+    L = len(types) if layers is None else layers
+    pk = pack_omni(seqs)
+    T = pk["T"]
+    mask = ranges_mask(pk["rng"], T)
+    ec, es, eb = model.t["embed"]
+    x = gather(pk["ids"], ec, es, eb)
+    x, normed = add_rmsnorm(x, None, model.t["layers.0.operator_norm"], eps, add=False, acc=acc)
+    for i in range(L):
+        p = f"layers.{i}."
+        if types[i] == "conv":
+            z = matmul(normed, model.w16(p + "in_proj"), acc)
+            o = matmul(short_conv(z, H, model.t[p + "conv"], pk["taps"], acc), model.w16(p + "out_proj"), acc)
+        else:
+            z = matmul(normed, model.w16(p + "qkv"), acc)
+            z = qk_norm_rope(z, h, kv, D, pk["pos"], model.t[p + "q_norm"], model.t[p + "k_norm"], False, eps,
+                             c["rope_theta"], acc=acc)
+            o = matmul(attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc), model.w16(p + "o_proj"), acc)
+        x, normed = add_rmsnorm(x, o, model.t[p + "ffn_norm"], eps, acc=acc)
+        ab = matmul(normed, model.w16(p + "w13"), acc)
+        o = matmul(silu_mul(ab[:, :I], ab[:, I:], acc), model.w16(p + "w2"), acc)
+        nxt = f"layers.{i + 1}.operator_norm" if i + 1 < L else "final_norm"
+        x, normed = add_rmsnorm(x, o, model.t[nxt], eps, acc=acc)
+    trunk = normed
+    hh, ln = c["head_heads"], c["ln_eps"]
+    Dh = H // hh
+    x = add_rows(trunk, pk["qtype"], model.t["head.type_emb"], acc)
+    o = None
+    for i in range(c["head_layers"]):
+        p = f"head.{i}."
+        x, n1 = add_layernorm(x, o, model.t[p + "norm1"], model.t[p + "norm1_bias"], ln, add=i > 0, acc=acc)
+        z = bias_act(matmul(n1, model.w16(p + "in_proj"), acc), model.t[p + "in_proj_bias"], 0, acc)
+        y = attention(z, hh, hh, Dh, mask, 1.0 / math.sqrt(Dh), acc)
+        o = bias_act(matmul(y, model.w16(p + "out_proj"), acc), model.t[p + "out_proj_bias"], 0, acc)
+        x, n2 = add_layernorm(x, o, model.t[p + "norm2"], model.t[p + "norm2_bias"], ln, acc=acc)
+        f = bias_act(matmul(n2, model.w16(p + "linear1"), acc), model.t[p + "linear1_bias"], 1, acc)
+        o = bias_act(matmul(f, model.w16(p + "linear2"), acc), model.t[p + "linear2_bias"], 0, acc)
+    x, sn = add_layernorm(x, o, model.t["scorer.norm"], model.t["scorer.norm_bias"], ln, add=o is not None, acc=acc)
+    g = sn[pk["markers"].astype(np.int64)]
+    gf = bias_act(matmul(g, model.w16("scorer.fc"), acc), model.t["scorer.fc_bias"], 2, acc)
+    return score(gf, model.t["scorer.out"], model.t["scorer.out_bias"], acc), {"trunk": trunk, "head": x}
+
+
 # ---------------------------------------------------------------- host tail (gpu.ts, d1.ts, questions.ts)
 
 def softmax(s):

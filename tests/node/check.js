@@ -62,6 +62,23 @@ async function main(req) {
       const pk = host.packShared(req.seqs, req.groups === null ? undefined : req.groups);
       return { ids: typed(pk.ids), pos: typed(pk.pos), rng: typed(pk.rng), pairs: typed(pk.pairs), T: pk.T, P: pk.P };
     }
+    case "packomni": {
+      const pk = host.packOmni(req.seqs);
+      const out = { T: pk.T, M: pk.M };
+      for (const k of ["ids", "pos", "qtype", "taps", "rng", "markers"]) out[k] = typed(pk[k]);
+      return out;
+    }
+    case "omni": {
+      const d = await host.Decision.load(req.model, req.opts || {});
+      try {
+        const out = { kind: d.kind };
+        out.batch = await d.systemOneBatch(req.batch);
+        out.logits = (await d.engine.logits(req.seqs)).logits;
+        return out;
+      } finally {
+        d.destroy();
+      }
+    }
     case "packenc": {
       const pk = host.packEncoder(req.seqs);
       return { ids: typed(pk.ids), meta: typed(pk.meta), full: typed(pk.full), ranges: typed(pk.ranges), T: pk.T, S: pk.S };

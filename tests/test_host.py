@@ -242,3 +242,110 @@ def test_run_d3_temperature_noul_and_groups(pkg):
     D.share_state = True
     D.probabilities_batch([([1, 2], list(qs.values())), ([3], list(qs.values())[:2])])
     assert eng.calls[-1] == (5, [3, 2])
+
+
+def _omni_seqs(rng, n):
+    types = ["choice", "noul", "score"]
+    out = []
+    for k in range(n):
+        L = int(rng.integers(1, 12))
+        out.append({"ids": [int(x) for x in rng.integers(0, 50, L)], "type": types[k % 3],
+                    "markers": sorted(int(x) for x in rng.choice(L, min(L, int(rng.integers(1, 4))), replace=False))})
+    return out
+
+
+def test_omni_packing_matches_oracle_bit_exact(pkg):
+    """omni.pack_omni (the product path of D1OmniEngine.logits's packing, omni-engine.ts:62-75) equals the
+    oracle's restatement bit for bit: ids, positions, question types, centred taps that never cross a sequence
+    (one-token sequences read only themselves), key ranges, marker rows; a marker past its sequence is refused."""
+    from decision_js_amd import omni
+    rng = np.random.default_rng(8)
+    for n in (1, 2, 5, 9):
+        seqs = _omni_seqs(rng, n)
+        got, want = omni.pack_omni(seqs), ref.pack_omni(seqs)
+        for k in ("ids", "pos", "qtype", "taps", "rng", "markers"):
+            assert got[k].dtype == want[k].dtype and np.array_equal(got[k], want[k]), k
+        assert got["T"] == want["T"] and got["M"] == len(want["markers"])
+    one = omni.pack_omni([{"ids": [7], "markers": [0], "type": "noul"}])
+    assert one["taps"].tolist() == [[-1, 0, -1, 0]] and one["qtype"].tolist() == [2]
+    with pytest.raises(ValueError, match="marker outside"):
+        omni.pack_omni([{"ids": [1, 2], "markers": [2], "type": "choice"}])
+
+
+def test_omni_temperature_keys(pkg):
+    """temperature() of omni-engine.ts:22-26: the type:bucket key, else the type, else 1."""
+    from decision_js_amd import omni
+    c = {"temperatures": {"choice": 1.1, "choice:2": 1.05, "choice:3-5": 1.15, "score:6-10": 0.8, "noul": 1.2}}
+    assert omni.temperature(c, "choice", 2) == 1.05 and omni.temperature(c, "choice", 5) == 1.15
+    assert omni.temperature(c, "choice", 6) == 1.1 and omni.temperature(c, "score", 10) == 0.8
+    assert omni.temperature(c, "score", 11) == 1.0 and omni.temperature(c, "noul", 2) == 1.2
+    for k in (2, 3, 5, 6, 10, 11):
+        assert omni.temperature(c, "choice", k) == ref.omni_temperature(c["temperatures"], "choice", k)
+
+
+class FakeOmni:
+    """OmniEngine.logits stand-in: marker j of a sequence scores j * (its length) / 10; records each pass."""
+
+    def __init__(self, temps):
+        self.calls, self.m = [], {"config": {"temperatures": temps}}
+
+    def logits(self, seqs):
+        self.calls.append([len(s["ids"]) for s in seqs])
+        return {"logits": [[j * len(s["ids"]) / 10 for j in range(len(s["markers"]))] for s in seqs]}
+
+    def destroy(self):
+        pass
+
+
+def test_run_omni_sequences_temperatures_and_noul(pkg):
+    """runEncoder (d1.ts:121-147) for d1-omni: one sequence per question (state ids then question ids, markers
+    shifted past the state), the temperature of the question's type and option-count bucket, a noul reversed
+    from [false, true]; score legends rendered as omni's criterion (the text, else json.dumps); whole requests
+    per pass up to the token budget; markers that do not match the options are refused."""
+    from decision_js_amd import d1
+    temps = {"choice:3-5": 2.0, "noul": 0.5, "score": 4.0}
+    eng = FakeOmni(temps)
+    D = d1.Decision("d1-omni", eng, d1.IdPrompt(), 30)
+    qs = _qs()
+    qs["topic"]["markers"] = [0, 1, 1]
+    qs["churn"]["markers"] = [0, 0]
+    qs["urgency"]["markers"] = [0, 1, 2]
+    qs["urgency"]["criteria"] = ["low", {"x": 1.5}, 3]
+    r = D.system_one([9] * 5, qs)
+    n = {"topic": 7, "churn": 6, "urgency": 8}
+    assert eng.calls == [[7, 6, 8]]
+    assert abs(r["answers"]["topic"]["confidence"] - max(ref.softmax([j * 7 / 10 / 2.0 for j in range(3)]))) < 1e-12
+    churn = ref.softmax([0.0, n["churn"] / 10 / 0.5])
+    assert abs(r["answers"]["churn"]["noul"] - churn[1]) < 1e-12  # [false, true] reversed to [yes, no]
+    assert r["answers"]["urgency"]["legend"] == {"0": "low", "1": '{"x": 1.5}', "2": "3"}
+    assert r["usage"]["input_tokens"] == 21
+    D.probabilities_batch([([1] * 10, list(qs.values())), ([2] * 3, list(qs.values()))])
+    assert eng.calls[1:] == [[12, 11, 13], [5, 4, 6]]  # 36 tokens, then 15: one request per pass at 30
+    bad = dict(qs["topic"], markers=[0, 1])
+    with pytest.raises(d1.Q.QuestionError, match="2 markers for a choice with 3 options"):
+        D.probabilities([1], [bad])
+
+
+class FakeEncoder:
+    """EncoderEngine stand-in for runEg2: the embedding of a text is its one-hot on its first id's axis."""
+
+    def __init__(self):
+        self.m, self.host = {"config": {"temperatures": {"noul": 1.0}}}, {}
+
+    def embed(self, texts):
+        e = np.zeros((len(texts), 8), np.float32)
+        for k, t in enumerate(texts):
+            e[k, t[0] % 8] = 1.0
+        return {"embeddings": e}
+
+
+def test_run_eg2_reverses_noul(pkg):
+    """runEg2 (d1.ts:196-198): a noul's option texts are listed [no, yes] and its probabilities reversed to
+    [yes, no]: with "yes" the option nearest to state + question, P(yes) is the larger."""
+    from decision_js_amd import d1
+    D = d1.Decision("eg2", FakeEncoder(), d1.IdPrompt(), 4096)
+    q = {"type": "noul", "instructions": "?", "ids": [1], "option_ids": [[5], [1]]}  # no: axis 5, yes: axis 1
+    p = D.probabilities([1], [q])[0]
+    assert p[0] > p[1]
+    r = D.system_one([1], {"q": q})
+    assert r["answers"]["q"]["noul"] == p[0]

@@ -790,3 +790,83 @@ def test_short_conv(pkg, ctx, H):
     err = np.abs(got.astype(np.float64) - want.astype(np.float64))
     assert (err <= 2.0 ** -10 * np.abs(want.astype(np.float64)) + 4 * 2.0 ** -24 * mag + 1e-7).all()
     assert not np.isnan(got.astype(np.float32)).any()
+
+
+# ---------------------------------------------------------------- d1-omni's decision head ops
+
+def test_add_rows_bit_exact(pkg, ctx):
+    """dj_add_rows against ADD_ROWS (kernels.ts:188-201): f16(f32 + f32) is exactly rounded, so bit for bit; a
+    type index past the table reads its last row."""
+    rng = np.random.default_rng(51)
+    T, H = 301, 1024
+    X, E = rand_f16(rng, (T, H)), rand_f16(rng, (3, H), 0.5)
+    idx = rng.integers(0, 3, T).astype(np.uint32)
+    idx[:2] = [7, 2]
+    dX, di, dE, dO = ctx.array(X), ctx.array(idx), ctx.array(E), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.add_rows(T, H, dX, di, dE, 3, dO))
+    assert np.array_equal(dO.read(np.uint16, (T, H)), ref.add_rows(X, idx, E).view(np.uint16))
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_bias_act(pkg, ctx, act):
+    """dj_bias_act against BIAS_ACT (kernels.ts:203-222): no activation and ReLU bit for bit; GELU with the A&S
+    erf within one f16 rounding of the float64 value (the erf's exp is libm's, not numpy's)."""
+    rng = np.random.default_rng(60 + act)
+    T, N = 77, 3072
+    Y, b = rand_f16(rng, (T, N), 2.0), rand_f16(rng, (N,), 0.5)
+    dY, db = ctx.array(Y), ctx.array(b)
+    run(ctx, lambda r: r.bias_act(T, N, dY, db, act))
+    got = dY.read(np.float16, (T, N))
+    if act < 2:
+        assert np.array_equal(got.view(np.uint16), ref.bias_act(Y, b, act).view(np.uint16))
+    else:
+        want = ref.bias_act(Y, b, 2, np.float64)
+        assert f16_close(got, want, ulps=1.0, atol=2e-7) <= 1.0
+
+
+@pytest.mark.parametrize("H,add", [(1024, True), (1024, False), (2048, True), (768, True)])
+def test_add_layernorm(pkg, ctx, H, add):
+    """dj_add_layernorm against ADD_LAYERNORM (kernels.ts:224-255): the stored sum bit for bit; the normalised
+    output within one f16 ulp of the float64 value (rows with a large mean included: E[x^2] - mean^2)."""
+    rng = np.random.default_rng(H + 7 * add)
+    T = 131
+    X, Y = rand_f16(rng, (T, H)), rand_f16(rng, (T, H))
+    X[:5] += np.float16(6.0)
+    w = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    b = rand_f16(rng, (H,), 0.1)
+    dX, dY, dw, db, dO = ctx.array(X), ctx.array(Y), ctx.array(w), ctx.array(b), ctx.alloc(T * H * 2)
+    run(ctx, lambda r: r.add_layernorm(T, H, add, 1e-5, dX, dY, dw, db, dO))
+    Xn, O = ref.add_layernorm(X, Y, w, b, 1e-5, add=add, acc=np.float64)
+    assert np.array_equal(dX.read(np.uint16, (T, H)), Xn.view(np.uint16))
+    assert f16_close(dO.read(np.float16, (T, H)), O, ulps=1.0, atol=1e-4) <= 1.0
+
+
+def test_gather_rows_and_score(pkg, ctx):
+    """dj_gather_rows (GATHER_ROWS, kernels.ts:257-267) bit for bit, rows past T clamped; dj_score (SCORE,
+    kernels.ts:269-283) within f32 accumulation error of the float64 dot product plus the bias."""
+    rng = np.random.default_rng(71)
+    T, H, M = 500, 1024, 37
+    X = rand_f16(rng, (T, H))
+    rows = rng.integers(0, T, M).astype(np.uint32)
+    rows[0] = T + 3
+    w, b = rand_f16(rng, (H,), 0.05), np.array([0.3, 0.0], dtype=np.float16)
+    dX, dr, dG, dw, db, dout = ctx.array(X), ctx.array(rows), ctx.alloc(M * H * 2), ctx.array(w), ctx.array(b), ctx.alloc(M * 4)
+    run(ctx, lambda r: (r.gather_rows(M, H, T, dX, dr, dG), r.score(M, H, dG, dw, db, dout)))
+    G = dG.read(np.float16, (M, H))
+    assert np.array_equal(G.view(np.uint16), X[np.minimum(rows, T - 1)].view(np.uint16))
+    want = ref.score(G, w, b, np.float64)
+    mag = np.abs(G.astype(np.float64)) @ np.abs(w.astype(np.float64))
+    assert (np.abs(dout.read(np.float32, (M,)) - want) <= 2.0 ** -18 * (mag + 0.3) + 1e-6).all()
+
+
+def test_head_ops_refuse_bad_shapes(pkg, ctx):
+    dj = _dj()
+    buf = ctx.alloc(4096)
+    rec = ctx.recorder()
+    try:
+        with pytest.raises(dj.DJError, match="multiple of 8"):
+            rec.add_layernorm(2, 100, True, 1e-5, buf, buf, buf, buf, buf)
+        with pytest.raises(dj.DJError, match="act 0..2"):
+            rec.bias_act(2, 64, buf, buf, 3)
+    finally:
+        rec.abort()

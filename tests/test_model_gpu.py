@@ -38,6 +38,7 @@ def models(pkg, tmp_path_factory):
         "enc": synth.reduced("eg2-encoder-q8", layers=2, vocab=4096),
         "d3": synth.reduced("d3-attn-0.8b-q8", layers=2, vocab=4096),
         "lfm2": synth.reduced("lfm2-d1-3b-q4", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
+        "omni": synth.reduced("d1-omni-q8", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
     }
     for k, cfg in specs.items():
         out[k] = synth.generate(cfg, str(root / k), seed=0, norm_std=0.1)
@@ -459,3 +460,84 @@ def test_lfm2_conv_forest_matches_oracle(pkg, models):
             eng.prefill([1, 2, 3])
     finally:
         eng.destroy()
+
+
+def _omni_requests(rng, V):
+    """Ragged d1-omni sequences: every question type, one-token and marker-at-either-end cases."""
+    out = []
+    for n, markers, t in ((180, [40, 90, 150], "choice"), (1, [0, 0], "noul"), (57, [0, 56], "noul"),
+                          (333, [10, 20, 30, 40, 50, 300], "score"), (24, [3, 7, 11, 15, 19], "choice")):
+        out.append({"ids": [int(x) for x in rng.integers(0, V, n)], "markers": markers, "type": t})
+    return out
+
+
+def test_omni_matches_oracle(pkg, models):
+    """d1-omni on the product path (D1OmniEngine.logits, omni-engine.ts:55-149): the bidirectional LFM2 trunk on
+    centred taps and whole-sequence ranges, the head (type rows, pre-norm layers with biases, ReLU FFN) and the
+    marker scorer, several sequences packed: the trunk output and the head's stream within 2e-2 relative L2 of
+    the oracle, each question's calibrated probabilities within 1e-3; eager, captured and replayed forwards
+    identical; a sequence's logits do not depend on what it is packed with (to rounding)."""
+    from decision_js_amd.omni import OmniEngine, temperature
+    model = ref.Model(models["omni"])
+    rng = np.random.default_rng(21)
+    seqs = _omni_requests(rng, 4096)
+    eng = OmniEngine.load(models["omni"])
+    try:
+        runs = [eng.logits(seqs) for _ in range(3)]  # eager, capture, replay
+        assert runs[0]["logits"] == runs[1]["logits"] == runs[2]["logits"]
+        dbg = eng.logits(seqs, debug=True)
+        assert dbg["logits"] == runs[0]["logits"]
+        want, wdbg = ref.omni_forward(model, seqs, acc=np.float64)
+        assert rel_l2(dbg["debug"]["trunk"], wdbg["trunk"]) < HIDDEN_TOL
+        assert rel_l2(dbg["debug"]["head"], wdbg["head"]) < HIDDEN_TOL
+        k = 0
+        for s, got in zip(seqs, runs[0]["logits"]):
+            w = want[k:k + len(s["markers"])]
+            k += len(s["markers"])
+            t = temperature(model.c, s["type"], len(w))
+            assert max(abs(a - b) for a, b in zip(ref.softmax(np.asarray(got) / t), ref.softmax(w / t))) < PROB_TOL
+            assert np.abs(np.asarray(got) - w).max() < 2e-2 * max(1.0, np.abs(w).max())
+        alone = eng.logits([seqs[2]])["logits"][0]
+        assert max(abs(a - b) for a, b in zip(ref.softmax(alone), ref.softmax(runs[0]["logits"][2]))) < INVARIANCE_TOL
+    finally:
+        eng.destroy()
+
+
+def test_decision_api_omni(pkg, models):
+    """The d1-omni kind through the Decision API (runEncoder, d1.ts:121-147): answers equal the oracle's
+    (the temperature of the question's type and option-count bucket, a noul reversed from [false, true]), usage
+    counts every question's sequence, passes follow the token budget."""
+    from decision_js_amd.d1 import Decision
+    from decision_js_amd.omni import temperature
+    rng = np.random.default_rng(23)
+    V = 4096
+    model = ref.Model(models["omni"])
+    d = Decision.load(models["omni"], {"tokens_per_pass": 300})
+    try:
+        assert d.kind == "d1-omni"
+        ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+        qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(20),
+                        "markers": [2, 9, 15]},
+              "churn": {"type": "noul", "instructions": "?", "ids": ids(8), "markers": [1, 5]},
+              "urgency": {"type": "score", "instructions": "?", "criteria": ["l", "m", "h", "x"], "ids": ids(14),
+                          "markers": [1, 4, 7, 10]}}
+        states = [ids(150), ids(40)]
+        seen = []
+        got = d.system_one_batch([(s, qs) for s in states], {"on_progress": lambda a, b: seen.append((a, b))})
+        assert seen == [(1, 2), (2, 2)]  # 3 * 150 + 42 tokens > 300: one request per pass
+        for s, r in zip(states, got):
+            assert r["usage"]["input_tokens"] == 3 * len(s) + 42
+            seqs = [{"ids": s + q["ids"], "markers": [len(s) + m for m in q["markers"]], "type": q["type"]} for q in qs.values()]
+            want, _ = ref.omni_forward(model, seqs, acc=np.float64)
+            k = 0
+            for (name, q), sq in zip(qs.items(), seqs):
+                z = want[k:k + len(sq["markers"])]
+                k += len(sq["markers"])
+                p = ref.softmax(z / temperature(model.c, q["type"], len(z)))
+                a = r["answers"][name]
+                if q["type"] == "noul":
+                    assert abs(a["noul"] - p[1]) < PROB_TOL  # [false, true] reversed to [yes, no]
+                else:
+                    assert abs(a["confidence"] - p.max()) < PROB_TOL
+    finally:
+        d.destroy()

@@ -107,9 +107,13 @@ def test_encoder_packing_kinds_and_head_match_python_host():
     assert js["T"] == py["T"] and js["S"] == py["S"]
     for k in ("ids", "meta", "full", "ranges"):
         assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), k
-    kinds = node({"cmd": "kinds", "configs": [{"model": "decoder"}, {"model": "d1-3b"}, {"model": "eg2-encoder"},
-                                                {"model": "eg2"}, {"model": "omni", "head_layers": 2}]})
-    assert kinds[:4] == ["d1-3b", "d1-3b", "eg2", "eg2"] and "error" in kinds[4]
+    configs = [{"model": "decoder"}, {"model": "d1-3b"}, {"model": "eg2-encoder"}, {"model": "eg2"}, {"model": "d3"},
+               {"model": "d1-omni", "head_layers": 2}, {"head_layers": 2}, {"model": "laya", "head_layers": 2},
+               {"model": "d1-3b", "head_layers": 2}]
+    kinds = node({"cmd": "kinds", "configs": configs})
+    assert kinds == ["d1-3b", "d1-3b", "eg2", "eg2", "d3", "d1-omni", "d1-omni", "laya", "d1-3b"]
+    from decision_js_amd import d1
+    assert [d1._kind(c) for c in configs] == kinds
     import test_eg2_head as H
     tensors = H._tensors(3)
     rng = np.random.default_rng(4)
@@ -377,3 +381,51 @@ def test_node_lfm2_matches_python_host(tmp_path):
     finally:
         eng.destroy()
     assert np.array_equal(np.asarray(js["logits"], dtype=np.float32), py)
+
+
+def test_omni_packing_matches_python_host():
+    """packOmni (Node) == omni.pack_omni (Python) bit for bit."""
+    load_pkg()
+    from decision_js_amd import omni
+    seqs = [{"ids": [5, 6, 7, 8], "markers": [1, 3], "type": "choice"}, {"ids": [1], "markers": [0], "type": "noul"},
+            {"ids": list(range(30)), "markers": [0, 10, 29], "type": "score"}]
+    js = node({"cmd": "packomni", "seqs": seqs})
+    py = omni.pack_omni(seqs)
+    assert js["T"] == py["T"] and js["M"] == py["M"]
+    for k in ("ids", "pos", "qtype", "taps", "rng", "markers"):
+        assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), k
+
+
+@pytest.mark.gpu
+def test_node_omni_matches_python_host(tmp_path):
+    """The d1-omni kind through Node (kindOf -> runOmni -> OmniEngine: trunk, head, scorer) against the Python
+    host: identical marker logits (the same packing, op sequence and library) and the same answers."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.reduced("d1-omni-q8", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"])
+    mdir = synth.generate(cfg, str(tmp_path / "omni"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(17)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(16),
+                    "markers": [2, 7, 12]},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(6), "markers": [1, 4]},
+          "urgency": {"type": "score", "instructions": "?", "criteria": ["low", {"x": 2.5}], "ids": ids(9), "markers": [3, 6]}}
+    batch = [[ids(70), qs], [ids(25), qs]]
+    seqs = [{"ids": ids(40), "markers": [3, 9, 30], "type": "choice"}, {"ids": ids(12), "markers": [0, 11], "type": "noul"}]
+    js = node({"cmd": "omni", "model": mdir, "batch": batch, "seqs": seqs}, timeout=300)
+    assert js["kind"] == "d1-omni"
+    d = Decision.load(mdir)
+    try:
+        assert d.kind == "d1-omni"
+        py = d.system_one_batch([(s, q) for s, q in batch])
+        for a, b in zip(js["batch"], py):
+            assert a["usage"] == b["usage"]
+            assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-12
+            assert a["answers"]["topic"]["choice"] == b["answers"]["topic"]["choice"]
+            assert a["answers"]["urgency"]["legend"] == b["answers"]["urgency"]["legend"] == {"0": "low", "1": '{"x": 2.5}'}
+        want = d.engine.logits(seqs)["logits"]
+        for a, b in zip(js["logits"], want):
+            assert np.array_equal(np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
+    finally:
+        d.destroy()

@@ -621,3 +621,182 @@ def test_planted_lfm2_branch_taps_slip_is_caught(tiny_lfm2, monkeypatch):
     monkeypatch.setattr(ref, "forest_taps", slip)
     with pytest.raises(AssertionError):
         _compare_lfm2(tiny_lfm2)
+
+
+# ---------------------------------------------------------------- d1-omni: trunk, head and scorer
+
+TINY_OMNI = dict(layers=3, hidden=64, intermediate=96, heads=4, kv_heads=2, head_dim=16, vocab=512,
+                 layer_types=["conv", "full_attention", "conv"], head_layers=2, head_heads=4, head_ff=128)
+
+
+@pytest.fixture(scope="module")
+def tiny_omni(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("omni")
+    return synth.generate(synth.reduced("d1-omni-q8", **TINY_OMNI), str(d / "omni"), norm_std=0.1, std=0.125)
+
+
+def _omni_seqs(rng, V):
+    return [{"ids": [int(x) for x in rng.integers(0, V, n)], "markers": m, "type": t}
+            for n, m, t in ((23, [5, 9, 14], "choice"), (11, [2, 7], "noul"), (17, [0, 4, 8, 12, 16], "score"))]
+
+
+def _torch_omni(model: ref.Model, monkeypatch):
+    """The d1-omni forward from library modules, float64: transformers' Lfm2Model as the trunk, made
+    bidirectional the way d1-omni reads it (an all-zero additive attention mask; the short conv centred: its
+    causal conv replaced by F.conv1d with padding 1, a cross-correlation whose taps 0, 1, 2 read t-1, t, t+1),
+    then torch.nn.TransformerEncoderLayer(norm_first=True, ReLU) for each head layer and
+    Sequential(LayerNorm, Linear, GELU, Linear(H, 1)) as the scorer (export-omni.py:70-90)."""
+    from transformers.models.lfm2 import modeling_lfm2
+    monkeypatch.setattr(modeling_lfm2, "causal_conv1d_fn",
+                        lambda x, w, b=None, seq_idx=None, **kw: F.conv1d(x, w.unsqueeze(1), b, padding=1, groups=x.shape[1]))
+    trunk = _hf_lfm2(model)
+    c = model.c
+    H, hh, ff, ln = c["hidden"], c["head_heads"], c["head_ff"], c["ln_eps"]
+    layers = []
+    for i in range(c["head_layers"]):
+        p = f"head.{i}."
+        lay = torch.nn.TransformerEncoderLayer(H, hh, ff, dropout=0.0, activation="relu", layer_norm_eps=ln,
+                                               batch_first=True, norm_first=True).to(torch.float64).eval()
+        sd = {"self_attn.in_proj_weight": model.w16(p + "in_proj"), "self_attn.in_proj_bias": model.t[p + "in_proj_bias"],
+              "self_attn.out_proj.weight": model.w16(p + "out_proj"), "self_attn.out_proj.bias": model.t[p + "out_proj_bias"],
+              "linear1.weight": model.w16(p + "linear1"), "linear1.bias": model.t[p + "linear1_bias"],
+              "linear2.weight": model.w16(p + "linear2"), "linear2.bias": model.t[p + "linear2_bias"],
+              "norm1.weight": model.t[p + "norm1"], "norm1.bias": model.t[p + "norm1_bias"],
+              "norm2.weight": model.t[p + "norm2"], "norm2.bias": model.t[p + "norm2_bias"]}
+        lay.load_state_dict({k: _t(v) for k, v in sd.items()})
+        layers.append(lay)
+    scorer = torch.nn.Sequential(torch.nn.LayerNorm(H, eps=ln), torch.nn.Linear(H, H), torch.nn.GELU(),
+                                 torch.nn.Linear(H, 1)).to(torch.float64).eval()
+    scorer.load_state_dict({"0.weight": _t(model.t["scorer.norm"]), "0.bias": _t(model.t["scorer.norm_bias"]),
+                            "1.weight": _t(model.w16("scorer.fc")), "1.bias": _t(model.t["scorer.fc_bias"]),
+                            "3.weight": _t(model.t["scorer.out"]).reshape(1, H), "3.bias": _t(model.t["scorer.out_bias"][:1])})
+    type_emb = _t(model.t["head.type_emb"])
+
+    def run(seq):
+        T = len(seq["ids"])
+        with torch.no_grad():
+            mask = {"full_attention": torch.zeros(1, 1, T, T, dtype=torch.float64), "conv": None}
+            x = trunk(input_ids=torch.tensor([seq["ids"]]), attention_mask=mask).last_hidden_state
+            t = x.clone()
+            h = x + type_emb[["choice", "score", "noul"].index(seq["type"])]
+            for lay in layers:
+                h = lay(h)
+            return t[0].numpy(), h[0].numpy(), scorer(h)[0, seq["markers"], 0].numpy()
+    return run
+
+
+def _compare_omni(path, monkeypatch, model=None):
+    """The oracle's packed omni forward (float64 accumulation, f16 storage points) against the library modules
+    on each sequence alone: trunk output and the head's stream within 5e-3 relative L2, the marker logits within
+    1e-2 of their scale."""
+    model = model or ref.Model(path)
+    seqs = _omni_seqs(np.random.default_rng(5), model.c["vocab"])
+    logits, dbg = ref.omni_forward(model, seqs, acc=np.float64)
+    run = _torch_omni(ref.Model(path), monkeypatch)  # the library side always reads the untouched file
+    off, k = 0, 0
+    for s in seqs:
+        n, m = len(s["ids"]), len(s["markers"])
+        trunk, head, want = run(s)
+        assert _rel_l2(dbg["trunk"][off:off + n], trunk) < 5e-3, f"{s['type']}: trunk"
+        assert _rel_l2(dbg["head"][off:off + n], head) < 5e-3, f"{s['type']}: head stream"
+        got = logits[k:k + m].astype(np.float64)
+        assert np.abs(got - want).max() < 1e-2 * max(np.abs(want).max(), 1e-3), f"{s['type']}: marker logits"
+        off += n
+        k += m
+
+
+def test_omni_forward_matches_library_modules(tiny_omni, monkeypatch):
+    _compare_omni(tiny_omni, monkeypatch)
+
+
+def test_planted_omni_causal_taps_slip_is_caught(tiny_omni, monkeypatch):
+    """The decoder's causal taps (t-2, t-1, t) in place of d1-omni's centred ones."""
+    orig = ref.pack_omni
+
+    def slip(seqs):
+        pk = orig(seqs)
+        t = pk["taps"]
+        pk["taps"] = np.stack([np.where(t[:, 0] >= 0, t[:, 0] - 1, -1), t[:, 0], t[:, 1], t[:, 3]], 1).astype(np.int32)
+        pk["taps"][pk["taps"][:, 0] < np.repeat(pk["rng"][:, 0], 1), 0] = -1
+        return pk
+    monkeypatch.setattr(ref, "pack_omni", slip)
+    with pytest.raises(AssertionError):
+        _compare_omni(tiny_omni, monkeypatch)
+
+
+def test_planted_omni_taps_across_sequences_slip_is_caught(tiny_omni, monkeypatch):
+    """Centred taps that read the neighbouring sequence's edge token."""
+    orig = ref.pack_omni
+
+    def slip(seqs):
+        pk = orig(seqs)
+        T = pk["T"]
+        t = np.arange(T)
+        pk["taps"][:, 0] = t - 1
+        pk["taps"][:, 2] = np.where(t + 1 < T, t + 1, -1)
+        return pk
+    monkeypatch.setattr(ref, "pack_omni", slip)
+    with pytest.raises(AssertionError):
+        _compare_omni(tiny_omni, monkeypatch)
+
+
+@pytest.mark.parametrize("slip", ["relu_gelu_swapped", "no_in_proj_bias", "post_norm_scorer", "type_rows"])
+def test_planted_omni_head_slips_are_caught(tiny_omni, monkeypatch, slip):
+    """ReLU and GELU swapped; the fused in_proj bias dropped; the scorer's LayerNorm read before the last
+    residual add; the question-type rows in the wrong order."""
+    if slip == "relu_gelu_swapped":
+        orig = ref.bias_act
+        monkeypatch.setattr(ref, "bias_act", lambda Y, b, act=0, acc=np.float32: orig(Y, b, {1: 2, 2: 1}.get(act, act), acc))
+    elif slip == "no_in_proj_bias":
+        orig = ref.bias_act
+        fused = 3 * TINY_OMNI["hidden"]
+        monkeypatch.setattr(ref, "bias_act", lambda Y, b, act=0, acc=np.float32: orig(Y, b * 0 if b.shape[0] == fused else b, act, acc))
+    elif slip == "post_norm_scorer":
+        orig = ref.add_layernorm
+        calls = {"n": 0}
+
+        def ln(X, Y, w, b, eps, add=True, acc=np.float32):
+            calls["n"] += 1
+            if calls["n"] % (2 * TINY_OMNI["head_layers"] + 1) == 0:  # the scorer's: normalise X before adding Y
+                Xn, O = orig(X, Y, w, b, eps, add, acc)
+                return Xn, orig(X, None, w, b, eps, False, acc)[1]
+            return orig(X, Y, w, b, eps, add, acc)
+        monkeypatch.setattr(ref, "add_layernorm", ln)
+    else:
+        orig = ref.pack_omni
+
+        def rows(seqs):
+            pk = orig(seqs)
+            pk["qtype"] = np.array([{0: 1, 1: 0}.get(int(q), int(q)) for q in pk["qtype"]], dtype=np.uint32)
+            return pk
+        monkeypatch.setattr(ref, "pack_omni", rows)
+    with pytest.raises(AssertionError):
+        _compare_omni(tiny_omni, monkeypatch)
+
+
+def test_erf_as_error_bound():
+    """BIAS_ACT's erf (A&S 7.1.26) within its published 1.5e-7 of erf on [-6, 6]; a changed coefficient is caught."""
+    x = np.linspace(-6, 6, 24001)
+    exact = np.array([math.erf(v) for v in x])
+    assert np.abs(ref.erf_as(x) - exact).max() < 1.5e-7
+    bad = 1.0 - ((((1.061405429 * (t := 1.0 / (1.0 + 0.3275911 * np.abs(x))) - 1.453152027) * t + 1.421413741) * t
+                  - 0.284496736) * t + 0.254829592 * 1.001) * t * np.exp(-x * x)
+    assert np.abs(np.where(x >= 0, bad, -bad) - exact).max() > 1.5e-7
+
+
+def test_add_layernorm_matches_torch_layer_norm():
+    """ADD_LAYERNORM (kernels.ts:224-255) in float64 against F.layer_norm of X + Y (the variance as
+    E[x^2] - mean^2 agrees with the two-pass form to rounding); the stored sum is f16(X + Y)."""
+    rng = np.random.default_rng(3)
+    X = (rng.standard_normal((9, 192)) * 2 + 0.5).astype(np.float16)
+    Y = rng.standard_normal((9, 192)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(192)).astype(np.float16)
+    b = (0.1 * rng.standard_normal(192)).astype(np.float16)
+    for add in (False, True):
+        Xn, O = ref.add_layernorm(X, Y, w, b, 1e-5, add=add, acc=np.float64)
+        v = X.astype(np.float64) + (Y.astype(np.float64) if add else 0)
+        assert np.array_equal(Xn, v.astype(np.float16))
+        want = F.layer_norm(_t(Xn.astype(np.float64)), (192,), _t(w), _t(b), 1e-5).numpy()
+        assert np.abs(O.astype(np.float64) - want).max() < 2e-3 * np.abs(want).max()
+        assert np.abs(O.astype(np.float64) - want).max() <= np.abs(want).max() * 2.0 ** -10  # one f16 rounding
