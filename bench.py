@@ -68,15 +68,28 @@ def make_tickets(n, V, seq_len=384, seed=1, answer_seed=3, sizes=(2, 3, 5)):
     return tickets
 
 
-def model_flops_bytes(c, T, seqs_len, causal=True):
+def model_flops_bytes(c, T, seqs_len, causal=True, markers=0):
     """Appendix-B algorithmic work of one forward: 2 T sum(N K) over the linears plus 4 D h (allowed
-    query-key pairs) per layer; bytes = quantized linear weights + gathered embedding rows."""
-    H, I, h, kv, D, L = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["layers"]
-    nk = (h + 2 * kv) * D * H + H * h * D + 2 * I * H + H * I
+    query-key pairs) per attention layer; bytes = quantized linear weights + gathered embedding rows. LFM2 conv
+    layers count in_proj (3H x H) and out_proj (H x H); a d1-omni head counts its layers' in_proj (3H x H),
+    out_proj, linear1/linear2 on every token and bidirectional attention, and the scorer's H x H product on
+    `markers` rows."""
+    H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
+    types = c.get("layer_types") or ["full_attention"] * c["layers"]
+    attn_nk, conv_nk, ffn_nk = (h + 2 * kv) * D * H + H * h * D, 4 * H * H, 2 * I * H + H * I
+    nk = sum(conv_nk if t == "conv" else attn_nk for t in types) + len(types) * ffn_nk
     pairs = sum(n * (n + 1) // 2 if causal else n * n for n in seqs_len)
-    flops = 2 * T * nk * L + 4 * D * h * pairs * L
+    n_attn = sum(t != "conv" for t in types)
+    flops = 2 * T * nk + 4 * D * h * pairs * n_attn
+    wnk = nk
+    if c.get("head_layers"):
+        hl, ff = c["head_layers"], c["head_ff"]
+        head_nk = hl * (4 * H * H + 2 * ff * H)
+        bidir = sum(n * n for n in seqs_len)
+        flops += 2 * T * head_nk + 4 * H * bidir * hl + 2 * markers * H * H
+        wnk += head_nk + H * H
     qbytes = 1.0625 if c.get("bits", 8) == 8 else 0.5625
-    return flops, nk * L * qbytes + T * H * qbytes
+    return flops, wnk * qbytes + T * H * qbytes
 
 
 def roofline_from_profile(table):
@@ -188,9 +201,9 @@ def _line(metric, value, unit, steps, warmup, ms, dtype, workload, roofline, ext
     return out
 
 
-def _forward_fraction(cfg, T, seqs, ms, causal=True):
+def _forward_fraction(cfg, T, seqs, ms, causal=True, markers=0):
     """Appendix-B roofline of a forward: achieved TFLOP/s (and weight GB/s) over the measured time."""
-    flops, wbytes = model_flops_bytes(cfg, T, seqs, causal)
+    flops, wbytes = model_flops_bytes(cfg, T, seqs, causal, markers)
     t_mfma, t_hbm = flops / (MFMA_F16_PEAK_TFLOPS * 1e12), wbytes / (HBM_PEAK_GBS * 1e9)
     s = ms * 1e-3
     if t_mfma >= t_hbm:
@@ -377,6 +390,8 @@ def run_workload(args):
                     roof, {"gpu_ms_per_step": round(gpu_ms, 3), "question_alone_ms": round(1e3 * q_wall, 4),
                            "question_alone_gpu_ms": round(q_gpu, 4), "question_alone_roofline": q_roof})
         eng.destroy()
+    elif args.workload == "omni":
+        out = omni_ticket(args, steps, warmup)
     else:
         from decision_js_amd.encoder import EncoderEngine, cosine_logits
         cfg = synth.CONFIGS["eg2-encoder-q8"]
@@ -413,6 +428,78 @@ def run_workload(args):
     print(json.dumps(out), flush=True)
 
 
+def omni_tickets(cfg, n, seq_len=384, q_len=44):
+    """n d1-omni tickets: a state of seq_len - q_len random ids (PCG64 seed 1) read by 3 questions (a noul, a
+    3-way choice, a 5-level score) of q_len ids each, one sequence per question, markers 6 ids apart in the
+    question."""
+    rng = np.random.Generator(np.random.PCG64(1))
+    V, P = cfg["vocab"], seq_len - q_len
+    out = []
+    for _ in range(n):
+        state = [int(x) for x in rng.integers(0, V, P)]
+        out.append([{"ids": state + [int(x) for x in rng.integers(0, V, q_len)], "type": t,
+                     "markers": [P + 2 + 6 * j for j in range(k)]} for t, k in (("noul", 2), ("choice", 3), ("score", 5))])
+    return out
+
+
+def omni_ticket(args, steps, warmup):
+    """d1-omni tickets (the form of the reference's published 34 ms/ticket on an Apple M5 Pro, README.md:31):
+    3 questions over one 340-id state, each question its own 384-id sequence (the state read anew per question,
+    omni-engine.ts:5), packed in one forward (T = 1152): bidirectional LFM2 trunk, decision head, marker scorer,
+    then the temperature softmax on the host. A step is one ticket, inputs staged in HBM."""
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import softmax
+    from decision_js_amd.omni import OmniEngine, temperature
+    cfg = synth.CONFIGS["d1-omni-q8"]
+    mdir = os.path.join(args.model_dir, "d1-omni-q8")
+    synth.generate(cfg, mdir, seed=0, threads=16)
+    eng = OmniEngine.load(mdir, {"graphs": not args.no_graphs})
+    tickets = omni_tickets(cfg, warmup + steps)
+    staged = [eng.stage(t) for t in tickets]
+
+    def unit(st):
+        z = eng.run_staged(st)["logits"]
+        return [softmax(np.asarray(l) / temperature(cfg, s["type"], len(l))) for s, l in zip(st["seqs"], z)]
+
+    for st in staged[:warmup]:
+        unit(st)
+    eng.ctx.timer_begin()
+    t0 = time.perf_counter()
+    times = []
+    for st in staged[warmup:]:
+        a = time.perf_counter()
+        unit(st)
+        times.append(time.perf_counter() - a)
+    wall = time.perf_counter() - t0
+    gpu_ms = eng.ctx.timer_end() / steps
+    ms = 1e3 * wall / steps
+    lens = [len(s["ids"]) for s in tickets[0]]
+    T = sum(lens)
+    roof = _forward_fraction(cfg, T, lens, gpu_ms, causal=False, markers=10)
+    eng.graphs = False
+    eng.ctx.profile_reset()
+    eng.ctx.profile(True)
+    for st in staged[:3]:
+        eng.run_staged(st)
+    eng.ctx.profile(False)
+    table = eng.ctx.profile_table()
+    total = sum(v[0] for v in table.values())
+    for k, (t_ms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
+        log(f"  {k:48s} {t_ms / 3:8.4f} ms/ticket  {100 * t_ms / total:5.1f}%  ({cnt // 3}/ticket, {1e3 * t_ms / cnt:7.2f} us each)")
+    p50 = 1e3 * float(np.median(times))
+    log(f"omni: ticket (T={T}) {ms:.3f} ms wall (p50 {p50:.3f}), {gpu_ms:.3f} ms GPU, {3 * steps / wall:.1f} decisions/s")
+    for st in staged:
+        eng.free_staged(st)
+    eng.destroy()
+    return _line("decisions/sec (d1-omni tickets: 3 questions, one 384-id sequence each) on 1 MI355X", 3 * steps / wall,
+                 "decisions/s", steps, warmup, ms, "f16",
+                 "d1-omni-q8 (LFM2-350M-shaped bidirectional trunk, 16 layers, 2-layer head), 3 x 384 random ids in one "
+                 "forward, 10 markers", roof,
+                 {"gpu_ms_per_step": round(gpu_ms, 4), "p50_ms_per_ticket": round(p50, 4),
+                  "reference_published_ms_per_ticket": {"value": 34.0, "hardware": "Apple M5 Pro, Chrome WebGPU",
+                                                        "model": "d1-omni-600M q8 (real weights)", "source": "README.md:31"}})
+
+
 def _linear_shapes(c):
     """(N, K) of one decoder layer's linears: qkv, o_proj, w13, w2."""
     H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
@@ -431,7 +518,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calib-mb", type=int, default=0, help="also run a plain device copy of this many MiB (counter calibration)")
-    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder"],
+    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni"],
                     help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
                          "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
     ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")
