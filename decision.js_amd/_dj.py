@@ -75,6 +75,8 @@ SIGNATURES = {
     "dj_matmul_qkv_rope": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P],
     "dj_attention": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_attention_noalloc": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
+    "dj_attention_gated": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P, _I, _P],
+    "dj_gdn": [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _P, _F, _P],
     "dj_kv_store": [_P, _I, _I, _I, _P, _I, _I, _P, _I],
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
     "dj_readout": [_P, _I, _I, _I, _P, _P, _I, _P, _P],
@@ -304,6 +306,14 @@ class Recorder:
 
     def attention(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))
+
+    def attention_gated(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, G, g_stride, O):
+        check(lib().dj_attention_gated(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(G),
+                                       g_stride, ptr(O)))
+
+    def gdn(self, T, nspans, spans, LH, stride, Z, conv_w, A_log, dt_bias, gnorm, eps, Y):
+        check(lib().dj_gdn(self.h, T, nspans, ptr(spans), LH, stride, ptr(Z), ptr(conv_w), ptr(A_log), ptr(dt_bias),
+                           ptr(gnorm), eps, ptr(Y)))
 
     def attention_noalloc(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention_noalloc(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))

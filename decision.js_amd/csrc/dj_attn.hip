@@ -85,7 +85,8 @@ __device__ __forceinline__ int wave_reduce(int v) {
 template <int D, int RING, int KG, int HG>
 __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
-                                              uint16_t *__restrict__ O, int splits, float *__restrict__ part) {
+                                              uint16_t *__restrict__ O, dj_attn_gate gate, int splits,
+                                              float *__restrict__ part) {
   using S = AttnShape<D, RING, KG, HG>;
   constexpr int KW = 64 / KG;          // keys of each tile this wave scores (KG key groups split a tile)
   constexpr int NB = KW / 16;          // 16-key blocks of S^T per wave and tile
@@ -353,11 +354,18 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
   if (qi < T) {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
     uint16_t *orow = O + (size_t)qi * heads * D + (size_t)h * D;
+    const uint16_t *grow = gate.g ? gate.g + (size_t)qi * gate.stride + (size_t)h * D : nullptr;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
       h4 v;
+      if (grow) {  // the output gate of d3's attention (d3-kernels.ts:232-236): acc / l / (1 + exp(-gate))
+        const h4 gv = *(const h4 *)(grow + 16 * db + 4 * g);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = (_Float16)(o[db][r] * inv);
+        for (int r = 0; r < 4; ++r) v[r] = (_Float16)(o[db][r] * inv / (1.0f + expf(-(float)gv[r])));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = (_Float16)(o[db][r] * inv);
+      }
       *(h4 *)(orow + 16 * db + 4 * g) = v;
     }
   }
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
 // order on values broadcast from lane s.
 template <int DPL>
 __global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int splits, const float *__restrict__ part,
-                                                      uint16_t *__restrict__ O) {
+                                                      uint16_t *__restrict__ O, dj_attn_gate gate) {
   constexpr int D = 64 * DPL, PRE = 16;
   const int pair = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (pair >= T * heads) return;
@@ -413,18 +421,25 @@ __global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int spli
     }
   }
   uint16_t *o = O + row0 * D + lane * DPL;
+  const uint16_t *gr = gate.g ? gate.g + (size_t)q * gate.stride + (size_t)h * D + lane * DPL : nullptr;
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) o[i] = __builtin_bit_cast(uint16_t, (_Float16)(L > 0.f ? acc[i] / L : 0.f));
+  for (int i = 0; i < DPL; ++i) {
+    float v = L > 0.f ? acc[i] / L : 0.f;
+    if (gr) v = v / (1.0f + expf(-(float)__builtin_bit_cast(_Float16, gr[i])));
+    o[i] = __builtin_bit_cast(uint16_t, (_Float16)v);
+  }
 }
 
 // Launch with one workgroup shape; a shape whose K/V tile does not split into whole 1 KB DMAs per wave is never
 // picked, nor one that would spill registers (the launcher falls back to HG 1 for them).
 template <int D, int RING, int KG, int HG>
 static void attn_launch(dim3 g3, hipStream_t s, int T, int heads, int kv, const uint16_t *Q, int q_stride,
-                        dj_kv_src A, dj_kv_src B, const int4 *r4, float scale, uint16_t *O, int splits, float *part) {
+                        dj_kv_src A, dj_kv_src B, const int4 *r4, float scale, uint16_t *O, dj_attn_gate gate, int splits,
+                        float *part) {
   if constexpr ((64 * 2 * D) % (1024 * 4 * KG * HG) == 0 && D * HG <= 256 &&  // (D 128 x HG 4 would spill)
                 RING * 2 * (64 * 2 * D) <= 160 * 1024)
-    k_attn<D, RING, KG, HG><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);
+    k_attn<D, RING, KG, HG><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits,
+                                                         part);
 }
 
 // The split-KV plan of a launch: small grids (a short question against a long state: one query block per head)
@@ -446,7 +461,8 @@ static int attn_splits(int cus, int T, int heads, int D, const dj_kv_src &A, con
 }
 
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
-                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats) {
+                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
+                        dj_attn_gate gate) {
   hipStream_t s = c->stream;
   const int qblocks = dj_cdiv(T, 64);
   const long grid = (long)qblocks * heads;
@@ -476,12 +492,12 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
   const dim3 g3(qblocks, heads / hg, splits);
 #define DJ_ATTN_CASE(DD)                                                                                              \
   case DD:                                                                                                            \
-    if (kg > 1) attn_launch<DD, 2, 2, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);         \
-    else if (hg == 2) attn_launch<DD, 0, 1, 2>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);   \
-    else if (hg == 4) attn_launch<DD, 0, 1, 4>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);   \
-    else if (ring == 3) attn_launch<DD, 3, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); \
-    else if (ring == 4) attn_launch<DD, 4, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part); \
-    else attn_launch<DD, 2, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, splits, part);                \
+    if (kg > 1) attn_launch<DD, 2, 2, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part);         \
+    else if (hg == 2) attn_launch<DD, 0, 1, 2>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part);   \
+    else if (hg == 4) attn_launch<DD, 0, 1, 4>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part);   \
+    else if (ring == 3) attn_launch<DD, 3, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part); \
+    else if (ring == 4) attn_launch<DD, 4, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part); \
+    else attn_launch<DD, 2, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part);                \
     break;
   switch (D) {
     DJ_ATTN_CASE(64)
@@ -492,9 +508,9 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
 #undef DJ_ATTN_CASE
   if (splits > 1) {
     const unsigned blocks = (unsigned)dj_cdiv((long)T * heads, 4);
-    if (D == 64) k_attn_combine<1><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
-    else if (D == 128) k_attn_combine<2><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
-    else k_attn_combine<4><<<blocks, 256, 0, s>>>(T, heads, splits, part, O);
+    if (D == 64) k_attn_combine<1><<<blocks, 256, 0, s>>>(T, heads, splits, part, O, gate);
+    else if (D == 128) k_attn_combine<2><<<blocks, 256, 0, s>>>(T, heads, splits, part, O, gate);
+    else k_attn_combine<4><<<blocks, 256, 0, s>>>(T, heads, splits, part, O, gate);
   }
   return DJ_OK;
 }
@@ -521,6 +537,27 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
   char shape[48];
   snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
   return dj_op_end(rec, "attention", shape);
+}
+
+extern "C" int dj_attention_gated(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
+                                  dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, const uint16_t *G,
+                                  int g_stride, uint16_t *O) {
+  DJ_REQUIRE(Q && rng && O && G && T >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && q_stride % 8 == 0 &&
+                 q_stride >= heads * D && g_stride % 8 == 0 && g_stride >= heads * D && ((uintptr_t)G & 7) == 0,
+             "decision.js: attention_gated: bad arguments (heads %d, kv %d, q_stride %d, g_stride %d)", heads, kv,
+             q_stride, g_stride);
+  DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
+  DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
+  DJ_OP_BEGIN(rec, "attention_gated");
+  if (T > 0) {
+    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O, rec->ctx->gemm_ws,
+                                 rec->ctx->gemm_ws_floats, dj_attn_gate{G, g_stride});
+    if (st) return st;
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
+  return dj_op_end(rec, "attention_gated", shape);
 }
 
 // ---------------------------------------------------------------- the entry point that allocates nothing

@@ -138,8 +138,14 @@ int dj_take_held_split(dj_rec *rec, const uint16_t *Y, int T, int H, const float
 int dj_launch_qk_norm_rope(hipStream_t s, int T, int heads, int kv, int D, int stride, uint16_t *Z, const uint16_t *qn,
                            const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps, float theta, int rot,
                            int mode);
+// The optional output gate of d3's attention: O = f16(attention / (1 + exp(-G[q, h D + d]))), G rows of `stride`.
+struct dj_attn_gate {
+  const uint16_t *g;
+  int stride;
+};
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
-                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats);
+                        dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
+                        dj_attn_gate gate = dj_attn_gate{nullptr, 0});
 // Takes the device address of the static attention scratch on the current device into c->attn_scratch.
 int dj_attn_scratch_init(dj_ctx *c);
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);

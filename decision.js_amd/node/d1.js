@@ -13,6 +13,7 @@
 const { DecoderEngine } = require("./engine");
 const { EncoderEngine, cosineLogits } = require("./encoder");
 const { OmniEngine, temperature: omniTemperature } = require("./omni");
+const { D3Engine } = require("./d3");
 const { criterion } = require("./py");
 const { Eg2Head } = require("./eg2_head");
 const { fileFetch } = require("./format");
@@ -71,6 +72,7 @@ class D1 {
     const kind = kindOf(manifest.config);
     if (kind === "laya") throw new Error("decision.js: Laya (ModernBERT) models do not run on this build");
     const engine = kind === "eg2" ? await EncoderEngine.load(base, opts) : kind === "d1-omni" ? await OmniEngine.load(base, opts)
+      : kind === "d3" && "linear_heads" in manifest.config ? await D3Engine.load(base, opts) // the shipped d3-lite
       : await DecoderEngine.load(base, opts);
     return new D1(kind, engine, opts);
   }

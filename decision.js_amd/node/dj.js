@@ -131,6 +131,12 @@ class Recorder {
   attention(T, heads, kv, D, Q, qStride, A, B, rng, scale, O) {
     lib().attention(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, O);
   }
+  attentionGated(T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O) {
+    lib().attentionGated(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O);
+  }
+  gdn(T, nspans, spans, LH, stride, Z, convW, Alog, dtBias, gnorm, eps, Y) {
+    lib().gdn(this.h, T, nspans, spans, LH, stride, Z, convW, Alog, dtBias, gnorm, eps, Y);
+  }
   kvStore(T, kv, D, Z, stride, kCol, cache, row0) { lib().kvStore(this.h, T, kv, D, Z, stride, kCol, cache, row0); }
   meanPool(T, S, H, X, seqs, out) { lib().meanPool(this.h, T, S, H, X, seqs, out); }
   readout(T, P, H, X, R, codes, pairs, out) { lib().readout(this.h, T, P, H, X, R, codes, pairs, out); }

@@ -5,6 +5,7 @@ const { D1, Decision, softmax } = require("./d1");
 const { DecoderEngine, packForest, packShared, groupMax } = require("./engine");
 const { EncoderEngine, packEncoder } = require("./encoder");
 const { OmniEngine, packOmni } = require("./omni");
+const { D3Engine, gdnSpans } = require("./d3");
 const { Eg2Head } = require("./eg2_head");
 const { loadWeights, fileFetch } = require("./format");
 const questions = require("./questions");
@@ -12,5 +13,5 @@ const dj = require("./dj");
 
 module.exports = {
   D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, OmniEngine,
-  Eg2Head, packForest, packShared, packEncoder, packOmni, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+  D3Engine, Eg2Head, packForest, packShared, packEncoder, packOmni, gdnSpans, groupMax, loadWeights, fileFetch, softmax, questions, dj,
 };

@@ -38,6 +38,17 @@ CONFIGS = {
                             head_dim=128, vocab=151936, eps=1e-6, rope_theta=1e6, qk_norm=True,
                             codes=["A", "B", "C", "D", "E", "F", "G", "H"], temperature=1.0,
                             choices={"norm_weights": 1.0, "layers": "attention only (no Gated DeltaNet)"}),
+    # d3-lite as shipped (D3Engine, d3-engine.ts; export-d3.py): a Qwen3.5-0.8B-shaped backbone, 18 Gated DeltaNet
+    # layers and every fourth a gated attention layer with 256-dim heads (RoPE on the first 64 dims), the f32
+    # code readout. The widths follow the published 803 MB q8 size (export-d3.py:56-60 names the keys); theta,
+    # the gate parameters' ranges and the codes are choices.
+    "d3-lite-q8": dict(model="d3", bits=8, layers=24, hidden=1024, intermediate=3584, heads=8, kv_heads=2, head_dim=256,
+                       rotary_dim=64, vocab=248320, eps=1e-6, rope_theta=1e7,
+                       layer_types=["full_attention" if i % 4 == 3 else "linear_attention" for i in range(24)],
+                       linear_heads=16, linear_key_dim=128, linear_value_dim=128, conv_kernel=4, linear_rows=8320,
+                       codes=["A", "B", "C", "D", "E", "F", "G", "H"], temperature=1.0,
+                       choices={"norm_weights": 1.0, "rope_theta": "1e7 (not stated)",
+                                "A_log": "log U(0.01, 1)", "dt_bias": "N(0, 0.5)", "conv taps": "N(0, 0.5)"}),
     # d1-3B's LFM2 backbone form (D13BEngine, d1-3b-engine.ts; export-3b.py): short-conv layers with attention
     # layers between them, 64-dim heads with q/k norm, q4 linears, f16 conv taps [H, 3]. Not a BASELINE config:
     # the layer pattern, widths and vocabulary are choices.
@@ -95,7 +106,21 @@ def tensor_plan(cfg: dict):
     """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
     H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
     plan = [("embed", "q", (V, H))]
-    if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
+    if cfg["model"] == "d3" and "linear_heads" in cfg:  # d3-lite as exported (export-d3.py:66-102)
+        LH, QK, A = cfg["linear_heads"], cfg["linear_heads"] * 128, (2 * h + 2 * kv) * D
+        plan += [("final_norm", "n", (H,)), ("readout", "r", (len(cfg["codes"]), H))]
+        for i, t in enumerate(cfg["layer_types"]):
+            p = f"layers.{i}."
+            plan += [(p + "input_norm", "n", (H,)), (p + "post_norm", "n", (H,)), (p + "w13", "q", (2 * I, H)),
+                     (p + "w2", "q", (H, I))]
+            if t == "linear_attention":
+                plan += [(p + "in", "q", (cfg["linear_rows"], H)), (p + "conv", "c", (3 * QK, 4)),
+                         (p + "A_log", "alog", (LH,)), (p + "dt_bias", "b5", (LH,)), (p + "gnorm", "n", (128,)),
+                         (p + "out", "q", (H, QK))]
+            else:
+                plan += [(p + "qkvg", "q", (A, H)), (p + "q_norm", "n", (D,)), (p + "k_norm", "n", (D,)),
+                         (p + "o", "q", (H, h * D))]
+    elif cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
         plan.append(("final_norm", "n", (H,)))
         types = cfg.get("layer_types") or ["full_attention"] * L
         for i in range(L):
@@ -178,6 +203,10 @@ def _make(cfg, name, kind, shape, seed, norm_std, std):
         return name, kind, normal(name, shape, std, seed), None
     if kind == "c":  # f16 conv taps, N(0, 0.5): each tap moves its channel by about as much as the others
         return name, kind, normal(name, shape, 0.5, seed), None
+    if kind == "alog":  # log of the DeltaNet decay rates, log U(0.01, 1): per-token decays of ~0.3 to ~1
+        return name, kind, np.log(0.01 + 0.99 * _rng(name, seed).random(shape, dtype=np.float32)), None
+    if kind == "b5":  # f16 biases, N(0, 0.5)
+        return name, kind, normal(name, shape, 0.5, seed), None
     if kind == "b":  # f16 biases, N(0, 0.1)
         return name, kind, normal(name, shape, 0.1, seed), None
     if kind == "e":  # the f16 question-type rows, N(0, 0.5): each type moves the head's input visibly
@@ -214,7 +243,7 @@ def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads:
         futs = [ex.submit(_make, cfg, n, k, s, seed, norm_std, std) for n, k, s in plan]
         for (name, kind, shape), fut in zip(plan, futs):
             _, _, a, b = fut.result()
-            if kind in ("n", "c", "b", "e", "v", "s"):
+            if kind in ("n", "c", "b", "e", "v", "s", "alog", "b5"):
                 blob.f16(name, a)
             elif kind == "r":
                 blob.f32(name, a)

@@ -250,6 +250,24 @@ int dj_kv_store(dj_rec *rec, int T, int kv, int D, const uint16_t *Z_dev, int st
 int dj_short_conv(dj_rec *rec, int T, int H, const uint16_t *Z_dev, const uint16_t *w_dev, const int32_t *taps_dev,
                   uint16_t *Y_dev);
 
+/* ---------------------------------------------------------------- ops: d3-lite's mixers (d3-kernels.ts) */
+
+/* The Gated DeltaNet mixer after the in-projection, for every (sequence, head) (gdnLayer, d3-kernels.ts:9-149):
+ * Z [T, stride] f16 rows q | k | v | z (LH x 128 each) | b | a (LH each); conv_w f16 [3 LH 128, 4] (causal taps,
+ * tap 3 the token itself); A_log, dt_bias f16 [LH]; gnorm f16 [128]. spans (device, u32 [nspans, 4]): (a start,
+ * a length | write_a << 31, b start, b length): a sequence is span a then span b (a shared trunk rescanned by
+ * each question, then the question; or the whole sequence and an empty b); span a's outputs are written only
+ * when write_a is set. Y [T, LH 128] f16 = gated RMSNorm (eps) of the delta rule's output. Key and value heads
+ * are 128 wide and equal in number; the conv has 4 taps. Replaces dispatch(gdnLayer(...)) (d3-engine.ts:116). */
+int dj_gdn(dj_rec *rec, int T, int nspans, const uint32_t *spans_dev, int LH, int stride, const uint16_t *Z_dev,
+           const uint16_t *conv_w_dev, const uint16_t *A_log_dev, const uint16_t *dt_bias_dev,
+           const uint16_t *gnorm_dev, float eps, uint16_t *Y_dev);
+/* dj_attention with d3's output gate: O = f16(attention / (1 + exp(-G[t, h D + d]))), G rows of g_stride halves
+ * (the gate heads of the fused q | k | v | gate rows). Replaces attention256 (d3-kernels.ts:180-240). */
+int dj_attention_gated(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride, dj_kv_src A,
+                       dj_kv_src B, const int32_t *rng_dev, float scale, const uint16_t *G_dev, int g_stride,
+                       uint16_t *O_dev);
+
 /* ---------------------------------------------------------------- ops: d1-omni's decision head (kernels.ts:186-283) */
 
 /* Xo[t, :] = f16(f32(Xi[t, :]) + f32(E[idx[t], :])) for E f16 [rows, H] (the question-type embedding); idx past

@@ -312,10 +312,12 @@ def pack_encoder(seqs, window=None):
 
 # ---------------------------------------------------------------- attention
 
-def attention(Z, heads, kv, D, mask, scale, acc=F32, q_stride=None, kv_rows=None):
+def attention(Z, heads, kv, D, mask, scale, acc=F32, q_stride=None, kv_rows=None, gate=None):
     """softmax(scale q.k) v over the allowed keys, per query and head (ATTENTION kernels.ts:114-147 and its
     tiled/eg2/d3 variants); f32 scores and sums, output f16(acc / l). mask [T, Tk] boolean. Z holds
-    [q | k | v] rows; kv_rows (optional) is a separate [Tk, 2 kv D] array of [k | v] rows."""
+    [q | k | v] rows; kv_rows (optional) is a separate [Tk, 2 kv D] array of [k | v] rows; gate (optional,
+    [T, heads D]) multiplies the output by sigmoid(gate) before its f16 rounding (d3's attention256,
+    d3-kernels.ts:232-236)."""
     T = Z.shape[0]
     q = Z[:, :heads * D].reshape(T, heads, D).astype(acc)
     if kv_rows is None:
@@ -332,7 +334,10 @@ def attention(Z, heads, kv, D, mask, scale, acc=F32, q_stride=None, kv_rows=None
         m = np.maximum(s.max(-1, keepdims=True), -1e30)
         p = np.where(mask, np.exp(s - m), 0.0)
         out[:, h, :] = (p @ v[:, h // g, :]) / p.sum(-1, keepdims=True)
-    return out.reshape(T, heads * D).astype(F16)
+    out = out.reshape(T, heads * D)
+    if gate is not None:
+        out = out / (1.0 + np.exp(-gate.astype(acc)))
+    return out.astype(F16)
 
 
 # ---------------------------------------------------------------- readouts
@@ -366,6 +371,123 @@ def mean_pool(X, ranges):
 def dense_f32(inp, codes, scales, bits):
     """f32 activations times the f32-dequantized weight (the pooled head)."""
     return (inp.astype(F32) @ dequant_f32(codes, scales, bits).T).astype(F32)
+
+
+# ---------------------------------------------------------------- d3-lite's Gated DeltaNet (d3-kernels.ts:9-149)
+
+def d3_spans(seqs, groups=None):
+    """The GDN scans of D3Engine.logits's packing (d3-engine.ts:89): per question (a start, a length | write_a <<
+    31, b start, b length): with a shared prefix P, a = the trunk (written by the group's first question only)
+    and b = the question's own tokens; without one, a = the whole sequence (written) and b empty. Rows follow
+    pack_shared's layout. [S, 4] u32."""
+    sizes = groups if groups is not None else [1] * len(seqs)
+    spans, si, off = [], 0, 0
+    for n in sizes:
+        group = seqs[si:si + n]
+        si += n
+        P = 0
+        if n > 1:
+            lim = min(len(s["ids"]) for s in group) - 1
+            while P < lim and all(s["ids"][P] == group[0]["ids"][P] for s in group):
+                P += 1
+        ts = off
+        off += P
+        for b, s in enumerate(group):
+            bs, L = off, len(s["ids"]) - P
+            off += L
+            if P:
+                spans.append((ts, P | (0x80000000 if b == 0 else 0), bs, L))
+            else:
+                spans.append((bs, L | 0x80000000, 0, 0))
+    return np.array(spans, dtype=np.uint32).reshape(-1, 4)
+
+
+def gdn(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc=F32):
+    """gdnLayer (d3-kernels.ts:9-149) in its textbook form: for each scan and head, the causal 4-tap conv (tap 3
+    the token itself, zero before the sequence start) + SiLU of the q, k, v channels, rounded to f16; q and k L2
+    normalised (eps 1e-6 inside the root), q scaled by 128^-1/2; decay = exp(-exp(A_log) softplus(a + dt_bias))
+    (softplus(x) = x past 20), beta = sigmoid(b); per token S <- decay S; delta = beta (v - S k); S <- S + delta
+    k^T; o = S q (S [v, k] in acc); then y = f16(o / sqrt(mean(o^2) + eps) * gnorm * silu(z)). Z rows q | k | v |
+    z (LH x 128 each) | b | a (LH each). Returns Y [T, LH 128] f16 (rows no scan writes stay 0)."""
+    T = Z.shape[0]
+    QK = LH * 128
+    Y = np.zeros((T, QK), dtype=F16)
+    W = conv_w.astype(acc).reshape(3 * QK, 4)
+    for a0, aw, b0, bl in np.asarray(spans, dtype=np.int64):
+        alen, write_a = int(aw) & 0x7fffffff, (int(aw) >> 31) & 1
+        rows = list(range(a0, a0 + alen)) + list(range(b0, b0 + bl))
+        n = len(rows)
+        if n == 0:
+            continue
+        X = Z[rows].astype(acc)
+        for h in range(LH):
+            ch = np.concatenate([np.arange(128) + h * 128, QK + np.arange(128) + h * 128, 2 * QK + np.arange(128) + h * 128])
+            x = np.concatenate([np.zeros((3, len(ch)), dtype=acc), X[:, ch]])
+            w = W[ch]
+            y = sum(w[:, j][None, :] * x[j:j + n] for j in range(4))
+            y = (y / (1.0 + np.exp(-y))).astype(F16).astype(acc)
+            q, k, v = y[:, :128], y[:, 128:256], y[:, 256:]
+            q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6) / np.sqrt(acc(128))
+            k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+            b = X[:, 4 * QK + h]
+            a = X[:, 4 * QK + LH + h] + acc(dt_bias[h])
+            sp = np.where(a > 20, a, np.log1p(np.exp(np.minimum(a, 20))))
+            dec = np.exp(-np.exp(acc(A_log[h])) * sp)
+            beta = 1.0 / (1.0 + np.exp(-b))
+            S = np.zeros((128, 128), dtype=acc)
+            o = np.zeros((n, 128), dtype=acc)
+            for t in range(n):
+                S = dec[t] * S
+                delta = beta[t] * (v[t] - S @ k[t])
+                S = S + np.outer(delta, k[t])
+                o[t] = S @ q[t]
+            inv = 1.0 / np.sqrt((o * o).mean(-1, keepdims=True) + eps)
+            z = X[:, 3 * QK + h * 128:3 * QK + (h + 1) * 128]
+            out = (o * inv * gnorm.astype(acc) * (z / (1.0 + np.exp(-z)))).astype(F16)
+            for i, r in enumerate(rows):
+                if i < alen and not write_a:
+                    continue
+                Y[r, h * 128:(h + 1) * 128] = out[i]
+    return Y
+
+
+def d3_forward(model: "Model", seqs, groups=None, acc=F32):
+    """D3Engine.logits (d3-engine.ts:67-139) on the shipped d3-lite layout: per layer the input RMSNorm (adding
+    the previous MLP output), then a Gated DeltaNet mixer (`in` product, gdn on d3_spans, `out` product) or a
+    gated attention layer (fused q | k | v | gate product, q/k RMSNorm over 256 with RoPE on the first
+    `rotary_dim` dims at each token's position, attention over pack_shared's key ranges at 1/sqrt(head_dim),
+    output times sigmoid(gate), `o` product), the post RMSNorm, SwiGLU; the final norm; READOUT at (row, code)
+    pairs. Returns (code logits f32 [pairs], final normed hidden f16 [T, H])."""
+    c = model.c
+    H, I, h, kv, D, eps = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["eps"]
+    LH = c["linear_heads"]
+    ids, meta, rng, pairs = pack_shared(seqs, groups)
+    spans = d3_spans(seqs, groups)
+    T = len(ids)
+    mask = ranges_mask(rng, T)
+    stride = (2 * h + 2 * kv) * D
+    ec, es, eb = model.t["embed"]
+    x = gather(ids, ec, es, eb)
+    o = None
+    for i, t in enumerate(c["layer_types"]):
+        p = f"layers.{i}."
+        x, normed = add_rmsnorm(x, o, model.t[p + "input_norm"], eps, add=i > 0, acc=acc)
+        if t == "linear_attention":
+            z = matmul(normed, model.w16(p + "in"), acc)
+            g = gdn(z, spans, LH, model.t[p + "conv"], model.t[p + "A_log"], model.t[p + "dt_bias"], model.t[p + "gnorm"],
+                    eps, acc)
+            o = matmul(g, model.w16(p + "out"), acc)
+        else:
+            z = matmul(normed, model.w16(p + "qkvg"), acc)
+            z = qk_norm_rope(z, h, kv, D, meta[:, 3], model.t[p + "q_norm"], model.t[p + "k_norm"], False, eps,
+                             c["rope_theta"], rot=c["rotary_dim"], acc=acc)
+            y = attention(z, h, kv, D, mask, 1.0 / math.sqrt(D), acc, gate=z[:, (h + 2 * kv) * D:stride])
+            o = matmul(y, model.w16(p + "o"), acc)
+        x, normed = add_rmsnorm(x, o, model.t[p + "post_norm"], eps, acc=acc)
+        ab = matmul(normed, model.w16(p + "w13"), acc)
+        o = matmul(silu_mul(ab[:, :I], ab[:, I:], acc), model.w16(p + "w2"), acc)
+    x, normed = add_rmsnorm(x, o, model.t["final_norm"], eps, acc=acc)
+    return readout(normed, model.t["readout"], pairs), normed
 
 
 # ---------------------------------------------------------------- d1-omni's decision head (kernels.ts:186-283)

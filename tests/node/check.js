@@ -62,6 +62,8 @@ async function main(req) {
       const pk = host.packShared(req.seqs, req.groups === null ? undefined : req.groups);
       return { ids: typed(pk.ids), pos: typed(pk.pos), rng: typed(pk.rng), pairs: typed(pk.pairs), T: pk.T, P: pk.P };
     }
+    case "gdnspans":
+      return typed(host.gdnSpans(req.seqs, req.groups === null ? undefined : req.groups));
     case "packomni": {
       const pk = host.packOmni(req.seqs);
       const out = { T: pk.T, M: pk.M };

@@ -870,3 +870,78 @@ def test_head_ops_refuse_bad_shapes(pkg, ctx):
             rec.bias_act(2, 64, buf, buf, 3)
     finally:
         rec.abort()
+
+
+# ---------------------------------------------------------------- d3-lite's mixers
+
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_gated(pkg, ctx, split, monkeypatch):
+    """dj_attention_gated (attention256, d3-kernels.ts:180-240): attention over d3's key ranges (a shared trunk +
+    each question, noncausal within them) times sigmoid(gate), one f16 rounding, against the float64 oracle;
+    with the split-KV plan forced the merge applies the gate."""
+    if split:
+        monkeypatch.setenv("DJ_ATTN_SPLITS", "3")
+    dj = _dj()
+    rng = np.random.default_rng(81)
+    heads, kv, D = 8, 2, 256
+    seqs = [{"ids": [1] * 40 + [int(x) for x in rng.integers(0, 9, n)], "options": 2} for n in (12, 1, 30)]
+    ids, meta, r4, pairs = ref.pack_shared(seqs, [3])
+    T = len(ids)
+    stride = (2 * heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride))
+    dZ, dr, dO = ctx.array(Z), ctx.array(r4), ctx.alloc(T * heads * D * 2)
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    goff = (heads + 2 * kv) * D
+    run(ctx, lambda r: r.attention_gated(T, heads, kv, D, dZ, stride, src, src, dr, 1 / 16, dZ.at(goff * 2), stride, dO))
+    got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+    want = ref.attention(Z, heads, kv, D, ref.ranges_mask(r4, T), 1 / 16, np.float64, gate=Z[:, goff:]).astype(np.float64)
+    err = np.abs(got - want).max()
+    print(f"gated attention T{T}: max abs err {err:.2e}")
+    assert err < 4e-3
+
+
+def _gdn_case(rng, LH, seqs, groups):
+    ids, meta, r4, pairs = ref.pack_shared(seqs, groups)
+    spans = ref.d3_spans(seqs, groups)
+    T, QK = len(ids), LH * 128
+    stride = 4 * QK + 2 * LH + 16
+    Z = rand_f16(rng, (T, stride))
+    conv = rand_f16(rng, (3 * QK, 4), 0.5)
+    A_log = np.log(0.01 + 0.99 * rng.random(LH)).astype(np.float16)
+    dt = rand_f16(rng, (LH,), 0.5)
+    gn = (1 + 0.1 * rng.standard_normal(128)).astype(np.float16)
+    return T, stride, spans, Z, conv, A_log, dt, gn
+
+
+@pytest.mark.parametrize("groups", [None, [3, 1], [4]])
+def test_gdn(pkg, ctx, groups):
+    """dj_gdn (gdnLayer, d3-kernels.ts:9-149) against the oracle's textbook recurrence in float64: sequences longer
+    than a 32-token chunk and of one token, a shared trunk rescanned by each question and written once. Bound: the f16 output within 3e-3 of the largest value (the state runs in f32 over
+    up to 110 tokens; the conv rounding points are the oracle's)."""
+    rng = np.random.default_rng(90 + (0 if groups is None else sum(groups)))
+    LH = 4
+    state = [int(x) for x in rng.integers(0, 9, 45)]
+    lens = (70, 1, 33, 5)
+    seqs = [{"ids": (state if groups else []) + [int(x) for x in rng.integers(0, 9, n)], "options": 2} for n in lens]
+    T, stride, spans, Z, conv, A_log, dt, gn = _gdn_case(rng, LH, seqs, groups)
+    dZ, ds, dc, da, ddt, dg = (ctx.array(a) for a in (Z, spans, conv, A_log, dt, gn))
+    Y0 = np.full((T, LH * 128), 7.0, dtype=np.float16)
+    dY = ctx.array(Y0)
+    run(ctx, lambda r: r.gdn(T, len(spans), ds, LH, stride, dZ, dc, da, ddt, dg, 1e-6, dY))
+    got = dY.read(np.float16, (T, LH * 128)).astype(np.float64)
+    want = ref.gdn(Z, spans, LH, conv, A_log, dt, gn, 1e-6, np.float64).astype(np.float64)
+    err = np.abs(got - want).max()
+    print(f"gdn groups {groups} T{T}: max abs err {err:.2e} (max |y| {np.abs(want).max():.2f})")
+    assert err < 3e-3 * np.abs(want).max()
+    assert not np.isnan(got).any()
+
+
+def test_gdn_refuses_short_rows(pkg, ctx):
+    dj = _dj()
+    buf = ctx.alloc(4096)
+    rec = ctx.recorder()
+    try:
+        with pytest.raises(dj.DJError, match="hold fewer than"):
+            rec.gdn(4, 1, buf, 2, 100, buf, buf, buf, buf, buf, 1e-6, buf)
+    finally:
+        rec.abort()

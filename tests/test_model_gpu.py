@@ -39,6 +39,8 @@ def models(pkg, tmp_path_factory):
         "d3": synth.reduced("d3-attn-0.8b-q8", layers=2, vocab=4096),
         "lfm2": synth.reduced("lfm2-d1-3b-q4", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
         "omni": synth.reduced("d1-omni-q8", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
+        "d3lite": synth.reduced("d3-lite-q8", layers=4, vocab=4096,
+                                layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"]),
     }
     for k, cfg in specs.items():
         out[k] = synth.generate(cfg, str(root / k), seed=0, norm_std=0.1)
@@ -539,5 +541,58 @@ def test_decision_api_omni(pkg, models):
                     assert abs(a["noul"] - p[1]) < PROB_TOL  # [false, true] reversed to [yes, no]
                 else:
                     assert abs(a["confidence"] - p.max()) < PROB_TOL
+    finally:
+        d.destroy()
+
+
+def test_d3_lite_matches_oracle(pkg, models):
+    """The shipped d3-lite layout on the product path (D3Engine.logits_d3, d3-engine.ts:67-139): Gated DeltaNet
+    layers on gdn_spans' scans and a gated attention layer on pack_shared's ranges, with and without each request's
+    prefix shared: the final normed hidden state within 2e-2 relative L2 of the oracle, each question's code
+    probabilities within 1e-3; eager, captured and replayed forwards identical."""
+    from decision_js_amd.d3 import D3Engine
+    model = ref.Model(models["d3lite"])
+    rng = np.random.default_rng(25)
+    seqs, groups = _d3_requests(rng, 4096)
+    eng = D3Engine.load(models["d3lite"])
+    try:
+        for g in (groups, None):
+            runs = [eng.logits_d3(seqs, g) for _ in range(3)]  # eager, capture, replay
+            assert runs[0] == runs[1] == runs[2]
+            dbg = eng.logits_d3(seqs, g, debug=True)
+            assert dbg["logits"] == runs[0]
+            want, normed = ref.d3_forward(model, seqs, g, acc=np.float64)
+            assert rel_l2(dbg["debug"]["final"], normed) < HIDDEN_TOL
+            k = 0
+            for s, got in zip(seqs, runs[0]):
+                w = want[k:k + s["options"]]
+                k += s["options"]
+                assert max(abs(a - b) for a, b in zip(ref.softmax(got), ref.softmax(w))) < PROB_TOL
+    finally:
+        eng.destroy()
+
+
+def test_decision_api_d3_lite(pkg, models):
+    """The shipped d3-lite through the Decision API: kind d3 on D3Engine, answers equal the oracle's (temperature
+    softmax, a noul reversed from [false, true]), share_state reading each request's state once."""
+    from decision_js_amd.d1 import Decision
+    rng = np.random.default_rng(26)
+    V = 4096
+    model = ref.Model(models["d3lite"])
+    d = Decision.load(models["d3lite"])
+    try:
+        assert d.kind == "d3" and type(d.engine).__name__ == "D3Engine"
+        state = [int(x) for x in rng.integers(0, V, 70)]
+        qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""},
+                        "ids": [int(x) for x in rng.integers(0, V, 12)]},
+              "churn": {"type": "noul", "instructions": "?", "ids": [int(x) for x in rng.integers(0, V, 7)]}}
+        for share in (False, True):
+            d.share_state = share
+            r = d.system_one(state, qs)
+            seqs = [{"ids": state + q["ids"], "options": 3 if n == "topic" else 2} for n, q in qs.items()]
+            want, _ = ref.d3_forward(model, seqs, [2] if share else None, acc=np.float64)
+            topic, churn = ref.softmax(want[:3]), ref.softmax(want[3:])
+            assert abs(r["answers"]["topic"]["confidence"] - topic.max()) < PROB_TOL
+            assert abs(r["answers"]["churn"]["noul"] - churn[1]) < PROB_TOL
     finally:
         d.destroy()

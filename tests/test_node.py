@@ -429,3 +429,45 @@ def test_node_omni_matches_python_host(tmp_path):
             assert np.array_equal(np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
     finally:
         d.destroy()
+
+
+def test_gdn_spans_match_python_host():
+    """gdnSpans (Node) == d3.gdn_spans (Python) bit for bit, with and without groups."""
+    load_pkg()
+    from decision_js_amd import d3
+    rng = np.random.default_rng(6)
+    state = [int(x) for x in rng.integers(0, 9, 12)]
+    seqs = [{"ids": state + [int(x) for x in rng.integers(0, 9, n)], "options": 2} for n in (3, 1, 7, 2)]
+    for groups in (None, [3, 1], [4], [1, 1, 2]):
+        js = node({"cmd": "gdnspans", "seqs": seqs, "groups": groups})
+        assert np.array_equal(np.asarray(js, dtype=np.uint32), d3.gdn_spans(seqs, groups).reshape(-1)), groups
+
+
+@pytest.mark.gpu
+def test_node_d3_lite_matches_python_host(tmp_path):
+    """The shipped d3-lite layout through Node (kindOf -> runD3 -> D3Engine: DeltaNet and gated attention layers,
+    READOUT) against the Python host: identical code probabilities with and without shareState."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.reduced("d3-lite-q8", layers=4, vocab=4096,
+                        layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"])
+    mdir = synth.generate(cfg, str(tmp_path / "d3lite"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(18)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": "", "d": ""}, "ids": ids(16)},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(5)}}
+    batch = [[ids(90), qs], [ids(33), qs]]
+    js = node({"cmd": "d3", "model": mdir, "batch": batch}, timeout=300)
+    assert js["kind"] == "d3"
+    d = Decision.load(mdir)
+    try:
+        assert type(d.engine).__name__ == "D3Engine"
+        for share, key in ((False, "plain"), (True, "shared")):
+            d.share_state = share
+            py = d.probabilities_batch([(s, list(q.values())) for s, q in batch])
+            for a, b in zip(js[key], py):
+                for x, y in zip(a, b):
+                    assert np.allclose(x, y, rtol=0, atol=1e-12)
+    finally:
+        d.destroy()

@@ -800,3 +800,212 @@ def test_add_layernorm_matches_torch_layer_norm():
         want = F.layer_norm(_t(Xn.astype(np.float64)), (192,), _t(w), _t(b), 1e-5).numpy()
         assert np.abs(O.astype(np.float64) - want).max() < 2e-3 * np.abs(want).max()
         assert np.abs(O.astype(np.float64) - want).max() <= np.abs(want).max() * 2.0 ** -10  # one f16 rounding
+
+
+# ---------------------------------------------------------------- d3-lite: Gated DeltaNet and gated attention
+
+TINY_D3 = dict(layers=4, hidden=128, intermediate=192, heads=2, kv_heads=1, head_dim=64, rotary_dim=16, vocab=512,
+               layer_types=["linear_attention", "linear_attention", "full_attention", "linear_attention"],
+               linear_heads=2, linear_rows=1056, codes=["A", "B", "C", "D", "E"])
+
+
+@pytest.fixture(scope="module")
+def tiny_d3(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("d3")
+    return synth.generate(synth.reduced("d3-lite-q8", **TINY_D3), str(d / "d3"), norm_std=0.1, std=0.09)
+
+
+def _hf_qwen35(model: ref.Model):
+    """A transformers Qwen3_5TextModel holding the oracle model's weights (float64): zero-centred norms get the
+    file's folded weight minus one, the fused q | k | v | gate rows go back to per-head [q; gate] rows, the
+    DeltaNet's `in` rows split into in_proj_qkv / z / b / a (export-d3.py:66-100)."""
+    tr = pytest.importorskip("transformers")
+    c = model.c
+    H, I, h, kv, D, LH = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"], c["linear_heads"]
+    cfg = tr.Qwen3_5TextConfig(vocab_size=c["vocab"], hidden_size=H, intermediate_size=I, num_hidden_layers=len(c["layer_types"]),
+                               num_attention_heads=h, num_key_value_heads=kv, head_dim=D, linear_num_key_heads=LH,
+                               linear_num_value_heads=LH, linear_key_head_dim=128, linear_value_head_dim=128,
+                               linear_conv_kernel_dim=4, layer_types=c["layer_types"], rms_norm_eps=c["eps"],
+                               rope_parameters={"rope_theta": c["rope_theta"], "rope_type": "default",
+                                                "partial_rotary_factor": c["rotary_dim"] / D})
+    m = tr.Qwen3_5TextModel(cfg)
+    m.config._attn_implementation = "eager"
+    m = m.to(torch.float64).eval()
+    QK = LH * 128
+    one = lambda name: _t(model.t[name].astype(np.float64) - 1.0)  # noqa: E731  (1 + w folded at export)
+    sd = {"embed_tokens.weight": _t(model.w16("embed")), "norm.weight": one("final_norm")}
+    for i, t in enumerate(c["layer_types"]):
+        p = f"layers.{i}."
+        sd[p + "input_layernorm.weight"] = one(p + "input_norm")
+        sd[p + "post_attention_layernorm.weight"] = one(p + "post_norm")
+        w13 = model.w16(p + "w13")
+        sd[p + "mlp.gate_proj.weight"], sd[p + "mlp.up_proj.weight"] = _t(w13[:I]), _t(w13[I:])
+        sd[p + "mlp.down_proj.weight"] = _t(model.w16(p + "w2"))
+        if t == "linear_attention":
+            w = model.w16(p + "in")
+            q = p + "linear_attn."
+            sd[q + "in_proj_qkv.weight"] = _t(w[:3 * QK])
+            sd[q + "in_proj_z.weight"] = _t(w[3 * QK:4 * QK])
+            sd[q + "in_proj_b.weight"] = _t(w[4 * QK:4 * QK + LH])
+            sd[q + "in_proj_a.weight"] = _t(w[4 * QK + LH:4 * QK + 2 * LH])
+            sd[q + "conv1d.weight"] = _t(model.t[p + "conv"]).reshape(3 * QK, 1, 4)
+            sd[q + "A_log"] = _t(model.t[p + "A_log"])
+            sd[q + "dt_bias"] = _t(model.t[p + "dt_bias"])
+            sd[q + "norm.weight"] = _t(model.t[p + "gnorm"])
+            sd[q + "out_proj.weight"] = _t(model.w16(p + "out"))
+        else:
+            w = model.w16(p + "qkvg")
+            qw, kw, vw, gw = w[:h * D], w[h * D:(h + kv) * D], w[(h + kv) * D:(h + 2 * kv) * D], w[(h + 2 * kv) * D:]
+            q = p + "self_attn."
+            sd[q + "q_proj.weight"] = _t(np.concatenate([qw.reshape(h, D, H), gw.reshape(h, D, H)], 1).reshape(2 * h * D, H))
+            sd[q + "k_proj.weight"], sd[q + "v_proj.weight"] = _t(kw), _t(vw)
+            sd[q + "o_proj.weight"] = _t(model.w16(p + "o"))
+            sd[q + "q_norm.weight"], sd[q + "k_norm.weight"] = one(p + "q_norm"), one(p + "k_norm")
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    return m
+
+
+def _d3_seqs(rng, V):
+    state = [int(x) for x in rng.integers(0, V, 37)]
+    return [{"ids": state + [int(x) for x in rng.integers(0, V, n)], "options": k} for n, k in ((9, 3), (1, 2), (15, 5))]
+
+
+def _compare_d3(path, model=None, groups=None):
+    """The oracle's d3-lite forward (float64 accumulation, f16 storage points) against Qwen3_5TextModel on each
+    sequence alone with d3's noncausal attention (an all-zero additive mask; the DeltaNet is causal by its
+    recurrence): the final normed hidden state within 5e-3 relative L2 and the code logits within 1e-2 of their
+    scale. With `groups` the shared prefix is read once: the DeltaNet still scans it in front of each question,
+    and the attention sees the trunk and the question; the library model runs the same on trunk + question,
+    the trunk tokens attending only to the trunk."""
+    model = model or ref.Model(path)
+    c = model.c
+    seqs = _d3_seqs(np.random.default_rng(9), c["vocab"])
+    logits, normed = ref.d3_forward(model, seqs, groups, acc=np.float64)
+    hf = _hf_qwen35(ref.Model(path))
+    R = model.t["readout"].astype(np.float64)
+    ids, meta, rng, pairs = ref.pack_shared(seqs, groups)
+    k = 0
+    for s in seqs:
+        n = len(s["ids"])
+        if groups is None:
+            mask = torch.zeros(1, 1, n, n, dtype=torch.float64)
+            rows = None
+        else:  # trunk of 37 shared: its tokens see the trunk only
+            P = 37
+            mask = torch.zeros(1, 1, n, n, dtype=torch.float64)
+            mask[0, 0, :P, P:] = -1e30
+            rows = None
+        with torch.no_grad():
+            final = hf(input_ids=torch.tensor([s["ids"]]), attention_mask={"full_attention": mask, "linear_attention": None}).last_hidden_state[0].numpy()
+        last = int(pairs[k][0])
+        got_last = normed[last].astype(np.float64)
+        assert _rel_l2(got_last, final[-1]) < 5e-3, "final hidden state at the readout row"
+        want = final[-1] @ R[:s["options"]].T
+        got = logits[k:k + s["options"]].astype(np.float64)
+        assert np.abs(got - want).max() < 1e-2 * max(np.abs(want).max(), 1e-3), "code logits"
+        k += s["options"]
+    if groups is None:  # every row of the first sequence (rows 0..n-1 of the packing)
+        n0 = len(seqs[0]["ids"])
+        with torch.no_grad():
+            final = hf(input_ids=torch.tensor([seqs[0]["ids"]]),
+                       attention_mask={"full_attention": torch.zeros(1, 1, n0, n0, dtype=torch.float64),
+                                       "linear_attention": None}).last_hidden_state[0].numpy()
+        assert _rel_l2(normed[:n0], final) < 5e-3
+
+
+def test_d3_forward_matches_transformers(tiny_d3):
+    _compare_d3(tiny_d3)
+
+
+def test_d3_forward_shared_prefix_matches_transformers(tiny_d3):
+    _compare_d3(tiny_d3, groups=[3])
+
+
+def test_d3_spans_match_oracle_and_packing(pkg):
+    """gdn_spans (the product path) == the oracle's d3_spans bit for bit, and every scan's rows are exactly its
+    question's tokens of pack_shared's layout, trunk first."""
+    from decision_js_amd import d3
+    rng = np.random.default_rng(4)
+    for groups in ([3, 1, 2], None, [1, 1, 1, 1, 1, 1], [6]):
+        seqs = []
+        for g in (groups or [1] * 6):
+            state = [int(x) for x in rng.integers(0, 9, rng.integers(0, 6))]
+            for _ in range(g):
+                seqs.append({"ids": state + [int(x) for x in rng.integers(0, 9, rng.integers(1, 5))], "options": 2})
+        seqs = seqs[:6] if groups is None else seqs
+        got = d3.gdn_spans(seqs, groups)
+        assert np.array_equal(got, ref.d3_spans(seqs, groups))
+        ids = ref.pack_shared(seqs, groups)[0]
+        for s, (a0, aw, b0, bl) in zip(seqs, got):
+            rows = list(range(a0, a0 + (aw & 0x7fffffff))) + list(range(b0, b0 + bl))
+            assert [int(ids[r]) for r in rows] == s["ids"]
+
+
+@pytest.mark.parametrize("slip", ["conv_taps_reversed", "decay_after_update", "no_q_scale", "no_gate", "full_rotary"])
+def test_planted_d3_slips_are_caught(tiny_d3, monkeypatch, slip):
+    """The conv taps in reverse order; the decay applied after the delta update; q not scaled by 128^-1/2; the
+    attention's output gate dropped; RoPE over the whole head instead of rotary_dim."""
+    model = ref.Model(tiny_d3)
+    if slip == "conv_taps_reversed":
+        for i, t in enumerate(model.c["layer_types"]):
+            if t == "linear_attention":
+                model.t[f"layers.{i}.conv"] = np.ascontiguousarray(model.t[f"layers.{i}.conv"][:, ::-1])
+    elif slip == "decay_after_update":
+        def gdn(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc=np.float32):
+            # the same as ref.gdn with S <- S + delta k^T applied before S <- decay S
+            return _gdn_variant(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc, decay_last=True)
+        monkeypatch.setattr(ref, "gdn", gdn)
+    elif slip == "no_q_scale":
+        def gdn(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc=np.float32):
+            return _gdn_variant(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc, q_scale=1.0)
+        monkeypatch.setattr(ref, "gdn", gdn)
+    elif slip == "no_gate":
+        orig = ref.attention
+        monkeypatch.setattr(ref, "attention", lambda *a, gate=None, **k: orig(*a, **k))
+    else:
+        model.c["rotary_dim"] = model.c["head_dim"]
+    with pytest.raises(AssertionError):
+        _compare_d3(tiny_d3, model)
+
+
+def _gdn_variant(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc, decay_last=False, q_scale=None):
+    """ref.gdn with one step changed (planted slips only)."""
+    T, QK = Z.shape[0], LH * 128
+    Y = np.zeros((T, QK), dtype=np.float16)
+    W = conv_w.astype(acc).reshape(3 * QK, 4)
+    for a0, aw, b0, bl in np.asarray(spans, dtype=np.int64):
+        alen, write_a = int(aw) & 0x7fffffff, (int(aw) >> 31) & 1
+        rows = list(range(a0, a0 + alen)) + list(range(b0, b0 + bl))
+        n = len(rows)
+        X = Z[rows].astype(acc)
+        for h in range(LH):
+            ch = np.concatenate([np.arange(128) + h * 128, QK + np.arange(128) + h * 128, 2 * QK + np.arange(128) + h * 128])
+            x = np.concatenate([np.zeros((3, len(ch)), dtype=acc), X[:, ch]])
+            y = sum(W[ch][:, j][None, :] * x[j:j + n] for j in range(4))
+            y = (y / (1.0 + np.exp(-y))).astype(np.float16).astype(acc)
+            q, k, v = y[:, :128], y[:, 128:256], y[:, 256:]
+            q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6) * (q_scale if q_scale is not None else 1 / np.sqrt(128.0))
+            k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+            a = X[:, 4 * QK + LH + h] + acc(dt_bias[h])
+            dec = np.exp(-np.exp(acc(A_log[h])) * np.where(a > 20, a, np.log1p(np.exp(np.minimum(a, 20)))))
+            beta = 1.0 / (1.0 + np.exp(-X[:, 4 * QK + h]))
+            S = np.zeros((128, 128), dtype=acc)
+            o = np.zeros((n, 128), dtype=acc)
+            for t in range(n):
+                if not decay_last:
+                    S = dec[t] * S
+                delta = beta[t] * (v[t] - S @ k[t])
+                S = S + np.outer(delta, k[t])
+                if decay_last:
+                    S = dec[t] * S
+                o[t] = S @ q[t]
+            inv = 1.0 / np.sqrt((o * o).mean(-1, keepdims=True) + eps)
+            z = X[:, 3 * QK + h * 128:3 * QK + (h + 1) * 128]
+            out = (o * inv * gnorm.astype(acc) * (z / (1.0 + np.exp(-z)))).astype(np.float16)
+            for i, r in enumerate(rows):
+                if i < alen and not write_a:
+                    continue
+                Y[r, h * 128:(h + 1) * 128] = out[i]
+    return Y
