@@ -392,6 +392,8 @@ def run_workload(args):
         eng.destroy()
     elif args.workload == "omni":
         out = omni_ticket(args, steps, warmup)
+    elif args.workload == "d3lite":
+        out = d3_lite_ticket(args, steps, warmup)
     else:
         from decision_js_amd.encoder import EncoderEngine, cosine_logits
         cfg = synth.CONFIGS["eg2-encoder-q8"]
@@ -500,6 +502,56 @@ def omni_ticket(args, steps, warmup):
                                                         "model": "d1-omni-600M q8 (real weights)", "source": "README.md:31"}})
 
 
+def d3_lite_ticket(args, steps, warmup):
+    """d3-lite tickets on its shipped layout (the reference publishes 95 ms per ticket, 58 ms with shareState, on
+    an Apple M5 Pro, README.md:33, 44): 3 questions over one 340-id state, each question a 384-id sequence with 2 /
+    3 / 5 codes read at its last token, packed in one forward (T = 1152; with shareState the state is read once:
+    T = 472). A step is one ticket of each form, inputs packed and uploaded by the host (as the API does)."""
+    from decision_js_amd import synth
+    from decision_js_amd.d3 import D3Engine
+    cfg = synth.CONFIGS["d3-lite-q8"]
+    mdir = os.path.join(args.model_dir, "d3-lite-q8")
+    synth.generate(cfg, mdir, seed=0, threads=16)
+    eng = D3Engine.load(mdir, {"graphs": not args.no_graphs})
+    rng = np.random.Generator(np.random.PCG64(1))
+    V = cfg["vocab"]
+    tickets = []
+    for _ in range(warmup + steps):
+        state = [int(x) for x in rng.integers(0, V, 340)]
+        tickets.append([{"ids": state + [int(x) for x in rng.integers(0, V, 44)], "options": k} for k in (2, 3, 5)])
+    res = {}
+    for name, groups in (("plain", None), ("shared", [3])):
+        for t in tickets[:warmup]:
+            eng.logits_d3(t, groups)
+        eng.ctx.timer_begin()
+        t0 = time.perf_counter()
+        for t in tickets[warmup:]:
+            eng.logits_d3(t, groups)
+        wall = time.perf_counter() - t0
+        res[name] = (1e3 * wall / steps, eng.ctx.timer_end() / steps)
+        log(f"d3-lite {name}: {res[name][0]:.3f} ms per ticket wall, {res[name][1]:.3f} ms GPU")
+    eng.graphs = False
+    eng.ctx.profile_reset()
+    eng.ctx.profile(True)
+    for t in tickets[:3]:
+        eng.logits_d3(t)
+    eng.ctx.profile(False)
+    table = eng.ctx.profile_table()
+    total = sum(v[0] for v in table.values())
+    for k, (t_ms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
+        log(f"  {k:48s} {t_ms / 3:8.4f} ms/ticket  {100 * t_ms / total:5.1f}%  ({cnt // 3}/ticket, {1e3 * t_ms / cnt:7.2f} us each)")
+    eng.destroy()
+    ms, gpu = res["plain"]
+    return _line("decisions/sec (d3-lite tickets: 3 questions, one 384-id sequence each) on 1 MI355X", 3e3 / ms,
+                 "decisions/s", steps, warmup, ms, "f16",
+                 "d3-lite-q8 (Qwen3.5-0.8B-shaped: 18 Gated DeltaNet + 6 gated attention layers), 3 x 384 random ids in one "
+                 "forward, 2/3/5 codes", None,
+                 {"gpu_ms_per_step": round(gpu, 4), "share_state_ms_per_ticket": round(res["shared"][0], 4),
+                  "share_state_gpu_ms": round(res["shared"][1], 4),
+                  "reference_published_ms_per_ticket": {"value": 95.0, "share_state": 58.0, "hardware": "Apple M5 Pro, Chrome WebGPU",
+                                                        "model": "d3-lite q8 (real weights)", "source": "README.md:33, 44"}})
+
+
 def _linear_shapes(c):
     """(N, K) of one decoder layer's linears: qkv, o_proj, w13, w2."""
     H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
@@ -518,7 +570,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calib-mb", type=int, default=0, help="also run a plain device copy of this many MiB (counter calibration)")
-    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni"],
+    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni", "d3lite"],
                     help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
                          "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
     ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")

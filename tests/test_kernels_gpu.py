@@ -913,11 +913,15 @@ def _gdn_case(rng, LH, seqs, groups):
     return T, stride, spans, Z, conv, A_log, dt, gn
 
 
+@pytest.mark.parametrize("form", ["split", "whole"])
 @pytest.mark.parametrize("groups", [None, [3, 1], [4]])
-def test_gdn(pkg, ctx, groups):
+def test_gdn(pkg, ctx, groups, form, monkeypatch):
     """dj_gdn (gdnLayer, d3-kernels.ts:9-149) against the oracle's textbook recurrence in float64: sequences longer
-    than a 32-token chunk and of one token, a shared trunk rescanned by each question and written once. Bound: the f16 output within 3e-3 of the largest value (the state runs in f32 over
+    than a 32-token chunk and of one token, a shared trunk rescanned by each question and written once; both forms
+    (state rows split over 8 workgroups with the norm in a second kernel, and one workgroup per head). Bound: the f16 output within 3e-3 of the largest value (the state runs in f32 over
     up to 110 tokens; the conv rounding points are the oracle's)."""
+    if form == "whole":
+        monkeypatch.setenv("DJ_GDN_FORM", "1")
     rng = np.random.default_rng(90 + (0 if groups is None else sum(groups)))
     LH = 4
     state = [int(x) for x in rng.integers(0, 9, 45)]
