@@ -77,6 +77,8 @@ SIGNATURES = {
     "dj_attention_noalloc": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_attention_gated": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P, _I, _P],
     "dj_gdn": [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _P, _F, _P],
+    "dj_ple_mix": [_P, _I, _I, _P, _P, _P, _F, _P],
+    "dj_pool_project": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "dj_kv_store": [_P, _I, _I, _I, _P, _I, _I, _P, _I],
     "dj_leaf_logits": [_P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P],
     "dj_readout": [_P, _I, _I, _I, _P, _P, _I, _P, _P],
@@ -314,6 +316,12 @@ class Recorder:
     def gdn(self, T, nspans, spans, LH, stride, Z, conv_w, A_log, dt_bias, gnorm, eps, Y):
         check(lib().dj_gdn(self.h, T, nspans, ptr(spans), LH, stride, ptr(Z), ptr(conv_w), ptr(A_log), ptr(dt_bias),
                            ptr(gnorm), eps, ptr(Y)))
+
+    def ple_mix(self, T, P, G, E, w, eps, O):
+        check(lib().dj_ple_mix(self.h, T, P, ptr(G), ptr(E), ptr(w), eps, ptr(O)))
+
+    def pool_project(self, T, S, H, N, X, seqs, W, out):
+        check(lib().dj_pool_project(self.h, T, S, H, N, ptr(X), ptr(seqs), ptr(W), ptr(out)))
 
     def attention_noalloc(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention_noalloc(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))

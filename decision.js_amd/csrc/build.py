@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 LIB = os.path.join(PKG, "lib", "libdj.so")
-SOURCES = ["dj_runtime.hip", "dj_ops.hip", "dj_gemm.hip", "dj_attn.hip", "dj_head.hip", "dj_gdn.hip"]
+SOURCES = ["dj_runtime.hip", "dj_ops.hip", "dj_gemm.hip", "dj_attn.hip", "dj_head.hip", "dj_gdn.hip", "dj_eg2.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

@@ -430,6 +430,117 @@ __global__ __launch_bounds__(256) void k_attn_combine(int T, int heads, int spli
   }
 }
 
+// 512-dim heads (EmbeddingGemma 2's global layers, eg2-kernels.ts:98-163): a VALU form. A workgroup holds 16
+// queries of one head, 16 lanes per query and 32 dims per lane (dims 8 part + 128 j .. +7, so the 16 lanes of a
+// query read 256 consecutive bytes of a key row); key/value tiles of 16 rows x 512 dims in LDS; per tile the 16
+// scores first (lane partials added over the 16 lanes), one online-softmax update, then P V. Both key ranges of
+// each query (over sources A and B) are walked; a query's keys outside its ranges weigh zero.
+constexpr int WD = 512, WQ = 16, WK = 16;
+__global__ __launch_bounds__(256) void k_attn_wide(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
+                                                   dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
+                                                   uint16_t *__restrict__ O, dj_attn_gate gate) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks[WK * WD];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[WK * WD];
+  __shared__ int4 bounds;
+  const int tid = threadIdx.x, qi = tid / 16, part = tid % 16;
+  const int h = blockIdx.y, kvh = h / (heads / kv);
+  const int q0 = blockIdx.x * WQ, t = min(q0 + qi, T - 1);
+  const bool live = q0 + qi < T;
+  float q[32];
+  {
+    const uint16_t *qr = Q + (size_t)t * q_stride + (size_t)h * WD + 8 * part;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const h8 v = *(const h8 *)(qr + 128 * j);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[8 * j + e] = (float)v[e] * scale;
+    }
+  }
+  const int4 r = rng[t];
+  // the block's key span per source: min of starts, max of ends over its live queries
+  if (tid == 0) bounds = make_int4(INT32_MAX, 0, INT32_MAX, 0);
+  __syncthreads();
+  if (part == 0 && live) {
+    if (r.y > r.x) {
+      atomicMin(&bounds.x, r.x);
+      atomicMax(&bounds.y, r.y);
+    }
+    if (r.w > r.z) {
+      atomicMin(&bounds.z, r.z);
+      atomicMax(&bounds.w, r.w);
+    }
+  }
+  __syncthreads();
+  const int4 bd = bounds;
+  float m = -1e30f, l = 0.f, acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  for (int src = 0; src < 2; ++src) {
+    const dj_kv_src X = src ? B : A;
+    const int lo = src ? bd.z : bd.x, hi = src ? bd.w : bd.y;
+    const int mylo = src ? r.z : r.x, myhi = src ? r.w : r.y;
+    for (int k0 = lo; k0 < hi; k0 += WK) {
+      // stage K and V rows k0 .. k0 + 15 (clamped to the source), 16 bytes per thread per pass
+      for (int i = tid; i < WK * WD / 8; i += 256) {
+        const int row = i / (WD / 8), c8 = (i % (WD / 8)) * 8;
+        const int kr = min(max(k0 + row, 0), X.rows - 1);
+        const uint16_t *base = X.base + (size_t)kr * X.stride;
+        *(uint4 *)(ks + row * WD + c8) = *(const uint4 *)(base + X.k_col + kvh * WD + c8);
+        *(uint4 *)(vs + row * WD + c8) = *(const uint4 *)(base + X.v_col + kvh * WD + c8);
+      }
+      __syncthreads();
+      float sc[WK];
+      float mb = m;
+#pragma unroll
+      for (int j = 0; j < WK; ++j) {
+        float d = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const h8 kv8 = *(const h8 *)(ks + j * WD + 128 * c + 8 * part);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d += q[8 * c + e] * (float)kv8[e];
+        }
+        d = group_sum<16>(d);
+        const int key = k0 + j;
+        sc[j] = key >= mylo && key < myhi && key < hi ? d : -1e30f;
+        mb = fmaxf(mb, sc[j]);
+      }
+      const float corr = expf(m - mb);
+      l *= corr;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] *= corr;
+#pragma unroll
+      for (int j = 0; j < WK; ++j) {
+        const float p = sc[j] > -1e29f ? expf(sc[j] - mb) : 0.f;
+        l += p;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const h8 v8 = *(const h8 *)(vs + j * WD + 128 * c + 8 * part);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[8 * c + e] += p * (float)v8[e];
+        }
+      }
+      m = mb;
+      __syncthreads();
+    }
+  }
+  if (!live) return;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  uint16_t *orow = O + (size_t)t * heads * WD + (size_t)h * WD + 8 * part;
+  const uint16_t *grow = gate.g ? gate.g + (size_t)t * gate.stride + (size_t)h * WD + 8 * part : nullptr;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    h8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[8 * c + e] * inv;
+      if (grow) v = v / (1.0f + expf(-(float)__builtin_bit_cast(_Float16, grow[128 * c + e])));
+      o[e] = (_Float16)v;
+    }
+    *(h8 *)(orow + 128 * c) = o;
+  }
+}
+
 // Launch with one workgroup shape; a shape whose K/V tile does not split into whole 1 KB DMAs per wave is never
 // picked, nor one that would spill registers (the launcher falls back to HG 1 for them).
 template <int D, int RING, int KG, int HG>
@@ -464,6 +575,11 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
                         dj_attn_gate gate) {
   hipStream_t s = c->stream;
+  if (D == WD) {  // 512-dim heads: the VALU form, whole
+    k_attn_wide<<<dim3(dj_cdiv(T, WQ), heads), 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, (const int4 *)rng, scale, O,
+                                                            gate);
+    return DJ_OK;
+  }
   const int qblocks = dj_cdiv(T, 64);
   const long grid = (long)qblocks * heads;
   const int4 *r4 = (const int4 *)rng;
@@ -525,7 +641,7 @@ extern "C" int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const 
   DJ_REQUIRE(Q && rng && O && T >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && q_stride % 8 == 0 &&
                  q_stride >= heads * D,
              "decision.js: attention: bad arguments (heads %d, kv %d, q_stride %d)", heads, kv, q_stride);
-  DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(D == 64 || D == 128 || D == 256 || D == 512, "decision.js: attention head dim %d (64, 128, 256 or 512)", D);
   DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_OP_BEGIN(rec, "attention");
@@ -546,7 +662,7 @@ extern "C" int dj_attention_gated(dj_rec *rec, int T, int heads, int kv, int D, 
                  q_stride >= heads * D && g_stride % 8 == 0 && g_stride >= heads * D && ((uintptr_t)G & 7) == 0,
              "decision.js: attention_gated: bad arguments (heads %d, kv %d, q_stride %d, g_stride %d)", heads, kv,
              q_stride, g_stride);
-  DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(D == 64 || D == 128 || D == 256 || D == 512, "decision.js: attention head dim %d (64, 128, 256 or 512)", D);
   DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_OP_BEGIN(rec, "attention_gated");
@@ -583,13 +699,13 @@ extern "C" int dj_attention_noalloc(dj_rec *rec, int T, int heads, int kv, int D
   DJ_REQUIRE(Q && rng && O && T >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && q_stride % 8 == 0 &&
                  q_stride >= heads * D,
              "decision.js: attention: bad arguments (heads %d, kv %d, q_stride %d)", heads, kv, q_stride);
-  DJ_REQUIRE(D == 64 || D == 128 || D == 256, "decision.js: attention head dim %d (64, 128 or 256)", D);
+  DJ_REQUIRE(D == 64 || D == 128 || D == 256 || D == 512, "decision.js: attention head dim %d (64, 128, 256 or 512)", D);
   DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
   DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D), "decision.js: attention: bad key/value source");
   DJ_REQUIRE(rec && rec->ctx && rec->ctx->attn_scratch, "decision.js: dj_attention_noalloc: no recorder or scratch");
   // the plan dj_attention takes; refused (not shrunk) where its partials exceed the scratch, so both entry
   // points always compute the same thing
-  const int splits = attn_splits(rec->ctx->cus, T, heads, D, A, B, rec->ctx->gemm_ws ? rec->ctx->gemm_ws_floats : 0);
+  const int splits = D == WD ? 1 : attn_splits(rec->ctx->cus, T, heads, D, A, B, rec->ctx->gemm_ws ? rec->ctx->gemm_ws_floats : 0);
   const size_t need = splits > 1 ? (size_t)splits * T * heads * (D + 2) : 0;
   DJ_REQUIRE(need <= kScratchFloats,
              "decision.js: dj_attention_noalloc: T %d x %d heads of %d dims split %d ways needs %.1f MB of scratch, "

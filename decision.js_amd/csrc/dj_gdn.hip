@@ -179,7 +179,7 @@ __global__ __launch_bounds__(NT2) void k_gdn_scan(int T, int LH, int stride, con
   __shared__ __attribute__((aligned(16))) float ks[C * DK];
   __shared__ float vs[C * RW];   // v, then o
   __shared__ float4 gs[C];       // (decay, beta, k . q, -)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int rs = blockIdx.x % RS, h = (blockIdx.x / RS) % LH;
   const uint4 sp = spans[blockIdx.x / (RS * LH)];
   const Span S{sp.x, sp.y & 0x7fffffffu, sp.z, sp.w, (sp.y >> 31) != 0};

@@ -146,6 +146,8 @@ struct dj_attn_gate {
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
                         dj_attn_gate gate = dj_attn_gate{nullptr, 0});
+// Mean of each sequence's rows of X [T, H] into out [S, H] f32 (seqs: (start, end) pairs).
+void dj_launch_mean_pool(hipStream_t s, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out);
 // Takes the device address of the static attention scratch on the current device into c->attn_scratch.
 int dj_attn_scratch_init(dj_ctx *c);
 int dj_launch_copy(hipStream_t s, void *dst, const void *src, size_t bytes);

@@ -556,10 +556,14 @@ __global__ __launch_bounds__(256) void k_mean_pool(int T, int H, const uint16_t 
   }
 }
 
+void dj_launch_mean_pool(hipStream_t s, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out) {
+  k_mean_pool<<<dim3(S, dj_cdiv(H, 64)), 256, 0, s>>>(T, H, X, seqs, out);
+}
+
 extern "C" int dj_mean_pool(dj_rec *rec, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out) {
   DJ_REQUIRE(X && seqs && out && T > 0 && S >= 0 && H > 0, "decision.js: mean_pool: bad arguments");
   DJ_OP_BEGIN(rec, "mean_pool");
-  if (S > 0) k_mean_pool<<<dim3(S, dj_cdiv(H, 64)), 256, 0, rec->ctx->stream>>>(T, H, X, seqs, out);
+  if (S > 0) dj_launch_mean_pool(rec->ctx->stream, T, S, H, X, seqs, out);
   return dj_op_end(rec, "mean_pool");
 }
 

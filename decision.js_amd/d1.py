@@ -17,6 +17,7 @@ import threading
 import numpy as np
 
 from . import questions as Q
+from .eg2 import Eg2Engine
 from .eg2_head import Eg2Head
 from .encoder import EncoderEngine, cosine_logits
 from .d3 import D3Engine
@@ -116,7 +117,8 @@ class Decision:
         if kind == "laya":
             raise ValueError("decision.js: Laya (ModernBERT) models do not run on this build")
         d3 = D3Engine if "linear_heads" in config else DecoderEngine  # the shipped d3-lite, or its attention-only form
-        engine = {"d1-3b": DecoderEngine, "d3": d3, "eg2": EncoderEngine, "d1-omni": OmniEngine}[kind].load(base, opts)
+        eg2 = Eg2Engine if "ple" in config else EncoderEngine  # the shipped EmbeddingGemma 2, or the configs[0] form
+        engine = {"d1-3b": DecoderEngine, "d3": d3, "eg2": eg2, "d1-omni": OmniEngine}[kind].load(base, opts)
         # the reference's defaults (d1.ts:78): 4096 tokens per pass for d1-3B, 8192 otherwise; pass a larger
         # tokens_per_pass to pack more requests into one forward (MI355X activations take ~25 KB per token)
         tpp = opts.get("tokens_per_pass") or opts.get("tokensPerPass") or (4096 if kind == "d1-3b" else 8192)

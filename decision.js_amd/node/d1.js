@@ -14,6 +14,7 @@ const { DecoderEngine } = require("./engine");
 const { EncoderEngine, cosineLogits } = require("./encoder");
 const { OmniEngine, temperature: omniTemperature } = require("./omni");
 const { D3Engine } = require("./d3");
+const { Eg2Engine } = require("./eg2");
 const { criterion } = require("./py");
 const { Eg2Head } = require("./eg2_head");
 const { fileFetch } = require("./format");
@@ -71,7 +72,8 @@ class D1 {
     const manifest = await (await opts.fetch(`${base}manifest.json`)).json();
     const kind = kindOf(manifest.config);
     if (kind === "laya") throw new Error("decision.js: Laya (ModernBERT) models do not run on this build");
-    const engine = kind === "eg2" ? await EncoderEngine.load(base, opts) : kind === "d1-omni" ? await OmniEngine.load(base, opts)
+    const engine = kind === "eg2" ? await ("ple" in manifest.config ? Eg2Engine : EncoderEngine).load(base, opts) // shipped / configs[0]
+      : kind === "d1-omni" ? await OmniEngine.load(base, opts)
       : kind === "d3" && "linear_heads" in manifest.config ? await D3Engine.load(base, opts) // the shipped d3-lite
       : await DecoderEngine.load(base, opts);
     return new D1(kind, engine, opts);

@@ -134,6 +134,8 @@ class Recorder {
   attentionGated(T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O) {
     lib().attentionGated(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O);
   }
+  pleMix(T, P, G, E, w, eps, O) { lib().pleMix(this.h, T, P, G, E, w, eps, O); }
+  poolProject(T, S, H, N, X, seqs, W, out) { lib().poolProject(this.h, T, S, H, N, X, seqs, W, out); }
   gdn(T, nspans, spans, LH, stride, Z, convW, Alog, dtBias, gnorm, eps, Y) {
     lib().gdn(this.h, T, nspans, spans, LH, stride, Z, convW, Alog, dtBias, gnorm, eps, Y);
   }

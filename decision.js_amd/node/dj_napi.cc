@@ -481,6 +481,16 @@ napi_value Gdn(napi_env env, napi_callback_info info) {
   END(dj_gdn(R(0), I(1), I(2), PU32(3), I(4), I(5), P16(6), P16(7), P16(8), P16(9), P16(10), F(11), P16(12)));
 }
 
+napi_value PleMix(napi_env env, napi_callback_info info) {
+  BEGIN(8);
+  END(dj_ple_mix(R(0), I(1), I(2), P16(3), P16(4), P16(5), F(6), P16(7)));
+}
+
+napi_value PoolProject(napi_env env, napi_callback_info info) {
+  BEGIN(9);
+  END(dj_pool_project(R(0), I(1), I(2), I(3), I(4), P16(5), PU32(6), P16(7), PF32(8)));
+}
+
 napi_value KvStore(napi_env env, napi_callback_info info) {
   BEGIN(9);
   END(dj_kv_store(R(0), I(1), I(2), I(3), P16(4), I(5), I(6), P16(7), I(8)));
@@ -547,7 +557,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
       {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
-      {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"attentionGated", AttentionGated}, {"gdn", Gdn}, {"addRows", AddRows}, {"biasAct", BiasAct},
+      {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"attentionGated", AttentionGated}, {"gdn", Gdn}, {"pleMix", PleMix},
+      {"poolProject", PoolProject}, {"addRows", AddRows}, {"biasAct", BiasAct},
       {"addLayernorm", AddLayernorm}, {"gatherRows", GatherRows}, {"score", Score}, {"meanPool", MeanPool}, {"denseF32", DenseF32},
   };
   for (const auto &f : fns) {

@@ -8,10 +8,12 @@ const { loadWeights } = require("./format");
 const { GpuEngine, layoutFor } = require("./engine");
 
 /** Eg2Engine.embed's packing (eg2-engine.ts:74-86): per token meta (start, end, -1, i) and its key range on
- * the global layers [start, end); per sequence (start, end). */
-function packEncoder(seqs) {
+ * the global layers [start, end) and, with a window, on the sliding layers [max(start, t-w), min(end, t+w+1));
+ * per sequence (start, end). */
+function packEncoder(seqs, window) {
   const T = seqs.reduce((a, s) => a + s.length, 0), S = seqs.length;
   const ids = new Uint32Array(T), meta = new Int32Array(T * 4), full = new Int32Array(T * 4), ranges = new Uint32Array(S * 2);
+  const slide = window === undefined ? null : new Int32Array(T * 4);
   let off = 0;
   seqs.forEach((s, k) => {
     for (let i = 0; i < s.length; ++i) {
@@ -20,12 +22,16 @@ function packEncoder(seqs) {
       meta.set([off, off + s.length, -1, i], 4 * t);
       full[4 * t] = off;
       full[4 * t + 1] = off + s.length;
+      if (slide) {
+        slide[4 * t] = Math.max(off, t - window);
+        slide[4 * t + 1] = Math.min(off + s.length, t + window + 1);
+      }
     }
     ranges[2 * k] = off;
     ranges[2 * k + 1] = off + s.length;
     off += s.length;
   });
-  return { ids, meta, full, ranges, T, S };
+  return { ids, meta, full, slide, ranges, T, S };
 }
 
 /** The cosine prior of Eg2Head.logits (eg2-head.ts:82-84, 97): cos(option, state + question). */

@@ -6,6 +6,7 @@ const { DecoderEngine, packForest, packShared, groupMax } = require("./engine");
 const { EncoderEngine, packEncoder } = require("./encoder");
 const { OmniEngine, packOmni } = require("./omni");
 const { D3Engine, gdnSpans } = require("./d3");
+const { Eg2Engine } = require("./eg2");
 const { Eg2Head } = require("./eg2_head");
 const { loadWeights, fileFetch } = require("./format");
 const questions = require("./questions");
@@ -13,5 +14,5 @@ const dj = require("./dj");
 
 module.exports = {
   D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, OmniEngine,
-  D3Engine, Eg2Head, packForest, packShared, packEncoder, packOmni, gdnSpans, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+  D3Engine, Eg2Engine, Eg2Head, packForest, packShared, packEncoder, packOmni, gdnSpans, groupMax, loadWeights, fileFetch, softmax, questions, dj,
 };

@@ -71,6 +71,20 @@ CONFIGS = {
                        choices={"norm_weights": 1.0, "layer_types": "LFM2-350M's pattern (not stated)",
                                 "head": "2 layers, 16 heads, ff 4096 (not stated)", "biases": "N(0, 0.1)",
                                 "type_emb": "N(0, 0.5)", "temperatures": "synthetic"}),
+    # EmbeddingGemma 2 as shipped (Eg2Engine, eg2-engine.ts; export-eg2.py): a 24-layer bidirectional Gemma text
+    # encoder at hidden 512 with per-layer embeddings (PLE_MIX's 512-wide rows), 256-dim heads on the sliding
+    # layers (a +-512-token window) and 512-dim heads on every sixth (global) layer, the f16 embedding projection
+    # after mean pooling, and the learned decision head on the host. Heads, widths, thetas, the projection width
+    # and the head width are choices (export-eg2.py writes them from the checkpoint).
+    "eg2-q8": dict(model="eg2", bits=8, layers=24, hidden=512, intermediate=2048, heads=4, vocab=262144, eps=1e-6,
+                   layer_types=["full_attention" if i % 6 == 5 else "sliding_attention" for i in range(24)], window=512,
+                   head_dim={"sliding_attention": 256, "full_attention": 512},
+                   kv_heads={"sliding_attention": 1, "full_attention": 1},
+                   rope_theta={"sliding_attention": 1e4, "full_attention": 1e6}, ple=512, embedding_dim=768,
+                   embed_dim=768, learned_head={"width": 256},
+                   choices={"norm_weights": 1.0, "heads": "4 query / 1 kv per layer type (not stated)",
+                            "intermediate": "2048 (not stated)", "rope_theta": "1e4 sliding, 1e6 global (not stated)",
+                            "embedding_dim": "768 (not stated)", "layer_scalars": 1.0}),
     # EmbeddingGemma-shaped bidirectional encoder, q8, mean-pool + 768->3072->768 head
     "eg2-encoder-q8": dict(model="encoder", bits=8, layers=24, hidden=768, intermediate=1152, heads=3, kv_heads=1,
                            head_dim=256, vocab=262144, eps=1e-6, rope_theta=1e4, head_width=3072, embed_dim=768,
@@ -104,6 +118,8 @@ def _norm(name, n, norm_std, seed):
 
 def tensor_plan(cfg: dict):
     """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
+    if cfg["model"] == "eg2":
+        return _eg2_plan(cfg)
     H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
     plan = [("embed", "q", (V, H))]
     if cfg["model"] == "d3" and "linear_heads" in cfg:  # d3-lite as exported (export-d3.py:66-102)
@@ -160,6 +176,21 @@ def tensor_plan(cfg: dict):
     return plan
 
 
+def _eg2_plan(cfg: dict):
+    """The shipped EmbeddingGemma 2 layout (export-eg2.py:92-118)."""
+    H, I, h, V, L, P = (cfg[k] for k in ("hidden", "intermediate", "heads", "vocab", "layers", "ple"))
+    plan = [("embed", "q", (V, H)), ("ple.norm", "n", (P,)), ("final_norm", "n", (H,)),
+            ("projection", "v", (cfg["embedding_dim"], H))]
+    for i, t in enumerate(cfg["layer_types"]):
+        p, D, kv = f"layers.{i}.", cfg["head_dim"][t], cfg["kv_heads"][t]
+        plan += [(p + "ple_in", "q", (P, H)), (p + "qkv", "q", ((h + 2 * kv) * D, H)), (p + "q_norm", "n", (D,)),
+                 (p + "k_norm", "n", (D,)), (p + "o", "q", (H, h * D)), (p + "gu", "q", (2 * I, H)), (p + "down", "q", (H, I)),
+                 (p + "ple_gate", "q", (P, H)), (p + "ple_proj", "q", (H, P)), (p + "ple_norm", "n", (H,))]
+        plan += [(p + n, "n", (H,)) for n in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                                                  "post_feedforward_layernorm")]
+    return plan
+
+
 def head_plan(cfg: dict):
     """[(name, shape)] of the learned EmbeddingGemma 2 decision head (eg2-head.ts:64-99) on embed_dim inputs:
     state/question/option projections, the field MLP, the type embedding, two LayerNorms and the residual MLP."""
@@ -177,6 +208,17 @@ def head_plan(cfg: dict):
 
 def manifest_config(cfg: dict) -> dict:
     c = {k: v for k, v in cfg.items() if k not in ("bits",)}
+    if cfg["model"] == "eg2":  # export-eg2.py:68-80's keys
+        c["layer_scalars"] = list(cfg.get("layer_scalars", [1.0] * cfg["layers"]))
+        c.setdefault("prompt", "")
+        c.setdefault("max_len", 8192)
+        lh = c.pop("learned_head")
+        c["question_types"] = ["choice", "score", "noul"]
+        c["temperatures"] = dict(lh.get("temperatures", {"choice": 1.0, "score": 1.0, "noul": 1.0}))
+        c["head"] = {"width": lh["width"], "ln_eps": 1e-5, "prior_scale": lh.get("prior_scale", 2.0),
+                     "joint_scale": lh.get("joint_scale", 5.0), "gate": lh.get("gate", 0.6),
+                     "residual_bias": lh.get("residual_bias", 0.1)}
+        return c
     c["layer_types"] = list(cfg.get("layer_types") or ["full_attention"] * cfg["layers"])
     if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
         c["model"] = cfg["model"]
@@ -216,7 +258,7 @@ def _make(cfg, name, kind, shape, seed, norm_std, std):
     if kind == "s":  # the scorer's bias and a zero half (export-omni.py:90: one aligned word)
         return name, kind, np.array([normal(name, (1,), 0.1, seed)[0], 0.0], dtype=np.float32), None
     w = normal(name, shape, std, seed)
-    if name == "embed" and cfg["model"] == "encoder":
+    if name == "embed" and cfg["model"] in ("encoder", "eg2"):
         w = w * np.float32(math.sqrt(cfg["hidden"]))  # Gemma's sqrt(hidden) embedding scale, folded in
     q = fmt.quantize8(w) if cfg["bits"] == 8 else fmt.quantize4(w)
     return name, kind, q[0], q[1]
@@ -249,7 +291,7 @@ def generate(cfg: dict, out: str, seed: int = 0, norm_std: float = 0.0, threads:
                 blob.f32(name, a)
             else:
                 blob.put_quant(name, a, b, shape, cfg["bits"])
-    if cfg["model"] == "encoder" and cfg.get("learned_head"):
+    if cfg["model"] in ("encoder", "eg2") and cfg.get("learned_head"):
         # f32 host tensors; LayerNorm weights around 1, everything else N(0, 1/sqrt(fan-in))
         for name, shape in head_plan(cfg):
             if name.endswith("norm.weight"):

@@ -268,6 +268,17 @@ int dj_attention_gated(dj_rec *rec, int T, int heads, int kv, int D, const uint1
                        dj_kv_src B, const int32_t *rng_dev, float scale, const uint16_t *G_dev, int g_stride,
                        uint16_t *O_dev);
 
+/* ---------------------------------------------------------------- ops: EmbeddingGemma 2's per-layer embeddings */
+
+/* O[t, :] = f16(gelu_tanh(G[t, :]) * E[t, :] / sqrt(mean(E[t, :]^2) + eps) * w), G, E, O f16 [T, P], w f16 [P],
+ * P % 8 == 0. Replaces PLE_MIX (eg2-kernels.ts:179-200). */
+int dj_ple_mix(dj_rec *rec, int T, int P, const uint16_t *G_dev, const uint16_t *E_dev, const uint16_t *w_dev, float eps,
+               uint16_t *O_dev);
+/* out[s, :] = mean(X[a_s:b_s, :]) . W^T in f32, W f16 [N, H] (the embedding projection), seqs (a, b) per
+ * sequence; H % 4 == 0. The mean is staged in the context workspace. Replaces POOL_PROJECT (eg2-kernels.ts:202-228). */
+int dj_pool_project(dj_rec *rec, int T, int S, int H, int N, const uint16_t *X_dev, const uint32_t *seqs_dev,
+                    const uint16_t *W_dev, float *out_dev);
+
 /* ---------------------------------------------------------------- ops: d1-omni's decision head (kernels.ts:186-283) */
 
 /* Xo[t, :] = f16(f32(Xi[t, :]) + f32(E[idx[t], :])) for E f16 [rows, H] (the question-type embedding); idx past

@@ -373,6 +373,62 @@ def dense_f32(inp, codes, scales, bits):
     return (inp.astype(F32) @ dequant_f32(codes, scales, bits).T).astype(F32)
 
 
+# ---------------------------------------------------------------- EmbeddingGemma 2 (eg2-kernels.ts, eg2-engine.ts)
+
+def ple_mix(G, E, w, eps, acc=F32):
+    """PLE_MIX (eg2-kernels.ts:179-200): f16(gelu_tanh(G) * E / sqrt(mean(E^2) + eps) * w)."""
+    e = E.astype(acc)
+    inv = 1.0 / np.sqrt((e * e).sum(-1, keepdims=True) / E.shape[-1] + eps)
+    return (gelu_tanh(G.astype(acc)) * e * inv * w.astype(acc)).astype(F16)
+
+
+def pool_project(X, ranges, W):
+    """POOL_PROJECT (eg2-kernels.ts:202-228): the f32 mean of each sequence's rows, times the f16 projection W
+    [N, H]^T, in f32."""
+    return (mean_pool(X, ranges).astype(F32) @ W.astype(F32).T).astype(F32)
+
+
+def eg2_forward(model: "Model", seqs, acc=F32, layers=None):
+    """Eg2Engine.embed (eg2-engine.ts:72-139) on the shipped layout: two gathers of the (sqrt(hidden)-scaled)
+    embedding (the residual stream x and the copy xe the per-layer embeddings read); per layer q/k/v RMSNorm +
+    RoPE (rotate-half over the whole head, 1/theta^(2d/D) of the layer type's theta) -> bidirectional attention
+    at scale 1 over the layer type's key ranges (the sequence, or +-window on the sliding layers) -> o ->
+    sandwich -> gate|up with the tanh GELU -> down -> x += rmsnorm(.) w; then the per-layer embedding:
+    gate = x . ple_gate^T, e = xe . ple_in^T, ple_proj(PLE_MIX(gate, e)) -> sandwich with ple_norm, the layer scalar
+    and the next input norm (final_norm after the last); POOL_PROJECT; the first embed_dim values L2-normalised.
+    Returns (embeddings f32 [S, embed_dim], final normed f16 [T, H])."""
+    c = model.c
+    H, I, h, eps, P = c["hidden"], c["intermediate"], c["heads"], c["eps"], c["ple"]
+    L = c["layers"] if layers is None else layers
+    ids, meta, full, slide, ranges = pack_encoder(seqs, c["window"])
+    T = len(ids)
+    masks = {"full_attention": ranges_mask(full, T), "sliding_attention": ranges_mask(slide, T)}
+    ec, es, eb = model.t["embed"]
+    x = gather(ids, ec, es, eb)
+    xe = x.copy()
+    x, normed = sandwich(x, None, None, model.t["layers.0.input_layernorm"], eps, 1.0, acc)
+    scalars = c.get("layer_scalars", [1.0] * c["layers"])
+    for i in range(L):
+        p, t = f"layers.{i}.", c["layer_types"][i]
+        D, kv = c["head_dim"][t], c["kv_heads"][t]
+        z = matmul(normed, model.w16(p + "qkv"), acc)
+        z = qk_norm_rope(z, h, kv, D, meta[:, 3], model.t[p + "q_norm"], model.t[p + "k_norm"], True, eps,
+                         c["rope_theta"][t], mode=1, acc=acc)
+        o = matmul(attention(z, h, kv, D, masks[t], 1.0, acc), model.w16(p + "o"), acc)
+        x, normed = sandwich(x, o, model.t[p + "post_attention_layernorm"], model.t[p + "pre_feedforward_layernorm"], eps, 1.0, acc)
+        gu = matmul(normed, model.w16(p + "gu"), acc)
+        o = matmul(gelu_mul(gu[:, :I], gu[:, I:], acc), model.w16(p + "down"), acc)
+        x, _ = sandwich(x, o, model.t[p + "post_feedforward_layernorm"], None, eps, 1.0, acc)
+        g = matmul(x, model.w16(p + "ple_gate"), acc)
+        e = matmul(xe, model.w16(p + "ple_in"), acc)
+        o = matmul(ple_mix(g, e, model.t["ple.norm"], eps, acc), model.w16(p + "ple_proj"), acc)
+        nxt = f"layers.{i + 1}.input_layernorm" if i + 1 < L else "final_norm"
+        x, normed = sandwich(x, o, model.t[p + "ple_norm"], model.t[nxt], eps, float(scalars[i]), acc)
+    out = pool_project(normed, ranges, model.t["projection"])[:, :c["embed_dim"]].astype(F64)
+    n = np.maximum(np.sqrt((out * out).sum(-1, keepdims=True)), 1e-12)
+    return (out / n).astype(F32), normed
+
+
 # ---------------------------------------------------------------- d3-lite's Gated DeltaNet (d3-kernels.ts:9-149)
 
 def d3_spans(seqs, groups=None):

@@ -949,3 +949,59 @@ def test_gdn_refuses_short_rows(pkg, ctx):
             rec.gdn(4, 1, buf, 2, 100, buf, buf, buf, buf, buf, 1e-6, buf)
     finally:
         rec.abort()
+
+
+# ---------------------------------------------------------------- EmbeddingGemma 2's per-layer embeddings
+
+def test_ple_mix(pkg, ctx):
+    """dj_ple_mix (PLE_MIX, eg2-kernels.ts:179-200) within one f16 ulp of the float64 oracle."""
+    rng = np.random.default_rng(101)
+    T, P = 133, 512
+    G, E = rand_f16(rng, (T, P), 1.5), rand_f16(rng, (T, P))
+    w = (1 + 0.1 * rng.standard_normal(P)).astype(np.float16)
+    dG, dE, dw, dO = ctx.array(G), ctx.array(E), ctx.array(w), ctx.alloc(T * P * 2)
+    run(ctx, lambda r: r.ple_mix(T, P, dG, dE, dw, 1e-6, dO))
+    want = ref.ple_mix(G, E, w, 1e-6, np.float64)
+    assert f16_close(dO.read(np.float16, (T, P)), want, ulps=1.0, atol=1e-6) <= 1.0
+
+
+def test_pool_project(pkg, ctx):
+    """dj_pool_project (POOL_PROJECT, eg2-kernels.ts:202-228): the f32 mean of each text's rows times the f16
+    projection, within f32 rounding of the float64 product; one-token texts included."""
+    rng = np.random.default_rng(102)
+    H, N = 512, 768
+    lens = [256, 24, 24, 1, 8, 40]
+    T = sum(lens)
+    X = rand_f16(rng, (T, H))
+    W = rand_f16(rng, (N, H), 0.05)
+    ranges = np.array([(sum(lens[:k]), sum(lens[:k + 1])) for k in range(len(lens))], dtype=np.uint32)
+    dX, dr, dW, dout = ctx.array(X), ctx.array(ranges), ctx.array(W), ctx.alloc(len(lens) * N * 4)
+    run(ctx, lambda r: r.pool_project(T, len(lens), H, N, dX, dr, dW, dout))
+    got = dout.read(np.float32, (len(lens), N)).astype(np.float64)
+    means = np.stack([X[a:b].astype(np.float64).mean(0) for a, b in ranges])
+    want = means @ W.astype(np.float64).T
+    mag = np.abs(means) @ np.abs(W.astype(np.float64)).T
+    assert (np.abs(got - want) <= 2.0 ** -18 * mag + 1e-6).all()
+
+
+@pytest.mark.parametrize("window", [None, 40])
+def test_attention_512(pkg, ctx, window):
+    """dj_attention with 512-dim heads (EmbeddingGemma 2's global layers; the windowed form too) against the float64
+    oracle; GQA 4:2; texts of 1 to 300 tokens."""
+    dj = _dj()
+    rng = np.random.default_rng(103 + (window or 0))
+    heads, kv, D = 4, 2, 512
+    seqs = [list(range(n)) for n in (300, 24, 1, 8, 77)]
+    ids, meta, full, slide, ranges = ref.pack_encoder(seqs, window=window)
+    r4 = full if window is None else slide
+    T = len(ids)
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride), 0.3)
+    dZ, dr, dO = ctx.array(Z), ctx.array(r4), ctx.alloc(T * heads * D * 2)
+    src = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    run(ctx, lambda r: r.attention(T, heads, kv, D, dZ, stride, src, src, dr, 1.0, dO))
+    got = dO.read(np.float16, (T, heads * D)).astype(np.float64)
+    want = ref.attention(Z, heads, kv, D, ref.ranges_mask(r4, T), 1.0, np.float64).astype(np.float64)
+    err = np.abs(got - want).max()
+    print(f"attention D512 window {window}: max abs err {err:.2e}")
+    assert err < 4e-3

@@ -39,6 +39,8 @@ def models(pkg, tmp_path_factory):
         "d3": synth.reduced("d3-attn-0.8b-q8", layers=2, vocab=4096),
         "lfm2": synth.reduced("lfm2-d1-3b-q4", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
         "omni": synth.reduced("d1-omni-q8", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
+        "eg2ship": synth.reduced("eg2-q8", layers=3, vocab=4096, window=16, layer_scalars=[0.9, 1.1, 0.8],
+                                 layer_types=["sliding_attention", "full_attention", "sliding_attention"]),
         "d3lite": synth.reduced("d3-lite-q8", layers=4, vocab=4096,
                                 layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"]),
     }
@@ -594,5 +596,63 @@ def test_decision_api_d3_lite(pkg, models):
             topic, churn = ref.softmax(want[:3]), ref.softmax(want[3:])
             assert abs(r["answers"]["topic"]["confidence"] - topic.max()) < PROB_TOL
             assert abs(r["answers"]["churn"]["noul"] - churn[1]) < PROB_TOL
+    finally:
+        d.destroy()
+
+
+def test_eg2_shipped_matches_oracle(pkg, models):
+    """EmbeddingGemma 2 as shipped on the product path (Eg2Engine.embed, eg2-engine.ts:72-139): windowed 256-dim
+    and global 512-dim attention layers, the per-layer embeddings with layer scalars, the pooled f16 projection:
+    the final normed hidden state within 2e-2 relative L2 of the oracle and every embedding within 1e-2 (unit
+    vectors); eager, captured and replayed forwards identical; a text's embedding does not depend on its
+    neighbours (to rounding)."""
+    from decision_js_amd.eg2 import Eg2Engine
+    model = ref.Model(models["eg2ship"])
+    rng = np.random.default_rng(27)
+    seqs = [[int(x) for x in rng.integers(0, 4096, n)] for n in (256, 24, 24, 24, 8, 8, 1, 40)]
+    eng = Eg2Engine.load(models["eg2ship"])
+    try:
+        runs = [eng.embed(seqs)["embeddings"] for _ in range(3)]  # eager, capture, replay
+        assert np.array_equal(runs[0], runs[1]) and np.array_equal(runs[0], runs[2])
+        dbg = eng.embed(seqs, debug=True)
+        want, normed = ref.eg2_forward(model, seqs, acc=np.float64)
+        assert rel_l2(dbg["debug"]["final"], normed) < HIDDEN_TOL
+        for g, w in zip(runs[0], want):
+            assert rel_l2(g, w) < 1e-2
+        alone = eng.embed([seqs[1]])["embeddings"][0]
+        assert rel_l2(alone, runs[0][1]) < 1e-2
+    finally:
+        eng.destroy()
+
+
+def test_decision_api_eg2_shipped(pkg, models):
+    """The shipped EmbeddingGemma 2 through the Decision API (runEg2, d1.ts:172-209): kind eg2 on Eg2Engine, each
+    distinct text embedded once, the learned head on the host: probabilities within 1e-3 of the head on the
+    oracle's embeddings (noul reversed from [no, yes])."""
+    from decision_js_amd.d1 import Decision
+    from decision_js_amd.eg2_head import Eg2Head
+    rng = np.random.default_rng(28)
+    V = 4096
+    ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+    model = ref.Model(models["eg2ship"])
+    d = Decision.load(models["eg2ship"])
+    try:
+        assert d.kind == "eg2" and type(d.engine).__name__ == "Eg2Engine" and d.engine.host
+        state = ids(200)
+        qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(24),
+                        "option_ids": [ids(8), ids(6), ids(9)]},
+              "churn": {"type": "noul", "instructions": "?", "ids": ids(20), "option_ids": [ids(3), ids(4)]}}
+        r = d.system_one(state, qs)
+        texts = [state, qs["topic"]["ids"], *qs["topic"]["option_ids"], qs["churn"]["ids"], *qs["churn"]["option_ids"]]
+        emb, _ = ref.eg2_forward(model, texts, acc=np.float64)
+        head = Eg2Head(model.c, d.engine.host)
+        e = lambda k: (("t", k), emb[k])  # noqa: E731
+        c = model.c
+        zt = head.logits("choice", e(0), e(1), [e(2), e(3), e(4)])
+        pt = ref.softmax(np.asarray(zt) / c["temperatures"]["choice"])
+        zc = head.logits("noul", e(0), e(5), [e(6), e(7)])
+        pc = ref.softmax(np.asarray(zc) / c["temperatures"]["noul"])
+        assert abs(r["answers"]["topic"]["confidence"] - pt.max()) < PROB_TOL
+        assert abs(r["answers"]["churn"]["noul"] - pc[1]) < PROB_TOL  # [no, yes] reversed to [yes, no]
     finally:
         d.destroy()

@@ -471,3 +471,35 @@ def test_node_d3_lite_matches_python_host(tmp_path):
                     assert np.allclose(x, y, rtol=0, atol=1e-12)
     finally:
         d.destroy()
+
+
+@pytest.mark.gpu
+def test_node_eg2_shipped_matches_python_host(tmp_path):
+    """The shipped EmbeddingGemma 2 through Node (kindOf -> runEg2 -> Eg2Engine, the learned head) against the
+    Python host: the same answers and embeddings."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.reduced("eg2-q8", layers=3, vocab=4096, window=16,
+                        layer_types=["sliding_attention", "full_attention", "sliding_attention"])
+    mdir = synth.generate(cfg, str(tmp_path / "eg2ship"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(19)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": ""}, "ids": ids(24),
+                    "option_ids": [ids(8), ids(6)]},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(20), "option_ids": [ids(3), ids(2)]}}
+    batch = [[ids(100), qs], [ids(37), qs]]
+    texts = [ids(30), ids(1), ids(64)]
+    js = node({"cmd": "encode", "model": mdir, "batch": batch, "texts": texts}, timeout=300)
+    assert js["kind"] == "eg2"
+    d = Decision.load(mdir)
+    try:
+        py = d.system_one_batch(batch)
+        for a, b in zip(js["batch"], py):
+            assert a["usage"] == b["usage"]
+            assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-6
+            assert abs(a["answers"]["topic"]["confidence"] - b["answers"]["topic"]["confidence"]) < 1e-6
+        emb = d.engine.embed(texts)["embeddings"]
+        assert np.allclose(np.asarray(js["embeddings"], dtype=np.float32), emb, rtol=0, atol=1e-6)
+    finally:
+        d.destroy()

@@ -1009,3 +1009,148 @@ def _gdn_variant(Z, spans, LH, conv_w, A_log, dt_bias, gnorm, eps, acc, decay_la
                     continue
                 Y[r, h * 128:(h + 1) * 128] = out[i]
     return Y
+
+
+# ---------------------------------------------------------------- EmbeddingGemma 2 as shipped (per-layer embeddings)
+
+TINY_EG2 = dict(layers=3, hidden=64, intermediate=96, heads=2, vocab=512, window=3,
+                layer_types=["sliding_attention", "full_attention", "sliding_attention"],
+                head_dim={"sliding_attention": 32, "full_attention": 64}, kv_heads={"sliding_attention": 1, "full_attention": 2},
+                rope_theta={"sliding_attention": 1e4, "full_attention": 1e6}, ple=32, embedding_dim=48, embed_dim=40,
+                learned_head={"width": 16}, layer_scalars=[0.9, 1.1, 0.8])
+
+
+@pytest.fixture(scope="module")
+def tiny_eg2(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("eg2")
+    return synth.generate(synth.reduced("eg2-q8", **TINY_EG2), str(d / "eg2"), norm_std=0.1, std=0.125)
+
+
+def _torch_eg2(model: ref.Model, seqs):
+    """Each text alone, float64, library routines (export-eg2.py's layout; eg2-engine.ts:72-139): embedding rows
+    (sqrt(H) folded in) as the residual stream and as the per-layer embeddings' source; per layer q/k/v
+    F.rms_norm (q, k weighted, v plain), RoPE as a complex rotation by pos / theta^(2d/D) of the layer type, SDPA at
+    scale 1 with a boolean mask |i - j| <= window on the sliding layers (GQA by repeat), post-attention norm into the
+    residual, pre-FF norm, gelu_tanh(gate) up, down, post-FF norm into the residual; then gelu_tanh(x ple_gate^T) *
+    rms_norm(xe ple_in^T, ple.norm), ple_proj, ple_norm into the residual, times the layer scalar; the next
+    layer's input norm (final_norm last); the mean over the text, the projection, the first embed_dim values
+    L2-normalised."""
+    c = model.c
+    H, I, h, eps, win = c["hidden"], c["intermediate"], c["heads"], c["eps"], c["window"]
+
+    def W(name):
+        return _t(model.w16(name))
+
+    def nw(name):
+        return _t(model.t[name])
+
+    def rms(x, w=None):
+        return F.rms_norm(x, (x.shape[-1],), weight=w, eps=eps)
+
+    E = W("embed")
+    out = []
+    for s in seqs:
+        n = len(s)
+        x = E[torch.tensor(s)]
+        xe = x.clone()
+        normed = rms(x, nw("layers.0.input_layernorm"))
+        pos = torch.arange(n, dtype=torch.float64)
+        for i, t in enumerate(c["layer_types"]):
+            p, D, kv, theta = f"layers.{i}.", c["head_dim"][t], c["kv_heads"][t], c["rope_theta"][t]
+            ang = pos[:, None] / theta ** (torch.arange(D // 2, dtype=torch.float64) * 2 / D)
+            rot = torch.polar(torch.ones_like(ang), ang)
+            z = normed @ W(p + "qkv").T
+            q = rms(z[:, :h * D].reshape(n, h, D), nw(p + "q_norm"))
+            k = rms(z[:, h * D:(h + kv) * D].reshape(n, kv, D), nw(p + "k_norm"))
+            v = rms(z[:, (h + kv) * D:].reshape(n, kv, D))
+
+            def rope(a):
+                cplx = torch.complex(a[..., :D // 2], a[..., D // 2:]) * rot[:, None, :]
+                return torch.cat([cplx.real, cplx.imag], -1)
+            q, k = rope(q), rope(k).repeat_interleave(h // kv, dim=1)
+            v = v.repeat_interleave(h // kv, dim=1)
+            mask = None
+            if t == "sliding_attention":
+                mask = (pos[:, None] - pos[None, :]).abs() <= win
+            y = F.scaled_dot_product_attention(q.transpose(0, 1), k.transpose(0, 1), v.transpose(0, 1), attn_mask=mask, scale=1.0)
+            o = y.transpose(0, 1).reshape(n, h * D) @ W(p + "o").T
+            x = x + rms(o, nw(p + "post_attention_layernorm"))
+            gu = rms(x, nw(p + "pre_feedforward_layernorm")) @ W(p + "gu").T
+            o = (F.gelu(gu[:, :I], approximate="tanh") * gu[:, I:]) @ W(p + "down").T
+            x = x + rms(o, nw(p + "post_feedforward_layernorm"))
+            mix = F.gelu(x @ W(p + "ple_gate").T, approximate="tanh") * rms(xe @ W(p + "ple_in").T, nw("ple.norm"))
+            x = (x + rms(mix @ W(p + "ple_proj").T, nw(p + "ple_norm"))) * c["layer_scalars"][i]
+            normed = rms(x, nw(f"layers.{i + 1}.input_layernorm" if i + 1 < len(c["layer_types"]) else "final_norm"))
+        e = (normed.mean(0) @ nw("projection").T)[:c["embed_dim"]]
+        out.append((e / e.norm()).numpy())
+    return np.stack(out)
+
+
+def _compare_eg2(path, model=None):
+    model = model or ref.Model(path)
+    rng = np.random.default_rng(19)
+    seqs = [[int(x) for x in rng.integers(0, model.c["vocab"], n)] for n in (23, 8, 1, 12)]
+    got, _ = ref.eg2_forward(model, seqs, acc=np.float64)
+    want = _torch_eg2(ref.Model(path), seqs)  # the untouched file
+    for i in range(len(seqs)):
+        assert _rel_l2(got[i], want[i]) < 5e-3, f"text {i}"
+
+
+def test_eg2_forward_matches_library_restatement(tiny_eg2):
+    _compare_eg2(tiny_eg2)
+
+
+@pytest.mark.parametrize("slip", ["window_exclusive", "stream_normed_after_mlp", "ple_operands_swapped",
+                                  "no_layer_scalar", "truncate_from_end"])
+def test_planted_eg2_slips_are_caught(tiny_eg2, monkeypatch, slip):
+    """The window's edge excluded; the residual stream RMS-normalised after the MLP (what the PLE gate reads);
+    PLE_MIX's gate and embedding swapped; the layer scalar dropped; the embedding truncated to its last embed_dim
+    values."""
+    model = ref.Model(tiny_eg2)
+    if slip == "window_exclusive":
+        orig = ref.pack_encoder
+
+        def pe(seqs, window=None):
+            return orig(seqs, None if window is None else window - 1)
+        monkeypatch.setattr(ref, "pack_encoder", pe)
+    elif slip == "stream_normed_after_mlp":
+        orig_s = ref.sandwich
+
+        def sw(X, Y, w1, w2, eps, scale, acc=np.float32):
+            Xn, O = orig_s(X, Y, w1, w2, eps, scale, acc)
+            if w2 is None and Y is not None:  # the post-FF sandwich: a normalised stream
+                a = Xn.astype(acc)
+                Xn = (a / np.sqrt((a * a).mean(-1, keepdims=True) + eps)).astype(np.float16)
+            return Xn, O
+        monkeypatch.setattr(ref, "sandwich", sw)
+    elif slip == "ple_operands_swapped":
+        orig = ref.ple_mix
+        monkeypatch.setattr(ref, "ple_mix", lambda G, E, w, eps, acc=np.float32: orig(E, G, w, eps, acc))
+    elif slip == "no_layer_scalar":
+        model.c["layer_scalars"] = [1.0] * len(model.c["layer_types"])
+    else:
+        orig_pp = ref.pool_project
+        monkeypatch.setattr(ref, "pool_project", lambda X, ranges, W: np.ascontiguousarray(orig_pp(X, ranges, W)[:, ::-1]))
+    with pytest.raises(AssertionError):
+        _compare_eg2(tiny_eg2, model)
+
+
+def test_ple_mix_and_pool_project_closed_forms():
+    """PLE_MIX element by element in float64 (torch's tanh GELU, the row's RMS); POOL_PROJECT as the explicit
+    mean then product (a 3 x 5 output from a 5 x 8 projection: a transposed operand fails)."""
+    rng = np.random.default_rng(12)
+    G, E = rng.standard_normal((4, 16)).astype(np.float16), rng.standard_normal((4, 16)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(16)).astype(np.float16)
+    got = ref.ple_mix(G, E, w, 1e-6, np.float64).astype(np.float64)
+    e = E.astype(np.float64)
+    want = F.gelu(_t(G), approximate="tanh").numpy() * e / np.sqrt((e * e).mean(-1, keepdims=True) + 1e-6) * w.astype(np.float64)
+    assert np.abs(got - want).max() <= 2 ** -10 * np.abs(want).max() + 1e-6
+    X = rng.standard_normal((9, 8)).astype(np.float16)
+    W = rng.standard_normal((5, 8)).astype(np.float16)
+    ranges = np.array([(0, 4), (4, 5), (5, 9)], dtype=np.uint32)
+    out = ref.pool_project(X, ranges, W)
+    assert out.shape == (3, 5)
+    for s, (a, b) in enumerate(ranges):
+        m = X[a:b].astype(np.float64).mean(0)
+        assert np.allclose(out[s], W.astype(np.float64) @ m, rtol=1e-5, atol=1e-5)
