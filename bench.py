@@ -394,6 +394,8 @@ def run_workload(args):
         out = omni_ticket(args, steps, warmup)
     elif args.workload == "d3lite":
         out = d3_lite_ticket(args, steps, warmup)
+    elif args.workload == "eg2":
+        out = eg2_ticket(args, steps, warmup)
     else:
         from decision_js_amd.encoder import EncoderEngine, cosine_logits
         cfg = synth.CONFIGS["eg2-encoder-q8"]
@@ -552,6 +554,50 @@ def d3_lite_ticket(args, steps, warmup):
                                                         "model": "d3-lite q8 (real weights)", "source": "README.md:33, 44"}})
 
 
+def eg2_ticket(args, steps, warmup):
+    """EmbeddingGemma 2 tickets on its shipped layout (the reference publishes 6 ms per ticket on an Apple M5 Pro with
+    the schema's embeddings cached and a ~70-token state per ticket, README.md:35): through the Decision API, 3
+    questions (a 3-way choice, a noul, a 5-level score) whose question and option texts are embedded once (first
+    ticket), then per ticket one new ~70-id state embedded and the learned head on the host."""
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.CONFIGS["eg2-q8"]
+    mdir = os.path.join(args.model_dir, "eg2-q8")
+    synth.generate(cfg, mdir, seed=0, threads=16)
+    d = Decision.load(mdir, {"graphs": not args.no_graphs})
+    rng = np.random.Generator(np.random.PCG64(1))
+    V = cfg["vocab"]
+    ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(24),
+                    "option_ids": [ids(8) for _ in range(3)]},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(20), "option_ids": [ids(4), ids(4)]},
+          "urgency": {"type": "score", "instructions": "?", "criteria": ["1", "2", "3", "4", "5"], "ids": ids(24),
+                      "option_ids": [ids(10) for _ in range(5)]}}
+    states = [ids(70) for _ in range(warmup + steps)]
+    for st in states[:warmup]:
+        d.system_one(st, qs)
+    d.engine.ctx.timer_begin()
+    times = []
+    t0 = time.perf_counter()
+    for st in states[warmup:]:
+        a = time.perf_counter()
+        d.system_one(st, qs)
+        times.append(time.perf_counter() - a)
+    wall = time.perf_counter() - t0
+    gpu = d.engine.ctx.timer_end() / steps
+    d.destroy()
+    ms = 1e3 * wall / steps
+    p50 = 1e3 * float(np.median(times))
+    log(f"eg2: {ms:.3f} ms per ticket (p50 {p50:.3f}), {gpu:.3f} ms GPU")
+    return _line("decisions/sec (EmbeddingGemma 2 tickets: 3 questions, schema cached, a 70-id state) on 1 MI355X",
+                 3e3 / ms, "decisions/s", steps, warmup, ms, "f16",
+                 "eg2-q8 (24 layers at hidden 512, per-layer embeddings, sliding 256-dim / global 512-dim heads), "
+                 "one 70-id state embedded per ticket, learned head on the host", None,
+                 {"gpu_ms_per_step": round(gpu, 4), "p50_ms_per_ticket": round(p50, 4),
+                  "reference_published_ms_per_ticket": {"value": 6.0, "hardware": "Apple M5 Pro, Chrome WebGPU",
+                                                        "model": "EmbeddingGemma 2 q8 (real weights)", "source": "README.md:35"}})
+
+
 def _linear_shapes(c):
     """(N, K) of one decoder layer's linears: qkv, o_proj, w13, w2."""
     H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
@@ -570,7 +616,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calib-mb", type=int, default=0, help="also run a plain device copy of this many MiB (counter calibration)")
-    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni", "d3lite"],
+    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni", "d3lite", "eg2"],
                     help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
                          "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
     ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")
