@@ -71,16 +71,19 @@ def make_tickets(n, V, seq_len=384, seed=1, answer_seed=3, sizes=(2, 3, 5)):
 def model_flops_bytes(c, T, seqs_len, causal=True, markers=0):
     """Appendix-B algorithmic work of one forward: 2 T sum(N K) over the linears plus 4 D h (allowed
     query-key pairs) per attention layer; bytes = quantized linear weights + gathered embedding rows. LFM2 conv
-    layers count in_proj (3H x H) and out_proj (H x H); a d1-omni head counts its layers' in_proj (3H x H),
-    out_proj, linear1/linear2 on every token and bidirectional attention, and the scorer's H x H product on
-    `markers` rows."""
-    H, I, h, kv, D = c["hidden"], c["intermediate"], c["heads"], c["kv_heads"], c["head_dim"]
+    layers count in_proj (3H x H) and out_proj (H x H); Laya's sliding layers count the pairs within their
+    window; a d1-omni / Laya head counts its layers' in_proj (3H x H), out_proj, linear1/linear2 on every token
+    and bidirectional attention, and the scorer's H x H product on `markers` rows."""
+    H, I, h = c["hidden"], c["intermediate"], c["heads"]
+    kv, D = c.get("kv_heads", h), c.get("head_dim", H // h)  # Laya: full-width heads
     types = c.get("layer_types") or ["full_attention"] * c["layers"]
     attn_nk, conv_nk, ffn_nk = (h + 2 * kv) * D * H + H * h * D, 4 * H * H, 2 * I * H + H * I
     nk = sum(conv_nk if t == "conv" else attn_nk for t in types) + len(types) * ffn_nk
     pairs = sum(n * (n + 1) // 2 if causal else n * n for n in seqs_len)
-    n_attn = sum(t != "conv" for t in types)
-    flops = 2 * T * nk + 4 * D * h * pairs * n_attn
+    w = c.get("window")
+    # Laya's local layers: each token sees the keys within +-window of it in its sequence
+    win_pairs = sum(sum(min(n, t + w + 1) - max(0, t - w) for t in range(n)) for n in seqs_len) if w else pairs
+    flops = 2 * T * nk + 4 * D * h * sum(win_pairs if t == "sliding_attention" else pairs for t in types if t != "conv")
     wnk = nk
     if c.get("head_layers"):
         hl, ff = c["head_layers"], c["head_ff"]
@@ -390,8 +393,8 @@ def run_workload(args):
                     roof, {"gpu_ms_per_step": round(gpu_ms, 3), "question_alone_ms": round(1e3 * q_wall, 4),
                            "question_alone_gpu_ms": round(q_gpu, 4), "question_alone_roofline": q_roof})
         eng.destroy()
-    elif args.workload == "omni":
-        out = omni_ticket(args, steps, warmup)
+    elif args.workload in ("omni", "laya"):
+        out = omni_ticket(args, steps, warmup, args.workload)
     elif args.workload == "d3lite":
         out = d3_lite_ticket(args, steps, warmup)
     elif args.workload == "eg2":
@@ -432,33 +435,52 @@ def run_workload(args):
     print(json.dumps(out), flush=True)
 
 
-def omni_tickets(cfg, n, seq_len=384, q_len=44):
+def omni_tickets(cfg, n, seq_len=384, q_len=44, question_first=False):
     """n d1-omni tickets: a state of seq_len - q_len random ids (PCG64 seed 1) read by 3 questions (a noul, a
     3-way choice, a 5-level score) of q_len ids each, one sequence per question, markers 6 ids apart in the
-    question."""
+    question. question_first: Laya's layout (laya-prompt.ts: the question's ids, then the state's)."""
     rng = np.random.Generator(np.random.PCG64(1))
     V, P = cfg["vocab"], seq_len - q_len
     out = []
     for _ in range(n):
         state = [int(x) for x in rng.integers(0, V, P)]
-        out.append([{"ids": state + [int(x) for x in rng.integers(0, V, q_len)], "type": t,
-                     "markers": [P + 2 + 6 * j for j in range(k)]} for t, k in (("noul", 2), ("choice", 3), ("score", 5))])
+        tk = []
+        for t, k in (("noul", 2), ("choice", 3), ("score", 5)):
+            q = [int(x) for x in rng.integers(0, V, q_len)]
+            at = 0 if question_first else P
+            tk.append({"ids": q + state if question_first else state + q, "type": t, "markers": [at + 2 + 6 * j for j in range(k)]})
+        out.append(tk)
     return out
 
 
-def omni_ticket(args, steps, warmup):
-    """d1-omni tickets (the form of the reference's published 34 ms/ticket on an Apple M5 Pro, README.md:31):
-    3 questions over one 340-id state, each question its own 384-id sequence (the state read anew per question,
-    omni-engine.ts:5), packed in one forward (T = 1152): bidirectional LFM2 trunk, decision head, marker scorer,
-    then the temperature softmax on the host. A step is one ticket, inputs staged in HBM."""
+MARKER_MODELS = {
+    # kind: (config, engine module and class, description, the reference's published ms/ticket)
+    "omni": ("d1-omni-q8", "omni", "OmniEngine", "LFM2-350M-shaped bidirectional trunk, 16 layers, 2-layer head",
+             {"value": 34.0, "hardware": "Apple M5 Pro, Chrome WebGPU", "model": "d1-omni-600M q8 (real weights)",
+              "source": "README.md:31"}),
+    "laya": ("laya-q8", "laya", "LayaEngine", "ModernBERT-shaped encoder, 28 layers (every third global, the others "
+             "+-64 tokens), 2-layer head", {"value": 39.0, "hardware": "Apple M5 Pro, Chrome WebGPU",
+                                            "model": "Laya q8 (real weights, 447 MB)", "source": "README.md:34"}),
+}
+
+
+def omni_ticket(args, steps, warmup, kind="omni"):
+    """d1-omni or Laya tickets (the form of the reference's published 34 / 39 ms per ticket on an Apple M5 Pro,
+    README.md:31, 34): 3 questions over one 340-id state, each question its own 384-id sequence (the state read
+    anew per question, omni-engine.ts:5; Laya's question first), packed in one forward (T = 1152): the trunk,
+    decision head, marker scorer, then the temperature softmax on the host. A step is one ticket, inputs staged
+    in HBM."""
+    import importlib
     from decision_js_amd import synth
     from decision_js_amd.d1 import softmax
-    from decision_js_amd.omni import OmniEngine, temperature
-    cfg = synth.CONFIGS["d1-omni-q8"]
-    mdir = os.path.join(args.model_dir, "d1-omni-q8")
+    from decision_js_amd.omni import temperature
+    name, mod, cls, desc, published = MARKER_MODELS[kind]
+    Engine = getattr(importlib.import_module(f"decision_js_amd.{mod}"), cls)
+    cfg = synth.CONFIGS[name]
+    mdir = os.path.join(args.model_dir, name)
     synth.generate(cfg, mdir, seed=0, threads=16)
-    eng = OmniEngine.load(mdir, {"graphs": not args.no_graphs})
-    tickets = omni_tickets(cfg, warmup + steps)
+    eng = Engine.load(mdir, {"graphs": not args.no_graphs})
+    tickets = omni_tickets(cfg, warmup + steps, question_first=kind == "laya")
     staged = [eng.stage(t) for t in tickets]
 
     def unit(st):
@@ -491,17 +513,15 @@ def omni_ticket(args, steps, warmup):
     for k, (t_ms, cnt) in sorted(table.items(), key=lambda kv: -kv[1][0])[:10]:
         log(f"  {k:48s} {t_ms / 3:8.4f} ms/ticket  {100 * t_ms / total:5.1f}%  ({cnt // 3}/ticket, {1e3 * t_ms / cnt:7.2f} us each)")
     p50 = 1e3 * float(np.median(times))
-    log(f"omni: ticket (T={T}) {ms:.3f} ms wall (p50 {p50:.3f}), {gpu_ms:.3f} ms GPU, {3 * steps / wall:.1f} decisions/s")
+    log(f"{kind}: ticket (T={T}) {ms:.3f} ms wall (p50 {p50:.3f}), {gpu_ms:.3f} ms GPU, {3 * steps / wall:.1f} decisions/s")
     for st in staged:
         eng.free_staged(st)
     eng.destroy()
-    return _line("decisions/sec (d1-omni tickets: 3 questions, one 384-id sequence each) on 1 MI355X", 3 * steps / wall,
-                 "decisions/s", steps, warmup, ms, "f16",
-                 "d1-omni-q8 (LFM2-350M-shaped bidirectional trunk, 16 layers, 2-layer head), 3 x 384 random ids in one "
-                 "forward, 10 markers", roof,
-                 {"gpu_ms_per_step": round(gpu_ms, 4), "p50_ms_per_ticket": round(p50, 4),
-                  "reference_published_ms_per_ticket": {"value": 34.0, "hardware": "Apple M5 Pro, Chrome WebGPU",
-                                                        "model": "d1-omni-600M q8 (real weights)", "source": "README.md:31"}})
+    label = "d1-omni" if kind == "omni" else "Laya"
+    return _line(f"decisions/sec ({label} tickets: 3 questions, one 384-id sequence each) on 1 MI355X", 3 * steps / wall,
+                 "decisions/s", steps, warmup, ms, "f16", f"{name} ({desc}), 3 x 384 random ids in one forward, 10 markers",
+                 roof, {"gpu_ms_per_step": round(gpu_ms, 4), "p50_ms_per_ticket": round(p50, 4),
+                        "reference_published_ms_per_ticket": published})
 
 
 def d3_lite_ticket(args, steps, warmup):
@@ -616,7 +636,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--profile-steps", type=int, default=5)
     ap.add_argument("--calib-mb", type=int, default=0, help="also run a plain device copy of this many MiB (counter calibration)")
-    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni", "d3lite", "eg2"],
+    ap.add_argument("--workload", default="ticket", choices=["ticket", "batch", "shared", "encoder", "omni", "laya", "d3lite", "eg2"],
                     help="ticket: configs[1] (the metric; configs[2] with --config qwen2.5-3b-q4 --seq-len 512); "
                          "batch: configs[3]; shared: configs[4]; encoder: configs[0]")
     ap.add_argument("--seq-len", type=int, default=384, help="tokens per question of a ticket")

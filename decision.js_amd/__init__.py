@@ -9,7 +9,12 @@ Modules
   fmt        manifest.json + weights.bin reader/writer, quantize8 / quantize4            ~ scripts/export_common.py
   synth      seeded synthetic models shaped as the benchmark configurations
   engine     GpuEngine + the causal decoder engine (forest packing, shared-state KV)     ~ src/gpu.ts, d1-3b-engine.ts, d3-engine.ts
-  encoder    the EmbeddingGemma-shaped encoder engine                                     ~ src/eg2-engine.ts
+  encoder    the EmbeddingGemma-shaped encoder engine (configs[0] form)                   ~ src/eg2-engine.ts
+  eg2        EmbeddingGemma 2 on its shipped layout (per-layer embeddings)                ~ src/eg2-engine.ts
+  eg2_head   the learned EmbeddingGemma 2 decision head on the host                       ~ src/eg2-head.ts
+  omni       d1-omni: bidirectional LFM2 trunk + marker head                              ~ src/omni-engine.ts
+  laya       Laya: ModernBERT encoder + d1-omni's marker head                             ~ src/laya-engine.ts
+  d3         d3-lite on its shipped layout (Gated DeltaNet + gated attention)             ~ src/d3-engine.ts
   questions  checkQuestion / answer                                                       ~ src/questions.ts
   d1         the Decision API (load, systemOne, systemOneBatch, probabilities)           ~ src/d1.ts
 """

@@ -15,7 +15,7 @@ DJ_OK, DJ_EINVAL, DJ_EHIP, DJ_ENOMEM, DJ_ESTATE, DJ_EINJECT = range(6)
 W_PLAIN, W_MFMA, W_MFMA_GLU = 0, 1, 2
 BIAS_NONE, BIAS_RELU, BIAS_GELU_ERF = 0, 1, 2
 W_DIRECT = 16  # flag: f16 weights dequantized once at load (the reference's directWeights)
-ACT_SILU, ACT_GELU_TANH = 0, 1
+ACT_SILU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2
 ROPE_POW_NEG, ROPE_INV_POW = 0, 1
 
 

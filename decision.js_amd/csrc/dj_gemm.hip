@@ -103,6 +103,19 @@ __device__ __forceinline__ float act_gelu_tanh(float x) {
   return 0.5f * x * (1.0f + (e - 1.0f) * __builtin_amdgcn_rcpf(e + 1.0f));
 }
 
+// GELU with the Abramowitz & Stegun 7.1.26 erf (|error| < 1.5e-7) of Laya's GELU_MUL (encoder-kernels.ts:30-40),
+// its reciprocal and exp on the hardware units
+__device__ __forceinline__ float act_gelu_erf(float x) {
+  const float z = 0.70710678f * x, az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * az);
+  const float y = 1.0f - ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) *
+                             t * __builtin_amdgcn_exp2f(-1.4426950408889634f * z * z);
+  return 0.5f * x * (1.0f + (z >= 0.0f ? y : -y));
+}
+__device__ __forceinline__ float act_apply(int act, float a) {
+  return act == DJ_ACT_SILU ? act_silu(a) : act == DJ_ACT_GELU_TANH ? act_gelu_tanh(a) : act_gelu_erf(a);
+}
+
 struct GemmArgs {
   const uint16_t *X;
   const uint8_t *Wc;
@@ -462,7 +475,7 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float a = (float)(_Float16)acc[i][j][r], b = (float)(_Float16)acc[i][j + 1][r];
-          v[r] = (_Float16)((g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b);
+          v[r] = (_Float16)(act_apply(g.act, a) * b);
         }
         if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
       }
@@ -500,7 +513,7 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float x = (float)(_Float16)a[r], u = (float)(_Float16)b[r];
-      v[r] = (_Float16)((act == DJ_ACT_SILU ? act_silu(x) : act_gelu_tanh(x)) * u);
+      v[r] = (_Float16)(act_apply(act, x) * u);
     }
     *(h4 *)(Y + (size_t)m * NO + c) = v;
   }
@@ -640,7 +653,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float a = (float)(_Float16)acc[i][0][r], b = (float)(_Float16)acc[i][1][r];
-        v[r] = (_Float16)((g.act == DJ_ACT_SILU ? act_silu(a) : act_gelu_tanh(a)) * b);
+        v[r] = (_Float16)(act_apply(g.act, a) * b);
       }
       if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
     }
@@ -1048,7 +1061,8 @@ static int matmul_now(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16
 
 extern "C" int dj_matmul_glu(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *H, int M, int act) {
   DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA_GLU, "decision.js: matmul_glu needs a fused w1|w3 weight (DJ_W_MFMA_GLU)");
-  DJ_REQUIRE(X && H && M >= 0 && (act == DJ_ACT_SILU || act == DJ_ACT_GELU_TANH), "decision.js: matmul_glu: bad arguments");
+  DJ_REQUIRE(X && H && M >= 0 && (act == DJ_ACT_SILU || act == DJ_ACT_GELU_TANH || act == DJ_ACT_GELU_ERF),
+             "decision.js: matmul_glu: bad arguments");
   DJ_OP_BEGIN(rec, "matmul_glu");
   const char *name = "matmul_glu";
   int splits = 1;

@@ -9,7 +9,9 @@ object turns states and questions into token ids. The default, IdPrompt, takes t
              for EmbeddingGemma 2, "option_ids" (one token-id list per option text, in the model's order: a
              noul as [no, yes], eg2-prompt.ts:27-33); for d1-omni, "markers" (the position of each option's
              marker within the question's ids, in the model's order: a noul as [false, true],
-             omni-prompt.ts:18-27)
+             omni-prompt.ts:18-27); for Laya the same markers, the question's ids laid out as
+             laya-prompt.ts does ([CLS] question [SEP], [MASK] and tokens per option, [SEP]) and read
+             before the state's
 """
 import json
 import threading
@@ -22,6 +24,7 @@ from .eg2_head import Eg2Head
 from .encoder import EncoderEngine, cosine_logits
 from .d3 import D3Engine
 from .engine import DecoderEngine
+from .laya import LayaEngine
 from .omni import OmniEngine, temperature as omni_temperature
 
 
@@ -69,6 +72,22 @@ class IdPrompt:
             raise Q.QuestionError("decision.js: a marker outside the question's ids")
         return {"ids": trunk + ids, "markers": [len(trunk) + m for m in markers], "type": q["type"]}
 
+    def sequence_laya(self, state, q, max_len=512):
+        """Laya's sequence of one question over one state (laya-prompt.ts:27-56 on ids): the question's ids first
+        ([CLS] question [SEP], each option's [MASK] and tokens, [SEP]; `markers` index them), then the state's (its
+        tokens and closing [SEP], cut to fit by the caller as laya-prompt.ts does), the whole cut to max_len tokens;
+        every option marker must fit."""
+        trunk, ids = self.trunk(state), self.branch(q)
+        markers = [int(m) for m in q["markers"]]
+        if len(markers) != Q.n_options(q):
+            raise Q.QuestionError(f"decision.js: {len(markers)} markers for a {q['type']} with {Q.n_options(q)} options")
+        if any(not 0 <= m < len(ids) for m in markers):
+            raise Q.QuestionError("decision.js: a marker outside the question's ids")
+        fit = [m for m in markers if m < max_len]
+        if len(fit) != len(markers):
+            raise Q.QuestionError(f"decision.js: only {len(fit)} of the {len(markers)} option markers fit in {max_len} tokens")
+        return {"ids": (ids + trunk)[:max_len], "markers": markers, "type": q["type"]}
+
 
 def criterion(v):
     """The legend text of a score level for every kind but d1-3b (omni-prompt.ts:16: the text, else Python's
@@ -93,7 +112,7 @@ def _kind(config):
 class Decision:
     """D1 (d1.ts:38-227): a model and the serial queue of its calls. `kind` is the reference's ModelKind
     (d1.ts:17): "d1-3b" for the causal decoders (run as d1-3B's forest), "d3" for the code readout, "d1-omni"
-    for the marker-head encoder, "eg2" for EmbeddingGemma 2."""
+    and "laya" for the marker-head encoders, "eg2" for EmbeddingGemma 2."""
 
     def __init__(self, kind, engine, prompt, tokens_per_pass, share_state=False, workflow=""):
         self.kind, self.engine, self.prompt = kind, engine, prompt
@@ -114,11 +133,9 @@ class Decision:
         from .fmt import load_manifest
         config = load_manifest(base if base.endswith("/") else base + "/")["config"]
         kind = _kind(config)
-        if kind == "laya":
-            raise ValueError("decision.js: Laya (ModernBERT) models do not run on this build")
         d3 = D3Engine if "linear_heads" in config else DecoderEngine  # the shipped d3-lite, or its attention-only form
         eg2 = Eg2Engine if "ple" in config else EncoderEngine  # the shipped EmbeddingGemma 2, or the configs[0] form
-        engine = {"d1-3b": DecoderEngine, "d3": d3, "eg2": eg2, "d1-omni": OmniEngine}[kind].load(base, opts)
+        engine = {"d1-3b": DecoderEngine, "d3": d3, "eg2": eg2, "d1-omni": OmniEngine, "laya": LayaEngine}[kind].load(base, opts)
         # the reference's defaults (d1.ts:78): 4096 tokens per pass for d1-3B, 8192 otherwise; pass a larger
         # tokens_per_pass to pack more requests into one forward (MI355X activations take ~25 KB per token)
         tpp = opts.get("tokens_per_pass") or opts.get("tokensPerPass") or (4096 if kind == "d1-3b" else 8192)
@@ -162,7 +179,7 @@ class Decision:
                 return self._run_shared(requests, on_progress) if self.share_state else self._run_decoder(requests, on_progress)
             if self.kind == "d3":
                 return self._run_d3(requests, on_progress)
-            if self.kind == "d1-omni":
+            if self.kind in ("d1-omni", "laya"):
                 return self._run_omni(requests, on_progress)
             return self._run_encoder(requests, on_progress)
 
@@ -220,13 +237,16 @@ class Decision:
         return out
 
     def _run_omni(self, requests, on_progress):
-        """runEncoder (d1.ts:121-147) for d1-omni: one sequence per question (the state read anew for each),
-        whole requests per pass up to the token budget; each question's marker logits divided by its
-        temperature (omni-prompt.ts temperatureKey: type and option-count bucket), softmax, a noul read as
-        [false, true] and reversed to [yes, no]."""
-        seqs = [[self.prompt.sequence(s, q) for q in qs] for s, qs in requests]
-        sizes = [sum(len(x["ids"]) for x in g) for g in seqs]
+        """runEncoder (d1.ts:121-147) for d1-omni and Laya: one sequence per question (the state read anew for
+        each; Laya's puts the question first, cut to max_len), whole requests per pass up to the token budget;
+        each question's marker logits divided by its temperature (omni-prompt.ts temperatureKey: type and
+        option-count bucket), softmax, a noul read as [false, true] and reversed to [yes, no]."""
         c = self.engine.m["config"]
+        if self.kind == "laya":
+            seqs = [[self.prompt.sequence_laya(s, q, c["max_len"]) for q in qs] for s, qs in requests]
+        else:
+            seqs = [[self.prompt.sequence(s, q) for q in qs] for s, qs in requests]
+        sizes = [sum(len(x["ids"]) for x in g) for g in seqs]
         out = [{"probs": [], "tokens": n} for n in sizes]
         for i, j in self._passes(sizes):
             logits = self.engine.logits([x for g in seqs[i:j] for x in g])["logits"]

@@ -26,7 +26,7 @@ def default_layout(name: str, info: dict) -> int:
     d1-3b-engine.ts:29)."""
     if name == "embed" or name.startswith("head.dense"):
         return _dj.W_PLAIN
-    if name.endswith("w13") or name.endswith(".gu"):
+    if name.endswith("w13") or name.endswith(".gu") or name.endswith(".wi"):
         return _dj.W_MFMA_GLU
     return _dj.W_MFMA
 

@@ -9,10 +9,12 @@
  * plus `ids` (its tokens) and `options` (one token-id group per option, [yes, no] for a noul; each option
  * scores its best token, d1-3b-engine.ts:112-121); for EmbeddingGemma 2, `option_ids` (one token-id list per
  * option text, in the model's order: a noul as [no, yes], eg2-prompt.ts:27-33); for d1-omni, `markers` (each
- * option's marker position within the question's ids, in the model's order: a noul as [false, true]). */
+ * option's marker position within the question's ids, in the model's order: a noul as [false, true]); for
+ * Laya the same markers, the question's ids laid out as laya-prompt.ts does and read before the state's. */
 const { DecoderEngine } = require("./engine");
 const { EncoderEngine, cosineLogits } = require("./encoder");
 const { OmniEngine, temperature: omniTemperature } = require("./omni");
+const { LayaEngine } = require("./laya");
 const { D3Engine } = require("./d3");
 const { Eg2Engine } = require("./eg2");
 const { criterion } = require("./py");
@@ -44,6 +46,16 @@ const idPrompt = {
     if (markers.some((m) => !(m >= 0 && m < ids.length))) throw new Q.QuestionError("decision.js: a marker outside the question's ids");
     return { ids: trunk.concat(ids), markers: markers.map((m) => trunk.length + m), type: q.type };
   },
+  // Laya: the question's ids first ([CLS] question [SEP], [MASK] and tokens per option, [SEP]), then the state's
+  // (laya-prompt.ts:27-56 on ids), the whole cut to maxLen; every option marker must fit
+  sequenceLaya: (state, q, maxLen = 512) => {
+    const trunk = Array.from(state.ids || state, Number), ids = Array.from(q.ids, Number), markers = Array.from(q.markers, Number);
+    if (markers.length !== Q.nOptions(q)) throw new Q.QuestionError(`decision.js: ${markers.length} markers for a ${q.type} with ${Q.nOptions(q)} options`);
+    if (markers.some((m) => !(m >= 0 && m < ids.length))) throw new Q.QuestionError("decision.js: a marker outside the question's ids");
+    const fit = markers.filter((m) => m < maxLen).length;
+    if (fit !== markers.length) throw new Q.QuestionError(`decision.js: only ${fit} of the ${markers.length} option markers fit in ${maxLen} tokens`);
+    return { ids: ids.concat(trunk).slice(0, maxLen), markers, type: q.type };
+  },
 };
 
 /** BatchOptions (d1.ts:33-35): {onProgress(done, total)}; a bare function is taken as that callback. */
@@ -71,9 +83,9 @@ class D1 {
     opts.fetch = opts.fetch || fileFetch();
     const manifest = await (await opts.fetch(`${base}manifest.json`)).json();
     const kind = kindOf(manifest.config);
-    if (kind === "laya") throw new Error("decision.js: Laya (ModernBERT) models do not run on this build");
     const engine = kind === "eg2" ? await ("ple" in manifest.config ? Eg2Engine : EncoderEngine).load(base, opts) // shipped / configs[0]
       : kind === "d1-omni" ? await OmniEngine.load(base, opts)
+      : kind === "laya" ? await LayaEngine.load(base, opts)
       : kind === "d3" && "linear_heads" in manifest.config ? await D3Engine.load(base, opts) // the shipped d3-lite
       : await DecoderEngine.load(base, opts);
     return new D1(kind, engine, opts);
@@ -133,7 +145,7 @@ class D1 {
     for (const [, qs] of requests) qs.forEach(Q.checkQuestion);
     if (this.kind === "eg2") return this.runEg2(requests, onProgress);
     if (this.kind === "d3") return this.runD3(requests, onProgress);
-    if (this.kind === "d1-omni") return this.runOmni(requests, onProgress);
+    if (this.kind === "d1-omni" || this.kind === "laya") return this.runOmni(requests, onProgress);
     return this.shareState ? this.runShared(requests, onProgress) : this.runDecoder(requests, onProgress);
   }
 
@@ -211,12 +223,13 @@ class D1 {
     return out;
   }
 
-  /** runEncoder (d1.ts:121-147) for d1-omni: one sequence per question (the state read anew for each), whole
-   * requests per pass up to the token budget; marker logits over the question's temperature (type and
-   * option-count bucket), softmax, a noul read as [false, true] and reversed to [yes, no]. */
+  /** runEncoder (d1.ts:121-147) for d1-omni and Laya: one sequence per question (the state read anew for each;
+   * Laya's puts the question first, cut to max_len), whole requests per pass up to the token budget; marker
+   * logits over the question's temperature (type and option-count bucket), softmax, a noul read as
+   * [false, true] and reversed to [yes, no]. */
   async runOmni(requests, onProgress) {
     const p = this.prompt, c = this.engine.m.config;
-    const seqs = requests.map(([s, qs]) => qs.map((q) => p.sequence(s, q)));
+    const seqs = requests.map(([s, qs]) => qs.map((q) => (this.kind === "laya" ? p.sequenceLaya(s, q, c.max_len) : p.sequence(s, q))));
     const sizes = seqs.map((g) => g.reduce((a, x) => a + x.ids.length, 0));
     const out = sizes.map((n) => ({ probs: [], tokens: n }));
     for (const [i, j] of this.passes(sizes)) {

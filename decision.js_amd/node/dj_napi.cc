@@ -570,7 +570,7 @@ napi_value Module(napi_env env, napi_value exports) {
     const char *name;
     int value;
   } consts[] = {{"W_PLAIN", DJ_W_PLAIN}, {"W_MFMA", DJ_W_MFMA}, {"W_MFMA_GLU", DJ_W_MFMA_GLU},
-                {"W_DIRECT", DJ_W_DIRECT}, {"ACT_SILU", DJ_ACT_SILU}, {"ACT_GELU_TANH", DJ_ACT_GELU_TANH},
+                {"W_DIRECT", DJ_W_DIRECT}, {"ACT_SILU", DJ_ACT_SILU}, {"ACT_GELU_TANH", DJ_ACT_GELU_TANH}, {"ACT_GELU_ERF", DJ_ACT_GELU_ERF},
                 {"ROPE_POW_NEG", DJ_ROPE_POW_NEG}, {"ROPE_INV_POW", DJ_ROPE_INV_POW},
                 {"BIAS_NONE", DJ_BIAS_NONE}, {"BIAS_RELU", DJ_BIAS_RELU}, {"BIAS_GELU_ERF", DJ_BIAS_GELU_ERF}, {"ABI_VERSION", DJ_ABI_VERSION}};
   for (const auto &k : consts) napi_set_named_property(env, exports, k.name, number(env, k.value));

@@ -13,7 +13,7 @@ function layoutFor(direct) {
   return (name) => {
     const L = lib();
     if (name === "embed" || name.startsWith("head.dense")) return L.W_PLAIN;
-    const base = name.endsWith("w13") || name.endsWith(".gu") ? L.W_MFMA_GLU : L.W_MFMA;
+    const base = name.endsWith("w13") || name.endsWith(".gu") || name.endsWith(".wi") ? L.W_MFMA_GLU : L.W_MFMA;
     return direct ? base | L.W_DIRECT : base;
   };
 }

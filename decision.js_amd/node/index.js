@@ -5,6 +5,7 @@ const { D1, Decision, softmax } = require("./d1");
 const { DecoderEngine, packForest, packShared, groupMax } = require("./engine");
 const { EncoderEngine, packEncoder } = require("./encoder");
 const { OmniEngine, packOmni } = require("./omni");
+const { LayaEngine, packLaya } = require("./laya");
 const { D3Engine, gdnSpans } = require("./d3");
 const { Eg2Engine } = require("./eg2");
 const { Eg2Head } = require("./eg2_head");
@@ -14,5 +15,5 @@ const dj = require("./dj");
 
 module.exports = {
   D1, Decision, answer: questions.answer, checkQuestion: questions.checkQuestion, DecoderEngine, EncoderEngine, OmniEngine,
-  D3Engine, Eg2Engine, Eg2Head, packForest, packShared, packEncoder, packOmni, gdnSpans, groupMax, loadWeights, fileFetch, softmax, questions, dj,
+  LayaEngine, D3Engine, Eg2Engine, Eg2Head, packForest, packShared, packEncoder, packOmni, packLaya, gdnSpans, groupMax, loadWeights, fileFetch, softmax, questions, dj,
 };

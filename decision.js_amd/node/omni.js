@@ -85,12 +85,12 @@ class OmniEngine extends DecoderEngine {
   /** Raw marker logits per sequence ([seq][marker], before the temperature); with `debug` also the trunk's
    * output and the head's stream before the scorer (f16 bits, [T * H]). */
   async logits(seqs, debug = false) {
-    const pk = packOmni(seqs);
+    const pk = this.pack(seqs);
     if (pk.T === 0) return { logits: seqs.map(() => []), debug: {} };
     const { T, M } = pk;
     this.ensure(T, M);
     const B = this.bufs;
-    for (const k of INPUTS) if (pk[k].length) B[k].upload(pk[k]);
+    for (const k of this.inputs) if (pk[k].length) B[k].upload(pk[k]);
     const rec = this.ctx.recorder(this.key(["omni", T, M, !!debug]));
     const snaps = {};
     const oi = rec.record(() => { // aborted on an error; a replay returns its snapshots in the order taken
@@ -107,6 +107,14 @@ class OmniEngine extends DecoderEngine {
     const dbg = {};
     for (const [n, i] of Object.entries(snaps)) dbg[n] = got[i];
     return { logits, debug: dbg };
+  }
+
+  pack(seqs) {
+    return packOmni(seqs);
+  }
+
+  get inputs() {
+    return INPUTS;
   }
 
   /** The decision head and scorer (omni-engine.ts:125-147). */

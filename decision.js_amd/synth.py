@@ -85,6 +85,16 @@ CONFIGS = {
                    choices={"norm_weights": 1.0, "heads": "4 query / 1 kv per layer type (not stated)",
                             "intermediate": "2048 (not stated)", "rope_theta": "1e4 sliding, 1e6 global (not stated)",
                             "embedding_dim": "768 (not stated)", "layer_scalars": 1.0}),
+    # Laya as shipped (LayaEngine, laya-engine.ts; export-laya.py): a ModernBERT-large-shaped encoder (bias-free
+    # LayerNorms, RoPE, every third layer global and the others a +-64-token window, GeGLU with the erf GELU) and
+    # d1-omni's decision head. The head sizes and temperatures are choices.
+    "laya-q8": dict(model="laya", bits=8, layers=28, hidden=1024, intermediate=2624, heads=16, vocab=50368, eps=1e-5,
+                    layer_types=["full_attention" if i % 3 == 0 else "sliding_attention" for i in range(28)], window=64,
+                    rope_theta={"full_attention": 160000.0, "sliding_attention": 10000.0},
+                    head_layers=2, head_heads=16, head_ff=4096, ln_eps=1e-5, max_len=512, head_max_len=192,
+                    temperatures={"choice": 1.1, "score": 0.9, "noul": 1.2, "choice:3-5": 1.15},
+                    choices={"norm_weights": 1.0, "head": "2 layers, 16 heads, ff 4096 (not stated)",
+                             "biases": "N(0, 0.1)", "type_emb": "N(0, 0.5)", "temperatures": "synthetic"}),
     # EmbeddingGemma-shaped bidirectional encoder, q8, mean-pool + 768->3072->768 head
     "eg2-encoder-q8": dict(model="encoder", bits=8, layers=24, hidden=768, intermediate=1152, heads=3, kv_heads=1,
                            head_dim=256, vocab=262144, eps=1e-6, rope_theta=1e4, head_width=3072, embed_dim=768,
@@ -120,6 +130,8 @@ def tensor_plan(cfg: dict):
     """[(name, kind, shape)] of a configuration: kind q (quantized linear) or n (norm weight)."""
     if cfg["model"] == "eg2":
         return _eg2_plan(cfg)
+    if cfg["model"] == "laya":
+        return _laya_plan(cfg)
     H, I, h, kv, D, V, L = (cfg[k] for k in ("hidden", "intermediate", "heads", "kv_heads", "head_dim", "vocab", "layers"))
     plan = [("embed", "q", (V, H))]
     if cfg["model"] == "d3" and "linear_heads" in cfg:  # d3-lite as exported (export-d3.py:66-102)
@@ -152,18 +164,7 @@ def tensor_plan(cfg: dict):
         if cfg["model"] == "d3":
             plan.append(("readout", "r", (len(cfg["codes"]), H)))  # f32 code matrix (d3-kernels.ts:242-260)
         if cfg["model"] == "d1-omni":  # the decision head and scorer (export-omni.py:70-90)
-            F = cfg["head_ff"]
-            plan.append(("head.type_emb", "e", (3, H)))
-            for i in range(cfg["head_layers"]):
-                p = f"head.{i}."
-                plan += [(p + "in_proj", "q", (3 * H, H)), (p + "in_proj_bias", "b", (3 * H,)),
-                         (p + "out_proj", "q", (H, H)), (p + "out_proj_bias", "b", (H,)),
-                         (p + "linear1", "q", (F, H)), (p + "linear1_bias", "b", (F,)),
-                         (p + "linear2", "q", (H, F)), (p + "linear2_bias", "b", (H,))]
-                for nm in ("norm1", "norm2"):
-                    plan += [(p + nm, "n", (H,)), (p + nm + "_bias", "b", (H,))]
-            plan += [("scorer.norm", "n", (H,)), ("scorer.norm_bias", "b", (H,)), ("scorer.fc", "q", (H, H)),
-                     ("scorer.fc_bias", "b", (H,)), ("scorer.out", "v", (H,)), ("scorer.out_bias", "s", (2,))]
+            plan += _marker_head_plan(cfg)
     else:
         for i in range(L):
             p = f"layers.{i}."
@@ -174,6 +175,36 @@ def tensor_plan(cfg: dict):
         plan += [("final_norm", "n", (H,)), ("head.dense1", "q", (cfg["head_width"], H)),
                  ("head.dense2", "q", (cfg["embed_dim"], cfg["head_width"]))]
     return plan
+
+
+def _marker_head_plan(cfg: dict):
+    """d1-omni's decision head and scorer (export-omni.py:70-90, export-laya.py:80-101)."""
+    H, F = cfg["hidden"], cfg["head_ff"]
+    plan = [("head.type_emb", "e", (3, H))]
+    for i in range(cfg["head_layers"]):
+        p = f"head.{i}."
+        plan += [(p + "in_proj", "q", (3 * H, H)), (p + "in_proj_bias", "b", (3 * H,)),
+                 (p + "out_proj", "q", (H, H)), (p + "out_proj_bias", "b", (H,)),
+                 (p + "linear1", "q", (F, H)), (p + "linear1_bias", "b", (F,)),
+                 (p + "linear2", "q", (H, F)), (p + "linear2_bias", "b", (H,))]
+        for nm in ("norm1", "norm2"):
+            plan += [(p + nm, "n", (H,)), (p + nm + "_bias", "b", (H,))]
+    plan += [("scorer.norm", "n", (H,)), ("scorer.norm_bias", "b", (H,)), ("scorer.fc", "q", (H, H)),
+             ("scorer.fc_bias", "b", (H,)), ("scorer.out", "v", (H,)), ("scorer.out_bias", "s", (2,))]
+    return plan
+
+
+def _laya_plan(cfg: dict):
+    """Laya's encoder (export-laya.py:70-79: no attention norm on layer 0) and the marker head."""
+    H, I, V = cfg["hidden"], cfg["intermediate"], cfg["vocab"]
+    plan = [("embed", "q", (V, H)), ("embed_norm", "n", (H,)), ("final_norm", "n", (H,))]
+    for i in range(cfg["layers"]):
+        p = f"layers.{i}."
+        if i > 0:
+            plan.append((p + "attn_norm", "n", (H,)))
+        plan += [(p + "mlp_norm", "n", (H,)), (p + "qkv", "q", (3 * H, H)), (p + "o", "q", (H, H)),
+                 (p + "wi", "q", (2 * I, H)), (p + "wo", "q", (H, I))]
+    return plan + _marker_head_plan(cfg)
 
 
 def _eg2_plan(cfg: dict):
@@ -220,7 +251,7 @@ def manifest_config(cfg: dict) -> dict:
                      "residual_bias": lh.get("residual_bias", 0.1)}
         return c
     c["layer_types"] = list(cfg.get("layer_types") or ["full_attention"] * cfg["layers"])
-    if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni"):
+    if cfg["model"] in ("decoder", "d3", "d1-3b", "d1-omni", "laya"):
         c["model"] = cfg["model"]
     else:
         c["model"] = "eg2-encoder"

@@ -171,12 +171,15 @@ int dj_sandwich(dj_rec *rec, int T, int H, float eps, float scale, uint16_t *X_d
  * of a held product is reported by the call that launched it. DJ_GEMV_SPLIT=0 turns this off. */
 int dj_matmul(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *Y_dev, int M);
 
-enum { DJ_ACT_SILU = 0, DJ_ACT_GELU_TANH = 1 };
+enum { DJ_ACT_SILU = 0, DJ_ACT_GELU_TANH = 1, DJ_ACT_GELU_ERF = 2 };
 /* Fused gated MLP input: for w = [w1; w3] (N = 2I, layout DJ_W_MFMA_GLU), Hout[M, I] =
  * f16(act(a) * b) with a = f16(X . w1^T), b = f16(X . w3^T) (rounded as the f16 matmul output).
  * act SILU: a / (1 + exp(-a)) (SILU_MUL / MATMUL_SWIGLU, kernels.ts:48-60, 591-599);
  * act GELU_TANH: 0.5 a (1 + tanh(0.7978845608 (a + 0.044715 a^3))), tanh argument clamped to +-15
- * (GELU_MUL, eg2-kernels.ts:9-13, 165-177). Replaces recorder().swiglu (gpu.ts:229-234). */
+ * (GELU_MUL, eg2-kernels.ts:9-13, 165-177);
+ * act GELU_ERF: 0.5 a (1 + erf(a / sqrt 2)), erf by Abramowitz & Stegun 7.1.26 (|error| < 1.5e-7; Laya's
+ * GELU_MUL, encoder-kernels.ts:25-41). Replaces recorder().swiglu (gpu.ts:229-234) and the separate GELU_MUL
+ * dispatches. */
 int dj_matmul_glu(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, uint16_t *H_dev, int M, int act);
 
 /* ---------------------------------------------------------------- ops: q/k norm + rope, attention */

@@ -651,6 +651,18 @@ def omni_forward(model: "Model", seqs, acc=F32, layers=None):
         nxt = f"layers.{i + 1}.operator_norm" if i + 1 < L else "final_norm"
         x, normed = add_rmsnorm(x, o, model.t[nxt], eps, acc=acc)
     trunk = normed
+    logits, x = marker_head(model, trunk, pk, mask, acc)
+    return logits, {"trunk": trunk, "head": x}
+
+
+def marker_head(model: "Model", trunk, pk, mask, acc=F32):
+    """d1-omni's decision head and scorer on the trunk's output (omni-engine.ts:125-147, laya-engine.ts:114-138):
+    the question-type row added, `head_layers` pre-norm layers (LayerNorm with bias, in_proj + bias, attention over
+    the sequence at 1/sqrt(D), out_proj + bias, LayerNorm, linear1 + bias + ReLU, linear2 + bias), the last residual
+    under the scorer's LayerNorm, then at each marker Linear + bias + GELU (erf) and Linear(H, 1). Returns (marker
+    logits f32 [M], the head's residual stream f16 [T, H])."""
+    c = model.c
+    H = c["hidden"]
     hh, ln = c["head_heads"], c["ln_eps"]
     Dh = H // hh
     x = add_rows(trunk, pk["qtype"], model.t["head.type_emb"], acc)
@@ -667,7 +679,59 @@ def omni_forward(model: "Model", seqs, acc=F32, layers=None):
     x, sn = add_layernorm(x, o, model.t["scorer.norm"], model.t["scorer.norm_bias"], ln, add=o is not None, acc=acc)
     g = sn[pk["markers"].astype(np.int64)]
     gf = bias_act(matmul(g, model.w16("scorer.fc"), acc), model.t["scorer.fc_bias"], 2, acc)
-    return score(gf, model.t["scorer.out"], model.t["scorer.out_bias"], acc), {"trunk": trunk, "head": x}
+    return score(gf, model.t["scorer.out"], model.t["scorer.out_bias"], acc), x
+
+
+def gelu_erf_mul(a16, b16, acc=F32):
+    """GELU_MUL of encoder-kernels.ts:25-41: f16(0.5 a (1 + erf_as(a / sqrt 2)) b)."""
+    a, b = a16.astype(acc), b16.astype(acc)
+    return (acc(0.5) * a * (acc(1) + erf_as(a * acc(0.70710678)).astype(acc)) * b).astype(F16)
+
+
+def laya_windows(rng, window):
+    """The local layers' key ranges of laya-engine.ts:64: token t of a sequence [start, end) sees
+    [max(start, t - window), min(end, t + window + 1)) (a per-token loop)."""
+    out = np.zeros((len(rng), 4), dtype=np.int32)
+    for t in range(len(rng)):
+        out[t, 0] = max(int(rng[t, 0]), t - window)
+        out[t, 1] = min(int(rng[t, 1]), t + window + 1)
+    return out
+
+
+def laya_forward(model: "Model", seqs, acc=F32):
+    """LayaEngine.logits (laya-engine.ts:55-150): the ModernBERT encoder — the embedding rows under the bias-free
+    embed_norm; per layer the attention input (layer 0: the stream itself; later layers: the bias-free attn_norm
+    after adding the previous MLP output), fused qkv, RoPE on q and k over the whole 64-dim head (pow(theta,
+    -2d/64) of the layer type's theta), attention at 1/8 over the sequence (global layers) or a +-window (the
+    others), Wo, add + mlp_norm, Wi with the erf-GELU gate, Wo; the last MLP output added under final_norm — then
+    d1-omni's head and scorer. Returns (marker logits f32 [M], {"trunk": f16 [T, H], "head": f16 [T, H]})."""
+    c = model.c
+    H, I, h, eps = c["hidden"], c["intermediate"], c["heads"], c["eps"]
+    D = H // h
+    pk = pack_omni(seqs)
+    T = pk["T"]
+    full = ranges_mask(pk["rng"], T)
+    slide = ranges_mask(laya_windows(pk["rng"], c["window"]), T)
+    zeros = np.zeros(H, dtype=F16)
+    ec, es, eb = model.t["embed"]
+    e = gather(pk["ids"], ec, es, eb)
+    _, x = add_layernorm(e, None, model.t["embed_norm"], zeros, eps, add=False, acc=acc)
+    o = None
+    for i, lt in enumerate(c["layer_types"]):
+        p = f"layers.{i}."
+        inp = x
+        if p + "attn_norm" in model.t:
+            x, inp = add_layernorm(x, o, model.t[p + "attn_norm"], zeros, eps, add=o is not None, acc=acc)
+        z = matmul(inp, model.w16(p + "qkv"), acc)
+        z = qk_norm_rope(z, h, h, D, pk["pos"], None, None, False, eps, c["rope_theta"][lt], acc=acc)
+        y = attention(z, h, h, D, full if lt == "full_attention" else slide, 1.0 / math.sqrt(D), acc)
+        o = matmul(y, model.w16(p + "o"), acc)
+        x, normed = add_layernorm(x, o, model.t[p + "mlp_norm"], zeros, eps, acc=acc)
+        ab = matmul(normed, model.w16(p + "wi"), acc)
+        o = matmul(gelu_erf_mul(ab[:, :I], ab[:, I:], acc), model.w16(p + "wo"), acc)
+    x, trunk = add_layernorm(x, o, model.t["final_norm"], zeros, eps, acc=acc)
+    logits, hx = marker_head(model, trunk, pk, full, acc)
+    return logits, {"trunk": trunk, "head": hx}
 
 
 # ---------------------------------------------------------------- host tail (gpu.ts, d1.ts, questions.ts)

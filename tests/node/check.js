@@ -70,6 +70,20 @@ async function main(req) {
       for (const k of ["ids", "pos", "qtype", "taps", "rng", "markers"]) out[k] = typed(pk[k]);
       return out;
     }
+    case "packlaya": {
+      const pk = host.packLaya(req.seqs, req.window);
+      const out = { T: pk.T, M: pk.M };
+      for (const k of ["ids", "pos", "qtype", "rng", "win", "markers"]) out[k] = typed(pk[k]);
+      return out;
+    }
+    case "layaprompt":
+      return req.calls.map(([state, q, maxLen]) => {
+        try {
+          return require(path.join(root, "d1")).idPrompt.sequenceLaya(state, q, maxLen);
+        } catch (e) {
+          return { error: e.message };
+        }
+      });
     case "omni": {
       const d = await host.Decision.load(req.model, req.opts || {});
       try {

@@ -272,6 +272,44 @@ def test_omni_packing_matches_oracle_bit_exact(pkg):
         omni.pack_omni([{"ids": [1, 2], "markers": [2], "type": "choice"}])
 
 
+def test_laya_packing_windows_bit_exact(pkg):
+    """laya.pack_laya (laya-engine.ts:57-66) is pack_omni plus each token's window; the windows equal the oracle's
+    per-token restatement bit for bit, and (the oracle pinned by the mask they stand for) a token sees key j
+    exactly when j is in its sequence and |t - j| <= window."""
+    from decision_js_amd import laya
+    rng = np.random.default_rng(9)
+    for n, w in ((1, 0), (3, 1), (7, 2), (9, 64)):
+        seqs = _omni_seqs(rng, n)
+        got, want = laya.pack_laya(seqs, w), ref.pack_omni(seqs)
+        for k in ("ids", "pos", "qtype", "rng", "markers"):
+            assert np.array_equal(got[k], want[k]), k
+        win = ref.laya_windows(want["rng"], w)
+        assert got["win"].dtype == win.dtype and np.array_equal(got["win"], win)
+        T = want["T"]
+        t = np.arange(T)
+        same = (want["rng"][:, None, 0] == want["rng"][None, :, 0])
+        assert np.array_equal(ref.ranges_mask(win, T), same & (np.abs(t[:, None] - t[None, :]) <= w))
+
+
+def test_laya_id_prompt_layout(pkg):
+    """IdPrompt.sequence_laya (laya-prompt.ts:27-56 on ids): the question's ids first and the state's after, cut
+    to max_len; markers index the question's ids unshifted; a marker past max_len is refused with the reference's
+    message, one outside the question's ids as for d1-omni."""
+    from decision_js_amd import questions as Q
+    from decision_js_amd.d1 import IdPrompt
+    p = IdPrompt()
+    q = {"type": "noul", "instructions": "?", "ids": [1, 2, 3, 4, 5], "markers": [1, 3]}
+    assert p.sequence_laya([9, 8, 7], q, 512) == {"ids": [1, 2, 3, 4, 5, 9, 8, 7], "markers": [1, 3], "type": "noul"}
+    assert p.sequence_laya({"ids": [9, 8, 7]}, q, 6)["ids"] == [1, 2, 3, 4, 5, 9]
+    assert p.sequence_laya([9], q, 4)["ids"] == [1, 2, 3, 4]
+    with pytest.raises(Q.QuestionError, match="only 1 of the 2 option markers fit in 3 tokens"):
+        p.sequence_laya([9], q, 3)
+    with pytest.raises(Q.QuestionError, match="outside the question"):
+        p.sequence_laya([9], dict(q, markers=[1, 5]), 512)
+    with pytest.raises(Q.QuestionError, match="3 markers for a noul"):
+        p.sequence_laya([9], dict(q, markers=[0, 1, 2]), 512)
+
+
 def test_omni_temperature_keys(pkg):
     """temperature() of omni-engine.ts:22-26: the type:bucket key, else the type, else 1."""
     from decision_js_amd import omni

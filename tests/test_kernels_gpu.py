@@ -157,7 +157,8 @@ def test_matmul_weights_bit_exact(pkg, ctx, bits, direct):
 
 
 @pytest.mark.parametrize("M,I,K,bits,act", [(384, 3072, 1024, 8, 0), (70, 1152, 768, 8, 1), (2200, 1024, 512, 4, 0), (19, 64, 128, 8, 1),
-                                             (32, 4608, 1536, 8, 0), (1, 1024, 2048, 4, 0), (64, 1152, 768, 8, 1)])
+                                             (32, 4608, 1536, 8, 0), (1, 1024, 2048, 4, 0), (64, 1152, 768, 8, 1),
+                                             (1500, 2624, 1024, 8, 2), (33, 96, 64, 8, 2), (1, 2624, 1024, 4, 2)])
 @pytest.mark.parametrize("direct", [False, True])
 def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
     dj = _dj()
@@ -170,19 +171,17 @@ def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
     run(ctx, lambda r: r.matmul_glu(dX, W, dH, M, act))
     got = dH.read(np.float16, (M, I))
     ab = ref.matmul(X, W16, np.float64)
-    want = (ref.silu_mul if act == 0 else ref.gelu_mul)(ab[:, :I], ab[:, I:], np.float64)
+    want = (ref.silu_mul, ref.gelu_mul, ref.gelu_erf_mul)[act](ab[:, :I], ab[:, I:], np.float64)
     # a and b are f16 matmul outputs and may each differ from the oracle's by one f16 ulp (their own
     # rounding); propagate that through act(a) * b, plus one ulp of the result
     a, b = ab[:, :I].astype(np.float64), ab[:, I:].astype(np.float64)
-    f = ref.silu_mul if act == 0 else ref.gelu_mul
-    act_a = (a / (1 + np.exp(-a))) if act == 0 else ref.gelu_tanh(a)
+    act_fn = ((lambda x: x / (1 + np.exp(-x))), ref.gelu_tanh, (lambda x: 0.5 * x * (1 + ref.erf_as(x * 0.70710678))))[act]
+    act_a = act_fn(a)
     hstep = np.maximum(np.abs(a) * 1e-4, 1e-6)
-    act_fn = (lambda x: x / (1 + np.exp(-x))) if act == 0 else ref.gelu_tanh
     dact = (act_fn(a + hstep) - act_fn(a - hstep)) / (2 * hstep)
     u = 2.0 ** -10
     bound = u * (np.abs(dact * a * b) + np.abs(act_a * b)) + u * np.abs(want.astype(np.float64)) + 1e-5
     worst = float((np.abs(got.astype(np.float64) - want.astype(np.float64)) / bound).max())
-    assert f is not None
     print(f"matmul_glu {M}x{I}x{K} q{bits} act{act}: worst/bound {worst:.3f}")
     assert worst <= 1.0
 

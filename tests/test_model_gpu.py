@@ -41,6 +41,8 @@ def models(pkg, tmp_path_factory):
         "omni": synth.reduced("d1-omni-q8", layers=3, vocab=4096, layer_types=["conv", "full_attention", "conv"]),
         "eg2ship": synth.reduced("eg2-q8", layers=3, vocab=4096, window=16, layer_scalars=[0.9, 1.1, 0.8],
                                  layer_types=["sliding_attention", "full_attention", "sliding_attention"]),
+        "laya": synth.reduced("laya-q8", layers=4, vocab=4096, window=16,
+                              layer_types=["full_attention", "sliding_attention", "sliding_attention", "full_attention"]),
         "d3lite": synth.reduced("d3-lite-q8", layers=4, vocab=4096,
                                 layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"]),
     }
@@ -543,6 +545,83 @@ def test_decision_api_omni(pkg, models):
                     assert abs(a["noul"] - p[1]) < PROB_TOL  # [false, true] reversed to [yes, no]
                 else:
                     assert abs(a["confidence"] - p.max()) < PROB_TOL
+    finally:
+        d.destroy()
+
+
+def test_laya_matches_oracle(pkg, models):
+    """Laya on the product path (LayaEngine.logits, laya-engine.ts:55-141): the ModernBERT encoder (bias-free
+    LayerNorms, plain RoPE per layer type, whole-sequence ranges on the global layers and +-16-token windows on the
+    others, the erf-GELU GLU epilogue) and d1-omni's head, sequences longer than the window packed together: the
+    encoder output and the head's stream within 2e-2 relative L2 of the oracle, each question's calibrated
+    probabilities within 1e-3; eager, captured and replayed forwards identical; a sequence's logits do not depend
+    on what it is packed with (to rounding)."""
+    from decision_js_amd.laya import LayaEngine
+    from decision_js_amd.omni import temperature
+    model = ref.Model(models["laya"])
+    rng = np.random.default_rng(27)
+    seqs = _omni_requests(rng, 4096)
+    eng = LayaEngine.load(models["laya"])
+    try:
+        runs = [eng.logits(seqs) for _ in range(3)]  # eager, capture, replay
+        assert runs[0]["logits"] == runs[1]["logits"] == runs[2]["logits"]
+        dbg = eng.logits(seqs, debug=True)
+        assert dbg["logits"] == runs[0]["logits"]
+        want, wdbg = ref.laya_forward(model, seqs, acc=np.float64)
+        assert rel_l2(dbg["debug"]["trunk"], wdbg["trunk"]) < HIDDEN_TOL
+        assert rel_l2(dbg["debug"]["head"], wdbg["head"]) < HIDDEN_TOL
+        k = 0
+        for s, got in zip(seqs, runs[0]["logits"]):
+            w = want[k:k + len(s["markers"])]
+            k += len(s["markers"])
+            t = temperature(model.c, s["type"], len(w))
+            assert max(abs(a - b) for a, b in zip(ref.softmax(np.asarray(got) / t), ref.softmax(w / t))) < PROB_TOL
+            assert np.abs(np.asarray(got) - w).max() < 2e-2 * max(1.0, np.abs(w).max())
+        alone = eng.logits([seqs[3]])["logits"][0]
+        assert max(abs(a - b) for a, b in zip(ref.softmax(alone), ref.softmax(runs[0]["logits"][3]))) < INVARIANCE_TOL
+    finally:
+        eng.destroy()
+
+
+def test_decision_api_laya(pkg, models):
+    """The laya kind through the Decision API (runEncoder with laya-prompt.ts's layout, d1.ts:121-147): the
+    question's ids first and the state's after, the whole cut to max_len; answers equal the oracle's on those
+    sequences; a question whose markers fall past max_len is refused with the reference's message."""
+    from decision_js_amd import questions as Q
+    from decision_js_amd.d1 import Decision
+    from decision_js_amd.omni import temperature
+    rng = np.random.default_rng(29)
+    V = 4096
+    model = ref.Model(models["laya"])
+    d = Decision.load(models["laya"], {"tokens_per_pass": 600})
+    try:
+        assert d.kind == "laya"
+        L = model.c["max_len"]
+        ids = lambda n: [int(x) for x in rng.integers(0, V, n)]  # noqa: E731
+        qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(20),
+                        "markers": [2, 9, 15]},
+              "churn": {"type": "noul", "instructions": "?", "ids": ids(8), "markers": [1, 5]},
+              "urgency": {"type": "score", "instructions": "?", "criteria": ["l", "m", "h", "x"], "ids": ids(14),
+                          "markers": [1, 4, 7, 10]}}
+        states = [ids(L + 40), ids(40)]  # the first state runs past max_len: cut
+        got = d.system_one_batch([(s, qs) for s in states])
+        for s, r in zip(states, got):
+            seqs = [{"ids": (q["ids"] + s)[:L], "markers": q["markers"], "type": q["type"]} for q in qs.values()]
+            assert r["usage"]["input_tokens"] == sum(len(x["ids"]) for x in seqs)
+            want, _ = ref.laya_forward(model, seqs, acc=np.float64)
+            k = 0
+            for (name, q), sq in zip(qs.items(), seqs):
+                z = want[k:k + len(sq["markers"])]
+                k += len(sq["markers"])
+                p = ref.softmax(z / temperature(model.c, q["type"], len(z)))
+                a = r["answers"][name]
+                if q["type"] == "noul":
+                    assert abs(a["noul"] - p[1]) < PROB_TOL  # [false, true] reversed to [yes, no]
+                else:
+                    assert abs(a["confidence"] - p.max()) < PROB_TOL
+        far = {"type": "noul", "instructions": "?", "ids": ids(L + 8), "markers": [3, L + 2]}
+        with pytest.raises(Q.QuestionError, match=f"only 1 of the 2 option markers fit in {L} tokens"):
+            d.system_one(ids(10), {"far": far})
     finally:
         d.destroy()
 

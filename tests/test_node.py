@@ -396,6 +396,70 @@ def test_omni_packing_matches_python_host():
         assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), k
 
 
+def test_laya_packing_and_prompt_match_python_host():
+    """packLaya (Node) == laya.pack_laya (Python) bit for bit, windows included; idPrompt.sequenceLaya gives
+    IdPrompt.sequence_laya's sequences and the same refusals."""
+    load_pkg()
+    from decision_js_amd import laya
+    from decision_js_amd.d1 import IdPrompt
+    seqs = [{"ids": list(range(40)), "markers": [3, 9, 30], "type": "choice"}, {"ids": [1], "markers": [0], "type": "noul"},
+            {"ids": list(range(13)), "markers": [0, 12], "type": "score"}]
+    for w in (0, 2, 64):
+        js = node({"cmd": "packlaya", "seqs": seqs, "window": w})
+        py = laya.pack_laya(seqs, w)
+        assert js["T"] == py["T"] and js["M"] == py["M"]
+        for k in ("ids", "pos", "qtype", "rng", "win", "markers"):
+            assert np.array_equal(np.asarray(js[k]), py[k].reshape(-1)), (w, k)
+    q = {"type": "noul", "instructions": "?", "ids": [1, 2, 3, 4, 5], "markers": [1, 3]}
+    calls = [[[9, 8, 7], q, 512], [{"ids": [9, 8, 7]}, q, 6], [[9], q, 3], [[9], dict(q, markers=[1, 5]), 512]]
+    js = node({"cmd": "layaprompt", "calls": calls})
+    p = IdPrompt()
+    for (state, qq, L), got in zip(calls, js):
+        try:
+            want = p.sequence_laya(state, qq, L)
+        except Exception as e:  # noqa: BLE001
+            assert got == {"error": str(e)}
+        else:
+            assert got == want
+
+
+@pytest.mark.gpu
+def test_node_laya_matches_python_host(tmp_path):
+    """The laya kind through Node (kindOf -> runOmni with sequenceLaya -> LayaEngine: ModernBERT encoder, head,
+    scorer) against the Python host: identical marker logits (the same packing, op sequence and library) and the
+    same answers."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.d1 import Decision
+    cfg = synth.reduced("laya-q8", layers=3, vocab=4096, window=8,
+                        layer_types=["full_attention", "sliding_attention", "sliding_attention"])
+    mdir = synth.generate(cfg, str(tmp_path / "laya"), seed=0, norm_std=0.1)
+    rng = np.random.default_rng(19)
+    ids = lambda n: [int(x) for x in rng.integers(0, 4096, n)]  # noqa: E731
+    qs = {"topic": {"type": "choice", "instructions": "?", "criteria": {"a": "", "b": "", "c": ""}, "ids": ids(16),
+                    "markers": [2, 7, 12]},
+          "churn": {"type": "noul", "instructions": "?", "ids": ids(6), "markers": [1, 4]},
+          "urgency": {"type": "score", "instructions": "?", "criteria": ["low", {"x": 2.5}], "ids": ids(9), "markers": [3, 6]}}
+    batch = [[ids(70), qs], [ids(600), qs]]  # the second state runs past max_len
+    seqs = [{"ids": ids(40), "markers": [3, 9, 30], "type": "choice"}, {"ids": ids(12), "markers": [0, 11], "type": "noul"}]
+    js = node({"cmd": "omni", "model": mdir, "batch": batch, "seqs": seqs}, timeout=300)
+    assert js["kind"] == "laya"
+    d = Decision.load(mdir)
+    try:
+        assert d.kind == "laya"
+        py = d.system_one_batch([(s, q) for s, q in batch])
+        for a, b in zip(js["batch"], py):
+            assert a["usage"] == b["usage"]
+            assert abs(a["answers"]["churn"]["noul"] - b["answers"]["churn"]["noul"]) < 1e-12
+            assert a["answers"]["topic"]["choice"] == b["answers"]["topic"]["choice"]
+            assert abs(a["answers"]["urgency"]["confidence"] - b["answers"]["urgency"]["confidence"]) < 1e-12
+        want = d.engine.logits(seqs)["logits"]
+        for a, b in zip(js["logits"], want):
+            assert np.array_equal(np.asarray(a, dtype=np.float32), np.asarray(b, dtype=np.float32))
+    finally:
+        d.destroy()
+
+
 @pytest.mark.gpu
 def test_node_omni_matches_python_host(tmp_path):
     """The d1-omni kind through Node (kindOf -> runOmni -> OmniEngine: trunk, head, scorer) against the Python

@@ -1154,3 +1154,135 @@ def test_ple_mix_and_pool_project_closed_forms():
     for s, (a, b) in enumerate(ranges):
         m = X[a:b].astype(np.float64).mean(0)
         assert np.allclose(out[s], W.astype(np.float64) @ m, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- Laya: ModernBERT encoder + d1-omni's head
+
+TINY_LAYA = dict(layers=4, hidden=64, intermediate=96, heads=4, vocab=512, window=3,
+                 layer_types=["full_attention", "sliding_attention", "sliding_attention", "full_attention"],
+                 head_layers=2, head_heads=4, head_ff=128)
+
+
+@pytest.fixture(scope="module")
+def tiny_laya(pkg, tmp_path_factory):
+    from decision_js_amd import synth
+    d = tmp_path_factory.mktemp("laya")
+    return synth.generate(synth.reduced("laya-q8", **TINY_LAYA), str(d / "laya"), norm_std=0.1, std=0.125)
+
+
+def _torch_laya(model: ref.Model):
+    """transformers' ModernBertModel (bias-free LayerNorms, RoPE per layer type, GeGLU with the erf GELU) holding the
+    oracle model's weights, float64, run with d1-omni-style per-sequence masks (all keys on the global layers,
+    |i - j| <= window on the others); then the head modules of _torch_omni's construction."""
+    tr = pytest.importorskip("transformers")
+    c = model.c
+    H, I, h = c["hidden"], c["intermediate"], c["heads"]
+    cfg = tr.ModernBertConfig(vocab_size=c["vocab"], hidden_size=H, intermediate_size=I, num_hidden_layers=c["layers"],
+                              num_attention_heads=h, layer_types=c["layer_types"], local_attention=2 * c["window"],
+                              norm_eps=c["eps"], norm_bias=False, hidden_activation="gelu", pad_token_id=0,
+                              bos_token_id=None, eos_token_id=None, cls_token_id=None, sep_token_id=None,
+                              rope_parameters={t: {"rope_type": "default", "rope_theta": th} for t, th in c["rope_theta"].items()})
+    m = tr.ModernBertModel(cfg)
+    m.config._attn_implementation = "eager"
+    m = m.to(torch.float64).eval()
+    sd = {"embeddings.tok_embeddings.weight": _t(model.w16("embed")), "embeddings.norm.weight": _t(model.t["embed_norm"]),
+          "final_norm.weight": _t(model.t["final_norm"])}
+    for i in range(c["layers"]):
+        p = f"layers.{i}."
+        if i > 0:
+            sd[p + "attn_norm.weight"] = _t(model.t[p + "attn_norm"])
+        sd[p + "mlp_norm.weight"] = _t(model.t[p + "mlp_norm"])
+        sd[p + "attn.Wqkv.weight"], sd[p + "attn.Wo.weight"] = _t(model.w16(p + "qkv")), _t(model.w16(p + "o"))
+        sd[p + "mlp.Wi.weight"], sd[p + "mlp.Wo.weight"] = _t(model.w16(p + "wi")), _t(model.w16(p + "wo"))
+    missing, unexpected = m.load_state_dict(sd, strict=False)
+    assert not unexpected and all("rotary" in k for k in missing), (missing, unexpected)
+    return m
+
+
+def _torch_marker_head(model: ref.Model):
+    c = model.c
+    H, hh, ff, ln = c["hidden"], c["head_heads"], c["head_ff"], c["ln_eps"]
+    layers = []
+    for i in range(c["head_layers"]):
+        p = f"head.{i}."
+        lay = torch.nn.TransformerEncoderLayer(H, hh, ff, dropout=0.0, activation="relu", layer_norm_eps=ln,
+                                               batch_first=True, norm_first=True).to(torch.float64).eval()
+        sd = {"self_attn.in_proj_weight": model.w16(p + "in_proj"), "self_attn.in_proj_bias": model.t[p + "in_proj_bias"],
+              "self_attn.out_proj.weight": model.w16(p + "out_proj"), "self_attn.out_proj.bias": model.t[p + "out_proj_bias"],
+              "linear1.weight": model.w16(p + "linear1"), "linear1.bias": model.t[p + "linear1_bias"],
+              "linear2.weight": model.w16(p + "linear2"), "linear2.bias": model.t[p + "linear2_bias"],
+              "norm1.weight": model.t[p + "norm1"], "norm1.bias": model.t[p + "norm1_bias"],
+              "norm2.weight": model.t[p + "norm2"], "norm2.bias": model.t[p + "norm2_bias"]}
+        lay.load_state_dict({k: _t(v) for k, v in sd.items()})
+        layers.append(lay)
+    scorer = torch.nn.Sequential(torch.nn.LayerNorm(H, eps=ln), torch.nn.Linear(H, H), torch.nn.GELU(),
+                                 torch.nn.Linear(H, 1)).to(torch.float64).eval()
+    scorer.load_state_dict({"0.weight": _t(model.t["scorer.norm"]), "0.bias": _t(model.t["scorer.norm_bias"]),
+                            "1.weight": _t(model.w16("scorer.fc")), "1.bias": _t(model.t["scorer.fc_bias"]),
+                            "3.weight": _t(model.t["scorer.out"]).reshape(1, H), "3.bias": _t(model.t["scorer.out_bias"][:1])})
+    return layers, scorer, _t(model.t["head.type_emb"])
+
+
+def _compare_laya(path, model=None):
+    """The oracle's packed Laya forward against ModernBertModel + the head modules on each sequence alone: encoder
+    output and head stream within 5e-3 relative L2, marker logits within 1e-2 of their scale."""
+    model = model or ref.Model(path)
+    seqs = _omni_seqs(np.random.default_rng(6), model.c["vocab"])
+    logits, dbg = ref.laya_forward(model, seqs, acc=np.float64)
+    fresh = ref.Model(path)
+    enc = _torch_laya(fresh)
+    layers, scorer, type_emb = _torch_marker_head(fresh)
+    w = fresh.c["window"]
+    off = k = 0
+    for s in seqs:
+        n, m = len(s["ids"]), len(s["markers"])
+        pos = torch.arange(n)
+        slide = torch.zeros(1, 1, n, n, dtype=torch.float64).masked_fill((pos[:, None] - pos[None, :]).abs() > w, -1e30)
+        with torch.no_grad():
+            x = enc(input_ids=torch.tensor([s["ids"]]), attention_mask={"full_attention": torch.zeros(1, 1, n, n, dtype=torch.float64),
+                                                                      "sliding_attention": slide}).last_hidden_state
+            trunk = x[0].numpy().copy()
+            hx = x + type_emb[["choice", "score", "noul"].index(s["type"])]
+            for lay in layers:
+                hx = lay(hx)
+            want = scorer(hx)[0, s["markers"], 0].numpy()
+        assert _rel_l2(dbg["trunk"][off:off + n], trunk) < 5e-3, f"{s['type']}: encoder output"
+        assert _rel_l2(dbg["head"][off:off + n], hx[0].numpy()) < 5e-3, f"{s['type']}: head stream"
+        got = logits[k:k + m].astype(np.float64)
+        assert np.abs(got - want).max() < 1e-2 * max(np.abs(want).max(), 1e-3), f"{s['type']}: marker logits"
+        off += n
+        k += m
+
+
+def test_laya_forward_matches_modernbert(tiny_laya):
+    _compare_laya(tiny_laya)
+
+
+@pytest.mark.parametrize("slip", ["global_on_every_layer", "theta_swapped", "window_plus_one", "attn_norm_on_layer0"])
+def test_planted_laya_slips_are_caught(tiny_laya, slip):
+    """Every layer global (no windows); the global and local RoPE thetas swapped; the window one key wider;
+    layer 0's attention reading a normed stream (ModernBERT's layer 0 has no attention norm). (The tanh GELU in
+    place of erf moves the outputs by less than f16's rounding: test_gelu_erf_mul_matches_torch pins it.)"""
+    model = ref.Model(tiny_laya)
+    if slip == "global_on_every_layer":
+        model.c["layer_types"] = ["full_attention"] * len(model.c["layer_types"])
+    elif slip == "theta_swapped":
+        th = model.c["rope_theta"]
+        model.c["rope_theta"] = {"full_attention": th["sliding_attention"], "sliding_attention": th["full_attention"]}
+    elif slip == "window_plus_one":
+        model.c["window"] += 1
+    else:
+        model.t["layers.0.attn_norm"] = np.full(model.c["hidden"], 0.5, dtype=np.float16)
+    with pytest.raises(AssertionError):
+        _compare_laya(tiny_laya, model)
+
+
+def test_gelu_erf_mul_matches_torch():
+    """gelu_erf_mul against torch's exact-erf GELU times b in f64: within one f16 rounding of the product (the erf
+    approximation adds < 1.5e-7 absolute), over inputs where the tanh form differs from erf by up to 4.7e-4."""
+    a = np.linspace(-6, 6, 4001).astype(np.float16)
+    b = np.random.default_rng(2).uniform(0.5, 4, a.shape).astype(np.float16)
+    got = ref.gelu_erf_mul(a, b, np.float64).astype(np.float64)
+    want = (F.gelu(torch.from_numpy(a.astype(np.float64)), approximate="none") * torch.from_numpy(b.astype(np.float64))).numpy()
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert (np.abs(got - want) <= 0.5 * ulp + 1e-6).all()
