@@ -133,9 +133,13 @@ struct GemmArgs {
 
 // Ring of LDS stages, each holding one 64-K step of the tile: A (BM rows x 128 bytes, XOR-swizzled 16-byte
 // chunks), the NB weight blocks of B in their global lane order, and (quantized B) each block's 16 scale words.
-template <int BITS, int WM, int WN, int FM, int FN, int RING>
+// WK = 2: two K wave sets split every paired-ring step pair (a step each), each set accumulating the whole
+// WM x WN wave tile; the sets' partial tiles are added through LDS at the end. Against a wave row twice as
+// wide on the same A rows, a wave reads half the A fragments per MFMA, and the per-pair chain (barrier,
+// fragment reads, dequantization, MFMAs) is one step long.
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int WK = 1>
 struct GemmShape {
-  static constexpr int NW = WM * WN, NT = NW * 64;
+  static constexpr int NW = WM * WN * WK, NT = NW * 64;
   static constexpr int BM = WM * FM * 16, BN = WN * FN * 16, NB = BN / 16;
   static constexpr int CB = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;  // bytes per 16x64 weight block
   static constexpr int A_BYTES = BM * 128;
@@ -161,11 +165,15 @@ struct GemmShape {
   static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
   static_assert(!PAIRED || (NS % 2 == 0 && NS >= 4 && (NS / 2 - 2) * 2 * I < 64), "paired ring");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
+  static_assert(WK == 1 || (WK == 2 && PAIRED), "K wave sets take a paired ring's steps");
+  // LDS: the ring, or the K wave sets' partial tiles where those are larger (they reuse the ring's bytes)
+  static constexpr int RED = (WK - 1) * BM * BN * 4, SMEM = NS * STAGE > RED ? NS * STAGE : RED;
+  static_assert(SMEM <= 160 * 1024, "LDS for the partial tiles");
   // waves per SIMD that LDS allows (workgroups per CU x waves per workgroup / 4 SIMDs): the register budget
   // the compiler may use without costing occupancy. Left to itself it squeezes a 128x128 tile to 120 VGPRs
   // to reach 4 waves per SIMD that LDS never grants, serializing the fragment reads (9-15% slower at 1536 x
   // 2048 x 11008, measured).
-  static constexpr int WG_PER_CU = 160 * 1024 / (NS * STAGE);
+  static constexpr int WG_PER_CU = 160 * 1024 / SMEM;
   static constexpr int WPE_RAW = WG_PER_CU * NW / 4;
   static constexpr int WPE = WPE_RAW < 1 ? 1 : WPE_RAW > 8 ? 8 : WPE_RAW;
   // MFMA loop order: weight fragment outermost where LDS holds occupancy to <= 3 waves per SIMD (up to 168
@@ -187,17 +195,17 @@ __device__ __forceinline__ void wait_steps_barrier(int n) {
 }
 
 // EPI: 0 plain store, 1 gated MLP, 2 QK_NORM_ROPE on a qkv weight (kernels.ts:86-112) before the store
-template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI>
-__global__ __launch_bounds__(WM *WN * 64)
-__attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE))) void k_gemm(GemmArgs g) {
-  using S = GemmShape<BITS, WM, WN, FM, FN, RING>;
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI, int WK>
+__global__ __launch_bounds__(WM *WN *WK * 64)
+__attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>::WPE))) void k_gemm(GemmArgs g) {
+  using S = GemmShape<BITS, WM, WN, FM, FN, RING, WK>;
   constexpr bool GLU = EPI == 1;
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::SMEM];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave / WN, wn = wave % WN;
+  const int wk = wave / (WM * WN), wm = (wave % (WM * WN)) / WN, wn = wave % WN;
   int tm, tn;
   map_tile(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * (WN * FN * 16);
@@ -294,7 +302,22 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
   for (int p = 0; p < (S::PAIRED ? NS - 2 : NS - 1); ++p)
     if (p < KS) issue(p, p);
 
-  if constexpr (S::PAIRED) {
+  if constexpr (S::PAIRED && WK > 1) {
+    // Paired ring with two K wave sets: the pair's waits, barrier and DMAs as below; set wk then reads and
+    // multiplies step 2 kp + wk only.
+    constexpr int NP = NS / 2;
+    const int KP = KS / 2;
+    for (int kp = 0; kp < KP; ++kp) {
+      wait_steps_barrier<2 * S::I, NP - 2>(min(NP - 2, KP - 1 - kp));
+      const int nx = kp + NP - 1;
+      if (nx < KP) { issue(2 * nx, (2 * nx) % NS); issue(2 * nx + 1, (2 * nx + 1) % NS); }
+      h8 a0[FM][2];
+      RawB<BITS> r0[FN];
+      uint32_t p0[FN];
+      DJ_READ(2 * kp + wk, a0, r0, p0);
+      DJ_MMA(a0, r0, p0);
+    }
+  } else if constexpr (S::PAIRED) {
     // Paired ring (NP = NS / 2 pairs of stages; KS even): steps land two at a time, so the counter wait and the
     // workgroup barrier come once per 128 K. At pair p: pairs p+1 .. p+NP-2 may still be in flight; after the
     // barrier every wave is done with pair p-1, whose stages take pair p+NP-1. Both steps' fragments are read
@@ -351,6 +374,28 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING>::WPE
 #undef DJ_READ
 #undef DJ_MMA
   wait_vm<0>();  // the clamped tail DMAs land before the wave moves on
+
+  if constexpr (WK > 1) {
+    // K wave sets 1 .. WK-1 leave their partial tiles in the (now idle) ring; set 0 adds them in set order
+    // (deterministic) and runs the epilogue alone
+    f4 *part = (f4 *)smem;
+    constexpr int FR = FM * FN;  // fragments per wave
+    __syncthreads();  // every DMA has landed and every wave is past its last fragment read
+    if (wk > 0) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) part[(((wk - 1) * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane] = acc[i][j];
+    }
+    __syncthreads();
+    if (wk > 0) return;
+#pragma unroll
+    for (int k = 0; k < WK - 1; ++k)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] += part[((k * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane];
+  }
 
   // The MFMAs take the weight fragment as their first operand, so each accumulator holds a 16x16 block of
   // Y^T: lane l has output row l%16 of the block and its 4 consecutive columns 4(l/16)..+3 — one 8-byte f16
@@ -687,10 +732,10 @@ static void launch_gemv(hipStream_t s, GemmArgs a) {
 
 // ---------------------------------------------------------------- dispatch
 
-// Tile configurations: waves along M and N, 16x16 fragments per wave along M and N, K groups.
+// Tile configurations: waves along M and N, 16x16 fragments per wave along M and N, ring, K wave sets.
 struct GemmCfg {
   const char *tag;
-  int wm, wn, fm, fn, ring;
+  int wm, wn, fm, fn, ring, wk;
   int bm() const { return wm * fm * 16; }
   int bn() const { return wn * fn * 16; }
 };
@@ -698,50 +743,52 @@ struct GemmCfg {
 // "n": one wave row (every wave spans all BM rows and owns distinct columns, so no two waves dequantize the
 // same weight fragment)
 #define DJ_GEMM_CFGS(X)                                                                                    \
-  X(0, "256x128", 2, 2, 8, 4, 0) X(1, "128x128", 2, 2, 4, 4, 0) X(2, "128x64", 2, 2, 4, 2, 0)              \
-  X(3, "64x128", 2, 2, 2, 4, 0) X(4, "64x64", 2, 2, 2, 2, 0) X(5, "32x128", 1, 4, 2, 2, 0)                 \
-  X(6, "128x32", 4, 1, 2, 2, 0) X(7, "128x16", 4, 1, 2, 1, 0) X(8, "32x64", 1, 4, 2, 1, 0)                 \
-  X(9, "64x32", 2, 2, 2, 1, 0) X(10, "128x128s2", 2, 2, 4, 4, 2) X(11, "128x128s3", 2, 2, 4, 4, 3)         \
-  X(12, "256x128s2", 2, 2, 8, 4, 2) X(13, "128x256", 2, 2, 4, 8, 0) X(14, "128x256s2", 2, 2, 4, 8, 2)      \
-  X(15, "64x64s2", 2, 2, 2, 2, 2) X(16, "32x128s2", 1, 4, 2, 2, 2) X(17, "64x128s2", 2, 2, 2, 4, 2)        \
-  X(18, "128x64s2", 2, 2, 4, 2, 2) X(19, "128x128n", 1, 4, 8, 2, 2) X(20, "128x128n3", 1, 4, 8, 2, 3)        \
-  X(21, "64x128n", 1, 4, 4, 2, 2) X(22, "128x256n", 1, 4, 8, 4, 2) X(23, "64x256n", 1, 4, 4, 4, 2)        \
-  X(24, "144x128n", 1, 4, 9, 2, 2) X(25, "144x64n", 1, 4, 9, 1, 2) X(26, "96x128n", 1, 4, 6, 2, 2)         \
-  X(27, "48x128n", 1, 4, 3, 2, 2) X(28, "144x128n4", 1, 4, 9, 2, 4) X(29, "144x128n5", 1, 4, 9, 2, 5)        \
-  X(30, "144x64n4", 1, 4, 9, 1, 4) X(31, "144x64n6", 1, 4, 9, 1, 6) X(32, "128x128n4", 1, 4, 8, 2, 4)        \
-  X(33, "128x128n6", 1, 4, 8, 2, 6) X(34, "64x128n4", 1, 4, 4, 2, 4) X(35, "64x128n6", 1, 4, 4, 2, 6)        \
-  X(36, "144x128w8", 1, 8, 9, 1, 2) X(37, "144x128w8r3", 1, 8, 9, 1, 3) X(38, "128x128w8", 2, 4, 4, 2, 2)     \
-  X(39, "64x128w8", 1, 8, 4, 1, 2) X(40, "32x64w8", 2, 4, 1, 1, 0) X(41, "128x256w8", 1, 8, 8, 2, 2)          \
-  X(42, "128x128w8r3", 2, 4, 4, 2, 3) X(43, "64x128w8r4", 1, 8, 4, 1, 4)                                    \
-  X(44, "32x64p4", 1, 4, 2, 1, -4) X(45, "32x64p6", 1, 4, 2, 1, -6) X(46, "128x128np4", 1, 4, 8, 2, -4)      \
-  X(47, "128x256w8p4", 1, 8, 8, 2, -4) X(48, "64x128np4", 1, 4, 4, 2, -4) X(49, "144x64np4", 1, 4, 9, 1, -4)      \
-  X(50, "144x128np4", 1, 4, 9, 2, -4)
-#define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring) {tag, wm, wn, fm, fn, ring},
+  X(0, "256x128", 2, 2, 8, 4, 0, 1) X(1, "128x128", 2, 2, 4, 4, 0, 1) X(2, "128x64", 2, 2, 4, 2, 0, 1)              \
+  X(3, "64x128", 2, 2, 2, 4, 0, 1) X(4, "64x64", 2, 2, 2, 2, 0, 1) X(5, "32x128", 1, 4, 2, 2, 0, 1)                 \
+  X(6, "128x32", 4, 1, 2, 2, 0, 1) X(7, "128x16", 4, 1, 2, 1, 0, 1) X(8, "32x64", 1, 4, 2, 1, 0, 1)                 \
+  X(9, "64x32", 2, 2, 2, 1, 0, 1) X(10, "128x128s2", 2, 2, 4, 4, 2, 1) X(11, "128x128s3", 2, 2, 4, 4, 3, 1)         \
+  X(12, "256x128s2", 2, 2, 8, 4, 2, 1) X(13, "128x256", 2, 2, 4, 8, 0, 1) X(14, "128x256s2", 2, 2, 4, 8, 2, 1)      \
+  X(15, "64x64s2", 2, 2, 2, 2, 2, 1) X(16, "32x128s2", 1, 4, 2, 2, 2, 1) X(17, "64x128s2", 2, 2, 2, 4, 2, 1)        \
+  X(18, "128x64s2", 2, 2, 4, 2, 2, 1) X(19, "128x128n", 1, 4, 8, 2, 2, 1) X(20, "128x128n3", 1, 4, 8, 2, 3, 1)        \
+  X(21, "64x128n", 1, 4, 4, 2, 2, 1) X(22, "128x256n", 1, 4, 8, 4, 2, 1) X(23, "64x256n", 1, 4, 4, 4, 2, 1)        \
+  X(24, "144x128n", 1, 4, 9, 2, 2, 1) X(25, "144x64n", 1, 4, 9, 1, 2, 1) X(26, "96x128n", 1, 4, 6, 2, 2, 1)         \
+  X(27, "48x128n", 1, 4, 3, 2, 2, 1) X(28, "144x128n4", 1, 4, 9, 2, 4, 1) X(29, "144x128n5", 1, 4, 9, 2, 5, 1)        \
+  X(30, "144x64n4", 1, 4, 9, 1, 4, 1) X(31, "144x64n6", 1, 4, 9, 1, 6, 1) X(32, "128x128n4", 1, 4, 8, 2, 4, 1)        \
+  X(33, "128x128n6", 1, 4, 8, 2, 6, 1) X(34, "64x128n4", 1, 4, 4, 2, 4, 1) X(35, "64x128n6", 1, 4, 4, 2, 6, 1)        \
+  X(36, "144x128w8", 1, 8, 9, 1, 2, 1) X(37, "144x128w8r3", 1, 8, 9, 1, 3, 1) X(38, "128x128w8", 2, 4, 4, 2, 2, 1)     \
+  X(39, "64x128w8", 1, 8, 4, 1, 2, 1) X(40, "32x64w8", 2, 4, 1, 1, 0, 1) X(41, "128x256w8", 1, 8, 8, 2, 2, 1)          \
+  X(42, "128x128w8r3", 2, 4, 4, 2, 3, 1) X(43, "64x128w8r4", 1, 8, 4, 1, 4, 1)                                    \
+  X(44, "32x64p4", 1, 4, 2, 1, -4, 1) X(45, "32x64p6", 1, 4, 2, 1, -6, 1) X(46, "128x128np4", 1, 4, 8, 2, -4, 1)      \
+  X(47, "128x256w8p4", 1, 8, 8, 2, -4, 1) X(48, "64x128np4", 1, 4, 4, 2, -4, 1) X(49, "144x64np4", 1, 4, 9, 1, -4, 1)      \
+  X(50, "144x128np4", 1, 4, 9, 2, -4, 1) X(51, "48x64k2", 1, 2, 3, 2, -4, 2)        \
+  X(52, "64x64k2", 1, 2, 4, 2, -4, 2) X(53, "80x64k2", 1, 2, 5, 2, -4, 2) X(54, "96x64k2", 1, 2, 6, 2, -4, 2)        \
+  X(55, "64x128k2", 1, 4, 4, 2, -4, 2) X(56, "80x64k2p8", 1, 2, 5, 2, -8, 2) X(57, "96x64k2p8", 1, 2, 6, 2, -8, 2)
+#define DJ_CFG_ROW(i, tag, wm, wn, fm, fn, ring, wk) {tag, wm, wn, fm, fn, ring, wk},
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI>
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI, int WK>
 static void launch_cfg(hipStream_t s, GemmArgs a) {
-  if constexpr ((EPI == 1 && FN % 2 != 0) || (EPI == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144))) {
+  if constexpr ((EPI == 1 && FN % 2 != 0) || (EPI == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144 || WK > 1))) {
     return;  // never picked: a gated tile needs gate/up fragment pairs, a RoPE tile is one 128-wide head of at
-             // most 144 rows (its epilogue holds every row pass in registers)
+             // most 144 rows (its epilogue holds every row pass in registers) on one set of waves
   } else {
     dim3 grid(a.tiles_m * a.tiles_n, a.splits);
-    k_gemm<BITS, WM, WN, FM, FN, RING, EPI><<<grid, WM * WN * 64, 0, s>>>(a);
+    k_gemm<BITS, WM, WN, FM, FN, RING, EPI, WK><<<grid, WM * WN * WK * 64, 0, s>>>(a);
   }
 }
 
 template <int BITS, int EPI>
 static void launch_index(int i, hipStream_t s, GemmArgs a) {
-#define DJ_CFG_CASE(i, tag, wm, wn, fm, fn, ring) \
-  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, EPI>(s, a); break;
+#define DJ_CFG_CASE(i, tag, wm, wn, fm, fn, ring, wk) \
+  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, EPI, wk>(s, a); break;
   switch (i) { DJ_GEMM_CFGS(DJ_CFG_CASE) }
 #undef DJ_CFG_CASE
 }
 
 // epi: 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (the tile is one 128-wide head, <= 144 rows)
 static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
-  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144)) &&
+  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144 && c.wk == 1)) &&
          (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time (the 2-stage
                                                // fallback of a paired tile takes any count; the check keeps
                                                // the rule simple)
@@ -761,8 +808,19 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
 //   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
 //               against 17-18 for 64x128n),
 //   64x128n     when it gives >= 2 tiles per CU,
-//   32x64p4     when it gives >= 2 tiles per CU (narrow N: o_proj, w2 at 1152 rows; the paired 4-stage ring,
-//               K / 64 even: 13.4 vs 13.9 us and 19.2 vs 19.9 us at 1152 x 1024 x 2048 / 3072), else 32x64,
+//   K wave set tiles (two wave sets, K / 64 even, K >= 2048; plain products): 80x64k2p8 or 96x64k2p8 where
+//               their tiles make one round at one workgroup per CU (0.75-1 per CU: the 8-stage paired ring keeps three pairs
+//               of weight blocks in flight, which is what products on weights cold in HBM wait for), else the one of
+//               48x64k2 / 64x64k2 / 80x64k2 / 96x64k2 (4 stages) whose grid is nearest 1.5 per CU, where that is
+//               1-3 per CU (below one per CU, e.g. the 0.8B state's 8-question pass at 256 rows, it measured
+//               slower in the forward than the rules below; so did K = 1024, Laya's 1152 x 3072 / 1024 x 1024
+//               products on weights cold in HBM: 2.875 vs 2.818 ms per Laya ticket). In the ticket's forward (T = 1152, same box): 80x64k2p8 for o_proj / w2, 2.534 ms
+//               per ticket, against 2.63 for 32x64p4 and for 48x64k2 (alone with weights cold in HBM, w2 16.8-18.0
+//               vs 19.3-20.5 us; with weights in the MALL 48x64k2 is the faster, 15.8-17.5 us, which the forward
+//               does not see). Alone, MALL-resident weights, against 32x64p4: 1152 x 2048 x 1024 10.2 vs 13.6 us,
+//               1536 x 2048 x 2048 q4 19.7 vs 28.0, 1280 x 1024 x 3584 18.5 vs 23.2, 576 x 1024 x 2048 10.8 vs
+//               10.8 (15.8 for the 128x16 the rules below gave it),
+//   32x64p4     when it gives >= 2 tiles per CU (the paired 4-stage ring, K / 64 even), else 32x64,
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
 static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &cfg, int &splits) {
@@ -784,6 +842,9 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
   // the 0.8B prefill's w2, 1024 x 1536 x 4608 q8, 32.8 against 36.6); below that, 64x128n split 4 ways at
   // 0.1-0.25 tiles per CU (the 0.8B 8-question pass's w2, 256 x 1536 x 4608: 19.7 against 23.8 on 32x64);
   // DJ_GEMM_LONGK_SPLIT=1 keeps the paired ring unsplit
+  const char *kss = getenv("DJ_GEMM_KSETS");  // DJ_GEMM_KSETS=0: no K wave set tiles (A/B sweeps)
+  const bool ksets_off = kss && atoi(kss) == 0;
+  const char *kst = getenv("DJ_GEMM_KSET_TILE");
   const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
   const int longk = lks ? atoi(lks) : 4;
   int rule_splits = 0;
@@ -791,9 +852,30 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
     static const struct { int cfg; double per_cu; int min_k; double max_per_cu; int ks; } rules[] = {
         {47, 0.75, 0, 1.0, 0}, {41, 8.0, 0, 1e9, 0}, {19, 1.5, 0, 1e9, 0}, {19, 0.25, 4096, 1.0, -1}, {19, 0.5, 4096, 1e9, 0},
         {21, 0.1, 4096, 0.25, -1},
-        {25, 2.0, 0, 1e9, 0}, {24, 1.0, 0, 1e9, 0}, {21, 2.0, 0, 1e9, 0}, {44, 2.0, 0, 1e9, 0}, {8, 2.0, 0, 1e9, 0},
-        {16, 2.0, 0, 1e9, 0}};
-    for (const auto &r : rules)
+        {25, 2.0, 0, 1e9, 0}, {24, 1.0, 0, 1e9, 0}, {21, 2.0, 0, 1e9, 0}, {-2, 1.0, 0, 3.0, 0}, {44, 2.0, 0, 1e9, 0},
+        {8, 2.0, 0, 1e9, 0}, {16, 2.0, 0, 1e9, 0}};
+    for (const auto &r : rules) {
+      if (r.cfg == -2) {  // the K wave set family (see above)
+        if (glu || ksets_off || K < 2048) continue;
+        int best = -1;
+        for (int i : {56, 57})  // one round of one-workgroup-per-CU tiles on the 8-stage ring, most tiles first
+          if (best < 0 && cfg_fits(kCfgs[i], N, K, glu) && tiles(i) >= 0.75 * cus && tiles(i) <= cus) best = i;
+        if (best < 0) {  // else the 4-stage tile nearest 1.5 per CU, within the rule's bounds
+          for (int i : {51, 52, 53, 54})
+            if (cfg_fits(kCfgs[i], N, K, glu) &&
+                (best < 0 || std::abs(tiles(i) - 1.5 * cus) < std::abs(tiles(best) - 1.5 * cus)))
+              best = i;
+          if (best >= 0 && (tiles(best) < r.per_cu * cus || tiles(best) > r.max_per_cu * cus)) best = -1;
+        }
+        if (kst)  // DJ_GEMM_KSET_TILE=<tag>: this rule's tile (A/B sweeps inside a forward)
+          for (int i = 0; i < kNumCfgs; ++i)
+            if (!strcmp(kst, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) best = i;
+        if (best >= 0) {
+          cfg = best;
+          break;
+        }
+        continue;
+      }
       if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
           tiles(r.cfg) <= r.max_per_cu * cus) {
         if (r.ks < 0) {  // a long-K rule: the split where it divides K and fits the workspace; else what the rules
@@ -810,6 +892,7 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
         cfg = r.cfg;
         break;
       }
+    }
     if (cfg < 0) {  // nothing fills the chip: the tile with the most workgroups among those no taller than
                     // the rows need (a 128-row tile on 32 rows does 4x the matrix work: 25 us against 9 for
                     // 32x64 on M = 32, 1536 x 4608)

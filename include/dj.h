@@ -206,7 +206,8 @@ int dj_rope_table(dj_rec *rec, int T, const int32_t *pos_dev, int pos_stride, fl
 
 /* recorder().matmul(X, w_qkv, Z, M) (gpu.ts:202-226) followed by QK_NORM_ROPE (kernels.ts:86-112) on Z: the
  * same results as dj_matmul then dj_qk_norm_rope(M, heads, kv, D, stride = w->N, Z, qn, kn, vnorm, pos,
- * pos_stride, eps, theta, rot, rope_mode). tab_dev: dj_rope_table of the same positions, theta, rot and mode
+ * pos_stride, eps, theta, rot, rope_mode) where that dj_matmul sums K in step order (its tiles with K wave
+ * sets add two partial sums instead: the same product to within its f32 rounding). tab_dev: dj_rope_table of the same positions, theta, rot and mode
  * (M rows). For D = 128, M > 64 and at most two 128-row head tiles per CU the norm and rotation run in the
  * product's epilogue on tab_dev's angles (one head per tile, one kernel instead of two); otherwise as the two
  * kernels. */

@@ -247,6 +247,80 @@ def test_matmul_forced_tiles_and_split_k(pkg, ctx, monkeypatch, tile, splits, gl
             assert f16_close(dY.read(np.float16, (M, N)), want, ulps=1.0, atol=2e-5) <= 1.0
 
 
+@pytest.mark.parametrize("tile", ["48x64k2", "64x64k2", "80x64k2", "96x64k2", "64x128k2", "80x64k2p8", "96x64k2p8"])
+@pytest.mark.parametrize("bits,glu,K", [(8, False, 2048), (8, False, 128), (4, False, 3072), (16, False, 1024),
+                                        (8, True, 1024), (4, True, 256)])
+def test_matmul_k_wave_sets(pkg, ctx, monkeypatch, tile, bits, glu, K):
+    """Tiles whose waves also split K (two wave sets, each taking one step of every paired-ring pair; the
+    partial tiles are added through LDS in set order): q8, q4 and direct f16 weights, one pair only (K = 128),
+    ragged rows (300), the gated epilogue; each within the product's one-ulp bound of the oracle, and
+    bit-identical on a second run."""
+    dj = _dj()
+    monkeypatch.setenv("DJ_GEMM_TILE", tile)
+    rng = np.random.default_rng(K + bits + glu)
+    M, N = 300, 1024
+    qb = 8 if bits == 16 else bits
+    codes, scales = quant(rng, N, K, qb)
+    W16 = ref.dequant_f16(codes, scales, qb)
+    layout = (dj.W_MFMA_GLU if glu else dj.W_MFMA) | (dj.W_DIRECT if bits == 16 else 0)
+    W = ctx.weight_q(codes, scales, N, K, qb, layout)
+    X = rand_f16(rng, (M, K))
+    dX = ctx.array(X)
+    outs = []
+    ctx.profile_reset()
+    ctx.profile(True)
+    try:
+        for _ in range(2):
+            dY = ctx.alloc(M * N * 2)
+            if glu:
+                run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
+                outs.append(dY.read(np.uint16, (M, N // 2)))
+            else:
+                run(ctx, lambda r: r.matmul(dX, W, dY, M))
+                outs.append(dY.read(np.uint16, (M, N)))
+    finally:
+        ctx.profile(False)
+    labels = [name for name in ctx.profile_table() if name.startswith("matmul")]
+    assert labels and all(f"_{tile}[" in name for name in labels), labels  # the forced tile is the one that ran
+    assert np.array_equal(outs[0], outs[1])
+    ab = ref.matmul(X, W16, np.float64)
+    if glu:
+        want = ref.silu_mul(ab[:, :N // 2], ab[:, N // 2:], np.float64)
+        got = outs[0].view(np.float16)
+        assert np.abs(got.astype(np.float64) - want.astype(np.float64)).max() < 2e-2
+    else:
+        assert f16_close(outs[0].view(np.float16), ab, ulps=1.0, atol=2e-5) <= 1.0
+
+
+@pytest.mark.parametrize("M,N,K,want", [(1152, 1024, 2048, "80x64k2p8"), (1152, 1024, 3072, "80x64k2p8"),
+                                         (1536, 2048, 2048, "96x64k2"), (2304, 1024, 2048, "96x64k2"),
+                                         (1536, 1024, 2048, "96x64k2p8"), (1152, 1024, 2624, "32x64"),
+                                         (1152, 2048, 1024, "32x64p4")])
+def test_matmul_policy_k_wave_sets(pkg, ctx, M, N, K, want):
+    """The tile policy's K wave set rule (256 CUs, K >= 2048): one round of the 8-stage tiles where that fills
+    0.75-1 per CU (the ticket's o_proj / w2), else the 4-stage tile whose grid is nearest 1.5 per CU; an odd
+    64-K step count (Laya's 2624) keeps the unpaired 32x64, and K = 1024 the paired 32x64p4."""
+    dj = _dj()
+    cus = ctx.info()["compute_units"]
+    if cus != 256:
+        pytest.skip(f"the rule's tile counts assume 256 CUs (this device: {cus})")
+    rng = np.random.default_rng(M + N + K)
+    codes, scales = quant(rng, N, K, 8)
+    W = ctx.weight_q(codes, scales, N, K, 8, dj.W_MFMA)
+    X = rand_f16(rng, (M, K))
+    dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+    ctx.profile_reset()
+    ctx.profile(True)
+    try:
+        run(ctx, lambda r: r.matmul(dX, W, dY, M))
+    finally:
+        ctx.profile(False)
+    labels = [name for name in ctx.profile_table() if name.startswith("matmul")]
+    assert labels == [f"matmul_q8_{want}[{M}x{N}x{K}]"], labels
+    want_y = ref.matmul(X, ref.dequant_f16(codes, scales, 8), np.float64)
+    assert f16_close(dY.read(np.float16, (M, N)), want_y, ulps=1.0, atol=2e-5) <= 1.0
+
+
 @pytest.mark.parametrize("waves", [1, 5, 8, 9, 16])
 @pytest.mark.parametrize("M,N,K,bits,glu", [(1, 2048, 832, 8, False), (32, 1536, 4608, 8, False),
                                             (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True),
@@ -422,10 +496,12 @@ def test_qk_norm_rope(pkg, ctx, heads, kv, D, qk, vnorm, mode, rot):
     (40, 16, 8, 128, True, False, 128, 8),     # skinny M: the product and the standalone kernel
     (300, 8, 4, 64, True, False, 64, 8),       # D 64: no 128-wide head tile, two kernels
 ])
-def test_matmul_qkv_rope_matches_two_ops(pkg, ctx, M, heads, kv, D, qk, vnorm, rot, bits):
+def test_matmul_qkv_rope_matches_two_ops(pkg, ctx, monkeypatch, M, heads, kv, D, qk, vnorm, rot, bits):
     """dj_matmul_qkv_rope (the forward's RoPE table, norm + rotation in the product's epilogue where it fits)
-    gives the same bits as dj_matmul followed by dj_qk_norm_rope (which computes its own angles); and the
-    table itself is the angles' cos and sin."""
+    gives the same bits as dj_matmul followed by dj_qk_norm_rope (which computes its own angles), the plain
+    product on a tile that sums K in step order (64x64: the K wave set tiles add two partial sums, a different
+    rounding; the RoPE tile ignores the forced plain tile); and the table itself is the angles' cos and sin."""
+    monkeypatch.setenv("DJ_GEMM_TILE", "64x64")
     dj = _dj()
     rng = np.random.default_rng(M + heads + D + rot)
     K = 1024
