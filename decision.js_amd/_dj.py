@@ -73,6 +73,9 @@ SIGNATURES = {
     "dj_qk_norm_rope": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P, _I, _F, _F, _I, _I],
     "dj_rope_table": [_P, _I, _P, _I, _F, _I, _I, _P],
     "dj_matmul_qkv_rope": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P],
+    "dj_matmul_residual": [_P, _P, _P, _I, _P, _P, _P, _P],
+    "dj_matmul_normed": [_P, _P, _P, _P, _I, _I, _P, _I, _F],
+    "dj_matmul_qkv_rope_normed": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P, _P, _I, _F],
     "dj_attention": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_attention_noalloc": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_attention_gated": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P, _I, _P],
@@ -305,6 +308,19 @@ class Recorder:
                         mode=ROPE_POW_NEG):
         check(lib().dj_matmul_qkv_rope(self.h, ptr(X), w.h, ptr(Z), M, heads, kv, D, ptr(qn), ptr(kn), 1 if vnorm else 0,
                                        ptr(pos), pos_stride, eps, theta, D if rot is None else rot, mode, ptr(tab)))
+
+    def matmul_residual(self, X, w: Weight, M, R, nw, XW, SS):
+        check(lib().dj_matmul_residual(self.h, ptr(X), w.h, M, ptr(R), ptr(nw), ptr(XW), ptr(SS)))
+
+    def matmul_normed(self, XW, w: Weight, Y, M, act, SS, H, eps):
+        """act: -1 plain, else a gated activation (ACT_*)."""
+        check(lib().dj_matmul_normed(self.h, ptr(XW), w.h, ptr(Y), M, act, ptr(SS), H, eps))
+
+    def matmul_qkv_rope_normed(self, XW, w: Weight, Z, M, heads, kv, D, qn, kn, vnorm, pos, pos_stride, eps, theta, tab,
+                               SS, H, norm_eps, rot=None, mode=ROPE_POW_NEG):
+        check(lib().dj_matmul_qkv_rope_normed(self.h, ptr(XW), w.h, ptr(Z), M, heads, kv, D, ptr(qn), ptr(kn),
+                                              1 if vnorm else 0, ptr(pos), pos_stride, eps, theta,
+                                              D if rot is None else rot, mode, ptr(tab), ptr(SS), H, norm_eps))
 
     def attention(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))

@@ -129,7 +129,23 @@ struct GemmArgs {
   const float2 *rtab;
   int heads, kv, vnorm, rot;
   float eps;
+  // residual epilogue (plain products, dj_matmul_residual): R += f16(acc) in place, XW = f16(R * nw * XW_SCALE),
+  // SS[m, n / 32] = the unrounded sums squared over each 32-column block. Y is not written.
+  uint16_t *resid;
+  const uint16_t *nw;
+  uint16_t *xw;
+  float *ssout;
+  // row norm (dj_matmul_normed): every accumulator row times 1 / (XW_SCALE sqrt(sum_b ssin[m, b] / Hn + neps))
+  // over Hn / 32 <= 32 blocks before any other epilogue step
+  const float *ssin;
+  int Hn;
+  float neps;
 };
+
+// The pre-scale of a residual epilogue's XW (and its inverse in the row norm): XW = R * w / 4 keeps |XW| < 65504
+// for norm weights up to 4 at any f16 residual value.
+constexpr float XW_SCALE = 0.25f;
+
 
 // Ring of LDS stages, each holding one 64-K step of the tile: A (BM rows x 128 bytes, XOR-swizzled 16-byte
 // chunks), the NB weight blocks of B in their global lane order, and (quantized B) each block's 16 scale words.
@@ -165,7 +181,6 @@ struct GemmShape {
   static_assert(NS >= 2 && (NS - 2) * I < 64, "vmcnt range");
   static_assert(!PAIRED || (NS % 2 == 0 && NS >= 4 && (NS / 2 - 2) * 2 * I < 64), "paired ring");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
-  static_assert(WK == 1 || (WK == 2 && PAIRED), "K wave sets take a paired ring's steps");
   // LDS: the ring, or the K wave sets' partial tiles where those are larger (they reuse the ring's bytes)
   static constexpr int RED = (WK - 1) * BM * BN * 4, SMEM = NS * STAGE > RED ? NS * STAGE : RED;
   static_assert(SMEM <= 160 * 1024, "LDS for the partial tiles");
@@ -194,18 +209,32 @@ __device__ __forceinline__ void wait_steps_barrier(int n) {
   }
 }
 
-// EPI: 0 plain store, 1 gated MLP, 2 QK_NORM_ROPE on a qkv weight (kernels.ts:86-112) before the store
+// EPI: 0 plain store, 1 gated MLP, 2 QK_NORM_ROPE on a qkv weight (kernels.ts:86-112) before the store, 3 plain
+// product into the residual epilogue (dj_matmul_residual); 4 + (0, 1 or 2): that epilogue after the row norm of
+// dj_matmul_normed (every accumulator row times 1 / (XW_SCALE rms) from the producer's partial sums)
 template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI, int WK>
 __global__ __launch_bounds__(WM *WN *WK * 64)
 __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>::WPE))) void k_gemm(GemmArgs g) {
   using S = GemmShape<BITS, WM, WN, FM, FN, RING, WK>;
-  constexpr bool GLU = EPI == 1;
+  static_assert(WK == 1 || (WK == 2 && S::PAIRED), "K wave sets take a paired ring's steps");
+  constexpr int BASE = EPI & 3;
+  constexpr bool GLU = BASE == 1, ROPE = BASE == 2, RES = EPI == 3, RN = (EPI & 4) != 0;
+  static_assert(!RN || WK == 1, "the row norm's scales are shared through a workgroup barrier: every wave live");
+  static_assert(!RES || FN % 2 == 0, "the residual epilogue sums 32-column blocks (fragment pairs)");
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::SMEM];
+  // the row norm's partial sums sit past the ring (and past the K wave sets' partial tiles, which reuse it)
+  constexpr int RN_OFF = S::SMEM, RN_BYTES = RN ? (BM * 132 + 1023) / 1024 * 1024 : 0;  // sums, then BM scales
+  static_assert(S::SMEM + RN_BYTES <= 160 * 1024, "LDS for the row norm's sums");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[S::SMEM + RN_BYTES];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int wk = wave / (WM * WN), wm = (wave % (WM * WN)) / WN, wn = wave % WN;
+  // Two K wave sets share the epilogue by fragment rows: set 0 takes i < FH, set 1 the rest (a RoPE tile needs
+  // whole heads: set 0 alone).
+  constexpr bool KSPLIT = WK > 1 && !ROPE;
+  constexpr int FH = (FM + 1) / 2;
+  auto mine = [&](int i) { return !KSPLIT || ((i < FH) == (wk == 0)); };
   int tm, tn;
   map_tile(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * (WN * FN * 16);
@@ -218,6 +247,25 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
+
+  // The accumulator layout: lane l holds output row l % 16 of each 16x16 fragment and its columns 4 (l / 16)..+3.
+  const int mrow = m0 + wm * FM * 16 + (lane & 15), c4 = 4 * (lane >> 4);
+  const int N = g.N;
+  // Epilogue inputs loaded before the ring starts, so that they land during the K loop (their DMAs / loads are
+  // older than the ring's, so the ring's exact counter waits only get stricter). Row norm: the tile's rows of
+  // partial sums (nb = Hn / 32 <= 32 floats a row, contiguous in memory) by LDS DMA into RN_OFF; the epilogue
+  // reads them there. Residual: the tile's stream values and norm weights, into registers.
+  h4 rx[RES ? FM : 1][RES ? FN : 1], rw[RES ? FN : 1];
+  if (RES && (KSPLIT || wk == 0)) {  // each wave set its own epilogue rows
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int n = n0 + wn * FN * 16 + j * 16 + c4;
+      rw[j] = *(const h4 *)(g.nw + n);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        if (mine(i)) rx[i][j] = *(const h4 *)(g.resid + (size_t)min(mrow + i * 16, M - 1) * N + n);
+    }
+  }
 
   // Per-lane DMA sources at step 0 of the split (a step adds 128 bytes to A, one block to B and scales).
   // A row q (1 KB = 8 rows of the tile): lane L fills LDS chunk L of it = row 8q + L/8, physical chunk L%8,
@@ -297,6 +345,16 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
   // have been issued (min(NS - 2, KS - 1) for t = 0), so min(NS - 3, KS - 1 - t) later steps may still be in
   // flight — the full ring depth until the tail, then exact counts (no re-loads of the last step to wait for).
+  if constexpr (RN) {  // the tile's partial sums: 1 KB DMAs, as many as BM rows of nb floats need, over the waves
+    const int nb = g.Hn >> 5;
+    const long last = (long)M * nb * 4 - 16;  // a tile's rows past M read the buffer's last 16 bytes
+    const char *src0 = (const char *)g.ssin + (size_t)m0 * nb * 4;
+    const int chunks = (BM * nb * 4 + 1023) / 1024;
+    for (int q = wv; q < chunks; q += NW) {  // wave-uniform (the LDS address goes to M0)
+      const long off = min((long)m0 * nb * 4 + (long)q * 1024 + lane * 16, last) - (long)m0 * nb * 4;
+      dma16(src0 + off, lds0 + RN_OFF + q * 1024);
+    }
+  }
   // prologue: steps 0 .. NS-2 in flight (paired ring: pairs 0 .. NS/2-2, steps 0 .. NS-3)
 #pragma unroll
   for (int p = 0; p < (S::PAIRED ? NS - 2 : NS - 1); ++p)
@@ -376,32 +434,80 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   wait_vm<0>();  // the clamped tail DMAs land before the wave moves on
 
   if constexpr (WK > 1) {
-    // K wave sets 1 .. WK-1 leave their partial tiles in the (now idle) ring; set 0 adds them in set order
-    // (deterministic) and runs the epilogue alone
+    // The K wave sets' partial tiles meet in the (now idle) ring. Split epilogue: each set leaves the fragments
+    // the other one stores and adds the other's to its own (a + b == b + a: the same bits as one set adding
+    // both). Otherwise sets 1 .. WK-1 leave theirs and set 0 adds them in set order and runs the epilogue alone.
     f4 *part = (f4 *)smem;
     constexpr int FR = FM * FN;  // fragments per wave
     __syncthreads();  // every DMA has landed and every wave is past its last fragment read
-    if (wk > 0) {
+    if constexpr (KSPLIT) {
+      static_assert(WK == 2, "the split epilogue pairs two wave sets");
 #pragma unroll
       for (int i = 0; i < FM; ++i)
+        if (!mine(i))
 #pragma unroll
-        for (int j = 0; j < FN; ++j) part[(((wk - 1) * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane] = acc[i][j];
+          for (int j = 0; j < FN; ++j) part[((wm * WN + wn) * FR + i * FN + j) * 64 + lane] = acc[i][j];
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        if (mine(i))
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] += part[((wm * WN + wn) * FR + i * FN + j) * 64 + lane];
+    } else {
+      if (wk > 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            part[(((wk - 1) * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane] = acc[i][j];
+      }
+      __syncthreads();
+      if (wk > 0) return;
+#pragma unroll
+      for (int k = 0; k < WK - 1; ++k)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] += part[((k * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane];
     }
-    __syncthreads();
-    if (wk > 0) return;
-#pragma unroll
-    for (int k = 0; k < WK - 1; ++k)
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] += part[((k * WM * WN + wm * WN + wn) * FR + i * FN + j) * 64 + lane];
   }
 
   // The MFMAs take the weight fragment as their first operand, so each accumulator holds a 16x16 block of
   // Y^T: lane l has output row l%16 of the block and its 4 consecutive columns 4(l/16)..+3 — one 8-byte f16
   // (16-byte f32) store instead of four scattered 2-byte ones.
-  const int mrow = m0 + wm * FM * 16 + (lane & 15), c4 = 4 * (lane >> 4);
-  const int N = g.N;
+  if constexpr (RN) {  // row norm: the consumer side of a residual epilogue
+    // Each row's scale once per workgroup, one lane a row, into LDS past the sums. With 32 sums a row (rows 128
+    // bytes apart: every row starts on bank 0) lane r reads its 16-byte chunks in the order k ^ (r % 8), so the
+    // 8 rows of one LDS cycle hit 8 different bank groups; a row's sum is then four interleaved partials.
+    const int nb = g.Hn >> 5;
+    const float *sums = (const float *)(smem + RN_OFF);
+    float *scale = (float *)(smem + RN_OFF + BM * 128);
+    const float inv_h = 1.0f / (float)g.Hn;
+    for (int r = wave * 64 + lane; r < BM; r += NW * 64) {
+      float v;
+      if (nb == 32) {
+        f4 p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const f4 x = *(const f4 *)(sums + r * 32 + (k ^ (r & 7)) * 4);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) p[c] += x[c];
+        }
+        v = (p[0] + p[1]) + (p[2] + p[3]);
+      } else {
+        v = 0.f;
+        for (int b = 0; b < nb; ++b) v += sums[r * nb + b];
+      }
+      scale[r] = rsqrtf(v * inv_h + g.neps) * (1.0f / XW_SCALE);
+    }
+    __syncthreads();  // (every wave's sum DMAs landed before its first ring wait and that wait's barrier)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const float rs = scale[wm * FM * 16 + i * 16 + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] *= rs;
+    }
+  }
   if (g.splits > 1) {
     // this split's partial tile, f32, into its slice; k_splitk_sum finishes the product
     float *slice = g.ws + (size_t)blockIdx.y * M * N;
@@ -410,12 +516,12 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int m = mrow + i * 16, n = n0 + wn * FN * 16 + j * 16 + c4;
-        if (m < M) *(f4 *)(slice + (size_t)m * N + n) = acc[i][j];
+        if (mine(i) && m < M) *(f4 *)(slice + (size_t)m * N + n) = acc[i][j];
       }
     return;
   }
 
-  if constexpr (EPI == 2) {
+  if constexpr (ROPE) {
     // The tile is one head of a qkv product (BN = D = 128, tile column n0 = head * 128). q and k heads (and v
     // heads with vnorm): the f16-rounded tile goes to LDS (the ring is free: every DMA has landed), then
     // LPH lanes per row run QK_NORM_ROPE's arithmetic (norm_rope_lane, shared with k_qk_norm_rope, cos/sin from
@@ -496,6 +602,42 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
     }
   }
 
+  if constexpr (RES) {
+    {
+      // residual epilogue: per 32-column block (fragments j, j + 1) the lane's 8 values, then the row's four
+      // lanes added, written by the first of them
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (!mine(i)) continue;
+        const int m = mrow + i * 16;
+#pragma unroll
+        for (int j = 0; j < FN; j += 2) {
+          float part = 0.f;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int n = n0 + wn * FN * 16 + (j + h) * 16 + c4;
+            const h4 x = rx[i][j + h], w = rw[j + h];
+            h4 xo, xwo;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float v = (float)x[r] + (float)(_Float16)acc[i][j + h][r];
+              part += v * v;
+              xo[r] = (_Float16)v;
+              xwo[r] = (_Float16)((float)xo[r] * (float)w[r] * XW_SCALE);
+            }
+            if (m < M) {
+              *(h4 *)(g.resid + (size_t)m * N + n) = xo;
+              *(h4 *)(g.xw + (size_t)m * N + n) = xwo;
+            }
+          }
+          part += __shfl_xor(part, 16);
+          part += __shfl_xor(part, 32);
+          if (m < M && lane < 16) g.ssout[(size_t)m * (N >> 5) + ((n0 + wn * FN * 16 + j * 16) >> 5)] = part;
+        }
+      }
+      return;
+    }
+  }
   if constexpr (!GLU) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -505,7 +647,7 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
         h4 v;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = (_Float16)acc[i][j][r];
-        if (m < M) *(h4 *)(g.Y + (size_t)m * N + n) = v;
+        if (mine(i) && m < M) *(h4 *)(g.Y + (size_t)m * N + n) = v;
       }
   } else {
     const int I = N >> 1;
@@ -515,6 +657,7 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
 #pragma unroll
       for (int j = 0; j < FN; j += 2) {
         const int m = mrow + i * 16;
+        if (!mine(i)) continue;
         const int col = ((wb0 + j) >> 1) * 16 + c4;  // physical block p even -> w1 block p / 2
         h4 v;
 #pragma unroll
@@ -533,16 +676,37 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
 // the tiled epilogue does.
 template <bool GLU>
 __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws, int splits, int M, int N, int act,
-                                                    uint16_t *__restrict__ Y) {
+                                                    uint16_t *__restrict__ Y, uint16_t *__restrict__ R,
+                                                    const uint16_t *__restrict__ nw, uint16_t *__restrict__ XW,
+                                                    float *__restrict__ SS) {
   const int NO = GLU ? N / 2 : N;  // output columns
   const long e = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (e >= (long)M * NO) return;
+  if (e >= (long)M * NO) return;  // whole 8-thread groups (M N is a multiple of 32 where R is given)
   const int m = (int)(e / NO), c = (int)(e % NO);
   const size_t slice = (size_t)M * N;
   if constexpr (!GLU) {
     const float *p = ws + (size_t)m * N + c;
     f4 s = *(const f4 *)p;
     for (int k = 1; k < splits; ++k) s += *(const f4 *)(p + k * slice);
+    if (R) {  // the residual epilogue of the tiled kernel; 8 consecutive threads hold one 32-column block
+      const h4 x = *(const h4 *)(R + e), w = *(const h4 *)(nw + c);
+      h4 xo, xwo;
+      float part = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = (float)x[r] + (float)(_Float16)s[r];
+        part += v * v;
+        xo[r] = (_Float16)v;
+        xwo[r] = (_Float16)((float)xo[r] * (float)w[r] * XW_SCALE);
+      }
+      *(h4 *)(R + e) = xo;
+      *(h4 *)(XW + e) = xwo;
+      part += __shfl_xor(part, 1);
+      part += __shfl_xor(part, 2);
+      part += __shfl_xor(part, 4);
+      if ((c & 31) == 0) SS[(size_t)m * (N >> 5) + (c >> 5)] = part;
+      return;
+    }
     h4 v;
 #pragma unroll
     for (int r = 0; r < 4; ++r) v[r] = (_Float16)s[r];
@@ -767,11 +931,45 @@ struct GemmCfg {
 static const GemmCfg kCfgs[] = {DJ_GEMM_CFGS(DJ_CFG_ROW)};
 static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
-template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI, int WK>
+// Whether a tile's LDS holds the row norm's sums past its ring (EPI 4-6) for these weight bits.
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int WK>
+constexpr bool rn_fits_cfg() {
+  return GemmShape<BITS, WM, WN, FM, FN, RING, WK>::SMEM + (WM * FM * 16 * 132 + 1023) / 1024 * 1024 <= 160 * 1024;
+}
+template <int BITS>
+static bool rn_fits(int i) {
+  switch (i) {
+#define DJ_RN_CASE(i, tag, wm, wn, fm, fn, ring, wk) \
+  case i: return rn_fits_cfg<BITS, wm, wn, fm, fn, ring, wk>();
+    DJ_GEMM_CFGS(DJ_RN_CASE)
+#undef DJ_RN_CASE
+  }
+  return false;
+}
+
+// The tiles built with the folded-norm epilogues (EPI 3-6): every tile the policy picks for a product of more
+// than 64 rows on the decoders' shapes, including the small-grid fallbacks; the rest are sweep-only tiles, not
+// built in those forms (cfg_fits keeps the policy off them there).
+constexpr bool fused_cfg(int i) {
+  switch (i) {
+    case 1: case 4: case 5: case 8: case 15: case 16: case 19: case 21: case 24: case 25: case 41: case 44: case 46:
+    case 47: case 50: case 51: case 52: case 53: case 54: case 55: case 56: case 57:
+      return true;
+    default:
+      return false;
+  }
+}
+
+template <int BITS, int WM, int WN, int FM, int FN, int RING, int EPI, int WK, bool FZ>
 static void launch_cfg(hipStream_t s, GemmArgs a) {
-  if constexpr ((EPI == 1 && FN % 2 != 0) || (EPI == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144 || WK > 1))) {
-    return;  // never picked: a gated tile needs gate/up fragment pairs, a RoPE tile is one 128-wide head of at
-             // most 144 rows (its epilogue holds every row pass in registers) on one set of waves
+  constexpr int BASE = EPI & 3;
+  if constexpr (((BASE == 1 || EPI == 3) && FN % 2 != 0) ||
+                (BASE == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144 || WK > 1)) ||
+                (WK > 1 && !GemmShape<BITS, WM, WN, FM, FN, RING, WK>::PAIRED) || (EPI >= 3 && !FZ) ||
+                ((EPI & 4) && (WK > 1 || !rn_fits_cfg<BITS, WM, WN, FM, FN, RING, WK>()))) {
+    return;  // never picked (cfg_fits): a gated tile and the residual epilogue need fragment pairs, a RoPE tile
+             // is one 128-wide head of at most 144 rows (its epilogue holds every row pass in registers) on one
+             // set of waves, K wave sets need their paired ring, the folded-norm forms exist for fused_cfg tiles
   } else {
     dim3 grid(a.tiles_m * a.tiles_n, a.splits);
     k_gemm<BITS, WM, WN, FM, FN, RING, EPI, WK><<<grid, WM * WN * WK * 64, 0, s>>>(a);
@@ -781,14 +979,30 @@ static void launch_cfg(hipStream_t s, GemmArgs a) {
 template <int BITS, int EPI>
 static void launch_index(int i, hipStream_t s, GemmArgs a) {
 #define DJ_CFG_CASE(i, tag, wm, wn, fm, fn, ring, wk) \
-  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, EPI, wk>(s, a); break;
+  case i: launch_cfg<BITS, wm, wn, fm, fn, ring, EPI, wk, fused_cfg(i)>(s, a); break;
   switch (i) { DJ_GEMM_CFGS(DJ_CFG_CASE) }
 #undef DJ_CFG_CASE
 }
 
-// epi: 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (the tile is one 128-wide head, <= 144 rows)
-static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
-  return N % c.bn() == 0 && (epi != 1 || c.fn % 2 == 0) && (epi != 2 || (c.bn() == 128 && c.bm() <= 144 && c.wk == 1)) &&
+// A K wave set tile needs its paired ring: at least 4 stages of its shape in LDS for these weight bits (a
+// 128x256 tile of direct f16 weights holds only 3).
+static bool ksets_fit(const GemmCfg &c, int bits) {
+  if (c.wk == 1) return true;
+  const int nw = c.wm * c.wn * c.wk, cb = bits == 8 ? 1024 : bits == 4 ? 512 : 2048;
+  const int stage = c.bm() * 128 + (c.bn() / 16 * cb + 1023) / 1024 * 1024 + (bits == 16 ? 0 : nw * 256);
+  return std::min(-c.ring, (160 * 1024 / stage) & ~1) >= 4;
+}
+
+// epi (the kernel's EPI): 0 plain, 1 gated (gate/up fragment pairs), 2 RoPE (one 128-wide head per tile, <= 144
+// rows), 3 plain with the residual epilogue (32-column blocks: fragment pairs); + 4: the row norm first. The
+// folded-norm forms (3-6) exist for fused_cfg tiles only.
+static bool cfg_fits(const GemmCfg &c, int N, int K, int epi, int bits) {
+  const int base = epi & 3;
+  return ksets_fit(c, bits) && N % c.bn() == 0 && ((base != 1 && epi != 3) || c.fn % 2 == 0) &&
+         (base != 2 || (c.bn() == 128 && c.bm() <= 144 && c.wk == 1)) && (epi < 3 || fused_cfg((int)(&c - kCfgs))) &&
+         (!(epi & 4) || (c.wk == 1 && (bits == 8    ? rn_fits<8>((int)(&c - kCfgs))
+                                       : bits == 4 ? rn_fits<4>((int)(&c - kCfgs))
+                                                   : rn_fits<16>((int)(&c - kCfgs))))) &&
          (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time (the 2-stage
                                                // fallback of a paired tile takes any count; the check keeps
                                                // the rule simple)
@@ -823,7 +1037,7 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi) {
 //   32x64p4     when it gives >= 2 tiles per CU (the paired 4-stage ring, K / 64 even), else 32x64,
 //   32x128s2    the same for gated weights (a GLU tile needs gate/up fragment pairs),
 //   else the tile with the most workgroups, split along K when even that leaves most CUs idle (skinny M).
-static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &cfg, int &splits) {
+static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floats, int &cfg, int &splits) {
   const bool ws_ok = ws_floats > 0;
   const char *force = getenv("DJ_GEMM_TILE");
   const char *fs = getenv("DJ_GEMM_SPLITK");
@@ -831,12 +1045,12 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
   splits = 1;
   if (force)
     for (int i = 0; i < kNumCfgs; ++i)
-      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) cfg = i;
+      if (!strcmp(force, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, epi, bits)) cfg = i;
   auto tiles = [&](int i) { return (long)dj_cdiv(M, kCfgs[i].bm()) * (N / kCfgs[i].bn()); };
   // the qkv product with the RoPE epilogue: 144x128 on a paired 4-stage ring where its tiles fill one round (one
   // workgroup per CU, so the deeper ring costs no occupancy; the 1152-row qkv, 256 tiles: 2.628 -> 2.616 ms
   // per ticket, same box)
-  if (cfg < 0 && glu == 2 && cfg_fits(kCfgs[50], N, K, glu) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
+  if (cfg < 0 && (epi & 3) == 2 && cfg_fits(kCfgs[50], N, K, epi, bits) && tiles(50) >= 0.75 * cus && tiles(50) <= cus) cfg = 50;
   // long K on at most one round of tiles (0.25-1 per CU): 128x128n split 4 ways along K (alone on cold weights,
   // the summing kernel included: the 3B w2, 1536 x 2048 x 11008 q4, 92.9 us against 107.0 on the paired ring;
   // the 0.8B prefill's w2, 1024 x 1536 x 4608 q8, 32.8 against 36.6); below that, 64x128n split 4 ways at
@@ -856,33 +1070,33 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
         {8, 2.0, 0, 1e9, 0}, {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules) {
       if (r.cfg == -2) {  // the K wave set family (see above)
-        if (glu || ksets_off || K < 2048) continue;
+        if ((epi & 3) == 1 || (epi & 3) == 2 || ksets_off || K < 2048) continue;
         int best = -1;
         for (int i : {56, 57})  // one round of one-workgroup-per-CU tiles on the 8-stage ring, most tiles first
-          if (best < 0 && cfg_fits(kCfgs[i], N, K, glu) && tiles(i) >= 0.75 * cus && tiles(i) <= cus) best = i;
+          if (best < 0 && cfg_fits(kCfgs[i], N, K, epi, bits) && tiles(i) >= 0.75 * cus && tiles(i) <= cus) best = i;
         if (best < 0) {  // else the 4-stage tile nearest 1.5 per CU, within the rule's bounds
           for (int i : {51, 52, 53, 54})
-            if (cfg_fits(kCfgs[i], N, K, glu) &&
+            if (cfg_fits(kCfgs[i], N, K, epi, bits) &&
                 (best < 0 || std::abs(tiles(i) - 1.5 * cus) < std::abs(tiles(best) - 1.5 * cus)))
               best = i;
           if (best >= 0 && (tiles(best) < r.per_cu * cus || tiles(best) > r.max_per_cu * cus)) best = -1;
         }
         if (kst)  // DJ_GEMM_KSET_TILE=<tag>: this rule's tile (A/B sweeps inside a forward)
           for (int i = 0; i < kNumCfgs; ++i)
-            if (!strcmp(kst, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, glu)) best = i;
+            if (!strcmp(kst, kCfgs[i].tag) && cfg_fits(kCfgs[i], N, K, epi, bits)) best = i;
         if (best >= 0) {
           cfg = best;
           break;
         }
         continue;
       }
-      if (cfg_fits(kCfgs[r.cfg], N, K, glu) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
+      if (cfg_fits(kCfgs[r.cfg], N, K, epi, bits) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
           tiles(r.cfg) <= r.max_per_cu * cus) {
         if (r.ks < 0) {  // a long-K rule: the split where it divides K and fits the workspace; else what the rules
                          // chose before it (the paired ring at 0.5-1 per CU, otherwise the rules below)
-          if (longk > 1 && ws_ok && glu != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats) {
+          if (longk > 1 && ws_ok && (epi & 3) != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats) {
             rule_splits = longk;
-          } else if (r.cfg == 19 && tiles(19) >= 0.5 * cus && cfg_fits(kCfgs[46], N, K, glu)) {
+          } else if (r.cfg == 19 && tiles(19) >= 0.5 * cus && cfg_fits(kCfgs[46], N, K, epi, bits)) {
             cfg = 46;
             break;
           } else {
@@ -901,7 +1115,7 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
       long best = -1;
       for (int pass = 0; pass < 2 && cfg < 0; ++pass)
         for (int i : small)
-          if (cfg_fits(kCfgs[i], N, K, glu) && (pass || kCfgs[i].bm() <= need) && tiles(i) > best) {
+          if (cfg_fits(kCfgs[i], N, K, epi, bits) && (pass || kCfgs[i].bm() <= need) && tiles(i) > best) {
             cfg = i;
             best = tiles(i);
           }
@@ -917,7 +1131,7 @@ static void pick(int M, int N, int K, int glu, int cus, size_t ws_floats, int &c
     const long t = tiles(cfg);
     while (t * splits * 4 < cus && KT % (splits * 2) == 0 && KT / (splits * 2) >= 4) splits *= 2;
   }
-  if (splits < 1 || KT % splits || !ws_ok || glu == 2 || kCfgs[cfg].ring < 0) splits = 1;
+  if (splits < 1 || KT % splits || !ws_ok || (epi & 3) == 2 || kCfgs[cfg].ring < 0) splits = 1;
 }
 
 // Profile labels "matmul[_glu|_rope]_<q4|q8|f16>_<tile>", built when the library loads.
@@ -939,9 +1153,10 @@ static const char *const kGemvNames[3][2] = {{"matmul_q4_gemv", "matmul_glu_q4_g
 // launcher state: the split-K workspace lives in the context
 int dj_gemm_workspace(dj_ctx *c, size_t need_floats, float **ws);
 
+// fx: the residual epilogue or the row norm (GemmArgs' fields of those; tiled kernel only)
 template <int BITS, bool GLU>
 static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int act, const char **name,
-                       int *splits_out) {
+                       int *splits_out, const GemmArgs *fx = nullptr, bool split_ok = true) {
   const int N = w->N, K = w->K;
   const char *force = getenv("DJ_GEMM_TILE");
   // skinny M: the GEMV-style kernel on weights up to 4096 outputs wide, and on any weight for M <= 16 (M = 1
@@ -949,7 +1164,7 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   // enough workgroups (M = 32 GLU 9216 x 1536: 9.8-10.3 against 13.3 us), measured on MI355X. (Long K stays
   // here: M = 32, 1536 x 4608 took 10.0 + 4.6 us tiled with split-K and its sum inside the 0.8B decoder's
   // forward, against about 12 for this kernel.)
-  const bool skinny = M <= 64 && N % (GLU ? 32 : 16) == 0 &&
+  const bool skinny = !fx && M <= 64 && N % (GLU ? 32 : 16) == 0 &&
                       (force ? !strcmp(force, "gemv") : M <= 16 || N <= 4096);
   if (skinny) {
     GemmArgs a{};
@@ -963,9 +1178,13 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   }
   float *ws = nullptr;
   int cfg, splits;
-  pick(M, N, K, GLU, c->cus, c->gemm_ws ? c->gemm_ws_floats : 0, cfg, splits);
+  const bool res = fx && fx->resid;
+  const int epi = (GLU ? 1 : res ? 3 : 0) | (fx && fx->ssin ? 4 : 0);
+  pick(M, N, K, epi, BITS, c->cus, c->gemm_ws && split_ok ? c->gemm_ws_floats : 0, cfg, splits);
   if (splits > 1 && dj_gemm_workspace(c, (size_t)splits * M * N, &ws) != DJ_OK) splits = 1;
-  if (cfg < 0) return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N, GLU ? " (gated: N % 32 == 0)" : "");
+  if (cfg < 0)
+    return dj_fail(DJ_EINVAL, "decision.js: no matmul tile fits N = %d%s", N,
+                   GLU ? " (gated: N % 32 == 0)" : res ? " (residual: N % 32 == 0)" : "");
   const char *label = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][GLU][cfg];
   GemmArgs a{};
   a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Y; a.ws = ws;
@@ -974,10 +1193,21 @@ static int launch_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_
   a.tiles_n = N / kCfgs[cfg].bn();
   a.splits = splits;
   a.ksteps = (K / 64) / splits;
-  launch_index<BITS, GLU ? 1 : 0>(cfg, c->stream, a);
+  if (fx) {
+    a.resid = fx->resid; a.nw = fx->nw; a.xw = fx->xw; a.ssout = fx->ssout;
+    a.ssin = fx->ssin; a.Hn = fx->Hn; a.neps = fx->neps;
+  }
+  switch (epi) {
+    case 0: launch_index<BITS, 0>(cfg, c->stream, a); break;
+    case 1: launch_index<BITS, 1>(cfg, c->stream, a); break;
+    case 3: launch_index<BITS, 3>(cfg, c->stream, a); break;
+    case 4: launch_index<BITS, 4>(cfg, c->stream, a); break;
+    default: launch_index<BITS, 5>(cfg, c->stream, a); break;
+  }
   if (splits > 1) {
     const long n4 = (long)M * (GLU ? N / 2 : N) / 4;
-    k_splitk_sum<GLU><<<(unsigned)dj_cdiv(n4, 256), 256, 0, c->stream>>>(ws, splits, M, N, act, Y);
+    k_splitk_sum<GLU><<<(unsigned)dj_cdiv(n4, 256), 256, 0, c->stream>>>(ws, splits, M, N, act, Y, a.resid, a.nw, a.xw,
+                                                                           a.ssout);
   }
   *name = label;
   *splits_out = a.splits;
@@ -996,7 +1226,7 @@ static int launch_rope_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, ui
   const int N = w->N, K = w->K;
   if (M <= 64) return 1;
   int cfg, splits;
-  pick(M, N, K, 2, c->cus, 0, cfg, splits);
+  pick(M, N, K, a.ssin ? 6 : 2, BITS, c->cus, 0, cfg, splits);
   if (cfg < 0 || (long)dj_cdiv(M, kCfgs[cfg].bm()) * (N / 128) > 2L * c->cus) return 1;
   a.X = X; a.Wc = w->codes; a.Ws = (const uint32_t *)w->scales; a.Y = Z; a.ws = nullptr;
   a.M = M; a.N = N; a.K = K; a.act = 0;
@@ -1004,26 +1234,65 @@ static int launch_rope_bits(dj_ctx *c, const uint16_t *X, const dj_weight *w, ui
   a.tiles_n = N / 128;
   a.splits = 1;
   a.ksteps = K / 64;
-  launch_index<BITS, 2>(cfg, c->stream, a);
+  if (a.ssin) launch_index<BITS, 6>(cfg, c->stream, a);
+  else launch_index<BITS, 2>(cfg, c->stream, a);
   *name = kNames.v[BITS == 4 ? 0 : BITS == 8 ? 1 : 2][2][cfg];
   return 0;
 }
 
+static __global__ __launch_bounds__(256) void k_rownorm_apply(int M, int H, const uint16_t *__restrict__ XW,
+                                                              const float *__restrict__ SS, float eps,
+                                                              uint16_t *__restrict__ O);
+static int qkv_rope_impl(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Z, int M, int heads, int kv, int D,
+                         const uint16_t *qn, const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps,
+                         float theta, int rot, int mode, const float *tab, const float *SS, int H, float neps);
+static int launch_gemm_fx(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
+                          const char **name, int *splits, const GemmArgs *fx, bool split_ok = true);
+
 extern "C" int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Z, int M, int heads, int kv,
                                   int D, const uint16_t *qn, const uint16_t *kn, int vnorm, const int32_t *pos,
                                   int pos_stride, float eps, float theta, int rot, int mode, const float *tab) {
+  return qkv_rope_impl(rec, X, w, Z, M, heads, kv, D, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode, tab, nullptr,
+                       0, 0.f);
+}
+
+extern "C" int dj_matmul_qkv_rope_normed(dj_rec *rec, const uint16_t *XW, const dj_weight *w, uint16_t *Z, int M,
+                                         int heads, int kv, int D, const uint16_t *qn, const uint16_t *kn, int vnorm,
+                                         const int32_t *pos, int pos_stride, float eps, float theta, int rot, int mode,
+                                         const float *tab, const float *SS, int H, float norm_eps) {
+  DJ_REQUIRE(SS && H > 0 && H % 32 == 0 && H <= 2048 && w && w->K == H,
+             "decision.js: matmul_qkv_rope_normed: bad norm arguments (H %d must be the weight's K, a multiple of 32, "
+             "at most 2048)", H);
+  return qkv_rope_impl(rec, XW, w, Z, M, heads, kv, D, qn, kn, vnorm, pos, pos_stride, eps, theta, rot, mode, tab, SS, H,
+                       norm_eps);
+}
+
+static int qkv_rope_impl(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16_t *Z, int M, int heads, int kv, int D,
+                         const uint16_t *qn, const uint16_t *kn, int vnorm, const int32_t *pos, int pos_stride, float eps,
+                         float theta, int rot, int mode, const float *tab, const float *SS, int H, float neps) {
   DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA, "decision.js: matmul_qkv_rope needs an MFMA-tiled weight (DJ_W_MFMA)");
   DJ_REQUIRE(mode == DJ_ROPE_POW_NEG || mode == DJ_ROPE_INV_POW, "decision.js: matmul_qkv_rope: unknown rope mode");
   DJ_REQUIRE(X && Z && pos && tab && M >= 0 && heads > 0 && kv > 0 && D > 0 && D <= 512 &&
                  w->N == (heads + 2 * kv) * D && rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0,
              "decision.js: matmul_qkv_rope: bad arguments (N %d for %d + 2 x %d heads of %d, rot %d)", w->N, heads, kv,
              D, rot);
-  DJ_OP_BEGIN(rec, "matmul_qkv_rope");
+  DJ_OP_BEGIN(rec, SS ? "matmul_qkv_rope_normed" : "matmul_qkv_rope");
   const char *name = "matmul_qkv_rope";
   if (M > 0) {
     GemmArgs a{};
     a.qn = qn; a.kn = kn; a.rtab = (const float2 *)tab;
     a.heads = heads; a.kv = kv; a.vnorm = vnorm; a.rot = rot; a.eps = eps;
+    a.ssin = SS; a.Hn = H; a.neps = neps;
+    if (SS && (M <= 64 || H > 1024)) {  // skinny or wide rows: the normalized rows first (in the workspace), then
+                                        // the plain form
+      float *ws = nullptr;
+      DJ_REQUIRE(dj_gemm_workspace(rec->ctx, ((size_t)M * H + 1) / 2, &ws) == DJ_OK,
+                 "decision.js: matmul_qkv_rope_normed: %d x %d rows exceed the workspace", M, H);
+      k_rownorm_apply<<<(unsigned)dj_cdiv((long)M * (H / 32), 256), 256, 0, rec->ctx->stream>>>(M, H, X, SS, neps,
+                                                                                               (uint16_t *)ws);
+      X = (const uint16_t *)ws;
+      a.ssin = nullptr;
+    }
     const int bits = (w->layout & DJ_W_DIRECT) ? 16 : w->bits;
     int st = 1;
     if (D == 128)
@@ -1032,7 +1301,7 @@ extern "C" int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X, const dj_weigh
                        : launch_rope_bits<16>(rec->ctx, X, w, Z, M, a, &name);
     if (st == 1) {  // the product, then the standalone kernel (its angles computed as the table's were)
       int splits = 1;
-      st = dj_launch_gemm(rec->ctx, X, w, Z, M, -1, &name, &splits);
+      st = launch_gemm_fx(rec->ctx, X, w, Z, M, -1, &name, &splits, a.ssin ? &a : nullptr, !SS);
       if (st) return st;
       dj_launch_qk_norm_rope(rec->ctx->stream, M, heads, kv, D, w->N, Z, qn, kn, vnorm, pos, pos_stride, eps, theta, rot,
                              mode);
@@ -1043,13 +1312,19 @@ extern "C" int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X, const dj_weigh
   return dj_op_end(rec, name, shape);
 }
 
-int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act, const char **name,
-                   int *splits) {
+// split_ok = false: no split-K (the caller keeps its own data in the workspace)
+static int launch_gemm_fx(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act,
+                          const char **name, int *splits, const GemmArgs *fx, bool split_ok) {
   const bool glu = glu_act >= 0;
   const int bits = (w->layout & DJ_W_DIRECT) ? 16 : w->bits;
-  if (bits == 8) return glu ? launch_bits<8, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<8, false>(c, X, w, Y, M, 0, name, splits);
-  if (bits == 4) return glu ? launch_bits<4, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<4, false>(c, X, w, Y, M, 0, name, splits);
-  return glu ? launch_bits<16, true>(c, X, w, Y, M, glu_act, name, splits) : launch_bits<16, false>(c, X, w, Y, M, 0, name, splits);
+  if (bits == 8) return glu ? launch_bits<8, true>(c, X, w, Y, M, glu_act, name, splits, fx, split_ok) : launch_bits<8, false>(c, X, w, Y, M, 0, name, splits, fx, split_ok);
+  if (bits == 4) return glu ? launch_bits<4, true>(c, X, w, Y, M, glu_act, name, splits, fx, split_ok) : launch_bits<4, false>(c, X, w, Y, M, 0, name, splits, fx, split_ok);
+  return glu ? launch_bits<16, true>(c, X, w, Y, M, glu_act, name, splits, fx, split_ok) : launch_bits<16, false>(c, X, w, Y, M, 0, name, splits, fx, split_ok);
+}
+
+int dj_launch_gemm(dj_ctx *c, const uint16_t *X, const dj_weight *w, uint16_t *Y, int M, int glu_act, const char **name,
+                   int *splits) {
+  return launch_gemm_fx(c, X, w, Y, M, glu_act, name, splits, nullptr);
 }
 
 // K splits for a held skinny product (1: not worth holding): two, where the 64-K steps divide evenly into
@@ -1135,6 +1410,110 @@ static int matmul_now(dj_rec *rec, const uint16_t *X, const dj_weight *w, uint16
   int splits = 1;
   if (M > 0) {
     int st = dj_launch_gemm(rec->ctx, X, w, Y, M, -1, &name, &splits);
+    if (st) return st;
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
+  return dj_op_end(rec, name, shape);
+}
+
+// ---------------------------------------------------------------- residual + norm folded into the products
+// Skinny rows (the GEMV kernel has no such epilogues): the same outputs by a small kernel after a plain product
+// (dj_matmul_residual), or before it (dj_matmul_normed). One thread per (row, 32-column block).
+__global__ __launch_bounds__(256) void k_residual_parts(int M, int N, const uint16_t *__restrict__ Y,
+                                                        uint16_t *__restrict__ R, const uint16_t *__restrict__ nw,
+                                                        uint16_t *__restrict__ XW, float *__restrict__ SS) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  if (t >= (long)M * (N / 32)) return;
+  const int m = (int)(t / (N / 32)), c0 = (int)(t % (N / 32)) * 32;
+  const size_t base = (size_t)m * N + c0;
+  float part = 0.f;
+  for (int k = 0; k < 32; k += 8) {
+    const h8 x = *(const h8 *)(R + base + k), y = *(const h8 *)(Y + base + k), w = *(const h8 *)(nw + c0 + k);
+    h8 xo, xwo;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float v = (float)x[r] + (float)y[r];
+      part += v * v;
+      xo[r] = (_Float16)v;
+      xwo[r] = (_Float16)((float)xo[r] * (float)w[r] * XW_SCALE);
+    }
+    *(h8 *)(R + base + k) = xo;
+    *(h8 *)(XW + base + k) = xwo;
+  }
+  SS[(size_t)m * (N / 32) + c0 / 32] = part;
+}
+
+static __global__ __launch_bounds__(256) void k_rownorm_apply(int M, int H, const uint16_t *__restrict__ XW,
+                                                              const float *__restrict__ SS, float eps,
+                                                              uint16_t *__restrict__ O) {
+  const long t = (long)blockIdx.x * 256 + threadIdx.x;
+  const int nb = H / 32;
+  if (t >= (long)M * nb) return;
+  const int m = (int)(t / nb), c0 = (int)(t % nb) * 32;
+  float s = 0.f;
+  for (int b = 0; b < nb; ++b) s += SS[(size_t)m * nb + b];
+  const float rs = (1.0f / sqrtf(s / (float)H + eps)) * (1.0f / XW_SCALE);
+  for (int k = 0; k < 32; k += 8) {
+    const h8 x = *(const h8 *)(XW + (size_t)m * H + c0 + k);
+    h8 o;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) o[r] = (_Float16)((float)x[r] * rs);
+    *(h8 *)(O + (size_t)m * H + c0 + k) = o;
+  }
+}
+
+extern "C" int dj_matmul_residual(dj_rec *rec, const uint16_t *X, const dj_weight *w, int M, uint16_t *R,
+                                  const uint16_t *nw, uint16_t *XW, float *SS) {
+  DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == DJ_W_MFMA, "decision.js: matmul_residual needs an MFMA-tiled weight (DJ_W_MFMA)");
+  DJ_REQUIRE(X && R && nw && XW && SS && M >= 0 && w->N % 32 == 0,
+             "decision.js: matmul_residual: bad arguments (N %d must be a multiple of 32)", w->N);
+  DJ_OP_BEGIN(rec, "matmul_residual");
+  const char *name = "matmul_residual";
+  int splits = 1;
+  const int N = w->N;
+  if (M > 0 && M <= 64) {  // skinny rows: the plain product into the workspace, then the epilogue's arithmetic
+    float *ws = nullptr;
+    DJ_REQUIRE(dj_gemm_workspace(rec->ctx, ((size_t)M * N + 1) / 2, &ws) == DJ_OK,
+               "decision.js: matmul_residual: %d x %d rows exceed the workspace", M, N);
+    int st = launch_gemm_fx(rec->ctx, X, w, (uint16_t *)ws, M, -1, &name, &splits, nullptr, false);
+    if (st) return st;
+    k_residual_parts<<<(unsigned)dj_cdiv((long)M * (N / 32), 256), 256, 0, rec->ctx->stream>>>(M, N, (const uint16_t *)ws,
+                                                                                              R, nw, XW, SS);
+  } else if (M > 0) {
+    GemmArgs fx{};
+    fx.resid = R; fx.nw = nw; fx.xw = XW; fx.ssout = SS;
+    int st = launch_gemm_fx(rec->ctx, X, w, nullptr, M, -1, &name, &splits, &fx);
+    if (st) return st;
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
+  return dj_op_end(rec, name, shape);
+}
+
+extern "C" int dj_matmul_normed(dj_rec *rec, const uint16_t *XW, const dj_weight *w, uint16_t *Y, int M, int act,
+                                const float *SS, int H, float eps) {
+  const bool glu = act >= 0;
+  DJ_REQUIRE(w && (w->layout & ~DJ_W_DIRECT) == (glu ? DJ_W_MFMA_GLU : DJ_W_MFMA),
+             "decision.js: matmul_normed needs %s", glu ? "a fused w1|w3 weight (DJ_W_MFMA_GLU)" : "an MFMA-tiled weight (DJ_W_MFMA)");
+  DJ_REQUIRE(XW && Y && SS && M >= 0 && H > 0 && H % 32 == 0 && H <= 2048 && w->K == H &&
+                 (act < 0 || act == DJ_ACT_SILU || act == DJ_ACT_GELU_TANH || act == DJ_ACT_GELU_ERF),
+             "decision.js: matmul_normed: bad arguments (H %d must be the weight's K, a multiple of 32, at most 2048)", H);
+  DJ_OP_BEGIN(rec, glu ? "matmul_glu_normed" : "matmul_normed");
+  const char *name = "matmul_normed";
+  int splits = 1;
+  if (M > 0 && (M <= 64 || H > 1024)) {  // skinny or wide rows: the normalized rows first, then the product
+    float *ws = nullptr;
+    DJ_REQUIRE(dj_gemm_workspace(rec->ctx, ((size_t)M * H + 1) / 2, &ws) == DJ_OK,
+               "decision.js: matmul_normed: %d x %d rows exceed the workspace", M, H);
+    k_rownorm_apply<<<(unsigned)dj_cdiv((long)M * (H / 32), 256), 256, 0, rec->ctx->stream>>>(M, H, XW, SS, eps,
+                                                                                             (uint16_t *)ws);
+    int st = launch_gemm_fx(rec->ctx, (const uint16_t *)ws, w, Y, M, act, &name, &splits, nullptr, false);
+    if (st) return st;
+  } else if (M > 0) {
+    GemmArgs fx{};
+    fx.ssin = SS; fx.Hn = H; fx.neps = eps;
+    int st = launch_gemm_fx(rec->ctx, XW, w, Y, M, act, &name, &splits, &fx);
     if (st) return st;
   }
   char shape[48];

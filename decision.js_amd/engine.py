@@ -6,6 +6,7 @@ with `graphs` on (the default), a forward whose shapes were seen before replays 
 """
 import itertools
 import math
+import os
 
 import numpy as np
 
@@ -294,6 +295,18 @@ class DecoderEngine(GpuEngine):
         self.stride = (self.h + 2 * self.kv) * self.D
         self.capacity = 0
         self.leaf_capacity = 0
+        # the residual + RMSNorm between products folded into them (dj_matmul_residual / dj_matmul_normed) on
+        # forwards of FUSED_ROWS rows and hidden sizes up to 1024 (the products' own row norm; wider rows would
+        # take an extra normalizing kernel). opts fused_norms, else DJ_FUSED_NORMS=0/1, else FUSED_DEFAULT.
+        env = os.environ.get("DJ_FUSED_NORMS")
+        want = self.opts.get("fused_norms", self.FUSED_DEFAULT if env is None else env != "0")
+        self.fused_norms = bool(want) and self.H % 32 == 0 and self.H <= 1024
+
+    # Where the folded norms pay: at 65-8192 rows the products' epilogues cost less than the separate norm
+    # kernels they replace (a 3 x 384-id ticket: 2.49 against 2.56 ms); past that the extra epilogue traffic and
+    # the row norm's LDS region cost more than the norm kernels (86k rows: 116 against 104 ms).
+    FUSED_DEFAULT = True
+    FUSED_ROWS = (65, 8192)
 
     # -- buffers (d1-3b-engine.ts:33-42: grown, never shrunk)
     def ensure(self, T: int, L: int = 0, n_ids: int = 0):
@@ -308,15 +321,24 @@ class DecoderEngine(GpuEngine):
         self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * zw * 2,
                      "y": cap * yw * 2, "h": cap * I * 2, "ids": cap * 4, "pos": cap * 4, "rng": cap * 16,
                      "taps": cap * 16, "rope": cap * (self.D // 2) * 8,
-                     "leaves": lcap * 4, "leaf_ids": lcap * 4, "out": lcap * 4})
+                     "leaves": lcap * 4, "leaf_ids": lcap * 4, "out": lcap * 4, **self._norm_bufs(cap)})
         self.capacity, self.leaf_capacity = cap, lcap
 
+    def _norm_bufs(self, cap):
+        """The folded norms' buffers: the norm-weighted residual rows and their per-32-column sums of squares."""
+        return {"xw": cap * self.H * 2, "ss": cap * (self.H // 32) * 4} if self.fused_norms else {}
+
     def _layers(self, rec, T, B, kv_a=None, kv_store=None, debug=(), snaps=None):
-        """The per-layer loop (d1-3b-engine.ts:88-105) on the recorder."""
+        """The per-layer loop (d1-3b-engine.ts:88-105) on the recorder. With fused norms (FUSED_ROWS rows) the residual add
+        + RMSNorm after o_proj / out_proj and after w2 runs in those products' epilogues (dj_matmul_residual) and
+        the next product scales its rows (dj_matmul_normed, dj_matmul_qkv_rope_normed); the last layer's w2 feeds
+        the final norm's kernel as before."""
         c, w = self.m["config"], self.w
         H, h, kv, D, eps = self.H, self.h, self.kv, self.D, self.eps
         z = B["z"]
         src = _dj.kv_src(z, T, self.stride, h * D, (h + kv) * D)
+        fused = self.fused_norms and self.FUSED_ROWS[0] <= T <= self.FUSED_ROWS[1] and "xw" in B
+        pending = False  # the next product reads B["xw"] / B["ss"] (a folded norm) instead of B["normed"]
         rec.gather_q(B["ids"], T, w["embed"], B["x"])
         rec.add_rmsnorm(T, H, False, eps, B["x"], B["o"], w["layers.0.operator_norm"], B["normed"])
         # the RoPE angles of this forward, once; every layer's qkv product applies q/k norm + RoPE with them
@@ -324,22 +346,41 @@ class DecoderEngine(GpuEngine):
         for i in range(self.layers):
             p = f"layers.{i}."
             if self.types[i] == "conv":  # LFM2 short conv (d1-3b-engine.ts:90-93)
-                rec.matmul(B["normed"], w[p + "in_proj"], z, T)
+                if pending:
+                    rec.matmul_normed(B["xw"], w[p + "in_proj"], z, T, -1, B["ss"], H, eps)
+                else:
+                    rec.matmul(B["normed"], w[p + "in_proj"], z, T)
                 rec.short_conv(T, H, z, w[p + "conv"], B["taps"], B["y"])
-                rec.matmul(B["y"], w[p + "out_proj"], B["o"], T)
+                second = w[p + "out_proj"]
             else:
-                rec.matmul_qkv_rope(B["normed"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"), w.get(p + "k_norm"),
-                                    False, B["pos"], 1, eps, self.theta, B["rope"])
+                if pending:
+                    rec.matmul_qkv_rope_normed(B["xw"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"),
+                                               w.get(p + "k_norm"), False, B["pos"], 1, eps, self.theta, B["rope"],
+                                               B["ss"], H, eps)
+                else:
+                    rec.matmul_qkv_rope(B["normed"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"),
+                                        w.get(p + "k_norm"), False, B["pos"], 1, eps, self.theta, B["rope"])
                 if kv_store is not None:
                     rec.kv_store(T, kv, D, z, self.stride, h * D, kv_store.at(i * T * 2 * kv * D * 2), 0)
                 a = src if kv_a is None else kv_a(i)
                 rec.attention(T, h, kv, D, z, self.stride, a, src, B["rng"], 1.0 / math.sqrt(D), B["y"])
-                rec.matmul(B["y"], w[p + "o_proj"], B["o"], T)
-            rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[p + "ffn_norm"], B["normed"])
-            rec.matmul_glu(B["normed"], w[p + "w13"], B["h"], T, _dj.ACT_SILU)
-            rec.matmul(B["h"], w[p + "w2"], B["o"], T)
-            nxt = f"layers.{i + 1}.operator_norm" if i + 1 < self.layers else "final_norm"
-            rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[nxt], B["normed"])
+                second = w[p + "o_proj"]
+            if fused:
+                rec.matmul_residual(B["y"], second, T, B["x"], w[p + "ffn_norm"], B["xw"], B["ss"])
+                rec.matmul_normed(B["xw"], w[p + "w13"], B["h"], T, _dj.ACT_SILU, B["ss"], H, eps)
+            else:
+                rec.matmul(B["y"], second, B["o"], T)
+                rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w[p + "ffn_norm"], B["normed"])
+                rec.matmul_glu(B["normed"], w[p + "w13"], B["h"], T, _dj.ACT_SILU)
+            last = i + 1 == self.layers
+            if fused and not last:
+                rec.matmul_residual(B["h"], w[p + "w2"], T, B["x"], w[f"layers.{i + 1}.operator_norm"], B["xw"], B["ss"])
+                pending = True
+            else:
+                rec.matmul(B["h"], w[p + "w2"], B["o"], T)
+                rec.add_rmsnorm(T, H, True, eps, B["x"], B["o"], w["final_norm" if last else f"layers.{i + 1}.operator_norm"],
+                                B["normed"])
+                pending = False
             if i in debug and snaps is not None:
                 snaps[i] = rec.snapshot(B["x"], T * H * 2, np.float16, (T, H))
 

@@ -125,6 +125,14 @@ class Recorder {
     lib().qkNormRope(this.h, T, heads, kv, D, stride, Z, qn, kn, vnorm ? 1 : 0, pos, posStride, eps, theta, rot, mode);
   }
   ropeTable(T, pos, posStride, theta, rot, tab, mode = lib().ROPE_POW_NEG) { lib().ropeTable(this.h, T, pos, posStride, theta, rot, mode, tab); }
+  matmulResidual(X, w, M, R, nw, XW, SS) { lib().matmulResidual(this.h, X, w.h, M, R, nw, XW, SS); }
+  /** act: -1 plain, else a gated activation (ACT_*) */
+  matmulNormed(XW, w, Y, M, act, SS, H, eps) { lib().matmulNormed(this.h, XW, w.h, Y, M, act, SS, H, eps); }
+  matmulQkvRopeNormed(XW, w, Z, M, heads, kv, D, qn, kn, vnorm, pos, posStride, eps, theta, tab, SS, H, normEps, rot = D,
+    mode = lib().ROPE_POW_NEG) {
+    lib().matmulQkvRopeNormed(this.h, XW, w.h, Z, M, heads, kv, D, qn, kn, vnorm ? 1 : 0, pos, posStride, eps, theta, rot, mode,
+      tab, SS, H, normEps);
+  }
   matmulQkvRope(X, w, Z, M, heads, kv, D, qn, kn, vnorm, pos, posStride, eps, theta, tab, rot = D, mode = lib().ROPE_POW_NEG) {
     lib().matmulQkvRope(this.h, X, w.h, Z, M, heads, kv, D, qn, kn, vnorm ? 1 : 0, pos, posStride, eps, theta, rot, mode, tab);
   }

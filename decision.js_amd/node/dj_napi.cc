@@ -17,7 +17,7 @@
 
 namespace {
 
-constexpr size_t kMaxArgs = 20;
+constexpr size_t kMaxArgs = 24;
 
 struct Call {
   napi_env env;
@@ -36,6 +36,7 @@ bool fail(napi_env env, const char *msg) {
 bool args(napi_env env, napi_callback_info info, Call &c, size_t need) {
   c.env = env;
   if (napi_get_cb_info(env, info, &c.argc, c.argv, nullptr, nullptr) != napi_ok) return fail(env, "decision.js: bad call");
+  if (need > kMaxArgs) return fail(env, "decision.js: binding takes more arguments than the call buffer holds");
   if (c.argc < need) {
     std::string m = "decision.js: expected " + std::to_string(need) + " arguments, got " + std::to_string(c.argc);
     return fail(env, m.c_str());
@@ -459,6 +460,19 @@ napi_value MatmulQkvRope(napi_env env, napi_callback_info info) {
   END(dj_matmul_qkv_rope(R(0), P16(1), W(2), P16(3), I(4), I(5), I(6), I(7), P16(8), P16(9), I(10), PI32(11), I(12),
                          F(13), F(14), I(15), I(16), PF32(17)));
 }
+napi_value MatmulResidual(napi_env env, napi_callback_info info) {
+  BEGIN(8);
+  END(dj_matmul_residual(R(0), P16(1), W(2), I(3), P16(4), P16(5), P16(6), PF32(7)));
+}
+napi_value MatmulNormed(napi_env env, napi_callback_info info) {
+  BEGIN(9);
+  END(dj_matmul_normed(R(0), P16(1), W(2), P16(3), I(4), I(5), PF32(6), I(7), F(8)));
+}
+napi_value MatmulQkvRopeNormed(napi_env env, napi_callback_info info) {
+  BEGIN(21);
+  END(dj_matmul_qkv_rope_normed(R(0), P16(1), W(2), P16(3), I(4), I(5), I(6), I(7), P16(8), P16(9), I(10), PI32(11), I(12),
+                                F(13), F(14), I(15), I(16), PF32(17), PF32(18), I(19), F(20)));
+}
 napi_value Attention(napi_env env, napi_callback_info info) {
   BEGIN(12);
   const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
@@ -556,7 +570,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
-      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
+      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"matmulResidual", MatmulResidual}, {"matmulNormed", MatmulNormed}, {"matmulQkvRopeNormed", MatmulQkvRopeNormed}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
       {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"attentionGated", AttentionGated}, {"gdn", Gdn}, {"pleMix", PleMix},
       {"poolProject", PoolProject}, {"addRows", AddRows}, {"biasAct", BiasAct},
       {"addLayernorm", AddLayernorm}, {"gatherRows", GatherRows}, {"score", Score}, {"meanPool", MeanPool}, {"denseF32", DenseF32},

@@ -228,6 +228,17 @@ class DecoderEngine extends GpuEngine {
     this.stride = (this.h + 2 * this.kv) * this.D;
     this.capacity = 0;
     this.leafCapacity = 0;
+    // the residual + RMSNorm between products folded into them on forwards of fusedRows rows (as the Python
+    // host): opts.fusedNorms, else DJ_FUSED_NORMS=0/1, else the class's fusedDefault
+    const fo = this.opts.fusedNorms !== undefined ? this.opts.fusedNorms : this.opts.fused_norms;
+    const env = process.env.DJ_FUSED_NORMS;
+    const want = fo !== undefined ? !!fo : env !== undefined ? env !== "0" : this.constructor.fusedDefault;
+    this.fusedNorms = want && this.H % 32 === 0 && this.H <= 1024;
+  }
+
+  /** The folded norms' buffers: the norm-weighted residual rows and their per-32-column sums of squares. */
+  normBufs(cap) {
+    return this.fusedNorms ? { xw: cap * this.H * 2, ss: cap * (this.H / 32) * 4 } : {};
   }
 
   /** Activation buffers, grown and never shrunk, capacity rounded to 64 rows (d1-3b-engine.ts:33-42). */
@@ -240,12 +251,13 @@ class DecoderEngine extends GpuEngine {
     const zw = Math.max(this.stride, this.conv ? 3 * H : 0), yw = Math.max(this.h * this.D, this.conv ? H : 0);
     this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * zw * 2, y: cap * yw * 2,
       h: cap * I * 2, ids: cap * 4, pos: cap * 4, rng: cap * 16, taps: cap * 16, rope: cap * (this.D / 2) * 8,
-      leaves: lcap * 4, leafIds: lcap * 4, out: lcap * 4 });
+      leaves: lcap * 4, leafIds: lcap * 4, out: lcap * 4, ...this.normBufs(cap) });
     this.capacity = cap;
     this.leafCapacity = lcap;
   }
 
-  /** The per-layer loop (d1-3b-engine.ts:88-105) on the recorder. */
+  /** The per-layer loop (d1-3b-engine.ts:88-105) on the recorder; on more than 64 rows the norms between
+   * products are folded into them (dj_matmul_residual / dj_matmul_normed), as the Python host does. */
   recordLayers(rec, T, B, kvA, kvStore) {
     const w = this.w, L = lib();
     const { H, h, kv, D, eps } = this;
@@ -256,24 +268,45 @@ class DecoderEngine extends GpuEngine {
     rec.addRmsnorm(T, H, false, eps, B.x.ptr, B.o.ptr, ptr("layers.0.operator_norm"), B.normed.ptr);
     // the RoPE angles of this forward, once; every layer's qkv product applies q/k norm + RoPE with them
     rec.ropeTable(T, B.pos.ptr, 1, this.theta, D, B.rope.ptr, L.ROPE_POW_NEG);
+    const [lo, hi] = this.constructor.fusedRows;
+    const fused = this.fusedNorms && T >= lo && T <= hi && !!B.xw;
+    let pending = false; // the next product reads B.xw / B.ss (a folded norm) instead of B.normed
     for (let i = 0; i < this.layers; ++i) {
       const p = `layers.${i}.`;
+      let second;
       if (this.types[i] === "conv") { // LFM2 short conv (d1-3b-engine.ts:90-93)
-        rec.matmul(B.normed.ptr, w[p + "in_proj"], z, T);
+        if (pending) rec.matmulNormed(B.xw.ptr, w[p + "in_proj"], z, T, -1, B.ss.ptr, H, eps);
+        else rec.matmul(B.normed.ptr, w[p + "in_proj"], z, T);
         rec.shortConv(T, H, z, ptr(p + "conv"), B.taps.ptr, B.y.ptr);
-        rec.matmul(B.y.ptr, w[p + "out_proj"], B.o.ptr, T);
+        second = w[p + "out_proj"];
       } else {
-        rec.matmulQkvRope(B.normed.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1,
-          eps, this.theta, B.rope.ptr, D, L.ROPE_POW_NEG);
+        if (pending)
+          rec.matmulQkvRopeNormed(B.xw.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1,
+            eps, this.theta, B.rope.ptr, B.ss.ptr, H, eps, D, L.ROPE_POW_NEG);
+        else
+          rec.matmulQkvRope(B.normed.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1,
+            eps, this.theta, B.rope.ptr, D, L.ROPE_POW_NEG);
         if (kvStore) rec.kvStore(T, kv, D, z, this.stride, h * D, kvStore.at(i * T * 2 * kv * D * 2), 0);
         rec.attention(T, h, kv, D, z, this.stride, kvA ? kvA(i) : src, src, B.rng.ptr, 1 / Math.sqrt(D), B.y.ptr);
-        rec.matmul(B.y.ptr, w[p + "o_proj"], B.o.ptr, T);
+        second = w[p + "o_proj"];
       }
-      rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(p + "ffn_norm"), B.normed.ptr);
-      rec.matmulGlu(B.normed.ptr, w[p + "w13"], B.h.ptr, T, L.ACT_SILU);
-      rec.matmul(B.h.ptr, w[p + "w2"], B.o.ptr, T);
-      const nxt = i + 1 < this.layers ? `layers.${i + 1}.operator_norm` : "final_norm";
-      rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(nxt), B.normed.ptr);
+      if (fused) {
+        rec.matmulResidual(B.y.ptr, second, T, B.x.ptr, ptr(p + "ffn_norm"), B.xw.ptr, B.ss.ptr);
+        rec.matmulNormed(B.xw.ptr, w[p + "w13"], B.h.ptr, T, L.ACT_SILU, B.ss.ptr, H, eps);
+      } else {
+        rec.matmul(B.y.ptr, second, B.o.ptr, T);
+        rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(p + "ffn_norm"), B.normed.ptr);
+        rec.matmulGlu(B.normed.ptr, w[p + "w13"], B.h.ptr, T, L.ACT_SILU);
+      }
+      const last = i + 1 === this.layers;
+      if (fused && !last) {
+        rec.matmulResidual(B.h.ptr, w[p + "w2"], T, B.x.ptr, ptr(`layers.${i + 1}.operator_norm`), B.xw.ptr, B.ss.ptr);
+        pending = true;
+      } else {
+        rec.matmul(B.h.ptr, w[p + "w2"], B.o.ptr, T);
+        rec.addRmsnorm(T, H, true, eps, B.x.ptr, B.o.ptr, ptr(last ? "final_norm" : `layers.${i + 1}.operator_norm`), B.normed.ptr);
+        pending = false;
+      }
     }
   }
 
@@ -414,5 +447,9 @@ class DecoderEngine extends GpuEngine {
     return groupMax(out, nIds, [{ groups }])[0];
   }
 }
+
+// where the folded norms pay (measured: a 3 x 384-id ticket gains, an 86k-row batch loses)
+DecoderEngine.fusedDefault = true;
+DecoderEngine.fusedRows = [65, 8192];
 
 module.exports = { packForest, packShared, commonPrefix, groupMax, GpuEngine, SharedState, DecoderEngine, layoutFor, Context };

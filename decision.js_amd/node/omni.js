@@ -77,7 +77,7 @@ class OmniEngine extends DecoderEngine {
     const zw = Math.max(this.stride, 3 * H), yw = Math.max(this.h * this.D, H);
     this.alloc({ x: cap * H * 2, normed: cap * H * 2, o: cap * H * 2, z: cap * zw * 2, y: cap * yw * 2,
       h: cap * Math.max(this.I, this.ff) * 2, ids: cap * 4, pos: cap * 4, qtype: cap * 4, rng: cap * 16, taps: cap * 16,
-      rope: cap * (this.D / 2) * 8, markers: mcap * 4, g: mcap * H * 2, gf: mcap * H * 2, out: mcap * 4 });
+      rope: cap * (this.D / 2) * 8, markers: mcap * 4, g: mcap * H * 2, gf: mcap * H * 2, out: mcap * 4, ...this.normBufs(cap) });
     this.capacity = cap;
     this.markerCapacity = mcap;
   }
@@ -148,5 +148,8 @@ class OmniEngine extends DecoderEngine {
     }
   }
 }
+
+// the omni trunk's products take slower tiles with the folded norms' epilogues: its norms stay separate by default
+OmniEngine.fusedDefault = false;
 
 module.exports = { OmniEngine, packOmni, temperature, QTYPES };

@@ -91,10 +91,13 @@ class OmniEngine(DecoderEngine):
         self._alloc({"x": cap * H * 2, "normed": cap * H * 2, "o": cap * H * 2, "z": cap * zw * 2, "y": cap * yw * 2,
                      "h": cap * max(self.I, self.ff) * 2, "ids": cap * 4, "pos": cap * 4, "qtype": cap * 4,
                      "rng": cap * 16, "taps": cap * 16, "rope": cap * (self.D // 2) * 8,
-                     "markers": mcap * 4, "g": mcap * H * 2, "gf": mcap * H * 2, "out": mcap * 4})
+                     "markers": mcap * 4, "g": mcap * H * 2, "gf": mcap * H * 2, "out": mcap * 4, **self._norm_bufs(cap)})
         self.capacity, self.marker_capacity = cap, mcap
 
     INPUTS = ("ids", "pos", "qtype", "rng", "taps", "markers")
+    # the omni trunk's products (9216-wide gated, 4608-deep split-K, 1024-wide 32x64) take slower tiles with the
+    # folded norms' epilogues: 2.06 against 1.95 ms a 3-question ticket, so its norms stay separate by default
+    FUSED_DEFAULT = False
 
     def logits(self, seqs, debug=False):
         """Raw marker logits per sequence ([seq][marker], before the temperature), and with `debug` the trunk's

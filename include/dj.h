@@ -215,6 +215,36 @@ int dj_matmul_qkv_rope(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, u
                        int kv, int D, const uint16_t *qn_dev, const uint16_t *kn_dev, int vnorm, const int32_t *pos_dev,
                        int pos_stride, float eps, float theta, int rot, int rope_mode, const float *tab_dev);
 
+/* The residual add and RMSNorm between the decoder's products folded into them (d1-3b-engine.ts:98-104: the
+ * o_proj and w2 products, each followed by ADD_RMSNORM, kernels.ts:23-46, whose output feeds the next product).
+ *
+ * dj_matmul_residual, the producer: with Y = f16(X . W^T) (rounded as dj_matmul's output),
+ *   R[m, n] <- f16(R + Y)                       the residual stream, in place (ADD_RMSNORM's X)
+ *   XW[m, n] = f16(R_new[m, n] * nw[n] / 4)     the norm weight applied, a quarter scale (no f16 overflow for
+ *                                               norm weights up to 4)
+ *   SS[m, b] = sum over the 32 columns of block b of (R + Y)^2, f32 on the unrounded sums (ADD_RMSNORM's
+ *              sum of squares in parts), N / 32 floats per row.
+ * Y itself is not stored. N % 32 == 0. */
+int dj_matmul_residual(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, int M, uint16_t *R_dev,
+                       const uint16_t *nw_dev, uint16_t *XW_dev, float *SS_dev);
+
+/* dj_matmul_normed, the consumer: the product of the normalized rows, every output row m scaled by
+ *   rs[m] = 4 / sqrt(sum_b SS[m, b] / H + eps)
+ * before its f16 rounding: RMSNorm(R_new) . W^T with the norm weight applied before the product and 1 / rms
+ * after (the same value as ADD_RMSNORM's O . W^T up to where the f16 roundings fall). XW and SS are
+ * dj_matmul_residual's outputs with H its N (= this weight's K; H % 32 == 0, H <= 2048; above 1024, or on 64
+ * rows or fewer, the rows are normalized by a small kernel into the context workspace first). act < 0: plain (DJ_W_MFMA weight); else the
+ * gated epilogue of dj_matmul_glu (DJ_W_MFMA_GLU weight) on the scaled gate and up values. */
+int dj_matmul_normed(dj_rec *rec, const uint16_t *XW_dev, const dj_weight *w, uint16_t *Y_dev, int M, int act,
+                     const float *SS_dev, int H, float eps);
+
+/* dj_matmul_qkv_rope on normalized rows (as dj_matmul_normed: XW, SS, H, norm_eps), the q/k norm and RoPE
+ * applied to the scaled product. */
+int dj_matmul_qkv_rope_normed(dj_rec *rec, const uint16_t *XW_dev, const dj_weight *w, uint16_t *Z_dev, int M,
+                              int heads, int kv, int D, const uint16_t *qn_dev, const uint16_t *kn_dev, int vnorm,
+                              const int32_t *pos_dev, int pos_stride, float eps, float theta, int rot, int rope_mode,
+                              const float *tab_dev, const float *SS_dev, int H, float norm_eps);
+
 /* Key/value source of dj_attention: `rows` rows of `stride` halves; K of kv head j at column k_col + j*D,
  * V at v_col + j*D. Key indices outside [0, rows) are clamped (never read out of bounds). */
 typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_col; } dj_kv_src;

@@ -321,6 +321,69 @@ def test_matmul_policy_k_wave_sets(pkg, ctx, M, N, K, want):
     assert f16_close(dY.read(np.float16, (M, N)), want_y, ulps=1.0, atol=2e-5) <= 1.0
 
 
+@pytest.mark.parametrize("M,H,K2,bits", [(1152, 1024, 2048, 8), (300, 1024, 3072, 8), (1536, 2048, 2048, 4), (40, 1024, 2048, 8),
+                                        (1152, 1024, 1024, 8), (200, 768, 1536, 8)])
+def test_matmul_residual_and_normed(pkg, ctx, M, H, K2, bits):
+    """The residual add + RMSNorm folded into the products: dj_matmul_residual (R += f16(X W^T) in place, XW = f16(R w
+    / 4), per-32-column sums of squares of the unrounded sums) and its consumers dj_matmul_normed (plain and gated)
+    and dj_matmul_qkv_rope_normed against the separate ADD_RMSNORM of the oracle followed by the product: the new
+    stream within one f16 rounding of the product's, XW bit-exact from it, the sums within 1e-5 relative, the
+    consumers within 4-16 f16 ulps + 3e-3 of the unfused form (the norm's 1 / rms lands after the product's sum
+    instead of before the input's f16 rounding, which moves the outputs by ~2.5e-4 rms); M = 40 takes the skinny
+    rows' kernels."""
+    dj = _dj()
+    rng = np.random.default_rng(M + H + K2)
+    eps = 1e-6
+    cX, sX = quant(rng, H, K2, bits)  # the producer: o_proj / w2, K2 -> H
+    W1 = ctx.weight_q(cX, sX, H, K2, bits, dj.W_MFMA)
+    X = rand_f16(rng, (M, K2))
+    R = rand_f16(rng, (M, H), std=0.5)
+    nw = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    dX, dR, dnw = ctx.array(X), ctx.array(R), ctx.array(nw)
+    dXW, dSS = ctx.alloc(M * H * 2), ctx.alloc(M * (H // 32) * 4)
+    run(ctx, lambda r: r.matmul_residual(dX, W1, M, dR, dnw, dXW, dSS))
+    Rn, XW, SS = dR.read(np.float16, (M, H)), dXW.read(np.float16, (M, H)), dSS.read(np.float32, (M, H // 32))
+    y = ref.matmul(X, ref.dequant_f16(cX, sX, bits), np.float64)
+    v = R.astype(np.float64) + y.astype(np.float64)
+    ulp_y = np.spacing(np.abs(y).astype(np.float16)).astype(np.float64)
+    assert (np.abs(Rn.astype(np.float64) - v) <= np.spacing(np.abs(v).astype(np.float16)).astype(np.float64) + ulp_y).all()
+    want_xw = (Rn.astype(np.float32) * nw.astype(np.float32) * np.float32(0.25)).astype(np.float16)
+    assert np.array_equal(XW.view(np.uint16), want_xw.view(np.uint16))
+    ss_want = (v * v).reshape(M, H // 32, 32).sum(-1)
+    assert np.abs(SS - ss_want).max() <= 1e-5 * ss_want.max() + 2 * (np.abs(v) * ulp_y).reshape(M, H // 32, 32).sum(-1).max()
+    # the consumers against the unfused form on the same stream: O = f16(R_new inv w), then the product
+    inv = 1.0 / np.sqrt(SS.astype(np.float64).sum(-1, keepdims=True) / H + eps)
+    normed = (Rn.astype(np.float64) * inv * nw.astype(np.float64)).astype(np.float16)
+    N2 = 1536
+    c2, s2 = quant(rng, N2, H, bits)
+    W16 = ref.dequant_f16(c2, s2, bits)
+    W2, dY = ctx.weight_q(c2, s2, N2, H, bits, dj.W_MFMA), ctx.alloc(M * N2 * 2)
+    run(ctx, lambda r: r.matmul_normed(dXW, W2, dY, M, -1, dSS, H, eps))
+    # the A roundings differ by up to an f16 ulp per element: about 2.5e-4 rms on these 0.9-sized outputs
+    assert f16_close(dY.read(np.float16, (M, N2)), ref.matmul(normed, W16, np.float64), ulps=4.0, atol=3e-3) <= 1.0
+    W3, dG = ctx.weight_q(c2, s2, N2, H, bits, dj.W_MFMA_GLU), ctx.alloc(M * N2 // 2 * 2)
+    run(ctx, lambda r: r.matmul_normed(dXW, W3, dG, M, dj.ACT_SILU, dSS, H, eps))
+    ab = ref.matmul(normed, W16, np.float64)
+    want_g = ref.silu_mul(ab[:, :N2 // 2], ab[:, N2 // 2:], np.float64)
+    assert f16_close(dG.read(np.float16, (M, N2 // 2)), want_g, ulps=6.0, atol=3e-3) <= 1.0
+    # qkv + RoPE on the normalized rows against the same op on the unfused rows (both on the GPU)
+    heads, kv, D = H // 128, max(1, H // 512), 128
+    N3 = (heads + 2 * kv) * D
+    c3, s3 = quant(rng, N3, H, bits)
+    W4 = ctx.weight_q(c3, s3, N3, H, bits, dj.W_MFMA)
+    pos = ctx.array((np.arange(M) % 384).astype(np.int32))
+    qn, kn = ctx.array(nw[:D].copy()), ctx.array(nw[D:2 * D].copy())
+    tab, dZa, dZb, dN = ctx.alloc(M * 64 * 8), ctx.alloc(M * N3 * 2), ctx.alloc(M * N3 * 2), ctx.array(normed)
+
+    def both(r):
+        r.rope_table(M, pos, 1, 1e6, D, tab)
+        r.matmul_qkv_rope(dN, W4, dZa, M, heads, kv, D, qn, kn, False, pos, 1, eps, 1e6, tab)
+        r.matmul_qkv_rope_normed(dXW, W4, dZb, M, heads, kv, D, qn, kn, False, pos, 1, eps, 1e6, tab, dSS, H, eps)
+    run(ctx, both)
+    za, zb = dZa.read(np.float16, (M, N3)), dZb.read(np.float16, (M, N3))
+    assert f16_close(zb, za, ulps=16.0, atol=4e-3) <= 1.0  # the q/k norm rescales the two roundings apart
+
+
 @pytest.mark.parametrize("waves", [1, 5, 8, 9, 16])
 @pytest.mark.parametrize("M,N,K,bits,glu", [(1, 2048, 832, 8, False), (32, 1536, 4608, 8, False),
                                             (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True),

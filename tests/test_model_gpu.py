@@ -184,6 +184,58 @@ def test_shared_state_equals_forest(pkg, models):
         eng.destroy()
 
 
+def test_fused_norms_match_oracle_and_separate_norms(pkg, models):
+    """The residual add + RMSNorm folded into the products (dj_matmul_residual, dj_matmul_normed,
+    dj_matmul_qkv_rope_normed) against the separate norm kernel, on a decoder forest (attention layers) and on
+    the omni trunk (conv layers: in_proj takes the row norm): both forms within 1e-3 of the oracle's answers and
+    2e-2 relative L2 of its hidden state / trunk output, and within rounding of each other; a forest of at most
+    64 rows takes the separate kernel either way (bit-identical)."""
+    from decision_js_amd.engine import DecoderEngine
+    from decision_js_amd.omni import OmniEngine
+    rng = np.random.default_rng(31)
+    V = 4096
+    model = ref.Model(models["q8"])
+    L = model.c["layers"]
+    trees = [_tree(rng, V, 200, [30, 45, 12]), _tree(rng, V, 0, [80])]
+    small = [_tree(rng, V, 20, [9, 7])]
+    want, dbg = _oracle_forest(model, trees, debug=(L - 1,))
+    got = {}
+    for fused in (True, False):
+        eng = DecoderEngine.load(models["q8"], {"fused_norms": fused})
+        try:
+            assert eng.fused_norms == fused
+            got[fused] = (eng.run(trees, debug_layers=[L - 1]), eng.run(small)["logits"])
+        finally:
+            eng.destroy()
+    for fused, (r, _) in got.items():
+        worst = max(abs(a - b) for gt, wt in zip(r["scores"], want) for gq, wq in zip(gt, wt)
+                    for a, b in zip(ref.softmax(gq), ref.softmax(wq)))
+        assert worst < PROB_TOL, (fused, worst)
+        assert rel_l2(r["debug"][L - 1], dbg[L - 1]) < HIDDEN_TOL
+    assert rel_l2(got[True][0]["debug"][L - 1], got[False][0]["debug"][L - 1]) < 5e-3
+    assert np.array_equal(got[True][1], got[False][1])
+
+    omodel = ref.Model(models["omni"])
+    seqs = _omni_requests(rng, V)
+    owant, owdbg = ref.omni_forward(omodel, seqs, acc=np.float64)
+    trunks = []
+    for fused in (True, False):
+        eng = OmniEngine.load(models["omni"], {"fused_norms": fused})
+        try:
+            assert eng.fused_norms == fused
+            r = eng.logits(seqs, debug=True)
+        finally:
+            eng.destroy()
+        assert rel_l2(r["debug"]["trunk"], owdbg["trunk"]) < HIDDEN_TOL
+        k = 0
+        for s, g in zip(seqs, r["logits"]):
+            w = owant[k:k + len(s["markers"])]
+            k += len(s["markers"])
+            assert max(abs(a - b) for a, b in zip(ref.softmax(np.asarray(g)), ref.softmax(w))) < PROB_TOL
+        trunks.append(r["debug"]["trunk"])
+    assert rel_l2(trunks[0], trunks[1]) < 5e-3
+
+
 def test_graph_replay_is_bit_identical(pkg, models):
     from decision_js_amd.engine import DecoderEngine
     eng = DecoderEngine.load(models["q8"])
@@ -298,10 +350,12 @@ def test_decision_api_encoder(pkg, models):
         d.destroy()
 
 
-@pytest.mark.parametrize("op,graphs", [("matmul", True), ("attention", False), ("matmul_glu", True)])
+@pytest.mark.parametrize("op,graphs", [("matmul", True), ("attention", False), ("matmul_glu_normed", True),
+                                       ("matmul_residual", False)])
 def test_injected_fault_surfaces_and_next_call_succeeds(pkg, models, monkeypatch, op, graphs):
-    """An error inside a forward (DJ_FAULT_INJECT=<op>:1: the op fails once, before launching anything)
-    surfaces as the library's "decision.js: ..." error, the failed recording is aborted (dj_rec_abort), and the
+    """An error inside a forward (DJ_FAULT_INJECT=<op>:1: the op fails once, before launching anything; the
+    state's forwards fold their norms into the products, matmul_residual / matmul_glu_normed) surfaces as the
+    library's "decision.js: ..." error, the failed recording is aborted (dj_rec_abort), and the
     next call on the same Decision succeeds with the answers a clean run gives (the reference's finish() error
     path, gpu.ts:255-260; SURVEY's injected-error check). Also through the shared-state path."""
     from decision_js_amd import _dj
