@@ -107,11 +107,14 @@ def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
     replayed `rounds` times between two HIP events on the engine's stream. Back-to-back launches in a graph
     leave no per-launch event overhead, so this is the kernel's own duration (what rocprofv3 reports). The
     fused qkv + q/k norm + RoPE product is timed as that op (layer 0's weight and norms, the RoPE table made
-    once beforehand), not as a plain product of its shape, which would pick another tile."""
+    once beforehand), not as a plain product of its shape, which would pick another tile; a product tagged
+    +rownorm (the folded norm's consumer) or +residual (its producer) is timed in that form, on seeded rows,
+    sums of squares and stream values."""
     from decision_js_amd import _dj
     M, N, K = shape
     glu = name.startswith("matmul_glu")
     rope = name.startswith("matmul_rope")
+    rownorm, residual = name.endswith("+rownorm"), name.endswith("+residual")
     want = _dj.W_MFMA_GLU if glu else _dj.W_MFMA
     w = next((w for w in eng.w.values() if isinstance(w, _dj.Weight) and w.N == N and w.K == K
               and (w.layout & ~_dj.W_DIRECT) == want), None)
@@ -123,7 +126,14 @@ def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
     rng = np.random.default_rng(5)
     X = ctx.array((rng.standard_normal((M, K)) * 0.5).astype(np.float16))
     Y = ctx.alloc(M * (N // 2 if glu else N) * 2)
-    key = 0x6A5EB0000 + (M * 131 + N * 7 + K) % 65521 + (1 << 20 if rope else 0)
+    key = 0x6A5EB0000 + (M * 131 + N * 7 + K) % 65521 + (1 << 20 if rope else 0) + (2 << 20 if rownorm else 0) \
+        + (4 << 20 if residual else 0)
+    if rownorm:  # per-32-column sums of squares of rows of about unit scale
+        SS = ctx.array((rng.random((M, K // 32)) * 16 + 16).astype(np.float32))
+    if residual:
+        R = ctx.array(rng.standard_normal((M, N)).astype(np.float16))
+        nw = ctx.array(np.ones(N, np.float16))
+        XW, SS = ctx.alloc(M * N * 2), ctx.alloc(M * (N // 32) * 4)
     if rope:
         pos = ctx.array((np.arange(M) % 384).astype(np.int32))
         tab = ctx.alloc(M * (eng.D // 2) * 8)
@@ -133,8 +143,15 @@ def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
         qn, kn = eng.w.get("layers.0.q_norm"), eng.w.get("layers.0.k_norm")
 
     def one(rec):
-        if rope:
+        if rope and rownorm:
+            rec.matmul_qkv_rope_normed(X, w, Y, M, eng.h, eng.kv, eng.D, qn, kn, False, pos, 1, eng.eps, eng.theta, tab,
+                                       SS, K, eng.eps)
+        elif rope:
             rec.matmul_qkv_rope(X, w, Y, M, eng.h, eng.kv, eng.D, qn, kn, False, pos, 1, eng.eps, eng.theta, tab)
+        elif rownorm:
+            rec.matmul_normed(X, w, Y, M, _dj.ACT_SILU if glu else -1, SS, K, eng.eps)
+        elif residual:
+            rec.matmul_residual(X, w, M, R, nw, XW, SS)
         elif glu:
             rec.matmul_glu(X, w, Y, M)
         else:
@@ -157,6 +174,8 @@ def isolated_gemm_ms(eng, name, shape, reps=50, rounds=4):
     if rope:
         pos.free()
         tab.free()
+    for b in ((SS,) if rownorm else (R, nw, XW, SS) if residual else ()):
+        b.free()
     return ms
 
 

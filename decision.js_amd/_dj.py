@@ -32,7 +32,7 @@ class KVSrc(C.Structure):
 
 
 class ProfileEntry(C.Structure):
-    _fields_ = [("name", C.c_char * 48), ("ms", C.c_double), ("launches", C.c_int64)]
+    _fields_ = [("name", C.c_char * 96), ("ms", C.c_double), ("launches", C.c_int64)]
 
 
 _P, _I, _F, _U64, _SZ = C.c_void_p, C.c_int, C.c_float, C.c_uint64, C.c_size_t

@@ -1307,8 +1307,8 @@ static int qkv_rope_impl(dj_rec *rec, const uint16_t *X, const dj_weight *w, uin
                              mode);
     }
   }
-  char shape[48];
-  snprintf(shape, sizeof shape, "[%dx%dx%d]", M, w->N, w->K);
+  char shape[48];  // (+rownorm: the normalized-rows form, so profiles tell it from the plain op)
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, SS ? "+rownorm" : "");
   return dj_op_end(rec, name, shape);
 }
 
@@ -1487,7 +1487,7 @@ extern "C" int dj_matmul_residual(dj_rec *rec, const uint16_t *X, const dj_weigh
     if (st) return st;
   }
   char shape[48];
-  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s+residual", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
   return dj_op_end(rec, name, shape);
 }
 
@@ -1517,7 +1517,7 @@ extern "C" int dj_matmul_normed(dj_rec *rec, const uint16_t *XW, const dj_weight
     if (st) return st;
   }
   char shape[48];
-  snprintf(shape, sizeof shape, "[%dx%dx%d]%s", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
+  snprintf(shape, sizeof shape, "[%dx%dx%d]%s+rownorm", M, w->N, w->K, splits > 1 ? (splits == 2 ? "/k2" : splits == 4 ? "/k4" : "/k8") : "");
   return dj_op_end(rec, name, shape);
 }
 

@@ -135,7 +135,7 @@ int dj_timer_end(dj_ctx *ctx, float *ms);
  * keyed by kernel name (the reference's globalThis.__d1Profile map). Ops in a captured graph are not
  * profiled. dj_profile_get copies up to `cap` entries and returns the count in *n. */
 int dj_profile_enable(dj_ctx *ctx, int on);
-typedef struct { char name[48]; double ms; int64_t launches; } dj_profile_entry;
+typedef struct { char name[96]; double ms; int64_t launches; } dj_profile_entry;
 int dj_profile_get(dj_ctx *ctx, dj_profile_entry *out, int cap, int *n);
 int dj_profile_reset(dj_ctx *ctx);
 
