@@ -652,21 +652,32 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   } else {
     const int I = N >> 1;
     const int wb0 = nb0 + wn * FN;
+    // The activation is chosen once, outside the unrolled fragments, and every value is formed before the
+    // first store: a per-value switch (or a store guard between values) puts each value's exp / rcp chain in
+    // a branch region of its own, and the chains then run one after another instead of interleaved.
+    auto gated = [&](auto act) {
+      h4 v[FM][FN / 2];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < FN; j += 2) {
-        const int m = mrow + i * 16;
-        if (!mine(i)) continue;
-        const int col = ((wb0 + j) >> 1) * 16 + c4;  // physical block p even -> w1 block p / 2
-        h4 v;
+        for (int j = 0; j < FN; j += 2)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float a = (float)(_Float16)acc[i][j][r], b = (float)(_Float16)acc[i][j + 1][r];
-          v[r] = (_Float16)(act_apply(g.act, a) * b);
+          for (int r = 0; r < 4; ++r) {
+            const float a = (float)(_Float16)acc[i][j][r], b = (float)(_Float16)acc[i][j + 1][r];
+            v[i][j / 2][r] = (_Float16)(act(a) * b);
+          }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; j += 2) {
+          const int m = mrow + i * 16;
+          const int col = ((wb0 + j) >> 1) * 16 + c4;  // physical block p even -> w1 block p / 2
+          if (mine(i) && m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v[i][j / 2];
         }
-        if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
-      }
+    };
+    if (g.act == DJ_ACT_SILU) gated([](float a) { return act_silu(a); });
+    else if (g.act == DJ_ACT_GELU_TANH) gated([](float a) { return act_gelu_tanh(a); });
+    else gated([](float a) { return act_gelu_erf(a); });
   }
 }
 
@@ -729,40 +740,14 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws
 }
 
 // ---------------------------------------------------------------- skinny M (GEMV-style, M <= 64)
-// Below a few dozen rows the product is bound by streaming the weights, and a tile grid has too few
-// workgroups to keep HBM busy. Measured (graph replay, q8): 0.85 TB/s at M = 1 and 0.4-0.6 TB/s at M = 32
-// on 1536-2048-wide weights, 2-3x the tiled kernel; the limit is that each workgroup re-reads X from L2
-// (M / 8.5 times the weight bytes at 16 columns per workgroup). Here a workgroup owns CB 16-column weight blocks (CB = 2 for a gated weight:
-// its gate and up blocks) and all of K; its KW waves take the 64-K steps round-robin. A wave loads BATCH
-// steps at once — weight blocks (16 bytes per lane, already in MFMA lane order), scale words and the X
-// fragments (L2-resident) — straight into registers, then runs their MFMAs; with up to 16 waves per
-// workgroup that keeps enough weight bytes in flight. The waves' partial tiles are added through LDS in wave
-// order (deterministic), and wave 0 runs the same epilogue as the tiled kernel.
-//
-// MAXW is the most waves a launch may use. MAXW = 16: 128 VGPRs per lane, so a batch stages about 80 VGPRs
-// (3 steps at M = 32) and past-the-end steps re-load the last one. MAXW = 8 (the default launch): two waves
-// per SIMD, 256 VGPRs per lane, so a batch stages about 176 VGPRs (9 steps at M = 32: all of a 4608-long K
-// over 8 waves in one round trip) and loads past the end are skipped, not repeated.
-template <int BITS, int MT, int CB, bool GLU, int MAXW>
-__global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
+// The skinny products' accumulation: KW waves take the KS 64-K steps from k0 round-robin (wave w: steps w,
+// w + KW, ...; BATCH of them loaded at once), each into its own accumulators (blocks of Y^T: weight fragment
+// first).
+template <int BITS, int MT, int CB, bool WIDE, int BATCH>
+__device__ __forceinline__ void gemv_accumulate(const GemmArgs &g, f4 (&acc)[MT][CB], int wave, int lane, int KW, int nb0,
+                                                int k0, int KS) {
   constexpr int CBYTES = BITS == 8 ? 1024 : BITS == 4 ? 512 : 2048;
-  // steps per load batch: the staging budget above over the VGPRs of one step (X fragments 8 MT, weight
-  // blocks 4 or 8 and a scale word per block)
-  constexpr bool WIDE = MAXW <= 8;
-  constexpr int PER_STEP = 8 * MT + (BITS == 16 ? 8 : 5) * CB;
-  constexpr int BUDGET = WIDE ? 176 : 80, BMAX = WIDE ? 12 : 8;
-  constexpr int BATCH = BUDGET / PER_STEP < 1 ? 1 : BUDGET / PER_STEP > BMAX ? BMAX : BUDGET / PER_STEP;
-  __shared__ f4 red[(MAXW - 1) * MT * CB * 64];
-  // `wave` through readfirstlane: the batch guards below must be scalar branches. As vector compares they
-  // become EXEC-masked regions, and an MFMA runs whatever EXEC says, so a skipped slot would still add its
-  // (unloaded) registers into the accumulator.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, KW = blockDim.x >> 6;
-  const int nb0 = blockIdx.x * CB;
   const int M = g.M, K = g.K, KT = K >> 6;
-  // split along K (gridDim.y > 1): this workgroup takes the KS steps from k0 and leaves f32 partials
-  const int KS = g.ksteps, k0 = blockIdx.y * KS;
-
-  f4 acc[MT][CB];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -810,6 +795,42 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
       }
     }
   }
+}
+
+// Below a few dozen rows the product is bound by streaming the weights, and a tile grid has too few
+// workgroups to keep HBM busy. Measured (graph replay, q8): 0.85 TB/s at M = 1 and 0.4-0.6 TB/s at M = 32
+// on 1536-2048-wide weights, 2-3x the tiled kernel; the limit is that each workgroup re-reads X from L2
+// (M / 8.5 times the weight bytes at 16 columns per workgroup). Here a workgroup owns CB 16-column weight blocks (CB = 2 for a gated weight:
+// its gate and up blocks) and all of K; its KW waves take the 64-K steps round-robin. A wave loads BATCH
+// steps at once — weight blocks (16 bytes per lane, already in MFMA lane order), scale words and the X
+// fragments (L2-resident) — straight into registers, then runs their MFMAs; with up to 16 waves per
+// workgroup that keeps enough weight bytes in flight. The waves' partial tiles are added through LDS in wave
+// order (deterministic), and wave 0 runs the same epilogue as the tiled kernel.
+//
+// MAXW is the most waves a launch may use. MAXW = 16: 128 VGPRs per lane, so a batch stages about 80 VGPRs
+// (3 steps at M = 32) and past-the-end steps re-load the last one. MAXW = 8 (the default launch): two waves
+// per SIMD, 256 VGPRs per lane, so a batch stages about 176 VGPRs (9 steps at M = 32: all of a 4608-long K
+// over 8 waves in one round trip) and loads past the end are skipped, not repeated.
+template <int BITS, int MT, int CB, bool GLU, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
+  // steps per load batch: the staging budget above over the VGPRs of one step (X fragments 8 MT, weight
+  // blocks 4 or 8 and a scale word per block)
+  constexpr bool WIDE = MAXW <= 8;
+  constexpr int PER_STEP = 8 * MT + (BITS == 16 ? 8 : 5) * CB;
+  constexpr int BUDGET = WIDE ? 176 : 80, BMAX = WIDE ? 12 : 8;
+  constexpr int BATCH = BUDGET / PER_STEP < 1 ? 1 : BUDGET / PER_STEP > BMAX ? BMAX : BUDGET / PER_STEP;
+  __shared__ f4 red[(MAXW - 1) * MT * CB * 64];
+  // `wave` through readfirstlane: the batch guards below must be scalar branches. As vector compares they
+  // become EXEC-masked regions, and an MFMA runs whatever EXEC says, so a skipped slot would still add its
+  // (unloaded) registers into the accumulator.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63, KW = blockDim.x >> 6;
+  const int nb0 = blockIdx.x * CB;
+  const int M = g.M;
+  // split along K (gridDim.y > 1): this workgroup takes the KS steps from k0 and leaves f32 partials
+  const int KS = g.ksteps, k0 = blockIdx.y * KS;
+
+  f4 acc[MT][CB];
+  gemv_accumulate<BITS, MT, CB, WIDE, BATCH>(g, acc, wave, lane, KW, nb0, k0, KS);
 
   // partial tiles of waves 1.. through LDS, added by wave 0 in wave order
   if (wave > 0) {
