@@ -112,9 +112,6 @@ __device__ __forceinline__ float act_gelu_erf(float x) {
                              t * __builtin_amdgcn_exp2f(-1.4426950408889634f * z * z);
   return 0.5f * x * (1.0f + (z >= 0.0f ? y : -y));
 }
-__device__ __forceinline__ float act_apply(int act, float a) {
-  return act == DJ_ACT_SILU ? act_silu(a) : act == DJ_ACT_GELU_TANH ? act_gelu_tanh(a) : act_gelu_erf(a);
-}
 
 struct GemmArgs {
   const uint16_t *X;
@@ -730,11 +727,13 @@ __global__ __launch_bounds__(256) void k_splitk_sum(const float *__restrict__ ws
       b += *(const f4 *)(p + k * slice + 16);
     }
     h4 v;
+    auto gated = [&](auto fn) {  // the activation chosen once (the four values' chains interleave)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float x = (float)(_Float16)a[r], u = (float)(_Float16)b[r];
-      v[r] = (_Float16)(act_apply(act, x) * u);
-    }
+      for (int r = 0; r < 4; ++r) v[r] = (_Float16)(fn((float)(_Float16)a[r]) * (float)(_Float16)b[r]);
+    };
+    if (act == DJ_ACT_SILU) gated([](float x) { return act_silu(x); });
+    else if (act == DJ_ACT_GELU_TANH) gated([](float x) { return act_gelu_tanh(x); });
+    else gated([](float x) { return act_gelu_erf(x); });
     *(h4 *)(Y + (size_t)m * NO + c) = v;
   }
 }
@@ -876,17 +875,23 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv(GemmArgs g) {
   } else {
     static_assert(!GLU || CB == 2, "a gated weight pairs gate and up blocks");
     const int I = N >> 1, col = (nb0 >> 1) * 16 + c4;  // block pair (2p, 2p + 1) -> w1/w3 block p
+    // the activation chosen once and every value formed before the stores (as the tiled epilogue)
+    auto gated = [&](auto fn) {
+      h4 v[MT];
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int m = 16 * i + (lane & 15);
-      h4 v;
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float a = (float)(_Float16)acc[i][0][r], b = (float)(_Float16)acc[i][1][r];
-        v[r] = (_Float16)(act_apply(g.act, a) * b);
+        for (int r = 0; r < 4; ++r)
+          v[i][r] = (_Float16)(fn((float)(_Float16)acc[i][0][r]) * (float)(_Float16)acc[i][1][r]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int m = 16 * i + (lane & 15);
+        if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v[i];
       }
-      if (m < M) *(h4 *)(g.Y + (size_t)m * I + col) = v;
-    }
+    };
+    if (g.act == DJ_ACT_SILU) gated([](float x) { return act_silu(x); });
+    else if (g.act == DJ_ACT_GELU_TANH) gated([](float x) { return act_gelu_tanh(x); });
+    else gated([](float x) { return act_gelu_erf(x); });
   }
 }
 
