@@ -206,6 +206,17 @@ __device__ __forceinline__ void wait_steps_barrier(int n) {
   }
 }
 
+// wait_vm with at most n (clamped to [0, MAXN]) steps of I DMAs each left in flight (no barrier)
+template <int I, int MAXN>
+__device__ __forceinline__ void wait_steps(int n) {
+  if constexpr (MAXN <= 0) {
+    wait_vm<0>();
+  } else {
+    if (n >= MAXN) wait_vm<MAXN * I>();
+    else wait_steps<I, MAXN - 1>(n);
+  }
+}
+
 // EPI: 0 plain store, 1 gated MLP, 2 QK_NORM_ROPE on a qkv weight (kernels.ts:86-112) before the store, 3 plain
 // product into the residual epilogue (dj_matmul_residual); 4 + (0, 1 or 2): that epilogue after the row norm of
 // dj_matmul_normed (every accumulator row times 1 / (XW_SCALE rms) from the producer's partial sums)
@@ -220,9 +231,10 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   static_assert(!RES || FN % 2 == 0, "the residual epilogue sums 32-column blocks (fragment pairs)");
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
-  // the row norm's partial sums sit past the ring (and past the K wave sets' partial tiles, which reuse it)
-  constexpr int RN_OFF = S::SMEM, RN_BYTES = RN ? (BM * 132 + 1023) / 1024 * 1024 : 0;  // sums, then BM scales
-  static_assert(S::SMEM + RN_BYTES <= 160 * 1024, "LDS for the row norm's sums");
+  // the row norm's per-row scales sit past the ring
+  constexpr int RN_OFF = S::SMEM, RN_BYTES = RN ? (BM * 4 + 1023) / 1024 * 1024 : 0;
+  static_assert(S::SMEM + RN_BYTES <= 160 * 1024, "LDS for the row norm's scales");
+  static_assert(!RN || BM <= S::NT, "a lane per row for the row norm");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[S::SMEM + RN_BYTES];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -248,10 +260,23 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   // The accumulator layout: lane l holds output row l % 16 of each 16x16 fragment and its columns 4 (l / 16)..+3.
   const int mrow = m0 + wm * FM * 16 + (lane & 15), c4 = 4 * (lane >> 4);
   const int N = g.N;
-  // Epilogue inputs loaded before the ring starts, so that they land during the K loop (their DMAs / loads are
-  // older than the ring's, so the ring's exact counter waits only get stricter). Row norm: the tile's rows of
-  // partial sums (nb = Hn / 32 <= 32 floats a row, contiguous in memory) by LDS DMA into RN_OFF; the epilogue
-  // reads them there. Residual: the tile's stream values and norm weights, into registers.
+  // Epilogue inputs loaded before the ring starts (their loads are older than the ring's DMAs, so the ring's
+  // exact counter waits only get stricter). Row norm: lane r < BM of the workgroup loads row m0 + r's nb = Hn /
+  // 32 partial sums (nb <= 32, a multiple of 4: whole 16-byte loads), waits for them alone once the prologue's
+  // DMAs are issued, and leaves the row's scale in LDS for the epilogue. Residual: the tile's stream values and
+  // norm weights, into registers.
+  f4 rnp[RN ? 8 : 1];
+  if constexpr (RN) {
+    const int nb4 = g.Hn >> 7;
+    const f4 *src = (const f4 *)(g.ssin + (size_t)min(m0 + tid, M - 1) * (g.Hn >> 5));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) rnp[c] = (f4){0.f, 0.f, 0.f, 0.f};
+    if (tid < BM) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (c < nb4) rnp[c] = src[c];
+    }
+  }
   h4 rx[RES ? FM : 1][RES ? FN : 1], rw[RES ? FN : 1];
   if (RES && (KSPLIT || wk == 0)) {  // each wave set its own epilogue rows
 #pragma unroll
@@ -342,20 +367,22 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   // Steps are issued only while they exist: before the wait for step t, steps up to min(t + NS - 3, KS - 1)
   // have been issued (min(NS - 2, KS - 1) for t = 0), so min(NS - 3, KS - 1 - t) later steps may still be in
   // flight — the full ring depth until the tail, then exact counts (no re-loads of the last step to wait for).
-  if constexpr (RN) {  // the tile's partial sums: 1 KB DMAs, as many as BM rows of nb floats need, over the waves
-    const int nb = g.Hn >> 5;
-    const long last = (long)M * nb * 4 - 16;  // a tile's rows past M read the buffer's last 16 bytes
-    const char *src0 = (const char *)g.ssin + (size_t)m0 * nb * 4;
-    const int chunks = (BM * nb * 4 + 1023) / 1024;
-    for (int q = wv; q < chunks; q += NW) {  // wave-uniform (the LDS address goes to M0)
-      const long off = min((long)m0 * nb * 4 + (long)q * 1024 + lane * 16, last) - (long)m0 * nb * 4;
-      dma16(src0 + off, lds0 + RN_OFF + q * 1024);
-    }
-  }
   // prologue: steps 0 .. NS-2 in flight (paired ring: pairs 0 .. NS/2-2, steps 0 .. NS-3)
+  constexpr int PRO = S::PAIRED ? NS - 2 : NS - 1;
 #pragma unroll
-  for (int p = 0; p < (S::PAIRED ? NS - 2 : NS - 1); ++p)
+  for (int p = 0; p < PRO; ++p)
     if (p < KS) issue(p, p);
+  if constexpr (RN) {
+    // the row sums have landed (older than the prologue's DMAs, which stay in flight): the row's scale
+    // 1 / (XW_SCALE rms) into LDS, read by the epilogue after its barrier
+    wait_steps<S::I, PRO>(min(PRO, KS));
+    f4 p = rnp[0];
+#pragma unroll
+    for (int c = 1; c < 8; ++c) p += rnp[c];
+    const float ssum = (p[0] + p[1]) + (p[2] + p[3]);
+    if (tid < BM)
+      ((float *)(smem + RN_OFF))[tid] = rsqrtf(ssum * (1.0f / (float)g.Hn) + g.neps) * (1.0f / XW_SCALE);
+  }
 
   if constexpr (S::PAIRED && WK > 1) {
     // Paired ring with two K wave sets: the pair's waits, barrier and DMAs as below; set wk then reads and
@@ -473,31 +500,8 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   // Y^T: lane l has output row l%16 of the block and its 4 consecutive columns 4(l/16)..+3 — one 8-byte f16
   // (16-byte f32) store instead of four scattered 2-byte ones.
   if constexpr (RN) {  // row norm: the consumer side of a residual epilogue
-    // Each row's scale once per workgroup, one lane a row, into LDS past the sums. With 32 sums a row (rows 128
-    // bytes apart: every row starts on bank 0) lane r reads its 16-byte chunks in the order k ^ (r % 8), so the
-    // 8 rows of one LDS cycle hit 8 different bank groups; a row's sum is then four interleaved partials.
-    const int nb = g.Hn >> 5;
-    const float *sums = (const float *)(smem + RN_OFF);
-    float *scale = (float *)(smem + RN_OFF + BM * 128);
-    const float inv_h = 1.0f / (float)g.Hn;
-    for (int r = wave * 64 + lane; r < BM; r += NW * 64) {
-      float v;
-      if (nb == 32) {
-        f4 p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const f4 x = *(const f4 *)(sums + r * 32 + (k ^ (r & 7)) * 4);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) p[c] += x[c];
-        }
-        v = (p[0] + p[1]) + (p[2] + p[3]);
-      } else {
-        v = 0.f;
-        for (int b = 0; b < nb; ++b) v += sums[r * nb + b];
-      }
-      scale[r] = rsqrtf(v * inv_h + g.neps) * (1.0f / XW_SCALE);
-    }
-    __syncthreads();  // (every wave's sum DMAs landed before its first ring wait and that wait's barrier)
+    const float *scale = (const float *)(smem + RN_OFF);
+    __syncthreads();  // every row's scale is in LDS
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const float rs = scale[wm * FM * 16 + i * 16 + (lane & 15)];
@@ -960,7 +964,8 @@ static const int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 // Whether a tile's LDS holds the row norm's sums past its ring (EPI 4-6) for these weight bits.
 template <int BITS, int WM, int WN, int FM, int FN, int RING, int WK>
 constexpr bool rn_fits_cfg() {
-  return GemmShape<BITS, WM, WN, FM, FN, RING, WK>::SMEM + (WM * FM * 16 * 132 + 1023) / 1024 * 1024 <= 160 * 1024;
+  return GemmShape<BITS, WM, WN, FM, FN, RING, WK>::SMEM + (WM * FM * 16 * 4 + 1023) / 1024 * 1024 <= 160 * 1024 &&
+         WM * FM * 16 <= WM * WN * WK * 64;
 }
 template <int BITS>
 static bool rn_fits(int i) {
@@ -1309,8 +1314,9 @@ static int qkv_rope_impl(dj_rec *rec, const uint16_t *X, const dj_weight *w, uin
     a.qn = qn; a.kn = kn; a.rtab = (const float2 *)tab;
     a.heads = heads; a.kv = kv; a.vnorm = vnorm; a.rot = rot; a.eps = eps;
     a.ssin = SS; a.Hn = H; a.neps = neps;
-    if (SS && (M <= 64 || H > 1024)) {  // skinny or wide rows: the normalized rows first (in the workspace), then
-                                        // the plain form
+    // skinny or wide rows (or H / 32 sums not in whole 16-byte loads): the normalized rows first (in the
+    // workspace), then the plain form
+    if (SS && (M <= 64 || H > 1024 || H % 128)) {
       float *ws = nullptr;
       DJ_REQUIRE(dj_gemm_workspace(rec->ctx, ((size_t)M * H + 1) / 2, &ws) == DJ_OK,
                  "decision.js: matmul_qkv_rope_normed: %d x %d rows exceed the workspace", M, H);
@@ -1528,7 +1534,8 @@ extern "C" int dj_matmul_normed(dj_rec *rec, const uint16_t *XW, const dj_weight
   DJ_OP_BEGIN(rec, glu ? "matmul_glu_normed" : "matmul_normed");
   const char *name = "matmul_normed";
   int splits = 1;
-  if (M > 0 && (M <= 64 || H > 1024)) {  // skinny or wide rows: the normalized rows first, then the product
+  // skinny or wide rows (or H / 32 sums not in whole 16-byte loads): the normalized rows first, then the product
+  if (M > 0 && (M <= 64 || H > 1024 || H % 128)) {
     float *ws = nullptr;
     DJ_REQUIRE(dj_gemm_workspace(rec->ctx, ((size_t)M * H + 1) / 2, &ws) == DJ_OK,
                "decision.js: matmul_normed: %d x %d rows exceed the workspace", M, H);

@@ -296,11 +296,12 @@ class DecoderEngine(GpuEngine):
         self.capacity = 0
         self.leaf_capacity = 0
         # the residual + RMSNorm between products folded into them (dj_matmul_residual / dj_matmul_normed) on
-        # forwards of FUSED_ROWS rows and hidden sizes up to 1024 (the products' own row norm; wider rows would
-        # take an extra normalizing kernel). opts fused_norms, else DJ_FUSED_NORMS=0/1, else FUSED_DEFAULT.
+        # forwards of FUSED_ROWS rows and hidden sizes up to 1024 in multiples of 128 (the products' own row norm
+        # and residual tiles; other widths would take an extra normalizing kernel). opts fused_norms, else
+        # DJ_FUSED_NORMS=0/1, else FUSED_DEFAULT.
         env = os.environ.get("DJ_FUSED_NORMS")
         want = self.opts.get("fused_norms", self.FUSED_DEFAULT if env is None else env != "0")
-        self.fused_norms = bool(want) and self.H % 32 == 0 and self.H <= 1024
+        self.fused_norms = bool(want) and self.H % 128 == 0 and self.H <= 1024
 
     # Where the folded norms pay: at 65-8192 rows the products' epilogues cost less than the separate norm
     # kernels they replace (a 3 x 384-id ticket: 2.49 against 2.56 ms); past that the extra epilogue traffic and

@@ -233,7 +233,7 @@ class DecoderEngine extends GpuEngine {
     const fo = this.opts.fusedNorms !== undefined ? this.opts.fusedNorms : this.opts.fused_norms;
     const env = process.env.DJ_FUSED_NORMS;
     const want = fo !== undefined ? !!fo : env !== undefined ? env !== "0" : this.constructor.fusedDefault;
-    this.fusedNorms = want && this.H % 32 === 0 && this.H <= 1024;
+    this.fusedNorms = want && this.H % 128 === 0 && this.H <= 1024;
   }
 
   /** The folded norms' buffers: the norm-weighted residual rows and their per-32-column sums of squares. */

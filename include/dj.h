@@ -232,8 +232,9 @@ int dj_matmul_residual(dj_rec *rec, const uint16_t *X_dev, const dj_weight *w, i
  *   rs[m] = 4 / sqrt(sum_b SS[m, b] / H + eps)
  * before its f16 rounding: RMSNorm(R_new) . W^T with the norm weight applied before the product and 1 / rms
  * after (the same value as ADD_RMSNORM's O . W^T up to where the f16 roundings fall). XW and SS are
- * dj_matmul_residual's outputs with H its N (= this weight's K; H % 32 == 0, H <= 2048; above 1024, or on 64
- * rows or fewer, the rows are normalized by a small kernel into the context workspace first). act < 0: plain (DJ_W_MFMA weight); else the
+ * dj_matmul_residual's outputs with H its N (= this weight's K; H % 32 == 0, H <= 2048; above 1024, off
+ * multiples of 128, or on 64 rows or fewer, the rows are normalized by a small kernel into the context workspace
+ * first). act < 0: plain (DJ_W_MFMA weight); else the
  * gated epilogue of dj_matmul_glu (DJ_W_MFMA_GLU weight) on the scaled gate and up values. */
 int dj_matmul_normed(dj_rec *rec, const uint16_t *XW_dev, const dj_weight *w, uint16_t *Y_dev, int M, int act,
                      const float *SS_dev, int H, float eps);
