@@ -406,7 +406,10 @@ __device__ __forceinline__ float block_sum256(float v, float *red) {
 }
 
 // ---------------------------------------------------------------- answer-row logits (kernels.ts:149-185)
-// normed = f32(X) * inv * f32(w) (kept in f32), dot with (f32(code) - zp) * f32(scale), all in f32.
+// normed = f32(X) * inv * f32(w) (kept in f32), dot with (f32(code) - zp) * f32(scale), all in f32. Workgroup
+// (leaf, g) forms its leaf's normed row in LDS, then wave w scores id 4 g + w: lane l takes 8 consecutive k per
+// 512-wide pass (one 8-byte q8 or 4-byte q4 load), the wave adds the lanes' sums — the ids in parallel, each a
+// single round trip, instead of one id after another behind two barriers.
 template <int BITS>
 __global__ __launch_bounds__(256) void k_leaf_logits(int T, int H, int nIds, float eps, const uint16_t *__restrict__ X,
                                                      const uint32_t *__restrict__ leaves, const uint16_t *__restrict__ W,
@@ -414,7 +417,7 @@ __global__ __launch_bounds__(256) void k_leaf_logits(int T, int H, int nIds, flo
                                                      const uint16_t *__restrict__ scales, float *__restrict__ out) {
   extern __shared__ float normed[];
   __shared__ float red[4];
-  const int leaf = blockIdx.x;
+  const int leaf = blockIdx.x, wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   uint32_t r = leaves[leaf];
   if (r >= (uint32_t)T) r = T - 1;
   const size_t row = (size_t)r * H;
@@ -426,18 +429,29 @@ __global__ __launch_bounds__(256) void k_leaf_logits(int T, int H, int nIds, flo
   const float inv = 1.0f / sqrtf(block_sum256(ss, red) / (float)H + eps);
   for (int k = threadIdx.x; k < H; k += 256) normed[k] = hf(X[row + k]) * inv * hf(W[k]);
   __syncthreads();
+  const int j = blockIdx.y * 4 + wave;
+  if (j >= nIds) return;
+  uint32_t id = ids[(size_t)leaf * nIds + j];
+  if (id >= (uint32_t)V) id = V - 1;
   const float zp = BITS == 8 ? 128.f : 8.f;
-  for (int j = 0; j < nIds; ++j) {
-    uint32_t id = ids[(size_t)leaf * nIds + j];
-    if (id >= (uint32_t)V) id = V - 1;
-    float dot = 0.f;
-    for (int k = threadIdx.x; k < H; k += 256) {
-      const uint32_t c = BITS == 8 ? codes[(size_t)id * H + k] : (codes[(size_t)id * (H / 2) + k / 2] >> ((k & 1) * 4)) & 15u;
-      dot += normed[k] * ((float)c - zp) * hf(scales[(size_t)id * (H / 32) + k / 32]);
+  float dot = 0.f;
+  for (int k0 = lane * 8; k0 < H; k0 += WAVE * 8) {
+    const float sc = hf(scales[(size_t)id * (H / 32) + k0 / 32]);
+    if constexpr (BITS == 8) {
+      const uint2 raw = *(const uint2 *)(codes + (size_t)id * H + k0);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t c = ((q < 4 ? raw.x : raw.y) >> (8 * (q & 3))) & 255u;
+        dot += normed[k0 + q] * ((float)c - zp) * sc;
+      }
+    } else {
+      const uint32_t raw = *(const uint32_t *)(codes + (size_t)id * (H / 2) + k0 / 2);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) dot += normed[k0 + q] * ((float)((raw >> (4 * q)) & 15u) - zp) * sc;
     }
-    dot = block_sum256(dot, red);
-    if (threadIdx.x == 0) out[(size_t)leaf * nIds + j] = dot;
   }
+  dot = wave_sum(dot);
+  if (lane == 0) out[(size_t)leaf * nIds + j] = dot;
 }
 
 extern "C" int dj_leaf_logits(dj_rec *rec, int T, int L, int H, int nIds, float eps, const uint16_t *X, const uint32_t *leaves,
@@ -449,10 +463,10 @@ extern "C" int dj_leaf_logits(dj_rec *rec, int T, int L, int H, int nIds, float 
   if (L > 0 && nIds > 0) {
     const size_t sh = (size_t)H * 4;
     if (e->bits == 8)
-      k_leaf_logits<8><<<L, 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
+      k_leaf_logits<8><<<dim3(L, dj_cdiv(nIds, 4)), 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
                                                          (const uint16_t *)e->scales, out);
     else
-      k_leaf_logits<4><<<L, 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
+      k_leaf_logits<4><<<dim3(L, dj_cdiv(nIds, 4)), 256, sh, rec->ctx->stream>>>(T, H, nIds, eps, X, leaves, W, ids, e->N, e->codes,
                                                          (const uint16_t *)e->scales, out);
   }
   return dj_op_end(rec, "leaf_logits");
