@@ -215,6 +215,26 @@ def test_fused_norms_match_oracle_and_separate_norms(pkg, models):
     assert rel_l2(got[True][0]["debug"][L - 1], got[False][0]["debug"][L - 1]) < 5e-3
     assert np.array_equal(got[True][1], got[False][1])
 
+    # the policy: the folded forms on the forest above (65-8192 rows), the separate norm kernel on the small one
+    eng = DecoderEngine.load(models["q8"])
+    try:
+        assert eng.fused_norms
+        labels = {}
+        for name, tr in (("big", trees), ("small", small)):
+            eng.graphs = False
+            eng.ctx.profile_reset()
+            eng.ctx.profile(True)
+            eng.run(tr)
+            eng.ctx.profile(False)
+            labels[name] = list(eng.ctx.profile_table())
+        big = labels["big"]
+        assert any(k.endswith("+residual") for k in big) and any(k.endswith("+rownorm") for k in big), big
+        # the embedding's and the final norm stay separate kernels
+        assert "add_rmsnorm" in big
+        assert not any(k.endswith(("+residual", "+rownorm")) for k in labels["small"]), labels["small"]
+    finally:
+        eng.destroy()
+
     omodel = ref.Model(models["omni"])
     seqs = _omni_requests(rng, V)
     owant, owdbg = ref.omni_forward(omodel, seqs, acc=np.float64)
