@@ -153,6 +153,39 @@ def test_varlen_batch_equals_single_runs(pkg, models):
         eng.destroy()
 
 
+def test_configs3_sized_batch(pkg, models):
+    """configs[3]'s shape at full size on the reduced model: 192 sequences of U[128, 768] ids packed into one
+    forward (T ~ 86k), which the tile policy gives its large-M tile (128x256 on 8 waves, >= 8 tiles per CU) and
+    the attention its head groups; sampled sequences give the answers they give alone, and the oracle's."""
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models["q8"])
+    eng = DecoderEngine.load(models["q8"])
+    try:
+        rng = np.random.default_rng(41)
+        V = model.c["vocab"]
+        lens = rng.integers(128, 769, 192)
+        trees = [_tree(rng, V, 0, [int(n)]) for n in lens]
+        T = int(lens.sum())
+        assert T > 60000
+        eng.graphs = False
+        eng.ctx.profile_reset()
+        eng.ctx.profile(True)
+        batch = eng.run(trees)["scores"]
+        eng.ctx.profile(False)
+        labels = list(eng.ctx.profile_table())
+        assert any(k.startswith("matmul_glu_q8_128x256w8[") and f"[{T}x" in k for k in labels), labels
+        assert not any(k.endswith(("+residual", "+rownorm")) for k in labels), labels  # past 8192 rows: separate
+        for k in (0, 77, 191):
+            alone = eng.run([trees[k]])["scores"][0]
+            assert max(abs(a - b) for a, b in zip(ref.softmax(alone[0]), ref.softmax(batch[k][0]))) < INVARIANCE_TOL
+        picks = [int(np.argmin(lens)), int(np.argmax(lens)), 5]
+        want, _ = _oracle_forest(model, [trees[k] for k in picks])
+        for k, wt in zip(picks, want):
+            assert max(abs(a - b) for a, b in zip(ref.softmax(batch[k][0]), ref.softmax(wt[0]))) < PROB_TOL
+    finally:
+        eng.destroy()
+
+
 def test_shared_state_equals_forest(pkg, models):
     """Config-5 style: a 1024-token state prefilled once and its K/V reused by 8 questions of 32 tokens gives
     the forest's answers (the model is causal, so both are exact), and the oracle's."""
