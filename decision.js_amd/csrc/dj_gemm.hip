@@ -1053,7 +1053,8 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi, int bits) {
 //   144x64n     when it gives >= 2 tiles per CU (1152-row qkv: 8 x 64 = 512 tiles, two per CU: 15-16 us
 //               against 17-18 for 64x128n),
 //   64x128n     when it gives >= 2 tiles per CU,
-//   K wave set tiles (two wave sets, K / 64 even, K >= 2048; plain products): 80x64k2p8 or 96x64k2p8 where
+//   K wave set tiles (two wave sets, K / 64 even, K >= 2048; plain products, and residual ones from K = 1024,
+//               where the 32x64 tiles cannot hold the epilogue's 32-column sums): 80x64k2p8 or 96x64k2p8 where
 //               their tiles make one round at one workgroup per CU (0.75-1 per CU: the 8-stage paired ring keeps three pairs
 //               of weight blocks in flight, which is what products on weights cold in HBM wait for), else the one of
 //               48x64k2 / 64x64k2 / 80x64k2 / 96x64k2 (4 stages) whose grid is nearest 1.5 per CU, where that is
@@ -1091,6 +1092,18 @@ static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floa
   const bool ksets_off = kss && atoi(kss) == 0;
   const char *kst = getenv("DJ_GEMM_KSET_TILE");
   const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
+  // A K wave set tile on the 8-stage ring that makes one round (0.75-1 tiles per CU) takes long-K products up to
+  // K = 8192 ahead of the split (the omni trunk's 1152 x 1024 x 4608 w2: 25-27 against 29.8 us alone, its ticket
+  // 1.933 -> 1.898 ms; fewer rows, e.g. the 0.8B prefill's 1024 x 1536 x 4608 at 312 tiles, keep the split,
+  // which measured faster in its forward). DJ_GEMM_LONGK_KSET=0 keeps the split everywhere.
+  const char *lkk = getenv("DJ_GEMM_LONGK_KSET");
+  bool longk_kset = !(lkk && atoi(lkk) == 0) && K <= 8192 && !ksets_off;
+  if (longk_kset) {
+    bool round = false;
+    for (int i : {56, 57})
+      round = round || (cfg_fits(kCfgs[i], N, K, epi, bits) && tiles(i) >= 0.75 * cus && tiles(i) <= cus);
+    longk_kset = round;
+  }
   const int longk = lks ? atoi(lks) : 4;
   int rule_splits = 0;
   if (cfg < 0) {
@@ -1101,7 +1114,7 @@ static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floa
         {8, 2.0, 0, 1e9, 0}, {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules) {
       if (r.cfg == -2) {  // the K wave set family (see above)
-        if ((epi & 3) == 1 || (epi & 3) == 2 || ksets_off || K < 2048) continue;
+        if ((epi & 3) == 1 || (epi & 3) == 2 || ksets_off || K < (epi == 3 ? 1024 : 2048)) continue;
         int best = -1;
         for (int i : {56, 57})  // one round of one-workgroup-per-CU tiles on the 8-stage ring, most tiles first
           if (best < 0 && cfg_fits(kCfgs[i], N, K, epi, bits) && tiles(i) >= 0.75 * cus && tiles(i) <= cus) best = i;
@@ -1123,6 +1136,8 @@ static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floa
       }
       if (cfg_fits(kCfgs[r.cfg], N, K, epi, bits) && K >= r.min_k && tiles(r.cfg) >= r.per_cu * cus &&
           tiles(r.cfg) <= r.max_per_cu * cus) {
+        // a residual epilogue in the split's summing kernel costs more than the K wave set tiles save: never split
+        if (r.ks < 0 && (epi == 3 || longk_kset)) continue;
         if (r.ks < 0) {  // a long-K rule: the split where it divides K and fits the workspace; else what the rules
                          // chose before it (the paired ring at 0.5-1 per CU, otherwise the rules below)
           if (longk > 1 && ws_ok && (epi & 3) != 2 && (K / 64) % longk == 0 && (size_t)longk * M * N <= ws_floats) {

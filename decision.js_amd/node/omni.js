@@ -149,7 +149,4 @@ class OmniEngine extends DecoderEngine {
   }
 }
 
-// the omni trunk's products take slower tiles with the folded norms' epilogues: its norms stay separate by default
-OmniEngine.fusedDefault = false;
-
 module.exports = { OmniEngine, packOmni, temperature, QTYPES };

@@ -95,9 +95,6 @@ class OmniEngine(DecoderEngine):
         self.capacity, self.marker_capacity = cap, mcap
 
     INPUTS = ("ids", "pos", "qtype", "rng", "taps", "markers")
-    # the omni trunk's products (9216-wide gated, 4608-deep split-K, 1024-wide 32x64) take slower tiles with the
-    # folded norms' epilogues: 2.06 against 1.95 ms a 3-question ticket, so its norms stay separate by default
-    FUSED_DEFAULT = False
 
     def logits(self, seqs, debug=False):
         """Raw marker logits per sequence ([seq][marker], before the temperature), and with `debug` the trunk's
