@@ -227,7 +227,8 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
   static_assert(WK == 1 || (WK == 2 && S::PAIRED), "K wave sets take a paired ring's steps");
   constexpr int BASE = EPI & 3;
   constexpr bool GLU = BASE == 1, ROPE = BASE == 2, RES = EPI == 3, RN = (EPI & 4) != 0;
-  static_assert(!RN || WK == 1, "the row norm's scales are shared through a workgroup barrier: every wave live");
+  static_assert(!RN || WK == 1 || !ROPE, "the row norm's scales are shared through a workgroup barrier: every wave "
+                                         "live (K wave sets share the epilogue, except on RoPE tiles)");
   static_assert(!RES || FN % 2 == 0, "the residual epilogue sums 32-column blocks (fragment pairs)");
   constexpr int NW = S::NW, BM = S::BM, NB = S::NB, CB = S::CB, NS = S::NS;
   constexpr int A_BYTES = S::A_BYTES, B_BYTES = S::B_BYTES, STAGE = S::STAGE;
@@ -997,7 +998,7 @@ static void launch_cfg(hipStream_t s, GemmArgs a) {
   if constexpr (((BASE == 1 || EPI == 3) && FN % 2 != 0) ||
                 (BASE == 2 && (WN * FN * 16 != 128 || WM * FM * 16 > 144 || WK > 1)) ||
                 (WK > 1 && !GemmShape<BITS, WM, WN, FM, FN, RING, WK>::PAIRED) || (EPI >= 3 && !FZ) ||
-                ((EPI & 4) && (WK > 1 || !rn_fits_cfg<BITS, WM, WN, FM, FN, RING, WK>()))) {
+                ((EPI & 4) && !rn_fits_cfg<BITS, WM, WN, FM, FN, RING, WK>())) {
     return;  // never picked (cfg_fits): a gated tile and the residual epilogue need fragment pairs, a RoPE tile
              // is one 128-wide head of at most 144 rows (its epilogue holds every row pass in registers) on one
              // set of waves, K wave sets need their paired ring, the folded-norm forms exist for fused_cfg tiles
@@ -1031,9 +1032,9 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi, int bits) {
   const int base = epi & 3;
   return ksets_fit(c, bits) && N % c.bn() == 0 && ((base != 1 && epi != 3) || c.fn % 2 == 0) &&
          (base != 2 || (c.bn() == 128 && c.bm() <= 144 && c.wk == 1)) && (epi < 3 || fused_cfg((int)(&c - kCfgs))) &&
-         (!(epi & 4) || (c.wk == 1 && (bits == 8    ? rn_fits<8>((int)(&c - kCfgs))
-                                       : bits == 4 ? rn_fits<4>((int)(&c - kCfgs))
-                                                   : rn_fits<16>((int)(&c - kCfgs))))) &&
+         (!(epi & 4) || (bits == 8    ? rn_fits<8>((int)(&c - kCfgs))
+                         : bits == 4 ? rn_fits<4>((int)(&c - kCfgs))
+                                     : rn_fits<16>((int)(&c - kCfgs)))) &&
          (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time (the 2-stage
                                                // fallback of a paired tile takes any count; the check keeps
                                                // the rule simple)
@@ -1091,6 +1092,8 @@ static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floa
   const char *kss = getenv("DJ_GEMM_KSETS");  // DJ_GEMM_KSETS=0: no K wave set tiles (A/B sweeps)
   const bool ksets_off = kss && atoi(kss) == 0;
   const char *kst = getenv("DJ_GEMM_KSET_TILE");
+  const char *kmk = getenv("DJ_GEMM_KSET_MINK");  // the plain products' least K for the K wave set tiles
+  const int kset_mink = kmk ? atoi(kmk) : 2048;
   const char *lks = getenv("DJ_GEMM_LONGK_SPLIT");
   // A K wave set tile on the 8-stage ring that makes one round (0.75-1 tiles per CU) takes long-K products up to
   // K = 8192 ahead of the split (the omni trunk's 1152 x 1024 x 4608 w2: 25-27 against 29.8 us alone, its ticket
@@ -1114,7 +1117,7 @@ static void pick(int M, int N, int K, int epi, int bits, int cus, size_t ws_floa
         {8, 2.0, 0, 1e9, 0}, {16, 2.0, 0, 1e9, 0}};
     for (const auto &r : rules) {
       if (r.cfg == -2) {  // the K wave set family (see above)
-        if ((epi & 3) == 1 || (epi & 3) == 2 || ksets_off || K < (epi == 3 ? 1024 : 2048)) continue;
+        if ((epi & 3) == 1 || (epi & 3) == 2 || ksets_off || K < (epi == 3 ? 1024 : kset_mink)) continue;
         int best = -1;
         for (int i : {56, 57})  // one round of one-workgroup-per-CU tiles on the 8-stage ring, most tiles first
           if (best < 0 && cfg_fits(kCfgs[i], N, K, epi, bits) && tiles(i) >= 0.75 * cus && tiles(i) <= cus) best = i;

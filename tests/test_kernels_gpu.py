@@ -384,6 +384,41 @@ def test_matmul_residual_and_normed(pkg, ctx, M, H, K2, bits):
     assert f16_close(zb, za, ulps=16.0, atol=4e-3) <= 1.0  # the q/k norm rescales the two roundings apart
 
 
+@pytest.mark.parametrize("tile", ["80x64k2p8", "96x64k2p8", "48x64k2", "80x64k2"])
+def test_matmul_normed_on_k_wave_sets(pkg, ctx, monkeypatch, tile):
+    """The row norm on K wave set tiles (both sets share the epilogue, so the row scales' barrier sees every
+    wave): dj_matmul_normed forced onto each such tile, and dj_matmul_residual on the same tile, against the
+    oracle's ADD_RMSNORM then product, at the bounds of the untiled-K form."""
+    dj = _dj()
+    M, H, K2, N2, bits, eps = 1152, 1024, 2048, 1024, 8, 1e-6
+    rng = np.random.default_rng(77)
+    cX, sX = quant(rng, H, K2, bits)
+    W1 = ctx.weight_q(cX, sX, H, K2, bits, dj.W_MFMA)
+    X, R = rand_f16(rng, (M, K2)), rand_f16(rng, (M, H), std=0.5)
+    nw = (1 + rng.standard_normal(H) * 0.1).astype(np.float16)
+    dX, dR, dnw = ctx.array(X), ctx.array(R), ctx.array(nw)
+    dXW, dSS = ctx.alloc(M * H * 2), ctx.alloc(M * (H // 32) * 4)
+    c2, s2 = quant(rng, N2, H, bits)
+    W2, dY = ctx.weight_q(c2, s2, N2, H, bits, dj.W_MFMA), ctx.alloc(M * N2 * 2)
+    monkeypatch.setenv("DJ_GEMM_TILE", tile)
+    ctx.profile_reset()
+    ctx.profile(True)
+    try:
+        run(ctx, lambda r: (r.matmul_residual(dX, W1, M, dR, dnw, dXW, dSS),
+                            r.matmul_normed(dXW, W2, dY, M, -1, dSS, H, eps)))
+    finally:
+        ctx.profile(False)
+    labels = [k for k in ctx.profile_table() if k.startswith("matmul")]
+    assert labels and all(f"_{tile}[" in k for k in labels), labels
+    Rn, SS = dR.read(np.float16, (M, H)), dSS.read(np.float32, (M, H // 32))
+    v = R.astype(np.float64) + ref.matmul(X, ref.dequant_f16(cX, sX, bits), np.float64).astype(np.float64)
+    assert np.abs(Rn.astype(np.float64) - v).max() <= 2 * np.spacing(np.abs(v).astype(np.float16)).max()
+    inv = 1.0 / np.sqrt(SS.astype(np.float64).sum(-1, keepdims=True) / H + eps)
+    normed = (Rn.astype(np.float64) * inv * nw.astype(np.float64)).astype(np.float16)
+    want = ref.matmul(normed, ref.dequant_f16(c2, s2, bits), np.float64)
+    assert f16_close(dY.read(np.float16, (M, N2)), want, ulps=4.0, atol=3e-3) <= 1.0
+
+
 @pytest.mark.parametrize("waves", [1, 5, 8, 9, 16])
 @pytest.mark.parametrize("M,N,K,bits,glu", [(1, 2048, 832, 8, False), (32, 1536, 4608, 8, False),
                                             (64, 512, 1024, 4, False), (17, 1024, 1536, 8, True),
