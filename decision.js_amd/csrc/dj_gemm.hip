@@ -387,37 +387,55 @@ __attribute__((amdgpu_waves_per_eu(1, GemmShape<BITS, WM, WN, FM, FN, RING, WK>:
 
   if constexpr (S::PAIRED && WK > 1) {
     // Paired ring with two K wave sets: the pair's waits, barrier and DMAs as below; set wk then reads and
-    // multiplies step 2 kp + wk only.
+    // multiplies step 2 kp + wk only (an odd count's last step: set 0).
     constexpr int NP = NS / 2;
     const int KP = KS / 2;
     for (int kp = 0; kp < KP; ++kp) {
-      wait_steps_barrier<2 * S::I, NP - 2>(min(NP - 2, KP - 1 - kp));
+      wait_steps_barrier<S::I, NS - 4>(min(NS - 4, KS - 2 * kp - 2));
       const int nx = kp + NP - 1;
-      if (nx < KP) { issue(2 * nx, (2 * nx) % NS); issue(2 * nx + 1, (2 * nx + 1) % NS); }
+      if (2 * nx < KS) issue(2 * nx, (2 * nx) % NS);
+      if (2 * nx + 1 < KS) issue(2 * nx + 1, (2 * nx + 1) % NS);
       h8 a0[FM][2];
       RawB<BITS> r0[FN];
       uint32_t p0[FN];
       DJ_READ(2 * kp + wk, a0, r0, p0);
       DJ_MMA(a0, r0, p0);
     }
+    if (KS & 1) {  // the last step alone: every DMA has been issued; all of them land, then the barrier
+      wait_vm_barrier<0>();
+      if (wk == 0) {
+        h8 a0[FM][2];
+        RawB<BITS> r0[FN];
+        uint32_t p0[FN];
+        DJ_READ(KS - 1, a0, r0, p0);
+        DJ_MMA(a0, r0, p0);
+      }
+    }
   } else if constexpr (S::PAIRED) {
-    // Paired ring (NP = NS / 2 pairs of stages; KS even): steps land two at a time, so the counter wait and the
-    // workgroup barrier come once per 128 K. At pair p: pairs p+1 .. p+NP-2 may still be in flight; after the
-    // barrier every wave is done with pair p-1, whose stages take pair p+NP-1. Both steps' fragments are read
-    // before the first MFMA.
+    // Paired ring (NP = NS / 2 pairs of stages): steps land two at a time, so the counter wait and the
+    // workgroup barrier come once per 128 K. At pair p: steps 2p + 2 .. 2p + NS - 3 may still be in flight; after
+    // the barrier every wave is done with pair p-1, whose stages take pair p+NP-1. Both steps' fragments are read
+    // before the first MFMA. An odd step count issues its last step alone, and computes it after the pairs.
     constexpr int NP = NS / 2;
     const int KP = KS / 2;
     h8 a0[FM][2], a1[FM][2];
     RawB<BITS> r0[FN], r1[FN];
     uint32_t p0[FN], p1[FN];
     for (int kp = 0; kp < KP; ++kp) {
-      wait_steps_barrier<2 * S::I, NP - 2>(min(NP - 2, KP - 1 - kp));
+      // steps issued so far: min(KS, NS - 2 + 2 kp); steps 0 .. 2 kp + 1 must have landed
+      wait_steps_barrier<S::I, NS - 4>(min(NS - 4, KS - 2 * kp - 2));
       const int nx = kp + NP - 1;
-      if (nx < KP) { issue(2 * nx, (2 * nx) % NS); issue(2 * nx + 1, (2 * nx + 1) % NS); }
+      if (2 * nx < KS) issue(2 * nx, (2 * nx) % NS);
+      if (2 * nx + 1 < KS) issue(2 * nx + 1, (2 * nx + 1) % NS);
       DJ_READ(2 * kp, a0, r0, p0);
       DJ_READ(2 * kp + 1, a1, r1, p1);
       DJ_MMA(a0, r0, p0);
       DJ_MMA(a1, r1, p1);
+    }
+    if (KS & 1) {  // the last step alone
+      wait_vm_barrier<0>();
+      DJ_READ(KS - 1, a0, r0, p0);
+      DJ_MMA(a0, r0, p0);
     }
   } else if constexpr (NS == 2) {
     // two stages: read a step's fragments right after its barrier, then compute it
@@ -1035,9 +1053,8 @@ static bool cfg_fits(const GemmCfg &c, int N, int K, int epi, int bits) {
          (!(epi & 4) || (bits == 8    ? rn_fits<8>((int)(&c - kCfgs))
                          : bits == 4 ? rn_fits<4>((int)(&c - kCfgs))
                                      : rn_fits<16>((int)(&c - kCfgs)))) &&
-         (c.ring >= 0 || (K / 64) % 2 == 0);  // a paired ring takes 64-K steps two at a time (the 2-stage
-                                               // fallback of a paired tile takes any count; the check keeps
-                                               // the rule simple)
+         (c.ring >= 0 || K / 64 >= 2);  // a paired ring takes 64-K steps two at a time (an odd count's last
+                                         // step alone)
 }
 
 // Picks (tile, splits). DJ_GEMM_TILE=<tag> and DJ_GEMM_SPLITK=<n> force them (tuning sweeps). Otherwise, from

@@ -187,11 +187,14 @@ def test_matmul_glu(pkg, ctx, M, I, K, bits, act, direct):
 
 
 @pytest.mark.parametrize("tile,K,glu", [("32x64p4", 128, False), ("32x64p4", 64, False), ("32x64p4", 1088, False),
-                                         ("128x256w8p4", 128, True), ("128x256w8p4", 1088, True),
-                                         ("128x128np4", 256, False)])
+                                         ("32x64p4", 192, False), ("128x256w8p4", 128, True), ("128x256w8p4", 1088, True),
+                                         ("128x128np4", 256, False), ("128x128np4", 320, False),
+                                         ("80x64k2p8", 1088, False), ("48x64k2", 2624, False), ("96x64k2", 192, True)])
 def test_matmul_paired_ring_edges(pkg, ctx, monkeypatch, tile, K, glu):
-    """Paired-ring tiles take 64-K steps two at a time: one pair only (K = 128), and step counts that are odd
-    (K = 64, 1088), where the forced tile does not apply and the policy picks another; all match the oracle."""
+    """Paired-ring tiles take 64-K steps two at a time: one pair only (K = 128), and odd step counts (3, 5, 17,
+    41), whose last step is issued alone and computed after the pairs (on K wave set tiles by the first set),
+    including a count whose last step is issued in the prologue (K = 192); a single step (K = 64) is below the
+    paired tiles and the policy picks another. All match the oracle; the forced tile is the one that ran."""
     dj = _dj()
     monkeypatch.setenv("DJ_GEMM_TILE", tile)
     rng = np.random.default_rng(K)
@@ -201,14 +204,23 @@ def test_matmul_paired_ring_edges(pkg, ctx, monkeypatch, tile, K, glu):
     W = ctx.weight_q(codes, scales, N, K, 8, dj.W_MFMA_GLU if glu else dj.W_MFMA)
     X = rand_f16(rng, (M, K))
     dX, dY = ctx.array(X), ctx.alloc(M * N * 2)
+    ctx.profile_reset()
+    ctx.profile(True)
+    try:
+        if glu:
+            run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
+        else:
+            run(ctx, lambda r: r.matmul(dX, W, dY, M))
+    finally:
+        ctx.profile(False)
+    labels = [name for name in ctx.profile_table() if name.startswith("matmul")]
+    assert (K >= 128) == all(f"_{tile}[" in name for name in labels), labels
     if glu:
-        run(ctx, lambda r: r.matmul_glu(dX, W, dY, M, 0))
         ab = ref.matmul(X, W16, np.float64)
         want = ref.silu_mul(ab[:, :N // 2], ab[:, N // 2:], np.float64)
         got = dY.read(np.float16, (M, N // 2))
         assert np.abs(got.astype(np.float64) - want.astype(np.float64)).max() < 2e-2
     else:
-        run(ctx, lambda r: r.matmul(dX, W, dY, M))
         want = ref.matmul(X, W16, np.float64)
         assert f16_close(dY.read(np.float16, (M, N)), want, ulps=1.0, atol=2e-5) <= 1.0
 
@@ -294,12 +306,12 @@ def test_matmul_k_wave_sets(pkg, ctx, monkeypatch, tile, bits, glu, K):
 
 @pytest.mark.parametrize("M,N,K,want", [(1152, 1024, 2048, "80x64k2p8"), (1152, 1024, 3072, "80x64k2p8"),
                                          (1536, 2048, 2048, "96x64k2"), (2304, 1024, 2048, "96x64k2"),
-                                         (1536, 1024, 2048, "96x64k2p8"), (1152, 1024, 2624, "32x64"),
+                                         (1536, 1024, 2048, "96x64k2p8"), (1152, 1024, 2624, "80x64k2p8"),
                                          (1152, 2048, 1024, "32x64p4")])
 def test_matmul_policy_k_wave_sets(pkg, ctx, M, N, K, want):
     """The tile policy's K wave set rule (256 CUs, K >= 2048): one round of the 8-stage tiles where that fills
-    0.75-1 per CU (the ticket's o_proj / w2), else the 4-stage tile whose grid is nearest 1.5 per CU; an odd
-    64-K step count (Laya's 2624) keeps the unpaired 32x64, and K = 1024 the paired 32x64p4."""
+    0.75-1 per CU (the ticket's o_proj / w2), else the 4-stage tile whose grid is nearest 1.5 per CU, an odd
+    64-K step count (Laya's 2624) included; K = 1024 keeps the paired 32x64p4."""
     dj = _dj()
     cus = ctx.info()["compute_units"]
     if cus != 256:
