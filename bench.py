@@ -663,7 +663,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported (the path shards by "
-              f"independent tickets: see DESIGN.md)", file=sys.stderr)
+              f"independent tickets: each GPU runs its own engine on its own share of them)", file=sys.stderr)
         sys.exit(2)
 
     # the reference's CPU path is probed before anything touches the GPU (child processes only)

@@ -410,7 +410,7 @@ def test_injected_fault_surfaces_and_next_call_succeeds(pkg, models, monkeypatch
     state's forwards fold their norms into the products, matmul_residual / matmul_glu_normed) surfaces as the
     library's "decision.js: ..." error, the failed recording is aborted (dj_rec_abort), and the
     next call on the same Decision succeeds with the answers a clean run gives (the reference's finish() error
-    path, gpu.ts:255-260; SURVEY's injected-error check). Also through the shared-state path."""
+    path, gpu.ts:255-260). Also through the shared-state path."""
     from decision_js_amd import _dj
     from decision_js_amd.d1 import Decision
     rng = np.random.default_rng(9)
