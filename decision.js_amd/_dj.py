@@ -78,6 +78,7 @@ SIGNATURES = {
     "dj_matmul_qkv_rope_normed": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P, _I, _F, _F, _I, _I, _P, _P, _I, _F],
     "dj_attention": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
     "dj_attention_noalloc": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P],
+    "dj_attention_qk_rope": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P, _P, _F, _P, _I, _P],
     "dj_attention_gated": [_P, _I, _I, _I, _I, _P, _I, KVSrc, KVSrc, _P, _F, _P, _I, _P],
     "dj_gdn": [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _P, _F, _P],
     "dj_ple_mix": [_P, _I, _I, _P, _P, _P, _F, _P],
@@ -324,6 +325,11 @@ class Recorder:
 
     def attention(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, O):
         check(lib().dj_attention(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(O)))
+
+    def attention_qk_rope(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, qn, kn, eps, tab, O,
+                          rot=None):
+        check(lib().dj_attention_qk_rope(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(qn),
+                                         ptr(kn), eps, ptr(tab), D if rot is None else rot, ptr(O)))
 
     def attention_gated(self, T, heads, kv, D, Q, q_stride, A: KVSrc, B: KVSrc, rng, scale, G, g_stride, O):
         check(lib().dj_attention_gated(self.h, T, heads, kv, D, ptr(Q), q_stride, A, B, ptr(rng), scale, ptr(G),

@@ -82,11 +82,47 @@ __device__ __forceinline__ int wave_reduce(int v) {
   return minmax<MAX>((int)b[0], (int)b[1]);
 }
 
-template <int D, int RING, int KG, int HG>
+// The sum of squares of one row for QK_NORM_ROPE, from the lanes holding its 8-lane layout's lanes g and g + 4
+// (lo = that layout's v_g, hi = v_{g+4}; the partners holding v_{3-g}, v_{7-g} at lane ^ X3 and the next pair
+// at lane ^ X1), added in that layout's order ((v0 + v7) + (v2 + v5)) + ((v1 + v6) + (v3 + v4)), so the row's
+// 1 / rms has the bits the standalone kernel computes.
+template <int X3, int X1>
+__device__ __forceinline__ float qkn_row_sum(float lo, float hi, int g) {
+  const float plo = __shfl_xor(lo, X3, 64), phi = __shfl_xor(hi, X3, 64);  // v_{3-g}, v_{7-g}
+  const float a = lo + phi, b = hi + plo;                                    // u_g, u_{3-g} (u_i = v_i + v_{7-i})
+  const float pa = __shfl_xor(a, X1, 64), pb = __shfl_xor(b, X1, 64);        // u_{g^1}, u_{3-(g^1)}
+  const float w02 = (g & 1) ? pa + b : a + pb, w13 = (g & 1) ? a + pb : pa + b;
+  return w02 + w13;
+}
+
+// Normalizes and rotates the two rotation-pair sets one lane holds of a 128-dim row: x0 / y0 = dims 8g..+7 and
+// 64 + 8g..+7, x1 / y1 = dims 32 + 8g..+7 and 96 + 8g..+7 (QKN's layout; lanes X3 / X1 apart as above).
+template <int X3, int X1>
+__device__ __forceinline__ void qkn_row(h8 &x0, h8 &y0, h8 &x1, h8 &y1, int g, const uint16_t *nw, const float2 *cs,
+                                        float eps) {
+  const bool w = nw != nullptr;
+  h8 w0 = {}, w1 = {}, w2 = {}, w3 = {};
+  if (w) {
+    w0 = *(const h8 *)(nw + 8 * g);
+    w1 = *(const h8 *)(nw + 32 + 8 * g);
+    w2 = *(const h8 *)(nw + 64 + 8 * g);
+    w3 = *(const h8 *)(nw + 96 + 8 * g);
+  }
+  const float inv = norm_inv(qkn_row_sum<X3, X1>(pair_sumsq(x0, y0), pair_sumsq(x1, y1), g), w, 128, eps);
+  const h8x2 lo = norm_rope_pairs(x0, y0, w0, w2, w, true, inv, [&](int i) { return cs[8 * g + i]; });
+  const h8x2 hi = norm_rope_pairs(x1, y1, w1, w3, w, true, inv, [&](int i) { return cs[32 + 8 * g + i]; });
+  x0 = lo.x;
+  y0 = lo.y;
+  x1 = hi.x;
+  y1 = hi.y;
+}
+
+template <int D, int RING, int KG, int HG, bool QKN = false>
 __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv, const uint16_t *__restrict__ Q, int q_stride,
                                               dj_kv_src A, dj_kv_src B, const int4 *__restrict__ rng, float scale,
                                               uint16_t *__restrict__ O, dj_attn_gate gate, int splits,
-                                              float *__restrict__ part) {
+                                              float *__restrict__ part, dj_attn_qkn qkn) {
+  static_assert(!QKN || (D == 128 && KG == 1 && HG == 1), "q/k norm folded in: 128-dim heads, one head of 4 waves");
   using S = AttnShape<D, RING, KG, HG>;
   constexpr int KW = 64 / KG;          // keys of each tile this wave scores (KG key groups split a tile)
   constexpr int NB = KW / 16;          // 16-key blocks of S^T per wave and tile
@@ -116,6 +152,9 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
   h8 qf[NS_];
 #pragma unroll
   for (int s = 0; s < NS_; ++s) qf[s] = *(const h8 *)(Q + (size_t)qc * q_stride + (size_t)h * D + s * 32 + g * 8);
+  // raw query rows (QKN): lane (c16, g) holds chunks g, 4 + g, 8 + g, 12 + g of its query, i.e. the rotation
+  // pairs of QK_NORM_ROPE's 8-lane layout's lanes g and g + 4; the query's four lanes are 16 apart
+  if constexpr (QKN) qkn_row<48, 16>(qf[0], qf[2], qf[1], qf[3], g, qkn.qn, qkn.tab + (size_t)qc * 64, qkn.eps);
 
   // The block's key span per source: lane l reads query q0 + l's ranges, the wave reduces them (every wave
   // does the same, so no LDS and no barrier before the first K/V loads).
@@ -219,13 +258,31 @@ __global__ __launch_bounds__(256 * KG * HG) void k_attn(int T, int heads, int kv
     // tile jj landed for this wave once at most the NS-2 later tiles' DMAs remain; after the barrier for every
     // wave, and every wave is done with tile jj-1's stage, which is refilled next
     wait_vm_barrier<(NS - 2) * S::I>();
-    issue(j0 + min(jj + NS - 1, nloc - 1), (jj + NS - 1) % NS);
+    if constexpr (!QKN) issue(j0 + min(jj + NS - 1, nloc - 1), (jj + NS - 1) % NS);
     const int j = j0 + jj;
-
     const uint8_t *st = smem + (jj % NS) * STAGE;
     const u32x4 *Ks = (const u32x4 *)st;
     const bool sb = j >= ntA;
     const int k0 = sb ? loB + (j - ntA) * 64 : loA + j * 64, hi = sb ? hiB : hiA;
+    if constexpr (QKN) {
+      if (sb) {
+        // source B's raw key rows, normalized and rotated in LDS before any wave reads them: 4 lanes a row,
+        // lane sub taking chunks sub, 4 + sub, 8 + sub, 12 + sub (the query fragments' layout, lanes 1 apart).
+        // Before the next tile's DMA is issued, so the waits for the weights and angles count no DMA.
+        const int kr = tid >> 2, sub = tid & 3;
+        uint8_t *row = smem + (jj % NS) * STAGE + kr * (2 * D);
+        h8 *c0 = (h8 *)(row + ((sub ^ (kr & KSW)) * 16)), *c1 = (h8 *)(row + (((4 + sub) ^ (kr & KSW)) * 16));
+        h8 *c2 = (h8 *)(row + (((8 + sub) ^ (kr & KSW)) * 16)), *c3 = (h8 *)(row + (((12 + sub) ^ (kr & KSW)) * 16));
+        h8 x0 = *c0, x1 = *c1, y0 = *c2, y1 = *c3;
+        qkn_row<3, 1>(x0, y0, x1, y1, sub, qkn.kn, qkn.tab + (size_t)min(k0 + kr, hi - 1) * 64, qkn.eps);
+        *c0 = x0;
+        *c1 = x1;
+        *c2 = y0;
+        *c3 = y1;
+        __syncthreads();
+      }
+      issue(j0 + min(jj + NS - 1, nloc - 1), (jj + NS - 1) % NS);
+    }
     const int qlo = sb ? rq.z : rq.x, qhi = sb ? rq.w : rq.y;
     const int kb0 = k0 + KW * kg;  // this wave's keys of the tile: [kb0, kb0 + KW)
     if (kb0 < whi[sb] && kb0 + KW > wlo[sb]) {
@@ -543,14 +600,14 @@ __global__ __launch_bounds__(256) void k_attn_wide(int T, int heads, int kv, con
 
 // Launch with one workgroup shape; a shape whose K/V tile does not split into whole 1 KB DMAs per wave is never
 // picked, nor one that would spill registers (the launcher falls back to HG 1 for them).
-template <int D, int RING, int KG, int HG>
+template <int D, int RING, int KG, int HG, bool QKN = false>
 static void attn_launch(dim3 g3, hipStream_t s, int T, int heads, int kv, const uint16_t *Q, int q_stride,
                         dj_kv_src A, dj_kv_src B, const int4 *r4, float scale, uint16_t *O, dj_attn_gate gate, int splits,
-                        float *part) {
+                        float *part, dj_attn_qkn qkn = dj_attn_qkn{}) {
   if constexpr ((64 * 2 * D) % (1024 * 4 * KG * HG) == 0 && D * HG <= 256 &&  // (D 128 x HG 4 would spill)
                 RING * 2 * (64 * 2 * D) <= 160 * 1024)
-    k_attn<D, RING, KG, HG><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits,
-                                                         part);
+    k_attn<D, RING, KG, HG, QKN><<<g3, 256 * KG * HG, 0, s>>>(T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate,
+                                                              splits, part, qkn);
 }
 
 // The split-KV plan of a launch: small grids (a short question against a long state: one query block per head)
@@ -573,8 +630,9 @@ static int attn_splits(int cus, int T, int heads, int D, const dj_kv_src &A, con
 
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
-                        dj_attn_gate gate) {
+                        dj_attn_gate gate, const dj_attn_qkn *qkn) {
   hipStream_t s = c->stream;
+  if (qkn && D != 128) return dj_fail(DJ_EINVAL, "decision.js: attention with q/k norm folded in: head dim %d (128)", D);
   if (D == WD) {  // 512-dim heads: the VALU form, whole
     k_attn_wide<<<dim3(dj_cdiv(T, WQ), heads), 256, 0, s>>>(T, heads, kv, Q, q_stride, A, B, (const int4 *)rng, scale, O,
                                                             gate);
@@ -615,12 +673,16 @@ int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16
     else if (ring == 4) attn_launch<DD, 4, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part); \
     else attn_launch<DD, 2, 1, 1>(g3, s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate, splits, part);                \
     break;
-  switch (D) {
-    DJ_ATTN_CASE(64)
-    DJ_ATTN_CASE(128)
-    DJ_ATTN_CASE(256)
-    default: return dj_fail(DJ_EINVAL, "decision.js: attention head dim %d (64, 128 or 256)", D);
-  }
+  if (qkn)  // q/k norm folded in: the 4-wave, 2-stage form (the form a short question's split launch takes)
+    attn_launch<128, 2, 1, 1, true>(dim3(qblocks, heads, splits), s, T, heads, kv, Q, q_stride, A, B, r4, scale, O, gate,
+                                    splits, part, *qkn);
+  else
+    switch (D) {
+      DJ_ATTN_CASE(64)
+      DJ_ATTN_CASE(128)
+      DJ_ATTN_CASE(256)
+      default: return dj_fail(DJ_EINVAL, "decision.js: attention head dim %d (64, 128 or 256)", D);
+    }
 #undef DJ_ATTN_CASE
   if (splits > 1) {
     const unsigned blocks = (unsigned)dj_cdiv((long)T * heads, 4);
@@ -674,6 +736,28 @@ extern "C" int dj_attention_gated(dj_rec *rec, int T, int heads, int kv, int D, 
   char shape[48];
   snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
   return dj_op_end(rec, "attention_gated", shape);
+}
+
+extern "C" int dj_attention_qk_rope(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride,
+                                    dj_kv_src A, dj_kv_src B, const int32_t *rng, float scale, const uint16_t *qn,
+                                    const uint16_t *kn, float eps, const float *tab, int rot, uint16_t *O) {
+  DJ_REQUIRE(Q && rng && O && tab && T >= 0 && heads > 0 && kv > 0 && heads % kv == 0 && q_stride % 8 == 0 &&
+                 q_stride >= heads * D,
+             "decision.js: attention_qk_rope: bad arguments (heads %d, kv %d, q_stride %d)", heads, kv, q_stride);
+  DJ_REQUIRE(D == 128 && rot == 128, "decision.js: attention_qk_rope: head dim %d, rot %d (128 and 128)", D, rot);
+  DJ_REQUIRE(scale > 0.f, "decision.js: attention: the score scale must be positive (got %g)", (double)scale);
+  DJ_REQUIRE(src_ok(A, kv, D) && src_ok(B, kv, D) && B.rows == T,
+             "decision.js: attention_qk_rope: bad key/value source (source B must be the %d query rows)", T);
+  DJ_OP_BEGIN(rec, "attention_qk_rope");
+  if (T > 0) {
+    const dj_attn_qkn q{qn, kn, (const float2 *)tab, eps};
+    int st = dj_launch_attention(rec->ctx, T, heads, kv, D, Q, q_stride, A, B, rng, scale, O, rec->ctx->gemm_ws,
+                                 rec->ctx->gemm_ws_floats, dj_attn_gate{nullptr, 0}, &q);
+    if (st) return st;
+  }
+  char shape[48];
+  snprintf(shape, sizeof shape, "[T%d h%d kv%d D%d]", T, heads, kv, D);
+  return dj_op_end(rec, "attention_qk_rope", shape);
 }
 
 // ---------------------------------------------------------------- the entry point that allocates nothing

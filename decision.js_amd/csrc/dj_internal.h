@@ -143,9 +143,17 @@ struct dj_attn_gate {
   const uint16_t *g;
   int stride;
 };
+// q/k RMSNorm + RoPE folded into attention (D = rot = 128): the query rows and source B's key rows are read raw
+// and normalized as QK_NORM_ROPE does (qn / kn: the norm weights, either null for no norm; tab: (cos, sin) of
+// the rot / 2 angles per row of B, which are also the query rows). Source A's keys are already rotated.
+struct dj_attn_qkn {
+  const uint16_t *qn, *kn;
+  const float2 *tab;
+  float eps;
+};
 int dj_launch_attention(dj_ctx *c, int T, int heads, int kv, int D, const uint16_t *Q, int q_stride, dj_kv_src A,
                         dj_kv_src B, const int32_t *rng, float scale, uint16_t *O, float *ws, size_t ws_floats,
-                        dj_attn_gate gate = dj_attn_gate{nullptr, 0});
+                        dj_attn_gate gate = dj_attn_gate{nullptr, 0}, const dj_attn_qkn *qkn = nullptr);
 // Mean of each sequence's rows of X [T, H] into out [S, H] f32 (seqs: (start, end) pairs).
 void dj_launch_mean_pool(hipStream_t s, int T, int S, int H, const uint16_t *X, const uint32_t *seqs, float *out);
 // Takes the device address of the static attention scratch on the current device into c->attn_scratch.
@@ -233,35 +241,53 @@ __device__ __forceinline__ float group_sum(float v) {
   v += dpp_f<0x4E>(v);
   return v + dpp_f<0xB1>(v);
 }
+// QK_NORM_ROPE's arithmetic in three pieces, so that every kernel applying it (the standalone kernel, the qkv
+// product's epilogue, attention with the norm folded in) computes the same bits from the same inputs: the sum
+// of squares of one lane's 8 rotation pairs (x[i], y[i]), the row's 1 / rms from the row's sum, and the
+// normalized, weighted, rotated pairs. Every fused multiply-add is written out, and each f32 result is rounded
+// to f32 before its conversion to f16 (f32_rounded): left to itself the compiler contracts either product of
+// a rotation, or folds the conversion into a mixed-precision fma that rounds once, differently per kernel.
+__device__ __forceinline__ float f32_rounded(float v) {
+  asm("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ float pair_sumsq(h8 x, h8 y) {
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss += __builtin_fmaf((float)x[i], (float)x[i], (float)y[i] * (float)y[i]);
+  return ss;
+}
+__device__ __forceinline__ float norm_inv(float ss, bool norm, int D, float eps) {
+  return norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
+}
+template <typename CS>
+__device__ __forceinline__ h8x2 norm_rope_pairs(h8 x, h8 y, h8 wx, h8 wy, bool has_w, bool rope, float inv, CS cs) {
+  h8 xo, yo;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float a = (float)x[i] * inv, b = (float)y[i] * inv;
+    if (has_w) {
+      a *= (float)wx[i];
+      b *= (float)wy[i];
+    }
+    if (rope) {
+      const float2 r = cs(i);
+      const float a2 = __builtin_fmaf(a, r.x, -(b * r.y)), b2 = __builtin_fmaf(b, r.x, a * r.y);
+      a = a2;
+      b = b2;
+    }
+    xo[i] = (_Float16)f32_rounded(a);
+    yo[i] = (_Float16)f32_rounded(b);
+  }
+  return {xo, yo};
+}
 template <int LPH, typename CS>
 __device__ __forceinline__ h8x2 norm_rope_lane(h8 x, h8 y, h8 wx, h8 wy, bool has_w, bool norm, bool rope, bool pl, int D,
                                                float eps, CS cs) {
-  h8 xo = {}, yo = {};
-  float ss = 0.f;
+  const float inv = norm_inv(group_sum<LPH>(pair_sumsq(x, y)), norm, D, eps);
+  if (pl) return norm_rope_pairs(x, y, wx, wy, has_w, rope, inv, cs);
+  h8 xo;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) ss += (float)x[i] * (float)x[i] + (float)y[i] * (float)y[i];
-  ss = group_sum<LPH>(ss);
-  const float inv = norm ? 1.0f / sqrtf(ss / (float)D + eps) : 1.f;
-  if (pl) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float a = (float)x[i] * inv, b = (float)y[i] * inv;
-      if (has_w) {
-        a *= (float)wx[i];
-        b *= (float)wy[i];
-      }
-      if (rope) {
-        const float2 r = cs(i);
-        const float a2 = a * r.x - b * r.y, b2 = b * r.x + a * r.y;
-        a = a2;
-        b = b2;
-      }
-      xo[i] = (_Float16)a;
-      yo[i] = (_Float16)b;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) xo[i] = (_Float16)(has_w ? (float)x[i] * inv * (float)wx[i] : (float)x[i] * inv);
-  }
-  return {xo, yo};
+  for (int i = 0; i < 8; ++i) xo[i] = (_Float16)f32_rounded(has_w ? (float)x[i] * inv * (float)wx[i] : (float)x[i] * inv);
+  return {xo, (h8){}};
 }

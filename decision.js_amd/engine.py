@@ -302,6 +302,16 @@ class DecoderEngine(GpuEngine):
         env = os.environ.get("DJ_FUSED_NORMS")
         want = self.opts.get("fused_norms", self.FUSED_DEFAULT if env is None else env != "0")
         self.fused_norms = bool(want) and self.H % 128 == 0 and self.H <= 1024
+        # a short question on a kept state (QK_ROWS rows): q/k norm + RoPE in the attention kernel
+        # (dj_attention_qk_rope) after a plain qkv product, one kernel fewer per layer. opts qk_attention, else
+        # DJ_ATTN_QK_ROPE=0/1, else on (128-dim heads).
+        env = os.environ.get("DJ_ATTN_QK_ROPE")
+        want = self.opts.get("qk_attention", True if env is None else env != "0")
+        self.qk_attention = bool(want) and self.D == 128
+
+    # Rows up to which a question on a kept state takes dj_attention_qk_rope: the skinny (GEMV) products' rows,
+    # where the standalone q/k norm kernel is a fixed cost of its own.
+    QK_ROWS = 64
 
     # Where the folded norms pay: at 65-8192 rows the products' epilogues cost less than the separate norm
     # kernels they replace (a 3 x 384-id ticket: 2.49 against 2.56 ms); past that the extra epilogue traffic and
@@ -340,6 +350,7 @@ class DecoderEngine(GpuEngine):
         src = _dj.kv_src(z, T, self.stride, h * D, (h + kv) * D)
         fused = self.fused_norms and self.FUSED_ROWS[0] <= T <= self.FUSED_ROWS[1] and "xw" in B
         pending = False  # the next product reads B["xw"] / B["ss"] (a folded norm) instead of B["normed"]
+        qk_attention = self.qk_attention and T <= self.QK_ROWS and kv_a is not None and kv_store is None and not fused
         rec.gather_q(B["ids"], T, w["embed"], B["x"])
         rec.add_rmsnorm(T, H, False, eps, B["x"], B["o"], w["layers.0.operator_norm"], B["normed"])
         # the RoPE angles of this forward, once; every layer's qkv product applies q/k norm + RoPE with them
@@ -353,6 +364,11 @@ class DecoderEngine(GpuEngine):
                     rec.matmul(B["normed"], w[p + "in_proj"], z, T)
                 rec.short_conv(T, H, z, w[p + "conv"], B["taps"], B["y"])
                 second = w[p + "out_proj"]
+            elif qk_attention:  # the kept state's keys are rotated already; the question's own are raw
+                rec.matmul(B["normed"], w[p + "qkv"], z, T)
+                rec.attention_qk_rope(T, h, kv, D, z, self.stride, kv_a(i), src, B["rng"], 1.0 / math.sqrt(D),
+                                      w.get(p + "q_norm"), w.get(p + "k_norm"), eps, B["rope"], B["y"])
+                second = w[p + "o_proj"]
             else:
                 if pending:
                     rec.matmul_qkv_rope_normed(B["xw"], w[p + "qkv"], z, T, h, kv, D, w.get(p + "q_norm"),

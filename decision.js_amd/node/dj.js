@@ -139,6 +139,9 @@ class Recorder {
   attention(T, heads, kv, D, Q, qStride, A, B, rng, scale, O) {
     lib().attention(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, O);
   }
+  attentionQkRope(T, heads, kv, D, Q, qStride, A, B, rng, scale, qn, kn, eps, tab, O, rot = D) {
+    lib().attentionQkRope(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, qn, kn, eps, tab, rot, O);
+  }
   attentionGated(T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O) {
     lib().attentionGated(this.h, T, heads, kv, D, Q, qStride, A, B, rng, scale, G, gStride, O);
   }

@@ -484,6 +484,12 @@ napi_value AttentionNoalloc(napi_env env, napi_callback_info info) {
   const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
   END(dj_attention_noalloc(R(0), I(1), I(2), I(3), I(4), P16(5), I(6), a, b, PI32(9), F(10), P16(11)));
 }
+napi_value AttentionQkRope(napi_env env, napi_callback_info info) {
+  BEGIN(17);
+  const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
+  END(dj_attention_qk_rope(R(0), I(1), I(2), I(3), I(4), P16(5), I(6), a, b, PI32(9), F(10), P16(11), P16(12), F(13),
+                           PF32(14), I(15), P16(16)));
+}
 napi_value AttentionGated(napi_env env, napi_callback_info info) {
   BEGIN(14);
   const dj_kv_src a = kvsrc(c, 7), b = kvsrc(c, 8);
@@ -570,7 +576,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"timerBegin", TimerBegin}, {"timerEnd", TimerEnd},
       {"profileEnable", ProfileEnable}, {"profileGet", ProfileGet}, {"profileReset", ProfileReset},
       {"gatherQ", GatherQ}, {"addRmsnorm", AddRmsnorm}, {"sandwich", Sandwich}, {"matmul", Matmul},
-      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"matmulResidual", MatmulResidual}, {"matmulNormed", MatmulNormed}, {"matmulQkvRopeNormed", MatmulQkvRopeNormed}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"kvStore", KvStore},
+      {"matmulGlu", MatmulGlu}, {"qkNormRope", QkNormRope}, {"ropeTable", RopeTable}, {"matmulQkvRope", MatmulQkvRope}, {"matmulResidual", MatmulResidual}, {"matmulNormed", MatmulNormed}, {"matmulQkvRopeNormed", MatmulQkvRopeNormed}, {"attention", Attention}, {"attentionNoalloc", AttentionNoalloc}, {"attentionQkRope", AttentionQkRope}, {"kvStore", KvStore},
       {"leafLogits", LeafLogits}, {"readout", Readout}, {"shortConv", ShortConv}, {"attentionGated", AttentionGated}, {"gdn", Gdn}, {"pleMix", PleMix},
       {"poolProject", PoolProject}, {"addRows", AddRows}, {"biasAct", BiasAct},
       {"addLayernorm", AddLayernorm}, {"gatherRows", GatherRows}, {"score", Score}, {"meanPool", MeanPool}, {"denseF32", DenseF32},

@@ -234,6 +234,11 @@ class DecoderEngine extends GpuEngine {
     const env = process.env.DJ_FUSED_NORMS;
     const want = fo !== undefined ? !!fo : env !== undefined ? env !== "0" : this.constructor.fusedDefault;
     this.fusedNorms = want && this.H % 128 === 0 && this.H <= 1024;
+    // a short question on a kept state (up to 64 rows): q/k norm + RoPE in the attention kernel
+    // (dj_attention_qk_rope) after a plain qkv product: opts.qkAttention, else DJ_ATTN_QK_ROPE=0/1, else on
+    const qo = this.opts.qkAttention !== undefined ? this.opts.qkAttention : this.opts.qk_attention;
+    const qenv = process.env.DJ_ATTN_QK_ROPE;
+    this.qkAttention = (qo !== undefined ? !!qo : qenv !== undefined ? qenv !== "0" : true) && this.D === 128;
   }
 
   /** The folded norms' buffers: the norm-weighted residual rows and their per-32-column sums of squares. */
@@ -271,6 +276,7 @@ class DecoderEngine extends GpuEngine {
     const [lo, hi] = this.constructor.fusedRows;
     const fused = this.fusedNorms && T >= lo && T <= hi && !!B.xw;
     let pending = false; // the next product reads B.xw / B.ss (a folded norm) instead of B.normed
+    const qkAttention = this.qkAttention && T <= 64 && !!kvA && !kvStore && !fused;
     for (let i = 0; i < this.layers; ++i) {
       const p = `layers.${i}.`;
       let second;
@@ -279,6 +285,11 @@ class DecoderEngine extends GpuEngine {
         else rec.matmul(B.normed.ptr, w[p + "in_proj"], z, T);
         rec.shortConv(T, H, z, ptr(p + "conv"), B.taps.ptr, B.y.ptr);
         second = w[p + "out_proj"];
+      } else if (qkAttention) { // the kept state's keys are rotated already; the question's own are raw
+        rec.matmul(B.normed.ptr, w[p + "qkv"], z, T);
+        rec.attentionQkRope(T, h, kv, D, z, this.stride, kvA(i), src, B.rng.ptr, 1 / Math.sqrt(D), ptr(p + "q_norm"),
+          ptr(p + "k_norm"), eps, B.rope.ptr, B.y.ptr);
+        second = w[p + "o_proj"];
       } else {
         if (pending)
           rec.matmulQkvRopeNormed(B.xw.ptr, w[p + "qkv"], z, T, h, kv, D, ptr(p + "q_norm"), ptr(p + "k_norm"), false, B.pos.ptr, 1,

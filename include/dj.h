@@ -261,6 +261,17 @@ typedef struct { const uint16_t *base; int rows; int stride; int k_col; int v_co
 int dj_attention(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
                  dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, uint16_t *O_dev);
 
+/* QK_NORM_ROPE (kernels.ts:86-112) on the query heads of Q and the key heads of source B, folded into
+ * dj_attention (kernels.ts:114-147), i.e. the pair of dispatches at d1-3b-engine.ts:95-96: the same results as dj_qk_norm_rope(T, heads, kv, 128, stride, Z, qn, kn,
+ * 0, pos, ...) on the fused rows, then dj_attention, except that Z keeps its raw q and k values. The angles come
+ * from tab_dev (dj_rope_table of the same T rows and positions, rot 128); source B must be the T query rows
+ * themselves (kvB.rows == T, its row t rotated with tab row t) and source A already normalized and rotated (a
+ * kept state). D = rot = 128 (else DJ_EINVAL). The short-question form of the forward: the qkv product then
+ * this, one launch fewer per layer than dj_qk_norm_rope + dj_attention. */
+int dj_attention_qk_rope(dj_rec *rec, int T, int heads, int kv, int D, const uint16_t *Q_dev, int q_stride,
+                         dj_kv_src kvA, dj_kv_src kvB, const int32_t *rng_dev, float scale, const uint16_t *qn_dev,
+                         const uint16_t *kn_dev, float eps, const float *tab_dev, int rot, uint16_t *O_dev);
+
 /* dj_attention that allocates nothing, for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid it). No counterpart in the reference. Same arguments and
  * results as dj_attention; its split-KV partials (a short question against a long kept state) live in the

@@ -774,6 +774,75 @@ def test_attention_kept_prefix(pkg, ctx, monkeypatch, P, splits, hg):
     assert np.abs(got - want).max() < 4e-3
 
 
+@pytest.mark.parametrize("T,P,qk,splits", [(32, 1056, True, None), (32, 1056, False, None), (17, 300, True, None),
+                                           (64, 1100, True, 4), (64, 1100, True, 1), (1, 700, True, None)])
+def test_attention_qk_rope_equals_norm_then_attention(pkg, ctx, monkeypatch, T, P, qk, splits):
+    """dj_attention_qk_rope on raw q/k rows against a kept state == dj_qk_norm_rope on the rows then
+    dj_attention, bit for bit (the same arithmetic in the same order, the row sums added in the standalone
+    kernel's lane order), with and without norm weights, split over workgroups by default, forced to 4 and off;
+    the rows keep their raw values. The result is also the oracle's attention of the oracle-normalized rows."""
+    if splits is not None:
+        monkeypatch.setenv("DJ_ATTN_SPLITS", str(splits))
+    dj = _dj()
+    rng = np.random.default_rng(T * 7 + P)
+    heads, kv, D, theta = 12, 2, 128, 1e6
+    stride = (heads + 2 * kv) * D
+    Z = rand_f16(rng, (T, stride))
+    cache = rand_f16(rng, (P, 2 * kv * D))  # a kept state's rotated K / V rows (any values)
+    pos = (P + np.arange(T)).astype(np.int32)
+    qn, kn = (1 + rng.standard_normal(D) * 0.1).astype(np.float16), (1 + rng.standard_normal(D) * 0.1).astype(np.float16)
+    rng4 = np.array([(0, P, 0, t + 1) for t in range(T)], dtype=np.int32)  # the whole state, causal question
+    dZ, dZ2, dC, drng, dpos = ctx.array(Z), ctx.array(Z), ctx.array(cache), ctx.array(rng4), ctx.array(pos)
+    dq, dk = (ctx.array(qn), ctx.array(kn)) if qk else (None, None)
+    dtab, dO1, dO2 = ctx.alloc(T * (D // 2) * 8), ctx.alloc(T * heads * D * 2), ctx.alloc(T * heads * D * 2)
+    A = dj.kv_src(dC, P, 2 * kv * D, 0, kv * D)
+    B1 = dj.kv_src(dZ, T, stride, heads * D, (heads + kv) * D)
+    B2 = dj.kv_src(dZ2, T, stride, heads * D, (heads + kv) * D)
+    scale = 1 / math.sqrt(D)
+
+    def fused(r):
+        r.rope_table(T, dpos, 1, theta, D, dtab)
+        r.attention_qk_rope(T, heads, kv, D, dZ, stride, A, B1, drng, scale, dq, dk, 1e-6, dtab, dO1)
+
+    def separate(r):
+        r.qk_norm_rope(T, heads, kv, D, stride, dZ2, dq, dk, False, dpos, 1, 1e-6, theta)
+        r.attention(T, heads, kv, D, dZ2, stride, A, B2, drng, scale, dO2)
+
+    run(ctx, fused)
+    run(ctx, separate)
+    got, want = dO1.read(np.float16, (T, heads * D)), dO2.read(np.float16, (T, heads * D))
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64)).max()
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16)), f"max |fused - separate| {diff:.3e}"
+    assert np.array_equal(dZ.read(np.float16, (T, stride)).view(np.uint16), Z.view(np.uint16))  # rows kept raw
+    Zn = ref.qk_norm_rope(Z, heads, kv, D, pos, qn if qk else None, kn if qk else None, False, 1e-6, theta, None, 0,
+                          np.float64)
+    kvrows = np.concatenate([cache, Zn[:, heads * D:(heads + 2 * kv) * D].astype(np.float16)])
+    mask = np.zeros((T, P + T), dtype=bool)
+    for t, (a0, a1, b0, b1) in enumerate(rng4):
+        mask[t, a0:a1] = True
+        mask[t, P + b0:P + b1] = True
+    oracle = ref.attention(Zn.astype(np.float16), heads, kv, D, mask, scale, np.float64, kv_rows=kvrows)
+    assert np.abs(got.astype(np.float64) - oracle).max() < 4e-3
+
+
+def test_attention_qk_rope_refuses_other_shapes(pkg, ctx):
+    """The folded form is 128-dim heads fully rotated, with source B the query rows: other shapes are refused
+    before anything is launched."""
+    dj = _dj()
+    heads, kv, T = 4, 2, 8
+    for D, rot, brows, msg in ((64, 64, T, "head dim"), (128, 64, T, "head dim"), (128, 128, T + 1, "source B")):
+        stride = (heads + 2 * kv) * D
+        dZ, dO, dtab = ctx.alloc((T + 1) * stride * 2), ctx.alloc(T * heads * D * 2), ctx.alloc(T * D * 8)
+        drng = ctx.array(np.array([(0, 0, 0, t + 1) for t in range(T)], dtype=np.int32))
+        src = dj.kv_src(dZ, brows, stride, heads * D, (heads + kv) * D)
+        rec = ctx.recorder()
+        try:
+            with pytest.raises(dj.DJError, match=msg):
+                rec.attention_qk_rope(T, heads, kv, D, dZ, stride, src, src, drng, 0.1, None, None, 1e-6, dtab, dO, rot=rot)
+        finally:
+            rec.finish()
+
+
 def test_attention_rejects_nonpositive_scale(pkg, ctx):
     """The kernel takes the row max on raw scores (it commutes with a positive scale): a scale <= 0 is refused
     before anything is launched."""

@@ -217,6 +217,37 @@ def test_shared_state_equals_forest(pkg, models):
         eng.destroy()
 
 
+def test_question_alone_qk_attention(pkg, models):
+    """A 32-token question alone on a kept state (configs[4]'s weight-streaming form): with q/k norm + RoPE in
+    the attention kernel (dj_attention_qk_rope after a plain qkv product, the default) the answers equal those
+    of the separate QK_NORM_ROPE kernel bit for bit, on eager runs and graph replays, and the oracle's."""
+    from decision_js_amd.engine import DecoderEngine
+    model = ref.Model(models["shared"])
+    rng = np.random.default_rng(11)
+    V = model.c["vocab"]
+    tree = _tree(rng, V, 1024, [32])
+    got = {}
+    for on in (True, False):
+        eng = DecoderEngine.load(models["shared"], {"qk_attention": on})
+        try:
+            assert eng.qk_attention == on
+            st = eng.prefill(tree["trunk"])
+            eng.ctx.profile_reset()
+            eng.ctx.profile(True)
+            got[on] = [eng.run_shared(st, tree["branches"], tree["groups"])]  # eager (its key's first use)
+            eng.ctx.profile(False)
+            names = " ".join(eng.ctx.profile_table())
+            assert ("attention_qk_rope[" in names) == on and ("attention[" in names) != on, names
+            got[on] += [eng.run_shared(st, tree["branches"], tree["groups"]) for _ in range(2)]  # capture, replay
+            st.free()
+        finally:
+            eng.destroy()
+    assert got[True][0] == got[True][1] == got[True][2] == got[False][0] == got[False][2]
+    want, _ = _oracle_forest(model, [tree])
+    for s, w in zip(got[True][0], want[0]):
+        assert max(abs(a - b) for a, b in zip(ref.softmax(s), ref.softmax(w))) < PROB_TOL
+
+
 def test_fused_norms_match_oracle_and_separate_norms(pkg, models):
     """The residual add + RMSNorm folded into the products (dj_matmul_residual, dj_matmul_normed,
     dj_matmul_qkv_rope_normed) against the separate norm kernel, on a decoder forest (attention layers) and on
