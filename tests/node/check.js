@@ -50,6 +50,20 @@ async function main(req) {
         d.destroy();
       }
     }
+    case "question": {
+      // one short question on a prefilled state, through DecoderEngine.runShared: its scores on three runs
+      // (eager, capture, replay)
+      const e = await host.DecoderEngine.load(req.model, req.opts || {});
+      try {
+        const st = await e.prefill(req.state);
+        const runs = [];
+        for (let k = 0; k < 3; ++k) runs.push(await e.runShared(st, req.branches, req.groups));
+        e.freeState(st);
+        return { qkAttention: e.qkAttention, runs };
+      } finally {
+        e.destroy();
+      }
+    }
     case "logits": {
       const e = await host.DecoderEngine.load(req.model, req.opts || {});
       try {

@@ -276,6 +276,37 @@ def test_graph_keys_from_second_use_match_python_host():
 
 
 @pytest.mark.gpu
+def test_node_question_alone_matches_python_host(tmp_path):
+    """One 24-token question on a prefilled 300-token state through each host's DecoderEngine: with the q/k
+    norm folded into attention (the default for at most 64 rows) and without it, the Node host's scores equal
+    the Python host's bit for bit, on eager runs, graph capture and replay alike."""
+    load_pkg()
+    from decision_js_amd import synth
+    from decision_js_amd.engine import DecoderEngine
+    mdir = synth.generate(synth.reduced("qwen3-0.6b-q8", layers=3, vocab=4096), str(tmp_path / "m"), seed=2, norm_std=0.1)
+    rng = np.random.default_rng(9)
+    state = [int(x) for x in rng.integers(0, 4096, 300)]
+    branches = [[int(x) for x in rng.integers(0, 4096, 24)]]
+    groups = [[[int(a)] for a in rng.choice(4096, 4, replace=False)]]
+    py = {}
+    for on in (True, False):
+        eng = DecoderEngine.load(mdir, {"qk_attention": on})
+        try:
+            st = eng.prefill(state)
+            py[on] = eng.run_shared(st, branches, groups)
+            st.free()
+        finally:
+            eng.destroy()
+    assert py[True] == py[False]
+    for on in (True, False):
+        js = node({"cmd": "question", "model": mdir, "state": state, "branches": branches, "groups": groups,
+                   "opts": {"qkAttention": on}}, timeout=300)
+        assert js["qkAttention"] == on
+        for run in js["runs"]:
+            assert run == py[True]
+
+
+@pytest.mark.gpu
 def test_node_encoder_matches_python_host(tmp_path):
     """The EmbeddingGemma-shaped encoder through the Node host (D1 kind "eg2", runEg2 with the learned decision
     head) against the Python host: the same embeddings and probabilities, progress through BatchOptions, and
